@@ -1,0 +1,83 @@
+"""Builds libgnn_hip.so (the gfx950 HIP kernels + C ABI) in-tree.
+
+Usage: python geometric-nn-ops_amd/build.py [--jobs N]
+
+Each csrc/*.hip file is compiled to an object in parallel with hipcc for gfx950 only,
+then linked into geometric_nn_ops_torch/_lib/libgnn_hip.so, which the package loads
+with ctypes. Always recompiles (it is the "does it build" check).
+"""
+
+import argparse
+import concurrent.futures
+import os
+import pathlib
+import shutil
+import subprocess
+import sys
+
+HERE = pathlib.Path(__file__).resolve().parent
+REPO = HERE.parent
+CSRC = HERE / "csrc"
+INCLUDE = REPO / "include"
+OUT_DIR = HERE / "geometric_nn_ops_torch" / "_lib"
+LIB = OUT_DIR / "libgnn_hip.so"
+BUILD_DIR = HERE / "_build"
+
+ARCH = "gfx950"
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    # Packed fp32 VALU ops stay off: hipcc would otherwise form v_pk_{add,mul,fma}_f32
+    # from ordinary float code.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{INCLUDE}",
+    f"-I{CSRC}",
+]
+
+
+def hipcc() -> str:
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    path = pathlib.Path(rocm) / "bin" / "hipcc"
+    if path.exists():
+        return str(path)
+    found = shutil.which("hipcc")
+    if not found:
+        raise RuntimeError("hipcc not found (set ROCM_PATH)")
+    return found
+
+
+def _compile(src: pathlib.Path) -> pathlib.Path:
+    obj = BUILD_DIR / (src.stem + ".o")
+    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    return obj
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> pathlib.Path:
+    BUILD_DIR.mkdir(exist_ok=True)
+    OUT_DIR.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    jobs = jobs or min(len(sources), os.cpu_count() or 1, 16)
+    with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
+        objs = list(pool.map(_compile, sources))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=None)
+    args = ap.parse_args()
+    build(args.jobs, verbose=True)
+    sys.exit(0)

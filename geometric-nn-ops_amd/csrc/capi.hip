@@ -1,0 +1,104 @@
+// extern "C" entry points of libgnn_hip.so (declared in include/gnn_triangle.h): argument
+// validation, the thread-local error message, and dispatch to the kernel launchers.
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "gnn_internal.hpp"
+
+namespace gnn {
+
+static thread_local std::string g_last_error;
+
+int set_error(int code, const char* msg) {
+  g_last_error = msg;
+  return code;
+}
+
+static int hip_status(hipError_t e, const char* who) {
+  if (e == hipSuccess) return GNN_OK;
+  char buf[256];
+  snprintf(buf, sizeof buf, "%s: HIP error %d (%s)", who, (int)e, hipGetErrorString(e));
+  g_last_error = buf;
+  return (int)e;
+}
+
+static bool aligned(const void* p, size_t n) { return ((uintptr_t)p % n) == 0; }
+
+static int check_triattn(const gnn_triattn_args& a) {
+  if (!a.q || !a.k || !a.v || !a.o)
+    return set_error(GNN_ERR_ARG, "triangle_attention: q, k, v and o are required");
+  if (a.B < 1 || a.S < 1 || a.N < 1 || a.H < 1 || a.D < 1)
+    return set_error(GNN_ERR_ARG, "triangle_attention: B, N_seq, N_res, H and D must be positive");
+  if (a.dtype != GNN_BF16 && a.dtype != GNN_F16 && a.dtype != GNN_F32)
+    return set_error(GNN_ERR_ARG, "triangle_attention: unknown dtype");
+  if (a.D % 8 != 0)
+    return set_error(GNN_ERR_ARG, "triangle_attention: D must be a multiple of 8 (pad on the host)");
+  const int64_t* st[4] = {a.q_stride, a.k_stride, a.v_stride, a.o_stride};
+  const void* ptr[4] = {a.q, a.k, a.v, a.o};
+  for (int t = 0; t < 4; ++t) {
+    if (!aligned(ptr[t], 16))
+      return set_error(GNN_ERR_ARG, "triangle_attention: q/k/v/o must be 16-byte aligned");
+    for (int d = 0; d < 4; ++d)
+      if (st[t][d] % 8 != 0)
+        return set_error(GNN_ERR_ARG, "triangle_attention: q/k/v/o strides must be multiples of 8 elements");
+  }
+  if (a.bias) {
+    if (a.bias_stride[3] != 1 || a.bias_stride[2] % 8 != 0 || !aligned(a.bias, 16))
+      return set_error(GNN_ERR_ARG,
+                       "triangle_attention: bias needs unit key stride, a query stride that is a multiple "
+                       "of 8 and 16-byte alignment");
+  }
+  return GNN_OK;
+}
+
+}  // namespace gnn
+
+using namespace gnn;
+
+extern "C" {
+
+int gnn_triattn_fwd(const gnn_triattn_args* args, void* stream) {
+  if (!args) return set_error(GNN_ERR_ARG, "triangle_attention: args is NULL");
+  if (int rc = check_triattn(*args)) return rc;
+  int rc = triattn_fwd(*args, (hipStream_t)stream);
+  if (rc < 0) return rc;
+  return hip_status((hipError_t)rc, "triangle_attention");
+}
+
+size_t gnn_trimul_workspace_bytes(int64_t B, int64_t N, int64_t C, int64_t Ch, int32_t dtype,
+                                  size_t off[4]) {
+  const TrimulLayout L = trimul_layout(B, N, C, Ch, dtype);
+  if (off) {
+    off[0] = L.off_a;
+    off[1] = L.off_b;
+    off[2] = L.off_g;
+    off[3] = L.off_o;
+  }
+  return L.total;
+}
+
+static int trimul_stage(const gnn_trimul_args* args, void* stream, int which) {
+  if (!args) return set_error(GNN_ERR_ARG, "trimul: args is NULL");
+  hipStream_t st = (hipStream_t)stream;
+  int rc = GNN_OK;
+  if (which & 1) rc = trimul_proj(*args, st);
+  if (rc == GNN_OK && (which & 2)) rc = trimul_contract(*args, st);
+  if (rc == GNN_OK && (which & 4)) rc = trimul_out(*args, st);
+  if (rc < 0) return rc;
+  return hip_status((hipError_t)rc, "trimul");
+}
+
+int gnn_trimul_fwd(const gnn_trimul_args* args, void* stream) { return trimul_stage(args, stream, 7); }
+int gnn_trimul_proj(const gnn_trimul_args* args, void* stream) { return trimul_stage(args, stream, 1); }
+int gnn_trimul_contract(const gnn_trimul_args* args, void* stream) {
+  return trimul_stage(args, stream, 2);
+}
+int gnn_trimul_out(const gnn_trimul_args* args, void* stream) { return trimul_stage(args, stream, 4); }
+
+const char* gnn_last_error(void) { return g_last_error.c_str(); }
+
+const char* gnn_version(void) { return "0.1.0 gfx950"; }
+
+}  // extern "C"

@@ -1,0 +1,182 @@
+// Shared device helpers for the gfx950 (CDNA4) triangle kernels.
+//
+// Every matrix product in this library is issued as 32x32 output tiles on the
+// 32x32xK MFMA units. The common currency is a "fragment": for one K=16 step of a
+// 32x32 tile, lane l holds 8 consecutive-k elements of row (l % 32) of its operand,
+// lane group g = l / 32 holding k = 8g .. 8g+7. A and B fragments use the same
+// (lane group, element) -> k assignment, so the product is correct for whichever
+// concrete k order the hardware uses inside one instruction, and callers may map
+// logical k indices onto (g, element) any way they like as long as A and B agree.
+//
+// The 32x32 fp32 accumulator (16 VGPRs) holds, in lane l and register r,
+//   row = 8 * (r / 4) + 4 * (l / 32) + (r % 4),   col = l % 32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gnn {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+enum Prec { PREC_NATIVE = 0, PREC_IEEE = 1, PREC_BF16X3 = 2 };
+
+// ---- element-type traits ------------------------------------------------------------
+template <typename T> struct TypeOps;
+
+template <> struct TypeOps<bf16> {
+  typedef bf16x8 V8;
+  typedef bf16x4 V4;
+  static __device__ __forceinline__ V8 from_f32(const f32x8& x) {
+    return __builtin_convertvector(x, bf16x8);
+  }
+  static __device__ __forceinline__ V4 from_f32(const f32x4& x) {
+    return __builtin_convertvector(x, bf16x4);
+  }
+  static __device__ __forceinline__ f32x8 to_f32(const V8& x) {
+    return __builtin_convertvector(x, f32x8);
+  }
+  static __device__ __forceinline__ f32x4 to_f32(const V4& x) {
+    return __builtin_convertvector(x, f32x4);
+  }
+  static __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+  static __device__ __forceinline__ bf16 from_f32(float x) { return (bf16)x; }
+};
+
+template <> struct TypeOps<f16> {
+  typedef f16x8 V8;
+  typedef f16x4 V4;
+  static __device__ __forceinline__ V8 from_f32(const f32x8& x) {
+    return __builtin_convertvector(x, f16x8);
+  }
+  static __device__ __forceinline__ V4 from_f32(const f32x4& x) {
+    return __builtin_convertvector(x, f16x4);
+  }
+  static __device__ __forceinline__ f32x8 to_f32(const V8& x) {
+    return __builtin_convertvector(x, f32x8);
+  }
+  static __device__ __forceinline__ f32x4 to_f32(const V4& x) {
+    return __builtin_convertvector(x, f32x4);
+  }
+  static __device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
+  static __device__ __forceinline__ f16 from_f32(float x) { return (f16)x; }
+};
+
+template <> struct TypeOps<float> {
+  typedef f32x8 V8;
+  typedef f32x4 V4;
+  static __device__ __forceinline__ V8 from_f32(const f32x8& x) { return x; }
+  static __device__ __forceinline__ V4 from_f32(const f32x4& x) { return x; }
+  static __device__ __forceinline__ f32x8 to_f32(const V8& x) { return x; }
+  static __device__ __forceinline__ f32x4 to_f32(const V4& x) { return x; }
+  static __device__ __forceinline__ float to_f32(float x) { return x; }
+  static __device__ __forceinline__ float from_f32(float x) { return x; }
+};
+
+// ---- vector memory access ---------------------------------------------------------------
+// 8 consecutive elements (16 B for 16-bit types, 32 B for fp32). Pointer must be aligned
+// to the vector size (the host checks base pointers and strides).
+template <typename T>
+__device__ __forceinline__ typename TypeOps<T>::V8 load8(const T* p) {
+  return *reinterpret_cast<const typename TypeOps<T>::V8*>(p);
+}
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const typename TypeOps<T>::V8& v) {
+  *reinterpret_cast<typename TypeOps<T>::V8*>(p) = v;
+}
+template <typename T>
+__device__ __forceinline__ typename TypeOps<T>::V4 load4(const T* p) {
+  return *reinterpret_cast<const typename TypeOps<T>::V4*>(p);
+}
+template <typename T>
+__device__ __forceinline__ void store4(T* p, const typename TypeOps<T>::V4& v) {
+  *reinterpret_cast<typename TypeOps<T>::V4*>(p) = v;
+}
+template <typename T>
+__device__ __forceinline__ typename TypeOps<T>::V8 zero8() {
+  return TypeOps<T>::from_f32(f32x8{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f});
+}
+
+// ---- 32x32 tile, one K=16 step ----------------------------------------------------------
+// acc[row, col] += sum_k A[row, k] * B[k, col] over the 16 k of this step, with both
+// operands given as fragments (see the file comment).
+template <typename T, int PREC> struct Mma;
+
+template <> struct Mma<bf16, PREC_NATIVE> {
+  static __device__ __forceinline__ void step(f32x16& acc, const bf16x8& a, const bf16x8& b) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+  }
+};
+
+template <> struct Mma<f16, PREC_NATIVE> {
+  static __device__ __forceinline__ void step(f32x16& acc, const f16x8& a, const f16x8& b) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
+  }
+};
+
+// Full fp32: eight K=2 fp32 MFMAs; instruction e consumes element e of both fragments.
+template <> struct Mma<float, PREC_IEEE> {
+  static __device__ __forceinline__ void step(f32x16& acc, const f32x8& a, const f32x8& b) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], b[e], acc, 0, 0, 0);
+  }
+};
+
+// bf16x3 emulation of an fp32 product: x = hi + lo with hi = bf16(x), lo = bf16(x - hi);
+// a*b ~= hi_a*hi_b + hi_a*lo_b + lo_a*hi_b (the lo*lo term is dropped), accumulated in fp32.
+__device__ __forceinline__ void split_bf16(const f32x8& x, bf16x8& hi, bf16x8& lo) {
+  hi = __builtin_convertvector(x, bf16x8);
+  f32x8 r = x - __builtin_convertvector(hi, f32x8);
+  lo = __builtin_convertvector(r, bf16x8);
+}
+
+template <> struct Mma<float, PREC_BF16X3> {
+  static __device__ __forceinline__ void step(f32x16& acc, const f32x8& a, const f32x8& b) {
+    bf16x8 ah, al, bh, bl;
+    split_bf16(a, ah, al);
+    split_bf16(b, bh, bl);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, acc, 0, 0, 0);
+  }
+};
+
+// ---- misc -------------------------------------------------------------------------------
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Value held by lane (l ^ 32).
+__device__ __forceinline__ float swap_halves(float x) {
+  int v = __builtin_bit_cast(int, x);
+  return __builtin_bit_cast(float, __builtin_amdgcn_permlane32_swap(v, v, false, false)[0]);
+}
+
+__device__ __forceinline__ float sigmoidf_fast(float x) {
+  return 1.0f / (1.0f + fast_exp2(-x * 1.4426950408889634f));
+}
+
+// MI355X dispatches consecutive workgroup ids round-robin over its 8 XCDs, each with a
+// private L2. Remap so that the workgroups resident on one XCD take a contiguous range
+// of the logical work order (a bijection for any grid size).
+__device__ __forceinline__ uint32_t xcd_remap(uint32_t bid, uint32_t nblk) {
+  constexpr uint32_t NXCD = 8;
+  const uint32_t xcd = bid % NXCD;
+  const uint32_t idx = bid / NXCD;
+  const uint32_t per = (nblk + NXCD - 1) / NXCD;  // blocks on the fuller XCDs
+  uint32_t tall = nblk % NXCD;
+  if (tall == 0) tall = NXCD;
+  if (xcd < tall) return xcd * per + idx;
+  return tall * per + (xcd - tall) * (per - 1) + idx;
+}
+
+}  // namespace gnn

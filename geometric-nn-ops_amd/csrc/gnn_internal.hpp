@@ -1,0 +1,25 @@
+// Host-side declarations shared by the kernel translation units and the C ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "gnn_triangle.h"
+
+namespace gnn {
+
+// Records `msg` as this thread's last error and returns `code`.
+int set_error(int code, const char* msg);
+
+int triattn_fwd(const gnn_triattn_args& a, hipStream_t stream);
+
+// Workspace layout shared by the three trimul stages (byte offsets, see the C header).
+struct TrimulLayout {
+  size_t off_a, off_b, off_g, off_o, total;
+};
+TrimulLayout trimul_layout(int64_t B, int64_t N, int64_t C, int64_t Ch, int32_t dtype);
+
+int trimul_proj(const gnn_trimul_args& a, hipStream_t stream);
+int trimul_contract(const gnn_trimul_args& a, hipStream_t stream);
+int trimul_out(const gnn_trimul_args& a, hipStream_t stream);
+
+}  // namespace gnn

@@ -1,0 +1,158 @@
+"""ctypes binding of libgnn_hip.so (C ABI declared in include/gnn_triangle.h).
+
+The library is loaded lazily on first use. There is no silent fallback: if a CUDA/HIP
+tensor reaches a kernel entry point and the library is missing or fails to load, the
+call raises RuntimeError naming the path that was tried.
+"""
+
+import ctypes
+import os
+import pathlib
+import threading
+
+import torch
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libgnn_hip.so"
+
+GNN_F32, GNN_BF16, GNN_F16 = 0, 1, 2
+GNN_PREC_IEEE, GNN_PREC_BF16X3 = 0, 1
+GNN_OK, GNN_ERR_ARG, GNN_ERR_UNSUPPORTED, GNN_ERR_WORKSPACE = 0, -1, -2, -3
+
+DTYPE_CODE = {torch.float32: GNN_F32, torch.bfloat16: GNN_BF16, torch.float16: GNN_F16}
+PRECISION_CODE = {"ieee": GNN_PREC_IEEE, "bf16x3": GNN_PREC_BF16X3}
+
+I64x3 = ctypes.c_int64 * 3
+I64x4 = ctypes.c_int64 * 4
+
+
+class TriAttnArgs(ctypes.Structure):
+    """Mirror of ``gnn_triattn_args``."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("mask", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("B", ctypes.c_int64),
+        ("S", ctypes.c_int64),
+        ("N", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("D", ctypes.c_int64),
+        ("q_stride", I64x4),
+        ("k_stride", I64x4),
+        ("v_stride", I64x4),
+        ("o_stride", I64x4),
+        ("bias_stride", I64x4),
+        ("mask_stride", I64x3),
+        ("scale", ctypes.c_float),
+        ("mask_value", ctypes.c_float),
+        ("dtype", ctypes.c_int32),
+        ("precision", ctypes.c_int32),
+    ]
+
+
+class TrimulArgs(ctypes.Structure):
+    """Mirror of ``gnn_trimul_args``."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("mask", ctypes.c_void_p),
+        ("mask_stride", I64x3),
+        ("ln_in_w", ctypes.c_void_p),
+        ("ln_in_b", ctypes.c_void_p),
+        ("p_in_w", ctypes.c_void_p),
+        ("p_in_b", ctypes.c_void_p),
+        ("g_in_w", ctypes.c_void_p),
+        ("g_in_b", ctypes.c_void_p),
+        ("ln_out_w", ctypes.c_void_p),
+        ("ln_out_b", ctypes.c_void_p),
+        ("p_out_w", ctypes.c_void_p),
+        ("p_out_b", ctypes.c_void_p),
+        ("g_out_w", ctypes.c_void_p),
+        ("g_out_b", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("B", ctypes.c_int64),
+        ("N", ctypes.c_int64),
+        ("C", ctypes.c_int64),
+        ("Ch", ctypes.c_int64),
+        ("eps", ctypes.c_float),
+        ("outgoing", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("precision", ctypes.c_int32),
+    ]
+
+
+# Every symbol include/gnn_triangle.h declares, with its ctypes signature.
+_SIGNATURES = {
+    "gnn_triattn_fwd": (ctypes.c_int, [ctypes.POINTER(TriAttnArgs), ctypes.c_void_p]),
+    "gnn_trimul_workspace_bytes": (
+        ctypes.c_size_t,
+        [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
+         ctypes.POINTER(ctypes.c_size_t)],
+    ),
+    "gnn_trimul_fwd": (ctypes.c_int, [ctypes.POINTER(TrimulArgs), ctypes.c_void_p]),
+    "gnn_trimul_proj": (ctypes.c_int, [ctypes.POINTER(TrimulArgs), ctypes.c_void_p]),
+    "gnn_trimul_contract": (ctypes.c_int, [ctypes.POINTER(TrimulArgs), ctypes.c_void_p]),
+    "gnn_trimul_out": (ctypes.c_int, [ctypes.POINTER(TrimulArgs), ctypes.c_void_p]),
+    "gnn_last_error": (ctypes.c_char_p, []),
+    "gnn_version": (ctypes.c_char_p, []),
+}
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+_lock = threading.Lock()
+_lib = None
+
+
+def library_path() -> pathlib.Path:
+    override = os.environ.get("GNN_HIP_LIB")
+    return pathlib.Path(override) if override else LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library; raises RuntimeError if it is missing or unloadable."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            path = library_path()
+            if not path.exists():
+                raise RuntimeError(
+                    f"libgnn_hip.so not found at {path}; build it with "
+                    "`python geometric-nn-ops_amd/build.py` (no fallback is taken for GPU tensors)"
+                )
+            try:
+                lib = ctypes.CDLL(str(path))
+            except OSError as exc:
+                raise RuntimeError(f"failed to load {path}: {exc}") from exc
+            for name, (res, argtypes) in _SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = argtypes
+            _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raise for a non-zero status from the library, with its message."""
+    if rc == GNN_OK:
+        return
+    msg = load().gnn_last_error().decode(errors="replace")
+    if rc == GNN_ERR_ARG:
+        raise ValueError(f"{what}: {msg}")
+    if rc == GNN_ERR_UNSUPPORTED:
+        raise NotImplementedError(f"{what}: {msg}")
+    raise RuntimeError(f"{what} failed with status {rc}: {msg}")
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()

@@ -1,0 +1,108 @@
+"""Host side of the HIP triangle-attention forward.
+
+``triangle_attention_hip`` takes the canonical 5D layout with a boolean mask and stands
+in for the reference's ``triangle_attention_triton`` + ``EvoformerAttention.forward``
+(geometric_nn_ops_torch/triangle/_kernels/triangle_attention.py:1447-1484, :1091-1276):
+same argument meaning, same shape assertions, ``scale=None`` meaning ``D**-0.5``, and the
+masked-key bias rounded to the input dtype. It is forward-only. q/k/v/bias views are
+passed to the kernel through their strides (no copies unless a stride or alignment is
+unusable), and the output is a fresh contiguous ``[B, N_seq, N_res, H, D]`` tensor.
+"""
+
+import ctypes
+
+import torch
+
+from ... import _lib, _precision
+from .._masking import rounded_mask_value
+
+MAX_HEAD_DIM = 128  # the kernel's largest head-dim tile
+MAX_N_RES = 32768
+
+
+def supports(q: torch.Tensor) -> bool:
+    """Whether the HIP kernel covers this input (dtype handled by the caller)."""
+    return q.shape[-1] <= MAX_HEAD_DIM and q.shape[-3] <= MAX_N_RES
+
+
+def _vectorizable(t: torch.Tensor, dims) -> bool:
+    elem = t.element_size()
+    return t.data_ptr() % 16 == 0 and t.stride(-1) == 1 and all(t.stride(d) % 8 == 0 for d in dims)
+
+
+def _prepare(t: torch.Tensor) -> torch.Tensor:
+    """q/k/v in a form the kernel can address: unit stride on D, other strides multiples
+    of 8 elements and a 16-byte aligned base; D padded to a multiple of 8."""
+    d = t.shape[-1]
+    if d % 8:
+        t = torch.nn.functional.pad(t, (0, 8 - d % 8))
+    if not _vectorizable(t, range(t.dim() - 1)):
+        t = t.contiguous()
+        if not _vectorizable(t, range(t.dim() - 1)):
+            t = t.clone()
+    return t
+
+
+def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=False, use_exp2=False,
+                           lse=None):
+    """Triangle attention forward on the canonical 5D layout.
+
+    q/k/v ``[B, N_seq, N_res, H, D]`` (bf16, fp16 or fp32, on a HIP device); bias
+    ``[B, 1, H, N_res, N_res]`` or ``None``; mask ``[B, N_seq, 1, 1, N_res]`` bool or
+    ``None``. ``dynamic`` is accepted for API parity and has no effect (N is always a
+    runtime argument); ``use_exp2`` likewise (the kernel always evaluates the softmax in
+    base 2). ``lse``, if given, is a float32 ``[B, N_seq, H, N_res]`` tensor that receives
+    the natural-log log-sum-exp of each query's logits.
+    """
+    del dynamic, use_exp2
+    lib = _lib.load()
+    if q.dtype not in _lib.DTYPE_CODE:
+        raise TypeError(f"triangle_attention_hip: unsupported dtype {q.dtype}")
+    dim_q, dim_k, dim_v = q.shape[-1], k.shape[-1], v.shape[-1]
+    assert dim_q == dim_k and dim_k == dim_v
+    B, S, N, H, D = q.shape
+    assert k.shape == q.shape and v.shape == q.shape, f"{tuple(k.shape)} / {tuple(v.shape)} != {tuple(q.shape)}"
+    if mask is not None:
+        assert mask.shape == (B, S, 1, 1, N), f"{tuple(mask.shape)} != {(B, S, 1, 1, N)}"
+    if bias is not None:
+        assert bias.shape == (B, 1, H, N, N), f"{tuple(bias.shape)} != {(B, 1, H, N, N)}"
+    if scale is None:
+        scale = D**-0.5
+
+    qk, kk, vk = _prepare(q), _prepare(k), _prepare(v)
+    Dp = qk.shape[-1]
+    o = torch.empty((B, S, N, H, Dp), device=q.device, dtype=q.dtype)
+
+    args = _lib.TriAttnArgs()
+    args.q, args.k, args.v, args.o = qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), o.data_ptr()
+    args.B, args.S, args.N, args.H, args.D = B, S, N, H, Dp
+    args.q_stride = _lib.I64x4(*qk.stride()[:4])
+    args.k_stride = _lib.I64x4(*kk.stride()[:4])
+    args.v_stride = _lib.I64x4(*vk.stride()[:4])
+    args.o_stride = _lib.I64x4(*o.stride()[:4])
+    if bias is not None:
+        bias = bias.to(q.dtype)
+        if not (bias.stride(-1) == 1 and bias.stride(-2) % 8 == 0 and bias.data_ptr() % 16 == 0):
+            bias = bias.contiguous()
+        args.bias = bias.data_ptr()
+        args.bias_stride = _lib.I64x4(bias.stride(0), bias.stride(2), bias.stride(3), bias.stride(4))
+    if mask is not None:
+        if mask.dtype != torch.bool:
+            raise ValueError(f"mask must be bool (keep=True/mask=False), got {mask.dtype}")
+        args.mask = mask.data_ptr()
+        args.mask_stride = _lib.I64x3(mask.stride(0), mask.stride(1), mask.stride(4))
+    if lse is not None:
+        assert lse.shape == (B, S, H, N) and lse.dtype == torch.float32 and lse.is_contiguous()
+        args.lse = lse.data_ptr()
+    args.scale = float(scale)
+    args.mask_value = rounded_mask_value(q.dtype)
+    args.dtype = _lib.DTYPE_CODE[q.dtype]
+    precision = _precision.matmul_precision(fp32_operands=q.dtype == torch.float32)
+    args.precision = _lib.PRECISION_CODE[precision]
+
+    with torch.cuda.device(q.device):
+        rc = lib.gnn_triattn_fwd(ctypes.byref(args), ctypes.c_void_p(_lib.stream_handle(q.device)))
+    _lib.check(rc, "gnn_triattn_fwd")
+    if Dp != D:
+        o = o[..., :D].contiguous()
+    return o

@@ -1,0 +1,86 @@
+"""Public ``triangle_multiplicative_update`` (reference geometric_nn_ops_torch/triangle/_trimul.py).
+
+Two backends with the same math:
+  * the gfx950 HIP kernels (forward only) in ``_kernels.trimul``;
+  * the pure-torch, autograd-differentiable path in ``_reference.trimul``.
+
+Dispatch follows the reference's rule (_trimul.py:31-36): the torch path runs when a
+backward could run (grad enabled and x or a weight requires grad), the tensor is not on
+a HIP device, or its dtype has no kernel; it also runs for channel counts the kernels do
+not tile (c_z or c_hidden not a multiple of 32, or above 512). Otherwise the HIP kernels
+run. A missing HIP library is an error on GPU tensors, never a silent fallback.
+
+``p_in_weight`` / ``g_in_weight`` are the concatenated ``[a; b]`` projections
+(``[2 * C_hidden, C_z]``).
+"""
+
+import torch
+
+from ._kernels import trimul as _hip
+from ._kernels.trimul import trimul_hip
+from ._reference.trimul import trimul_torch
+
+__all__ = ["triangle_multiplicative_update"]
+
+_KERNEL_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _needs_torch_path(x: torch.Tensor, weights) -> bool:
+    weights = dict(weights)
+    if not x.is_cuda or x.dtype not in _KERNEL_DTYPES:
+        return True
+    if weights.get("p_in_weight") is not None and not _hip.supports(x, weights["p_in_weight"]):
+        return True
+    return torch.is_grad_enabled() and (
+        x.requires_grad or any(w is not None and w.requires_grad for w in weights.values())
+    )
+
+
+def triangle_multiplicative_update(
+    x: torch.Tensor,
+    direction: str = "outgoing",
+    mask: torch.Tensor | None = None,
+    norm_in_weight: torch.Tensor | None = None,
+    norm_in_bias: torch.Tensor | None = None,
+    p_in_weight: torch.Tensor | None = None,
+    p_in_bias: torch.Tensor | None = None,
+    g_in_weight: torch.Tensor | None = None,
+    g_in_bias: torch.Tensor | None = None,
+    norm_out_weight: torch.Tensor | None = None,
+    norm_out_bias: torch.Tensor | None = None,
+    p_out_weight: torch.Tensor | None = None,
+    p_out_bias: torch.Tensor | None = None,
+    g_out_weight: torch.Tensor | None = None,
+    g_out_bias: torch.Tensor | None = None,
+    eps: float = 1e-5,
+) -> torch.Tensor:
+    """Triangle multiplicative update over a pair representation.
+
+    Args:
+        x: ``[*, N, N, C_z]`` pair representation.
+        direction: ``"outgoing"`` or ``"incoming"``.
+        mask: optional ``[*, N, N]`` pair mask (1 = keep), broadcastable over the leading dims.
+        *_weight / *_bias: LayerNorm / projection / gate parameters.
+        eps: LayerNorm epsilon.
+
+    Returns:
+        ``[*, N, N, C_z]`` updated pair representation.
+
+    fp32 products follow ``torch.backends.cuda.matmul.fp32_precision``.
+    """
+    weights = dict(
+        norm_in_weight=norm_in_weight,
+        norm_in_bias=norm_in_bias,
+        p_in_weight=p_in_weight,
+        p_in_bias=p_in_bias,
+        g_in_weight=g_in_weight,
+        g_in_bias=g_in_bias,
+        norm_out_weight=norm_out_weight,
+        norm_out_bias=norm_out_bias,
+        p_out_weight=p_out_weight,
+        p_out_bias=p_out_bias,
+        g_out_weight=g_out_weight,
+        g_out_bias=g_out_bias,
+    )
+    impl = trimul_torch if _needs_torch_path(x, weights.items()) else trimul_hip
+    return impl(x, direction, mask, eps=eps, **weights)

@@ -1,0 +1,185 @@
+"""CPU oracle for the triangle hot path -- TEST INFRASTRUCTURE ONLY.
+
+A numpy restatement of the reference's pure-torch math, used by tests/, by
+__graft_entry__.smoke() and by bench.py's cpu_baseline leg, and only as the checker (or
+the timed CPU baseline). The product (geometric-nn-ops_amd/) never imports it.
+
+Reference files followed (paths relative to AMDResearch/geometric-nn-ops):
+  * mask_val / masked_key_bias          geometric_nn_ops_torch/triangle/_masking.py:13-42
+  * triangle_attention                  geometric_nn_ops_torch/triangle/_reference/triangle_attention.py:11-44
+  * trimul (LayerNorm, gated projection, mask, combine, output LN, projection, gate)
+                                        geometric_nn_ops_torch/triangle/_reference/trimul.py:27-97
+  * layer_norm semantics                torch.nn.functional.layer_norm (biased variance,
+                                        1/sqrt(var + eps)), called at _reference/trimul.py:85,94
+
+Everything is computed in ``dtype`` (float64 by default). How each function is pinned
+(tests/test_oracle.py): triangle_attention against a pure-Python loop softmax-attention
+at tiny sizes and the reference's known-answer cases (one live key gives v, zero q gives
+mean(v), masked keys are bit-invariant to noise, fully masked rows give mean(v));
+combine against pure-Python triple loops for both directions; layer_norm against its
+closed-form moments and the zero-vector -> beta case; trimul end to end against the
+N = 1 closed form and the fully-masked constant field; mask_val against the reference's
+stated sentinel values.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+DIRECTIONS = ("outgoing", "incoming")
+
+
+# ---------------------------------------------------------------- masking (_masking.py:13-42)
+def mask_val(dtype_name: str) -> float:
+    """Sentinel magnitude per dtype name: fp64 1e18, fp32/bf16 1e9, fp16 finfo.max/2."""
+    if dtype_name == "float64":
+        return 1e18
+    if dtype_name in ("float32", "bfloat16"):
+        return 1e9
+    if dtype_name == "float16":
+        return float(np.finfo(np.float16).max) / 2
+    raise ValueError(f"Unsupported dtype {dtype_name}")
+
+
+def masked_key_bias(mask: np.ndarray, dtype=np.float64, dtype_name: str = "float64") -> np.ndarray:
+    """``mask_val * (mask - 1)``: +0.0 on kept keys, -mask_val on masked ones."""
+    return mask_val(dtype_name) * (mask.astype(dtype) - 1)
+
+
+# ------------------------------------------- triangle attention (_reference/triangle_attention.py)
+def _softmax(x: np.ndarray, axis: int = -1) -> np.ndarray:
+    m = np.max(x, axis=axis, keepdims=True)
+    e = np.exp(x - m)
+    return e / np.sum(e, axis=axis, keepdims=True)
+
+
+def triangle_attention(q, k, v, bias=None, mask=None, scale=None, *, dtype=np.float64,
+                       s_chunk: int | None = None) -> np.ndarray:
+    """Triangle attention on the canonical 5D layout ``[B, N_seq, N_res, H, D]``.
+
+    ``bias`` broadcastable to ``[B, 1, H, N, N]`` (4D ``[B, H, N, N]`` gains the N_seq
+    axis); ``mask`` boolean broadcastable to ``[B, N_seq, 1, 1, N]``. Logits are
+    ``(q * scale) . k + bias + masked_key_bias(mask)`` (triangle_attention.py:34-40), the
+    softmax runs over keys (:42) and the output is ``P @ v`` (:43). ``s_chunk`` processes
+    the N_seq axis in chunks to bound memory (the math is row-independent).
+    """
+    q = np.asarray(q, dtype=dtype)
+    k = np.asarray(k, dtype=dtype)
+    v = np.asarray(v, dtype=dtype)
+    B, S, N, H, D = q.shape
+    if scale is None:
+        scale = D ** -0.5
+    if bias is not None:
+        bias = np.asarray(bias, dtype=dtype)
+        if bias.ndim == 4:
+            bias = bias[:, None]
+        bias = np.broadcast_to(bias, (B, 1, H, N, N))
+    if mask is not None:
+        mask = np.broadcast_to(np.asarray(mask, dtype=bool), (B, S, 1, 1, N))
+        name = "float64" if dtype == np.float64 else "float32"
+        mbias = masked_key_bias(mask, dtype, name)  # [B, S, 1, 1, N]
+    out = np.empty((B, S, N, H, D), dtype=dtype)
+    step = s_chunk or S
+    for s0 in range(0, S, step):
+        s1 = min(S, s0 + step)
+        qs = np.transpose(q[:, s0:s1], (0, 1, 3, 2, 4)) * dtype(scale)  # [B, s, H, N, D]
+        ks = np.transpose(k[:, s0:s1], (0, 1, 3, 2, 4))
+        vs = np.transpose(v[:, s0:s1], (0, 1, 3, 2, 4))
+        logits = qs @ np.swapaxes(ks, -1, -2)  # [B, s, H, N, N]
+        if bias is not None:
+            logits = logits + bias
+        if mask is not None:
+            logits = logits + mbias[:, s0:s1]
+        probs = _softmax(logits, -1)
+        out[:, s0:s1] = np.transpose(probs @ vs, (0, 1, 3, 2, 4))
+    return out
+
+
+# ------------------------------------------------------------- trimul (_reference/trimul.py)
+def is_outgoing(direction: str) -> bool:
+    if direction not in DIRECTIONS:
+        raise ValueError(f"direction must be one of {DIRECTIONS}, got {direction!r}")
+    return direction == "outgoing"
+
+
+def layer_norm(x, weight=None, bias=None, eps=1e-5, *, dtype=np.float64) -> np.ndarray:
+    """LayerNorm over the last axis with torch's semantics: biased variance and
+    ``(x - mean) / sqrt(var + eps) * weight + bias``."""
+    x = np.asarray(x, dtype=dtype)
+    mean = x.mean(axis=-1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=-1, keepdims=True)
+    y = (x - mean) / np.sqrt(var + dtype(eps))
+    if weight is not None:
+        y = y * np.asarray(weight, dtype=dtype)
+    if bias is not None:
+        y = y + np.asarray(bias, dtype=dtype)
+    return y
+
+
+def linear(x, weight, bias=None, *, dtype=np.float64) -> np.ndarray:
+    """``x @ weight.T + bias`` with ``weight`` in nn.Linear layout ``[out, in]``."""
+    y = np.asarray(x, dtype=dtype) @ np.asarray(weight, dtype=dtype).T
+    if bias is not None:
+        y = y + np.asarray(bias, dtype=dtype)
+    return y
+
+
+def sigmoid(x):
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+def combine(a, b, outgoing: bool) -> np.ndarray:
+    """outgoing ``o[..., i, j, c] = sum_k a[..., i, k, c] b[..., j, k, c]``;
+    incoming ``o[..., i, j, c] = sum_k a[..., k, i, c] b[..., k, j, c]``
+    (_reference/trimul.py:44-54), evaluated as one matmul per channel."""
+    am = np.moveaxis(a, -1, -3)  # [..., C, N, N]
+    bm = np.moveaxis(b, -1, -3)
+    if outgoing:
+        o = am @ np.swapaxes(bm, -1, -2)
+    else:
+        o = np.swapaxes(am, -1, -2) @ bm
+    return np.moveaxis(o, -3, -1)
+
+
+def trimul_stages(x, direction="outgoing", mask=None, *, eps=1e-5, dtype=np.float64, **w):
+    """Every intermediate of the triangle multiplicative update, as a dict:
+    z (LN-in), a, b (masked gated projections), g (output gate), o (contraction),
+    on (LN-out), out (the op's result). Weight keywords as the public op."""
+    outgoing = is_outgoing(direction)
+    x = np.asarray(x, dtype=dtype)
+    c_hidden = np.asarray(w["p_in_weight"]).shape[0] // 2
+    z = layer_norm(x, w.get("norm_in_weight"), w.get("norm_in_bias"), eps, dtype=dtype)
+    p = linear(z, w["p_in_weight"], w.get("p_in_bias"), dtype=dtype) * sigmoid(
+        linear(z, w["g_in_weight"], w.get("g_in_bias"), dtype=dtype))
+    if mask is not None:
+        p = p * np.asarray(mask, dtype=dtype)[..., None]
+    a, b = p[..., :c_hidden], p[..., c_hidden:]
+    o = combine(a, b, outgoing)
+    on = layer_norm(o, w.get("norm_out_weight"), w.get("norm_out_bias"), eps, dtype=dtype)
+    g = sigmoid(linear(z, w["g_out_weight"], w.get("g_out_bias"), dtype=dtype))
+    out = linear(on, w["p_out_weight"], w.get("p_out_bias"), dtype=dtype) * g
+    return dict(z=z, a=a, b=b, g=g, o=o, on=on, out=out)
+
+
+def trimul(x, direction="outgoing", mask=None, *, eps=1e-5, dtype=np.float64, **w) -> np.ndarray:
+    """Triangle multiplicative update (_reference/trimul.py:57-97)."""
+    return trimul_stages(x, direction, mask, eps=eps, dtype=dtype, **w)["out"]
+
+
+# ------------------------------------------------------------------------- metrics
+def rel_fro(a, b) -> float:
+    """``||a - b|| / ||b||`` in fp64; ``b`` is the reference (testutil/metrics.py:40-47)."""
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.linalg.norm((a - b).ravel()) / max(np.linalg.norm(b.ravel()), 1e-30))
+
+
+def cos(a, b) -> float:
+    """Cosine similarity of the flattened arrays; two zero arrays count as 1
+    (testutil/metrics.py:26-37)."""
+    a = np.asarray(a, dtype=np.float64).ravel()
+    b = np.asarray(b, dtype=np.float64).ravel()
+    na, nb = np.linalg.norm(a), np.linalg.norm(b)
+    if na == 0 and nb == 0:
+        return 1.0
+    return float(a @ b / max(na * nb, 1e-300))

@@ -1,0 +1,342 @@
+"""HIP triangle-attention forward vs the CPU oracle, and the reference's structural tests.
+
+Structural cases restate AMDResearch/geometric-nn-ops tests/test_triangle_attention.py:88-443;
+accuracy cases use its SHAPES (:46-51) and tolerance table (testutil/metrics.py:103-108)
+against the fp64 oracle, plus this build's rel-Frobenius <= 1e-2 bar for 16-bit inputs.
+BASELINE configs C2 (N=256), the headline N=512 and C4 (N=768, ragged masks) are checked
+on rows sampled from the full-size run (the math is independent per (b, s) row).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (NORTH_STAR_REL_FRO, TRIANGLE_ATTENTION_TOL, Tolerance, assert_close_to_oracle,
+                     attention_inputs, gen, key_mask, randn, to_np)
+from oracle import triangle_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+SHAPES = [
+    pytest.param((1, 1, 32, 4, 32), id="pairformer_32"),
+    pytest.param((1, 4, 32, 8, 8), id="msa_d8"),
+    pytest.param((1, 1, 64, 16, 48), id="atom_d48"),
+    pytest.param((2, 2, 48, 4, 32), id="batched"),
+    pytest.param((1, 3, 100, 2, 64), id="ragged_d64"),
+    pytest.param((1, 2, 70, 2, 128), id="d128"),
+]
+DTYPE_PRECISION = pytest.mark.parametrize(
+    ("dtype", "precision"),
+    [(torch.float32, "ieee"), (torch.float32, "tf32"), (torch.bfloat16, "ieee"), (torch.float16, "ieee")],
+    ids=["fp32_ieee", "fp32_tf32", "bf16", "fp16"],
+)
+DTYPES = pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16],
+                                 ids=["fp32", "bf16", "fp16"])
+
+
+class matmul_precision:
+    """Sets torch.backends.cuda.matmul.fp32_precision for a block (not thread safe)."""
+
+    def __init__(self, precision):
+        self.precision = precision
+
+    def __enter__(self):
+        self.prev = torch.backends.cuda.matmul.fp32_precision
+        torch.backends.cuda.matmul.fp32_precision = self.precision
+
+    def __exit__(self, *exc):
+        torch.backends.cuda.matmul.fp32_precision = self.prev
+
+
+def hip_attn(**kw):
+    from geometric_nn_ops_torch.triangle._kernels.triangle_attention import triangle_attention_hip
+
+    with torch.no_grad():
+        return triangle_attention_hip(**kw)
+
+
+def public(*args, **kw):
+    from geometric_nn_ops_torch.triangle import triangle_attention
+
+    with torch.no_grad():
+        return triangle_attention(*args, **kw)
+
+
+def dev(tensors):
+    return {k: v.to(DEV) for k, v in tensors.items()}
+
+
+def oracle_of(t, mask=None, scale=None):
+    return O.triangle_attention(to_np(t["q"]), to_np(t["k"]), to_np(t["v"]),
+                                None if t.get("bias") is None else to_np(t["bias"]),
+                                None if mask is None else mask.cpu().numpy(), scale)
+
+
+# ------------------------------------------------------------------------------ accuracy
+@pytest.mark.parametrize("shape", SHAPES)
+@DTYPE_PRECISION
+def test_accuracy(shape, dtype, precision):
+    B, S, N, H, D = shape
+    t = attention_inputs(B, S, N, H, D, dtype, seed=3)
+    mask = key_mask(B, S, N, seed=1)
+    want = oracle_of(t, mask, D**-0.5)
+    with matmul_precision(precision):
+        got = hip_attn(**dev(t), mask=mask.to(DEV), scale=D**-0.5)
+    tol = TRIANGLE_ATTENTION_TOL[dtype, precision]
+    assert_close_to_oracle("out", got, want, tol,
+                           rel_fro_max=NORTH_STAR_REL_FRO if dtype != torch.float32 else None)
+
+
+@DTYPES
+def test_public_op_accuracy_and_exp2(dtype):
+    B, S, N, H, D = 1, 2, 40, 4, 32
+    t = attention_inputs(B, S, N, H, D, dtype, seed=3)
+    mask = key_mask(B, S, N, seed=2)
+    want = oracle_of(t, mask)
+    for use_exp2 in (False, True):
+        got = public(**dev(t), mask=mask.to(DEV), use_exp2=use_exp2)
+        assert_close_to_oracle("out", got, want, TRIANGLE_ATTENTION_TOL[dtype, "ieee"])
+
+
+def test_pairformer_shape():
+    """N=384, H=16, D=48 (reference test_triangle_attention.py:591-607)."""
+    B, S, N, H, D = 1, 1, 384, 16, 48
+    t = attention_inputs(B, S, N, H, D, torch.bfloat16, seed=21)
+    got = public(**dev(t), scale=None)
+    assert_close_to_oracle("out", got, oracle_of(t), Tolerance(1 - 1e-4, 5e-2), rel_fro_max=NORTH_STAR_REL_FRO)
+
+
+def test_lse_output():
+    B, S, N, H, D = 1, 2, 96, 2, 32
+    t = attention_inputs(B, S, N, H, D, torch.float32, seed=4)
+    mask = key_mask(B, S, N, seed=6)
+    lse = torch.empty(B, S, H, N, device=DEV)
+    hip_attn(**dev(t), mask=mask.to(DEV), lse=lse)
+    q, k = to_np(t["q"]), to_np(t["k"])
+    logits = np.einsum("bsihd,bsjhd->bshij", q * D**-0.5, k) + to_np(t["bias"]) + O.masked_key_bias(
+        mask.numpy(), np.float64, "float32")
+    mx = logits.max(-1)
+    want = mx + np.log(np.exp(logits - mx[..., None]).sum(-1))
+    np.testing.assert_allclose(lse.cpu().numpy(), want, rtol=1e-4, atol=1e-4)
+
+
+# ---------------------------------------------------------------------- structural (exact)
+@DTYPES
+@pytest.mark.parametrize("kept", [0, 7, 31], ids=["first", "interior", "last"])
+def test_one_unmasked_key_returns_that_key(dtype, kept):
+    B, S, N, H, D = 1, 2, 32, 4, 32
+    t = dev(attention_inputs(B, S, N, H, D, dtype, seed=3))
+    mask = torch.zeros(B, S, 1, 1, N, dtype=torch.bool, device=DEV)
+    mask[..., kept] = True
+    out = hip_attn(**t, mask=mask, scale=D**-0.5)
+    torch.testing.assert_close(out, t["v"][:, :, kept:kept + 1].expand_as(out), rtol=0, atol=0)
+
+
+def _uniform_inputs(B, S, N, H, D, dtype, seed):
+    v = torch.randint(-4, 5, (B, S, N, H, D), generator=gen(seed)).to(dtype)
+    z = torch.zeros(B, S, N, H, D, dtype=dtype)
+    return dict(q=z, k=z.clone(), v=v, bias=torch.zeros(B, 1, H, N, N, dtype=dtype))
+
+
+@DTYPES
+def test_uniform_logits(dtype):
+    B, S, N, H, D = 1, 1, 32, 4, 16
+    t = dev(_uniform_inputs(B, S, N, H, D, dtype, 5))
+    out = hip_attn(**t, mask=None, scale=D**-0.5)
+    expected = t["v"].double().mean(dim=2, keepdim=True).expand_as(out)
+    ulp = torch.finfo(torch.float32).eps * expected.abs().max().item()
+    torch.testing.assert_close(out.double(), expected, rtol=0, atol=ulp)
+
+
+def test_mask_none_equals_all_keep():
+    B, S, N, H, D = 1, 2, 32, 4, 32
+    t = dev(attention_inputs(B, S, N, H, D, torch.bfloat16, seed=13))
+    keep = torch.ones(B, S, 1, 1, N, dtype=torch.bool, device=DEV)
+    torch.testing.assert_close(hip_attn(**t, mask=None), hip_attn(**t, mask=keep), rtol=0, atol=0)
+
+
+@DTYPES
+def test_masked_values_are_ignored(dtype):
+    B, S, N, H, D = 1, 1, 32, 4, 32
+    t = attention_inputs(B, S, N, H, D, dtype, seed=3)
+    mask = key_mask(B, S, N, seed=5)
+    dead = ~mask.reshape(B, S, N, 1, 1)
+    noise = 1e3 * randn(t["v"].shape, dtype, seed=9)
+    pert = {**t, "v": torch.where(dead, t["v"] + noise, t["v"])}
+    t, pert, mask = dev(t), dev(pert), mask.to(DEV)
+    torch.testing.assert_close(hip_attn(**t, mask=mask), hip_attn(**pert, mask=mask), rtol=0, atol=0)
+    assert not torch.allclose(hip_attn(**t), hip_attn(**pert))
+
+
+@DTYPES
+def test_masked_logits_are_suppressed(dtype):
+    B, S, N, H, D = 1, 1, 32, 4, 32
+    t = attention_inputs(B, S, N, H, D, dtype, seed=3)
+    mask = key_mask(B, S, N, seed=5)
+    dead_k = ~mask.reshape(B, S, N, 1, 1)
+    pert = {
+        **t,
+        "k": torch.where(dead_k, t["k"] + 1e3 * randn(t["k"].shape, dtype, seed=7), t["k"]),
+        "bias": torch.where(~mask, t["bias"] + 1e3 * randn(t["bias"].shape, dtype, seed=11), t["bias"]),
+    }
+    t, pert, mask = dev(t), dev(pert), mask.to(DEV)
+    torch.testing.assert_close(hip_attn(**t, mask=mask), hip_attn(**pert, mask=mask), rtol=0, atol=0)
+    assert not torch.allclose(hip_attn(**t), hip_attn(**pert))
+
+
+def test_no_bias_equals_zero_bias():
+    B, S, N, H, D = 1, 2, 32, 4, 32
+    t = dev(attention_inputs(B, S, N, H, D, torch.bfloat16, seed=15))
+    without = {k: v for k, v in t.items() if k != "bias"}
+    zeroed = {**t, "bias": torch.zeros_like(t["bias"])}
+    torch.testing.assert_close(hip_attn(**without), hip_attn(**zeroed), rtol=0, atol=0)
+
+
+@DTYPES
+def test_fully_masked_row_small_logits(request, dtype):
+    """A fully masked row returns mean(v): the sentinel collapses every fp32 logit to one
+    value. fp16's sentinel (32752) is too small to collapse them, as in the reference."""
+    if dtype is torch.float16:
+        request.node.add_marker(pytest.mark.xfail(strict=True, reason="fp16 sentinel does not collapse logits"))
+    B, S, N, H, D = 1, 1, 32, 4, 16
+    values = torch.randint(-4, 5, (B, S, N, H, D), generator=gen(5))
+    t = dict(q=randn((B, S, N, H, D), dtype, seed=7), k=randn((B, S, N, H, D), dtype, seed=8),
+             v=values.to(dtype), bias=torch.zeros(B, 1, H, N, N, dtype=dtype))
+    mask = torch.zeros(B, S, 1, 1, N, dtype=torch.bool, device=DEV)
+    out = hip_attn(**dev(t), mask=mask, scale=D**-0.5)
+    expected = values.double().mean(dim=2, keepdim=True).expand_as(out).to(DEV)
+    ulp = torch.finfo(torch.float32).eps * expected.abs().max().item()
+    torch.testing.assert_close(out.double(), expected, rtol=0, atol=ulp)
+
+
+def test_fully_masked_row_against_oracle():
+    """Dead rows mixed with live rows in one batch, bf16, against the fp64 oracle."""
+    B, S, N, H, D = 1, 4, 64, 4, 32
+    t = attention_inputs(B, S, N, H, D, torch.bfloat16, seed=3)
+    mask = key_mask(B, S, N, seed=8)
+    mask[0, 1] = False
+    mask[0, 3, ..., 40:] = False
+    got = hip_attn(**dev(t), mask=mask.to(DEV))
+    assert_close_to_oracle("out", got, oracle_of(t, mask), TRIANGLE_ATTENTION_TOL[torch.bfloat16, "ieee"],
+                           rel_fro_max=NORTH_STAR_REL_FRO)
+
+
+def test_default_scale():
+    B, S, N, H, D = 1, 1, 32, 4, 32
+    t = dev(attention_inputs(B, S, N, H, D, torch.float32, seed=13))
+    default = hip_attn(**t, scale=None)
+    torch.testing.assert_close(default, hip_attn(**t, scale=D**-0.5), rtol=0, atol=0)
+    assert not torch.equal(default, hip_attn(**t, scale=D**-0.5 * 1.75))
+
+
+def test_non_boolean_mask_is_rejected():
+    t = dev(attention_inputs(1, 1, 32, 4, 32, torch.bfloat16, seed=11))
+    for dt in (torch.float32, torch.bfloat16, torch.uint8):
+        with pytest.raises(ValueError, match="mask must be bool"):
+            public(**t, mask=key_mask(1, 1, 32, seed=4).to(DEV).to(dt))
+
+
+def test_4d_input_and_4d_bias():
+    N_seq, N, H, D = 2, 32, 4, 32
+    t = dev(attention_inputs(1, N_seq, N, H, D, torch.bfloat16, seed=7))
+    mask = key_mask(1, N_seq, N, seed=9).to(DEV)
+    out_5d = public(**t, mask=mask)
+    un = {k: v[0] for k, v in t.items()}
+    out_4d = public(**un, mask=mask)
+    assert out_4d.shape == un["q"].shape
+    torch.testing.assert_close(out_4d, out_5d[0], rtol=0, atol=0)
+    torch.testing.assert_close(public(**{**t, "bias": t["bias"][:, 0]}, mask=mask), out_5d, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("rank", [5, 4, 3])
+def test_lower_rank_mask(rank):
+    B, S, N, H, D = 1, 2, 32, 4, 32
+    t = dev(attention_inputs(B, S, N, H, D, torch.bfloat16, seed=5))
+    canonical = key_mask(B, S, N, seed=9).to(DEV)
+    lower = canonical[(0,) * (5 - rank)]
+    explicit = lower.expand_as(canonical).contiguous()
+    torch.testing.assert_close(public(**t, mask=lower), public(**t, mask=explicit), rtol=0, atol=0)
+
+
+def test_6d_input():
+    nested = attention_inputs(6, 1, 32, 4, 32, torch.bfloat16, seed=11)
+    flat = dev(nested)
+    nested = {k: v.reshape(2, 3, *v.shape[1:]).to(DEV) for k, v in nested.items()}
+    out_6d = public(**nested)
+    assert out_6d.shape == nested["q"].shape
+    torch.testing.assert_close(out_6d.reshape(6, *out_6d.shape[2:]), public(**flat), rtol=0, atol=0)
+
+
+def test_dynamic_is_bit_identical():
+    t = dev(attention_inputs(1, 1, 32, 4, 32, torch.bfloat16, seed=19))
+    mask = key_mask(1, 1, 32, seed=21).to(DEV)
+    torch.testing.assert_close(public(**t, mask=mask, dynamic=False), public(**t, mask=mask, dynamic=True),
+                               rtol=0, atol=0)
+
+
+def test_tf32_changes_the_result():
+    t = dev(attention_inputs(1, 1, 32, 4, 32, torch.float32, seed=3))
+    mask = key_mask(1, 1, 32, seed=5).to(DEV)
+    with matmul_precision("ieee"):
+        full = hip_attn(**t, mask=mask)
+    with matmul_precision("tf32"):
+        reduced = hip_attn(**t, mask=mask)
+    assert not torch.equal(full, reduced)
+
+
+def test_strided_views_need_no_copy_and_match():
+    """Ending-node attention: q/k/v as transpose(1, 2) views and a transposed bias give
+    exactly the result of the same values laid out contiguously."""
+    B, S, N, H, D = 1, 48, 48, 4, 32
+    t = dev(attention_inputs(B, S, N, H, D, torch.bfloat16, seed=23))
+    views = {k: t[k].transpose(1, 2) for k in "qkv"}
+    bias_t = t["bias"].transpose(-1, -2)
+    got = hip_attn(**views, bias=bias_t)
+    want = hip_attn(**{k: v.contiguous() for k, v in views.items()}, bias=bias_t.contiguous())
+    torch.testing.assert_close(got, want, rtol=0, atol=0)
+
+
+# --------------------------------------------------------------- BASELINE configs (full size)
+def _rows_vs_oracle(t, mask, rows, scale, tol, rel_fro_max=None):
+    out = hip_attn(**dev(t), mask=None if mask is None else mask.to(DEV), scale=scale)
+    sel = lambda x: x[:, rows]  # noqa: E731
+    want = O.triangle_attention(to_np(sel(t["q"])), to_np(sel(t["k"])), to_np(sel(t["v"])),
+                                None if t.get("bias") is None else to_np(t["bias"]),
+                                None if mask is None else mask[:, rows].numpy(), scale)
+    assert_close_to_oracle("out", out[:, rows], want, tol, rel_fro_max=rel_fro_max)
+    return out
+
+
+def test_config_c2_n256():
+    """bf16 B=1 N=256 H=4 D=32 in the cueq layout [B,S,H,N,D] (passed as a transposed
+    view), bias N(0,1), keys 230..255 masked, scale 1/sqrt(32); every row checked."""
+    B, N, H, D = 1, 256, 4, 32
+    g = gen(0)
+    cueq = {k: randn((B, N, H, N, D), torch.bfloat16, g=g) for k in "qkv"}
+    t = {k: v.transpose(-2, -3) for k, v in cueq.items()}
+    t["bias"] = randn((B, 1, H, N, N), torch.bfloat16, g=g)
+    mask = torch.ones(B, N, 1, 1, N, dtype=torch.bool)
+    mask[..., N - 26:] = False
+    _rows_vs_oracle(t, mask, slice(0, N), D**-0.5, TRIANGLE_ATTENTION_TOL[torch.bfloat16, "ieee"],
+                    rel_fro_max=NORTH_STAR_REL_FRO)
+
+
+def test_headline_n512_rows():
+    B, N, H, D = 1, 512, 4, 32
+    t = attention_inputs(B, N, N, H, D, torch.bfloat16, seed=0, bias_scale=1.0)
+    rows = [0, 1, 127, 255, 300, 511]
+    _rows_vs_oracle(t, None, rows, D**-0.5, TRIANGLE_ATTENTION_TOL[torch.bfloat16, "ieee"],
+                    rel_fro_max=NORTH_STAR_REL_FRO)
+
+
+def test_config_c4_n768_ragged():
+    """bf16 N=768, bias 2*N(0,1), each row keeps a random prefix of length in [384, 768]."""
+    B, N, H, D = 1, 768, 4, 32
+    t = attention_inputs(B, N, N, H, D, torch.bfloat16, seed=0, bias_scale=2.0)
+    lengths = torch.randint(384, 769, (N,), generator=gen(99))
+    mask = (torch.arange(N)[None, :] < lengths[:, None]).reshape(B, N, 1, 1, N)
+    rows = [0, 5, int(lengths.argmin()), int(lengths.argmax()), 400, 767]
+    _rows_vs_oracle(t, mask, rows, D**-0.5, TRIANGLE_ATTENTION_TOL[torch.bfloat16, "ieee"],
+                    rel_fro_max=NORTH_STAR_REL_FRO)

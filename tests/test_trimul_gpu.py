@@ -1,0 +1,308 @@
+"""HIP triangle multiplicative update vs the CPU oracle, per stage and end to end.
+
+Structural cases restate AMDResearch/geometric-nn-ops tests/test_trimul.py:70-404; accuracy
+uses its tolerance table (testutil/metrics.py:96-101) against the fp64 oracle, plus this
+build's rel-Frobenius <= 1e-2 for bf16. BASELINE config C3 (N=512, both directions, last
+64 residues padded) runs at full size against the fp64 oracle.
+"""
+
+import contextlib
+from unittest import mock
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (NORTH_STAR_REL_FRO, TRIMUL_TOL, Tolerance, assert_close_to_oracle, gen, np_weights,
+                     pair_input, randn, to_np, trimul_weights)
+from oracle import triangle_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+DIRECTIONS = pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+DTYPE_PRECISION = pytest.mark.parametrize(
+    ("dtype", "precision"),
+    [(torch.float32, "ieee"), (torch.float32, "tf32"), (torch.bfloat16, "ieee"), (torch.float16, "ieee")],
+    ids=["fp32_ieee", "fp32_tf32", "bf16", "fp16"],
+)
+
+
+@contextlib.contextmanager
+def matmul_precision(precision):
+    prev = torch.backends.cuda.matmul.fp32_precision
+    torch.backends.cuda.matmul.fp32_precision = precision
+    try:
+        yield
+    finally:
+        torch.backends.cuda.matmul.fp32_precision = prev
+
+
+def hip(x, direction, mask, w):
+    from geometric_nn_ops_torch.triangle._kernels.trimul import trimul_hip
+
+    with torch.no_grad():
+        return trimul_hip(x.to(DEV), direction, None if mask is None else mask.to(DEV),
+                          **{k: v.to(DEV) for k, v in w.items()})
+
+
+def oracle(x, direction, mask, w, **kw):
+    return O.trimul(to_np(x), direction, None if mask is None else to_np(mask), **np_weights(w), **kw)
+
+
+# ------------------------------------------------------------------------------- accuracy
+@DIRECTIONS
+@DTYPE_PRECISION
+def test_accuracy(direction, dtype, precision):
+    w = trimul_weights(32, 32, dtype, seed=3)
+    x, mask = pair_input(1, 32, 32, dtype, seed=4)
+    with matmul_precision(precision):
+        got = hip(x, direction, mask, w)
+    assert_close_to_oracle("out", got, oracle(x, direction, mask, w), TRIMUL_TOL[dtype, precision],
+                           rel_fro_max=NORTH_STAR_REL_FRO)
+
+
+@DIRECTIONS
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_stages_against_oracle(direction, dtype):
+    """Each kernel's output region of the workspace against the oracle's intermediate:
+    a, b (channel-major, transposed per channel for 'incoming'), g and o."""
+    from geometric_nn_ops_torch.triangle._kernels import trimul as K
+
+    B, N, C, Ch = 2, 40, 64, 32
+    w = trimul_weights(C, Ch, dtype, seed=5, biases=True, ln_random=True)
+    x, mask = pair_input(B, N, C, dtype, seed=6)
+    wd = {k: v.to(DEV) for k, v in w.items()}
+    with torch.no_grad():
+        args, keep, out, ws, off = K.build_args(x.to(DEV), direction, mask.to(DEV), 1e-5, wd)
+        K.run_stage("gnn_trimul_proj", args, x.device if x.is_cuda else torch.device(DEV))
+        K.run_stage("gnn_trimul_contract", args, torch.device(DEV))
+        K.run_stage("gnn_trimul_out", args, torch.device(DEV))
+        torch.cuda.synchronize()
+    NP = (N + 31) // 32 * 32
+    el = x.element_size()
+
+    def region(i, shape):
+        n = int(np.prod(shape))
+        return ws[off[i]:off[i] + n * el].view(dtype).reshape(shape)
+
+    st = O.trimul_stages(to_np(x), direction, to_np(mask), **np_weights(w))
+    tol = TRIMUL_TOL[dtype, "ieee"]
+    a_cm = region(0, (B, Ch, N, NP))[..., :N]
+    b_cm = region(1, (B, Ch, N, NP))[..., :N]
+    o_cm = region(3, (B, Ch, N, NP))[..., :N]
+    perm = (0, 2, 3, 1) if direction == "outgoing" else (0, 3, 2, 1)
+    assert_close_to_oracle("a", a_cm.permute(*perm), st["a"], tol)
+    assert_close_to_oracle("b", b_cm.permute(*perm), st["b"], tol)
+    assert_close_to_oracle("g", region(2, (B, N, N, C)), st["g"], tol)
+    assert_close_to_oracle("o", o_cm.permute(0, 2, 3, 1), st["o"], tol)
+    assert_close_to_oracle("out", out, st["out"], tol)
+
+
+@DIRECTIONS
+@pytest.mark.parametrize("shape", [(2, 48, 48, 128), (2, 3, 40, 40, 128)], ids=["batched", "5D"])
+def test_batched(direction, shape):
+    *batch, N, _, C = shape
+    w = trimul_weights(C, C, torch.bfloat16, seed=7)
+    x, mask = pair_input(tuple(batch), N, C, torch.bfloat16, seed=11)
+    assert_close_to_oracle("out", hip(x, direction, mask, w), oracle(x, direction, mask, w),
+                           Tolerance(1 - 1e-4, 1.5e-2), rel_fro_max=NORTH_STAR_REL_FRO)
+
+
+@DIRECTIONS
+@pytest.mark.parametrize("true_length", [32, 48])
+def test_block_padded(direction, true_length):
+    N, C, batch = 64, 128, 2
+    w = trimul_weights(C, C, torch.bfloat16, seed=11)
+    x, _ = pair_input(batch, N, C, torch.bfloat16, seed=13)
+    g = gen(13)
+    mask = torch.zeros(batch, N, N, dtype=torch.bfloat16)
+    for i in range(batch):
+        live = max(1, true_length - 8 * i)
+        mask[i, :live, :live] = (torch.rand(live, live, generator=g) < 0.9).to(torch.bfloat16)
+    assert_close_to_oracle("out", hip(x, direction, mask, w), oracle(x, direction, mask, w),
+                           Tolerance(1 - 1e-4, 1.5e-2), rel_fro_max=NORTH_STAR_REL_FRO)
+
+
+@DIRECTIONS
+@pytest.mark.parametrize("channels", [96, 128, 256])
+def test_channel_widths(direction, channels):
+    w = trimul_weights(channels, channels, torch.bfloat16, seed=17)
+    x, mask = pair_input(1, 24, channels, torch.bfloat16, seed=18)
+    assert_close_to_oracle("out", hip(x, direction, mask, w), oracle(x, direction, mask, w),
+                           Tolerance(1 - 1e-4, 2e-2))
+
+
+@DIRECTIONS
+def test_hidden_differs_from_channels(direction):
+    w = trimul_weights(64, 32, torch.bfloat16, seed=19)
+    x, mask = pair_input(1, 24, 64, torch.bfloat16, seed=20)
+    assert_close_to_oracle("out", hip(x, direction, mask, w), oracle(x, direction, mask, w),
+                           Tolerance(1 - 1e-4, 2e-2))
+
+
+@DIRECTIONS
+@pytest.mark.parametrize("gamma", ["zero", "tiny", "learned"])
+def test_layernorm_affine(direction, gamma):
+    N, C = 24, 128
+    dt = torch.bfloat16
+    w = trimul_weights(C, C, dt, seed=19)
+    g = gen(23)
+    gin, gout = torch.ones(C), torch.ones(C)
+    if gamma == "zero":
+        gin[0] = gin[5] = 0.0
+        gout[3] = 0.0
+    elif gamma == "tiny":
+        gin[:3] = torch.tensor([1e-2, 1e-3, 1e-4])
+        gout[0] = 1e-3
+    else:
+        gin = torch.randn(C, generator=g) * 0.5 + 1
+        gout = torch.randn(C, generator=g) * 0.5 + 1
+    w["norm_in_weight"], w["norm_out_weight"] = gin.to(dt), gout.to(dt)
+    w["norm_in_bias"] = (torch.randn(C, generator=g) * 0.1).to(dt)
+    w["norm_out_bias"] = (torch.randn(C, generator=g) * 0.1).to(dt)
+    x, mask = pair_input(1, N, C, dt, seed=20)
+    assert_close_to_oracle("out", hip(x, direction, mask, w), oracle(x, direction, mask, w),
+                           Tolerance(1 - 1e-4, 2e-2))
+
+
+def test_none_parameters():
+    """LayerNorm weights/biases and projection biases may all be None."""
+    w = trimul_weights(32, 32, torch.float32, seed=2)
+    w = {k: v for k, v in w.items() if "norm" not in k}
+    x, mask = pair_input(1, 20, 32, torch.float32, seed=3)
+    for direction in ("outgoing", "incoming"):
+        assert_close_to_oracle("out", hip(x, direction, mask, w), oracle(x, direction, mask, w),
+                               TRIMUL_TOL[torch.float32, "ieee"])
+
+
+# ---------------------------------------------------------------------------- structural
+@pytest.mark.parametrize("biased", [False, True])
+@DIRECTIONS
+def test_fully_masked_input(biased, direction):
+    N, C = 32, 128
+    w = trimul_weights(C, C, torch.float32, seed=3, biases=biased)
+    w["norm_out_bias"] = torch.full((C,), 0.25)
+    w["g_out_weight"] = torch.zeros(C, C)
+    x, _ = pair_input(1, N, C, torch.float32, seed=4)
+    out = hip(x, direction, torch.zeros(1, N, N), w)
+    torch.testing.assert_close(out, out[:, :1, :1].expand_as(out), rtol=0, atol=1e-6)
+    assert out.abs().max() > 0.01
+
+
+@pytest.mark.parametrize("which", ["p_in_bias", "g_in_bias", "p_out_bias", "g_out_bias"])
+@DIRECTIONS
+def test_each_projection_bias_contributes(which, direction):
+    w = trimul_weights(32, 32, torch.float32, seed=47, biases=True)
+    x, mask = pair_input(1, 16, 32, torch.float32, seed=49)
+    out = hip(x, direction, mask, w)
+    zeroed = hip(x, direction, mask, {**w, which: torch.zeros_like(w[which])})
+    assert not torch.allclose(out, zeroed, atol=1e-5)
+
+
+def test_direction_changes_the_result():
+    w = trimul_weights(128, 128, torch.float32, seed=7)
+    x, mask = pair_input(1, 32, 128, torch.float32, seed=8)
+    assert not torch.allclose(hip(x, "outgoing", mask, w), hip(x, "incoming", mask, w), rtol=1e-2, atol=1e-2)
+
+
+def test_unknown_direction_is_rejected():
+    from geometric_nn_ops_torch.triangle import triangle_multiplicative_update
+
+    w = trimul_weights(32, 32, torch.float32, seed=7)
+    x, mask = pair_input(1, 12, 32, torch.float32, seed=8)
+    with pytest.raises(ValueError, match="direction must be one of"):
+        hip(x, "outgoin", mask, w)
+    with pytest.raises(ValueError, match="direction must be one of"):
+        triangle_multiplicative_update(x.to(DEV), "outgoin", mask.to(DEV), **{k: v.to(DEV) for k, v in w.items()})
+
+
+@DIRECTIONS
+def test_mask_none_matches_ones(direction):
+    w = trimul_weights(32, 32, torch.float32, seed=37)
+    x, _ = pair_input(1, 12, 32, torch.float32, seed=38)
+    torch.testing.assert_close(hip(x, direction, None, w), hip(x, direction, torch.ones(1, 12, 12), w),
+                               rtol=0, atol=0)
+
+
+@DIRECTIONS
+def test_broadcast_mask(direction):
+    w = trimul_weights(32, 32, torch.float32, seed=31)
+    x, mask = pair_input(2, 12, 32, torch.float32, seed=32)
+    out = hip(x, direction, mask[0], w)
+    assert out.shape == x.shape
+    torch.testing.assert_close(out, hip(x, direction, mask[0].expand(x.shape[:-1]), w), rtol=0, atol=0)
+
+
+def test_tf32_changes_the_result():
+    w = trimul_weights(32, 32, torch.float32, seed=3)
+    x, mask = pair_input(1, 32, 32, torch.float32, seed=4)
+    with matmul_precision("ieee"):
+        full = hip(x, "outgoing", mask, w)
+    with matmul_precision("tf32"):
+        reduced = hip(x, "outgoing", mask, w)
+    assert not torch.equal(full, reduced)
+
+
+# ------------------------------------------------------------------------------ dispatch
+@contextlib.contextmanager
+def dispatch_spy():
+    from geometric_nn_ops_torch.triangle import _trimul
+
+    with mock.patch.object(_trimul, "trimul_torch", wraps=_trimul.trimul_torch) as ref, \
+            mock.patch.object(_trimul, "trimul_hip", wraps=_trimul.trimul_hip) as kern:
+        yield ref, kern
+
+
+@pytest.mark.parametrize("no_backward", [torch.no_grad, torch.inference_mode])
+def test_no_grad_modes_use_the_kernel(no_backward):
+    from geometric_nn_ops_torch.triangle import triangle_multiplicative_update
+
+    w = {k: v.to(DEV).requires_grad_() for k, v in trimul_weights(32, 32, torch.float32, seed=1).items()}
+    x, mask = pair_input(1, 12, 32, torch.float32, seed=3)
+    x = x.to(DEV).requires_grad_()
+    with no_backward(), dispatch_spy() as (ref, kern):
+        triangle_multiplicative_update(x, "outgoing", mask.to(DEV), **w)
+    assert kern.called and not ref.called
+
+
+@pytest.mark.parametrize("case", ["input_requires_grad", "weights_require_grad", "float64"])
+def test_unsupported_configs_use_the_torch_path(case):
+    from geometric_nn_ops_torch.triangle import triangle_multiplicative_update
+
+    dtype = torch.float64 if case == "float64" else torch.float32
+    w = {k: v.to(DEV) for k, v in trimul_weights(32, 32, dtype, seed=1).items()}
+    x, mask = pair_input(1, 12, 32, dtype, seed=3)
+    x = x.to(DEV)
+    if case == "input_requires_grad":
+        x.requires_grad_()
+    if case == "weights_require_grad":
+        w = {k: v.requires_grad_() for k, v in w.items()}
+    with dispatch_spy() as (ref, kern):
+        triangle_multiplicative_update(x, "outgoing", mask.to(DEV), **w)
+    assert ref.called and not kern.called
+
+
+# ------------------------------------------------------------------ BASELINE configs (full size)
+def test_config_c1_n64_fp32():
+    """C1 shape (x [1,64,64,128] fp32, unit LN, weights N(0,1/128), all-ones mask) on the GPU."""
+    w = trimul_weights(128, 128, torch.float32, seed=0)
+    x = randn((1, 64, 64, 128), seed=1)
+    mask = torch.ones(1, 64, 64)
+    with matmul_precision("ieee"):
+        got = hip(x, "outgoing", mask, w)
+    assert_close_to_oracle("out", got, oracle(x, "outgoing", mask, w), TRIMUL_TOL[torch.float32, "ieee"])
+
+
+@DIRECTIONS
+def test_config_c3_n512(direction):
+    """bf16 N=512, c_z = c_hidden = 128, LN gamma ~ 1+0.1N, beta ~ 0.1N, last 64 residues
+    masked on both axes."""
+    N, C = 512, 128
+    w = trimul_weights(C, C, torch.bfloat16, seed=0, ln_random=True)
+    x = randn((1, N, N, C), torch.bfloat16, seed=1)
+    live = torch.arange(N) < N - 64
+    mask = (live[:, None] & live[None, :]).to(torch.bfloat16)[None]
+    got = hip(x, direction, mask, w)
+    want = oracle(x, direction, mask, w)
+    assert_close_to_oracle("out", got, want, TRIMUL_TOL[torch.bfloat16, "ieee"], rel_fro_max=NORTH_STAR_REL_FRO)
