@@ -1,0 +1,133 @@
+"""The C-ABI boundary on a CPU-only host: libgnn_hip.so loads, exports every function the
+header declares, its ctypes struct mirrors have the C layout, and argument errors come
+back as status codes + messages before any GPU work is attempted."""
+
+import ctypes
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+from geometric_nn_ops_torch import _lib
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "gnn_triangle.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gnn_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert names, "no declarations parsed from the header"
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in gnn_triangle.h but not exported"
+    assert set(names) == set(_lib.EXPORTED_SYMBOLS)
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.library_path())],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r" T (gnn_[a-z_0-9]+)", out))
+    assert set(names) <= exported
+
+
+def test_version():
+    assert _lib.load().gnn_version().decode().endswith("gfx950")
+
+
+def _c_layout():
+    """offsetof/sizeof of the C structs, from a tiny host program compiled with gcc."""
+    src = r"""
+    #include <stdio.h>
+    #include <stddef.h>
+    #include "gnn_triangle.h"
+    #define P(T, f) printf(#T "." #f " %zu\n", offsetof(T, f));
+    int main(void) {
+      printf("gnn_triattn_args %zu\n", sizeof(gnn_triattn_args));
+      printf("gnn_trimul_args %zu\n", sizeof(gnn_trimul_args));
+      P(gnn_triattn_args, lse) P(gnn_triattn_args, D) P(gnn_triattn_args, bias_stride)
+      P(gnn_triattn_args, mask_stride) P(gnn_triattn_args, scale) P(gnn_triattn_args, precision)
+      P(gnn_trimul_args, mask_stride) P(gnn_trimul_args, workspace_bytes) P(gnn_trimul_args, Ch)
+      P(gnn_trimul_args, eps) P(gnn_trimul_args, precision)
+      return 0;
+    }
+    """
+    return src
+
+
+def test_ctypes_structs_match_c_layout(tmp_path):
+    c = tmp_path / "layout.c"
+    c.write_text(_c_layout())
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{ROOT / 'include'}", str(c), "-o", str(exe)], check=True)
+    lines = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                                check=True).stdout.splitlines())
+    assert int(lines["gnn_triattn_args"]) == ctypes.sizeof(_lib.TriAttnArgs)
+    assert int(lines["gnn_trimul_args"]) == ctypes.sizeof(_lib.TrimulArgs)
+    for key, val in lines.items():
+        if "." not in key:
+            continue
+        struct, field = key.split(".")
+        cls = _lib.TriAttnArgs if struct == "gnn_triattn_args" else _lib.TrimulArgs
+        assert getattr(cls, field).offset == int(val), key
+
+
+def test_null_args_are_rejected_without_a_gpu():
+    lib = _lib.load()
+    assert lib.gnn_triattn_fwd(None, None) == _lib.GNN_ERR_ARG
+    assert b"NULL" in lib.gnn_last_error()
+    assert lib.gnn_trimul_fwd(None, None) == _lib.GNN_ERR_ARG
+
+
+def test_triattn_argument_errors():
+    lib = _lib.load()
+    a = _lib.TriAttnArgs()
+    assert lib.gnn_triattn_fwd(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    assert b"required" in lib.gnn_last_error()
+    a.q = a.k = a.v = a.o = 4096
+    a.B = a.S = a.N = a.H = 1
+    a.D = 12
+    assert lib.gnn_triattn_fwd(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    assert b"multiple of 8" in lib.gnn_last_error()
+    a.D = 16
+    a.q_stride = _lib.I64x4(16, 16, 12, 16)
+    assert lib.gnn_triattn_fwd(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    assert b"strides" in lib.gnn_last_error()
+    with pytest.raises(ValueError, match="strides"):
+        _lib.check(_lib.GNN_ERR_ARG, "gnn_triattn_fwd")
+
+
+def test_trimul_argument_errors_and_workspace():
+    lib = _lib.load()
+    off = (ctypes.c_size_t * 4)()
+    n = lib.gnn_trimul_workspace_bytes(1, 512, 128, 128, _lib.GNN_BF16, off)
+    plane = 128 * 512 * 512 * 2
+    assert off[0] == 0 and off[1] == plane and off[2] == 2 * plane
+    assert off[3] == 2 * plane + 512 * 512 * 128 * 2 and n == off[3] + plane
+    assert lib.gnn_trimul_workspace_bytes(1, 100, 32, 32, _lib.GNN_F32, None) % 256 == 0
+    a = _lib.TrimulArgs()
+    assert lib.gnn_trimul_fwd(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    a.x = a.out = a.p_in_w = a.g_in_w = a.p_out_w = a.g_out_w = 4096
+    a.B, a.N, a.C, a.Ch = 1, 8, 48, 32
+    a.dtype = _lib.GNN_BF16
+    assert lib.gnn_trimul_proj(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
+    assert b"multiples of 32" in lib.gnn_last_error()
+    a.C = 32
+    a.workspace = 4096
+    a.workspace_bytes = 10
+    assert lib.gnn_trimul_contract(ctypes.byref(a), None) == _lib.GNN_ERR_WORKSPACE
+    with pytest.raises(RuntimeError, match="workspace"):
+        _lib.check(_lib.GNN_ERR_WORKSPACE, "gnn_trimul_contract")
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setenv("GNN_HIP_LIB", str(tmp_path / "nope.so"))
+    with pytest.raises(RuntimeError, match="not found"):
+        _lib.load()
+    monkeypatch.delenv("GNN_HIP_LIB")
+    monkeypatch.setattr(_lib, "_lib", None)
+    _lib.load()
