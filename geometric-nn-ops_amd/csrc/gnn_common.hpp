@@ -155,11 +155,9 @@ template <> struct Mma<float, PREC_BF16X3> {
 // ---- misc -------------------------------------------------------------------------------
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Value held by lane (l ^ 32).
-__device__ __forceinline__ float swap_halves(float x) {
-  int v = __builtin_bit_cast(int, x);
-  return __builtin_bit_cast(float, __builtin_amdgcn_permlane32_swap(v, v, false, false)[0]);
-}
+// Reductions over the lane pair (l, l ^ 32).
+__device__ __forceinline__ float pair_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
+__device__ __forceinline__ float pair_sum(float x) { return x + __shfl_xor(x, 32); }
 
 __device__ __forceinline__ float sigmoidf_fast(float x) {
   return 1.0f / (1.0f + fast_exp2(-x * 1.4426950408889634f));

@@ -210,7 +210,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
     const int kbase = t * KT;
     const int nvalid = min(KT, N - kbase);
     const uint64_t valid = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
-    const bool all_live = live == valid;
+    const bool all_live = live == ~0ull;  // every one of the 64 keys exists and is kept
 
     f32x16 sc[2];
 #pragma unroll
@@ -264,7 +264,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
     for (int r = 1; r < 16; ++r) mt = fmaxf(mt, sc[0][r]);
 #pragma unroll
     for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[1][r]);
-    mt = fmaxf(mt, swap_halves(mt));
+    mt = pair_max(mt);
     if (__any(mt > m + RESCALE_THRESHOLD)) {
       const float mnew = fmaxf(m, mt);
       const float alpha = fast_exp2(m - mnew);  // 0 on the first tile (m = -inf)
@@ -314,7 +314,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
   (void)row_dead;
 
   // ---- normalise and store. o[c][r] is O[myq][32c + 8*(r/4) + 4g + r%4].
-  const float ltot = lsum + swap_halves(lsum);
+  const float ltot = pair_sum(lsum);
   const float inv = 1.0f / ltot;
   if (qvalid) {
     T* orow = op + (int64_t)myq * osn;

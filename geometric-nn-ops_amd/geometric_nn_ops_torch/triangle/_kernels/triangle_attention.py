@@ -26,7 +26,6 @@ def supports(q: torch.Tensor) -> bool:
 
 
 def _vectorizable(t: torch.Tensor, dims) -> bool:
-    elem = t.element_size()
     return t.data_ptr() % 16 == 0 and t.stride(-1) == 1 and all(t.stride(d) % 8 == 0 for d in dims)
 
 
@@ -83,7 +82,12 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
     if bias is not None:
         bias = bias.to(q.dtype)
         if not (bias.stride(-1) == 1 and bias.stride(-2) % 8 == 0 and bias.data_ptr() % 16 == 0):
-            bias = bias.contiguous()
+            # unit key stride and a query pitch that is a multiple of 8 elements; keys
+            # past N in the padded pitch are never read
+            pitch = (N + 7) // 8 * 8
+            padded = torch.empty((B, 1, H, N, pitch), device=bias.device, dtype=bias.dtype)
+            padded[..., :N] = bias
+            bias = padded
         args.bias = bias.data_ptr()
         args.bias_stride = _lib.I64x4(bias.stride(0), bias.stride(2), bias.stride(3), bias.stride(4))
     if mask is not None:

@@ -57,19 +57,18 @@ def build_args(x, direction, mask, eps, weights):
     N, N2, C = x.shape[-3], x.shape[-2], x.shape[-1]
     if N != N2:
         raise ValueError(f"x must be [*, N, N, C_z], got {tuple(x.shape)}")
+    for key in ("p_in_weight", "g_in_weight", "p_out_weight", "g_out_weight"):
+        if weights.get(key) is None:
+            raise ValueError(f"{key} is required")
     Ch = weights["p_in_weight"].shape[0] // 2
-    _expect("p_in_weight", weights["p_in_weight"], (2 * Ch, C))
-    _expect("g_in_weight", weights["g_in_weight"], (2 * Ch, C))
-    _expect("p_out_weight", weights["p_out_weight"], (C, Ch))
-    _expect("g_out_weight", weights["g_out_weight"], (C, C))
-    _expect("norm_in_weight", weights["norm_in_weight"], (C,))
-    _expect("norm_in_bias", weights["norm_in_bias"], (C,))
-    _expect("norm_out_weight", weights["norm_out_weight"], (Ch,))
-    _expect("norm_out_bias", weights["norm_out_bias"], (Ch,))
-    _expect("p_in_bias", weights["p_in_bias"], (2 * Ch,))
-    _expect("g_in_bias", weights["g_in_bias"], (2 * Ch,))
-    _expect("p_out_bias", weights["p_out_bias"], (C,))
-    _expect("g_out_bias", weights["g_out_bias"], (C,))
+    expected = {
+        "p_in_weight": (2 * Ch, C), "g_in_weight": (2 * Ch, C), "p_out_weight": (C, Ch),
+        "g_out_weight": (C, C), "norm_in_weight": (C,), "norm_in_bias": (C,),
+        "norm_out_weight": (Ch,), "norm_out_bias": (Ch,), "p_in_bias": (2 * Ch,),
+        "g_in_bias": (2 * Ch,), "p_out_bias": (C,), "g_out_bias": (C,),
+    }
+    for key, shape in expected.items():
+        _expect(key, weights.get(key), shape)
     lead = x.shape[:-3]
     B = math.prod(lead)
 
