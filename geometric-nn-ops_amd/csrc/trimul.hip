@@ -13,7 +13,7 @@
 //   contract (stage 2)  o_c = A_c B_c^T per (batch, channel): a 128x128-tile MFMA GEMM with
 //                       both operands k-contiguous, staged through LDS.
 //   out      (stage 3)  LN_out over the Ch channels of each pixel (the channel-major o tile
-//                       is transposed through LDS), then out = (LN(o) Wpo^T + bpo) * g.
+//                       is read down its columns in LDS), then out = (LN(o) Wpo^T + bpo) * g.
 //
 // Workspace (element type = input dtype): a, b, o are [B, Ch, N, NP] with a row pitch
 // NP = round_up(N, 32) so every row is 16-byte aligned; g is [B, N, N, C].
@@ -44,15 +44,24 @@ __host__ __device__ constexpr int lds_pad() {
 }
 
 // ============================== stage 1: LN-in + projections ==============================
+// One workgroup = PT pixels along one row ('outgoing') or column ('incoming') of the pair
+// grid. LDS holds the x tile (normalised in place to z), the LayerNorm parameters and the
+// tile's mask values. Work units per wave: 32 channels of the 2*Ch gated projection (p and
+// its gate g_in share the unit so the epilogue can combine them), or 32 channels of the
+// output gate. Weight fragments are read once per pair of 32-pixel sub-tiles.
 template <typename T, int PREC>
-__global__ __launch_bounds__(NT) void trimul_proj_kernel(const gnn_trimul_args a, int64_t NP,
-                                                         size_t off_a, size_t off_b,
-                                                         size_t off_g) {
+__global__ __launch_bounds__(NT, 2) void trimul_proj_kernel(const gnn_trimul_args a, int64_t NP,
+                                                            size_t off_a, size_t off_b,
+                                                            size_t off_g) {
   typedef typename TypeOps<T>::V8 V8;
+  typedef typename TypeOps<T>::V4 V4;
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  T* zs = reinterpret_cast<T*>(smem_raw);
   const int C = (int)a.C, Ch = (int)a.Ch, N = (int)a.N;
   const int ZR = C + lds_pad<T>();
+  T* zs = reinterpret_cast<T*>(smem_raw);                                   // [PT][ZR]
+  float* lnw = reinterpret_cast<float*>(smem_raw + (size_t)PT * ZR * sizeof(T));  // [C]
+  float* lnb = lnw + C;                                                      // [C]
+  float* mk = lnb + C;                                                       // [PT]
 
   const int ntile = (N + PT - 1) / PT;
   const int ct = blockIdx.x % ntile;
@@ -70,9 +79,25 @@ __global__ __launch_bounds__(NT) void trimul_proj_kernel(const gnn_trimul_args a
     return ((int64_t)b * N + pp) * N + qq;
   };
 
-  // ---- load the x tile (PT pixels x C channels) into LDS
+  for (int c = tid; c < C; c += NT) {
+    lnw[c] = ld_or<T>(a.ln_in_w, c, 1.f);
+    lnb[c] = ld_or<T>(a.ln_in_b, c, 0.f);
+  }
+  for (int pl = tid; pl < PT; pl += NT) {
+    float mval = 1.f;
+    if (a.mask && c0 + pl < N) {
+      const int cpos = c0 + pl;
+      const int pp = outgoing ? row : cpos;
+      const int qq = outgoing ? cpos : row;
+      mval = TypeOps<T>::to_f32(
+          ((const T*)a.mask)[b * a.mask_stride[0] + pp * a.mask_stride[1] + qq * a.mask_stride[2]]);
+    }
+    mk[pl] = mval;
+  }
+
+  // ---- x tile (PT pixels x C channels) into LDS
   const T* __restrict__ x = (const T*)a.x;
-  const int cpp = C / 8;  // 8-element chunks per pixel
+  const int cpp = C / 8;
   for (int c = tid; c < PT * cpp; c += NT) {
     const int pl = c / cpp, k0 = (c % cpp) * 8;
     V8 v = zero8<T>();
@@ -81,13 +106,14 @@ __global__ __launch_bounds__(NT) void trimul_proj_kernel(const gnn_trimul_args a
   }
   __syncthreads();
 
-  // ---- LayerNorm, 2 threads per pixel, in place
+  // ---- LayerNorm in place, 2 threads per pixel (fp32 statistics, biased variance)
   {
     const int pl = tid >> 1, half = tid & 1;
     const int k0 = half * (C / 2);
+    T* zrow = &zs[pl * ZR];
     float sum = 0.f;
     for (int k = k0; k < k0 + C / 2; k += 8) {
-      f32x8 v = TypeOps<T>::to_f32(load8(&zs[pl * ZR + k]));
+      const f32x8 v = TypeOps<T>::to_f32(load8(zrow + k));
 #pragma unroll
       for (int e = 0; e < 8; ++e) sum += v[e];
     }
@@ -95,7 +121,7 @@ __global__ __launch_bounds__(NT) void trimul_proj_kernel(const gnn_trimul_args a
     const float mean = sum / (float)C;
     float sq = 0.f;
     for (int k = k0; k < k0 + C / 2; k += 8) {
-      f32x8 v = TypeOps<T>::to_f32(load8(&zs[pl * ZR + k]));
+      const f32x8 v = TypeOps<T>::to_f32(load8(zrow + k));
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float d = v[e] - mean;
@@ -105,17 +131,21 @@ __global__ __launch_bounds__(NT) void trimul_proj_kernel(const gnn_trimul_args a
     sq += __shfl_xor(sq, 1);
     const float rstd = 1.0f / sqrtf(sq / (float)C + a.eps);
     for (int k = k0; k < k0 + C / 2; k += 8) {
-      f32x8 v = TypeOps<T>::to_f32(load8(&zs[pl * ZR + k]));
+      f32x8 v = TypeOps<T>::to_f32(load8(zrow + k));
+      const f32x4 w0 = *reinterpret_cast<const f32x4*>(lnw + k);
+      const f32x4 w1 = *reinterpret_cast<const f32x4*>(lnw + k + 4);
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(lnb + k);
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(lnb + k + 4);
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        v[e] = (v[e] - mean) * rstd * ld_or<T>(a.ln_in_w, k + e, 1.f) + ld_or<T>(a.ln_in_b, k + e, 0.f);
-      store8(&zs[pl * ZR + k], TypeOps<T>::from_f32(v));
+      for (int e = 0; e < 4; ++e) {
+        v[e] = (v[e] - mean) * rstd * w0[e] + b0[e];
+        v[e + 4] = (v[e + 4] - mean) * rstd * w1[e] + b1[e];
+      }
+      store8(zrow + k, TypeOps<T>::from_f32(v));
     }
   }
   __syncthreads();
 
-  // ---- projections. Units: [0, npg) gated p units of 32 channels of the 2*Ch projection
-  // (p and its gate in one wave), then C/32 units of the output gate.
   const int npg = 2 * Ch / 32;
   const int nunits = npg + C / 32;
   const int nk = C / 16;
@@ -128,61 +158,82 @@ __global__ __launch_bounds__(NT) void trimul_proj_kernel(const gnn_trimul_args a
 
   for (int u = wave; u < nunits; u += 4) {
     if (u < npg) {
-      const int cc0 = 32 * u;
-      float bp[16], bg[16];
+      // acc[s][.] = [pixel][channel] tiles: row = pixel 32*sub + 8*(r/4) + 4g + r%4, col = channel
+      const int ch = 32 * u + l32;  // channel of the 2*Ch projection held by this lane
+      const float bp = ld_or<T>(a.p_in_b, ch, 0.f);
+      const float bg = ld_or<T>(a.g_in_b, ch, 0.f);
+      T* dst = ch < Ch ? a_cm : b_cm;
+      const int chh = ch < Ch ? ch : ch - Ch;
+      T* drow = dst + (((int64_t)b * Ch + chh) * N + row) * NP + c0;
+      const T* wprow = wp + (int64_t)ch * C + 8 * g;
+      const T* wgrow = wg + (int64_t)ch * C + 8 * g;
+      for (int sp = 0; sp < PT / 32; sp += 2) {
+        f32x16 accp[2], accg[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int ch = cc0 + 8 * (r / 4) + 4 * g + (r % 4);
-        bp[r] = ld_or<T>(a.p_in_b, ch, 0.f);
-        bg[r] = ld_or<T>(a.g_in_b, ch, 0.f);
-      }
-      for (int sub = 0; sub < PT / 32; ++sub) {
-        f32x16 accp, accg;
+        for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) accp[r] = accg[r] = 0.f;
+          for (int r = 0; r < 16; ++r) accp[s][r] = accg[s][r] = 0.f;
         for (int k = 0; k < nk; ++k) {
-          const V8 zf = load8(&zs[(32 * sub + l32) * ZR + 16 * k + 8 * g]);
-          const V8 wpf = load8(wp + (int64_t)(cc0 + l32) * C + 16 * k + 8 * g);
-          const V8 wgf = load8(wg + (int64_t)(cc0 + l32) * C + 16 * k + 8 * g);
-          Mma<T, PREC>::step(accp, wpf, zf);  // [channel][pixel]
-          Mma<T, PREC>::step(accg, wgf, zf);
-        }
-        const int pl = 32 * sub + l32;
-        if (c0 + pl < N) {
-          float mval = 1.f;
-          if (a.mask) {
-            const int cpos = c0 + pl;
-            const int pp = outgoing ? row : cpos;
-            const int qq = outgoing ? cpos : row;
-            mval = TypeOps<T>::to_f32(((const T*)a.mask)[b * a.mask_stride[0] + pp * a.mask_stride[1] +
-                                                         qq * a.mask_stride[2]]);
-          }
+          const V8 wpf = load8(wprow + 16 * k);
+          const V8 wgf = load8(wgrow + 16 * k);
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int ch = cc0 + 8 * (r / 4) + 4 * g + (r % 4);
-            const float v = (accp[r] + bp[r]) * sigmoid_acc(accg[r] + bg[r]) * mval;
-            T* dst = ch < Ch ? a_cm : b_cm;
-            const int chh = ch < Ch ? ch : ch - Ch;
-            dst[(((int64_t)b * Ch + chh) * N + row) * NP + c0 + pl] = TypeOps<T>::from_f32(v);
+          for (int s = 0; s < 2; ++s) {
+            const V8 zf = load8(&zs[(32 * (sp + s) + l32) * ZR + 16 * k + 8 * g]);
+            Mma<T, PREC>::step(accp[s], zf, wpf);
+            Mma<T, PREC>::step(accg[s], zf, wgf);
           }
         }
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int rg = 0; rg < 4; ++rg) {
+            const int pl = 32 * (sp + s) + 8 * rg + 4 * g;
+            f32x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              v[e] = (accp[s][4 * rg + e] + bp) * sigmoid_acc(accg[s][4 * rg + e] + bg) * mk[pl + e];
+            if (c0 + pl + 3 < N) {
+              store4(drow + pl, TypeOps<T>::from_f32(v));
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (c0 + pl + e < N) drow[pl + e] = TypeOps<T>::from_f32(v[e]);
+            }
+          }
       }
     } else {
-      const int ch = 32 * (u - npg) + l32;
-      const float bgo = ld_or<T>(a.g_out_b, ch, 0.f);
-      for (int sub = 0; sub < PT / 32; ++sub) {
-        f32x16 acc;
+      // acc[s] = [channel][pixel]: row = channel c00 + 8*(r/4) + 4g + r%4, col = pixel
+      const int c00 = 32 * (u - npg);
+      float bgo[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+      for (int r = 0; r < 16; ++r) bgo[r] = ld_or<T>(a.g_out_b, c00 + 8 * (r / 4) + 4 * g + (r % 4), 0.f);
+      const T* wrow = wgo + (int64_t)(c00 + l32) * C + 8 * g;
+      for (int sp = 0; sp < PT / 32; sp += 2) {
+        f32x16 acc[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[s][r] = 0.f;
         for (int k = 0; k < nk; ++k) {
-          const V8 zf = load8(&zs[(32 * sub + l32) * ZR + 16 * k + 8 * g]);
-          const V8 wf = load8(wgo + (int64_t)ch * C + 16 * k + 8 * g);
-          Mma<T, PREC>::step(acc, zf, wf);  // [pixel][channel]
+          const V8 wf = load8(wrow + 16 * k);
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            const V8 zf = load8(&zs[(32 * (sp + s) + l32) * ZR + 16 * k + 8 * g]);
+            Mma<T, PREC>::step(acc[s], wf, zf);
+          }
         }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int pl = 32 * sub + 8 * (r / 4) + 4 * g + (r % 4);
-          if (c0 + pl < N) gout[pix_index(pl) * C + ch] = TypeOps<T>::from_f32(sigmoid_acc(acc[r] + bgo));
+        for (int s = 0; s < 2; ++s) {
+          const int pl = 32 * (sp + s) + l32;
+          if (c0 + pl >= N) continue;
+          T* grow = gout + pix_index(pl) * C + c00 + 4 * g;
+#pragma unroll
+          for (int rg = 0; rg < 4; ++rg) {
+            f32x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = sigmoid_acc(acc[s][4 * rg + e] + bgo[4 * rg + e]);
+            store4(grow + 8 * rg, TypeOps<T>::from_f32(v));
+          }
         }
       }
     }
@@ -307,97 +358,132 @@ __global__ __launch_bounds__(NT, 2) void trimul_contract_kernel(const T* __restr
 }
 
 // ============================== stage 3: LN-out + p_out + gate ============================
+// One workgroup = PTO pixels of one row of the pair grid. The channel-major o tile is
+// loaded with 16-byte rows, normalised per pixel (4 threads per pixel reading down the
+// channel columns), written back pixel-major, then multiplied by p_out on MFMA with the
+// gate applied in the epilogue (8-byte loads of g, 8-byte stores of out).
+constexpr int PTO = 64;
+
 template <typename T, int PREC>
-__global__ __launch_bounds__(NT) void trimul_out_kernel(const gnn_trimul_args a, int64_t NP,
-                                                        size_t off_g, size_t off_o) {
+__global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args a, int64_t NP,
+                                                           size_t off_g, size_t off_o) {
   typedef typename TypeOps<T>::V8 V8;
+  typedef typename TypeOps<T>::V4 V4;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int C = (int)a.C, Ch = (int)a.Ch, N = (int)a.N;
-  const int OR = PT + lds_pad<T>();   // raw o tile [Ch][PT]
-  const int ZR = Ch + lds_pad<T>();   // normalised tile [PT][Ch]
+  const int OR = PTO + lds_pad<T>();  // raw o tile [Ch][OR]
+  const int ZR = Ch + lds_pad<T>();   // normalised tile [PTO][ZR]
   T* ot = reinterpret_cast<T*>(smem_raw);
-  T* zs = ot + Ch * OR;
+  T* zs = ot + (size_t)Ch * OR;
+  float* lnw = reinterpret_cast<float*>(zs + (size_t)PTO * ZR);
+  float* lnb = lnw + Ch;
 
-  const int ntile = (N + PT - 1) / PT;
+  const int ntile = (N + PTO - 1) / PTO;
   const int ct = blockIdx.x % ntile;
   const int p = (blockIdx.x / ntile) % N;
   const int b = blockIdx.x / (ntile * N);
-  const int q0 = ct * PT;
+  const int q0 = ct * PTO;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
 
   const T* __restrict__ ocm = (const T*)((const unsigned char*)a.workspace + off_o);
   const T* __restrict__ gg = (const T*)((const unsigned char*)a.workspace + off_g);
   T* __restrict__ out = (T*)a.out;
 
-  // ---- o tile, channel-major: rows are channels, PT consecutive pixels each
-  for (int c = tid; c < Ch * (PT / 8); c += NT) {
-    const int ch = c / (PT / 8), k0 = (c % (PT / 8)) * 8;
+  for (int c = tid; c < Ch; c += NT) {
+    lnw[c] = ld_or<T>(a.ln_out_w, c, 1.f);
+    lnb[c] = ld_or<T>(a.ln_out_b, c, 0.f);
+  }
+  for (int c = tid; c < Ch * (PTO / 8); c += NT) {
+    const int ch = c / (PTO / 8), k0 = (c % (PTO / 8)) * 8;
     V8 v = zero8<T>();
     if (q0 + k0 < N) v = load8(ocm + (((int64_t)b * Ch + ch) * N + p) * NP + q0 + k0);
     store8(&ot[ch * OR + k0], v);
   }
   __syncthreads();
 
-  // ---- LayerNorm over channels, 2 threads per pixel; result pixel-major in zs
+  // ---- LayerNorm over channels: 4 threads per pixel, each a quarter of the channels
   {
-    const int pl = tid >> 1, half = tid & 1;
-    const int k0 = half * (Ch / 2);
+    const int pl = tid >> 2, qtr = tid & 3;
+    const int k0 = qtr * (Ch / 4), k1 = k0 + Ch / 4;
     float sum = 0.f;
-    for (int k = k0; k < k0 + Ch / 2; ++k) sum += TypeOps<T>::to_f32(ot[k * OR + pl]);
+    for (int k = k0; k < k1; ++k) sum += TypeOps<T>::to_f32(ot[k * OR + pl]);
     sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
     const float mean = sum / (float)Ch;
     float sq = 0.f;
-    for (int k = k0; k < k0 + Ch / 2; ++k) {
+    for (int k = k0; k < k1; ++k) {
       const float d = TypeOps<T>::to_f32(ot[k * OR + pl]) - mean;
       sq += d * d;
     }
     sq += __shfl_xor(sq, 1);
+    sq += __shfl_xor(sq, 2);
     const float rstd = 1.0f / sqrtf(sq / (float)Ch + a.eps);
-    for (int k = k0; k < k0 + Ch / 2; k += 8) {
+    for (int k = k0; k < k1; k += 8) {
       f32x8 v;
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        v[e] = (TypeOps<T>::to_f32(ot[(k + e) * OR + pl]) - mean) * rstd *
-                   ld_or<T>(a.ln_out_w, k + e, 1.f) +
-               ld_or<T>(a.ln_out_b, k + e, 0.f);
+        v[e] = (TypeOps<T>::to_f32(ot[(k + e) * OR + pl]) - mean) * rstd * lnw[k + e] + lnb[k + e];
       store8(&zs[pl * ZR + k], TypeOps<T>::from_f32(v));
     }
   }
   __syncthreads();
 
-  // ---- out[pixel][c] = (z Wpo^T + bpo) * g; units = pixel sub-tile x 32 output channels
+  // ---- out = (z Wpo^T + bpo) * g. acc[s] = [cout][pixel]: row = cout 32ctile + 8(r/4) + 4g + r%4
   const T* __restrict__ wpo = (const T*)a.p_out_w;
-  const int nct = C / 32;
   const int nk = Ch / 16;
-  for (int u = wave; u < (PT / 32) * nct; u += 4) {
-    const int ps = u / nct, ctile = u % nct;
-    const int ch = 32 * ctile + l32;
-    f32x16 acc;
+  for (int ctile = wave; ctile < C / 32; ctile += 4) {
+    const int cbase = 32 * ctile + 4 * g;
+    float bpo[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    for (int r = 0; r < 16; ++r) bpo[r] = ld_or<T>(a.p_out_b, cbase + 8 * (r / 4) + (r % 4), 0.f);
+    const T* wrow = wpo + (int64_t)(32 * ctile + l32) * Ch + 8 * g;
+    f32x16 acc[PTO / 32];
+#pragma unroll
+    for (int s = 0; s < PTO / 32; ++s)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[s][r] = 0.f;
     for (int k = 0; k < nk; ++k) {
-      const V8 zf = load8(&zs[(32 * ps + l32) * ZR + 16 * k + 8 * g]);
-      const V8 wf = load8(wpo + (int64_t)ch * Ch + 16 * k + 8 * g);
-      Mma<T, PREC>::step(acc, zf, wf);  // [pixel][channel]
-    }
-    const float bpo = ld_or<T>(a.p_out_b, ch, 0.f);
+      const V8 wf = load8(wrow + 16 * k);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int q = q0 + 32 * ps + 8 * (r / 4) + 4 * g + (r % 4);
-      if (q < N) {
-        const int64_t pix = ((int64_t)b * N + p) * N + q;
-        const float gv = TypeOps<T>::to_f32(gg[pix * C + ch]);
-        out[pix * C + ch] = TypeOps<T>::from_f32((acc[r] + bpo) * gv);
+      for (int s = 0; s < PTO / 32; ++s) {
+        const V8 zf = load8(&zs[(32 * s + l32) * ZR + 16 * k + 8 * g]);
+        Mma<T, PREC>::step(acc[s], wf, zf);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < PTO / 32; ++s) {
+      const int q = q0 + 32 * s + l32;
+      if (q >= N) continue;
+      const int64_t pix = ((int64_t)b * N + p) * N + q;
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int64_t off = pix * C + cbase + 8 * rg;
+        const f32x4 gv = TypeOps<T>::to_f32(load4(gg + off));
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (acc[s][4 * rg + e] + bpo[4 * rg + e]) * gv[e];
+        store4(out + off, TypeOps<T>::from_f32(v));
       }
     }
   }
+}
+
+template <typename T>
+size_t proj_smem(const gnn_trimul_args& a) {
+  return (size_t)PT * (a.C + lds_pad<T>()) * sizeof(T) + (2 * (size_t)a.C + PT) * sizeof(float);
+}
+
+template <typename T>
+size_t out_smem(const gnn_trimul_args& a) {
+  return ((size_t)a.Ch * (PTO + lds_pad<T>()) + (size_t)PTO * (a.Ch + lds_pad<T>())) * sizeof(T) +
+         2 * (size_t)a.Ch * sizeof(float);
 }
 
 template <typename T, int PREC>
 int launch_proj(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
   const int64_t NP = round_up(a.N, 32);
   const int64_t ntile = (a.N + PT - 1) / PT;
-  const size_t smem = (size_t)PT * (a.C + lds_pad<T>()) * sizeof(T);
+  const size_t smem = proj_smem<T>(a);
   if (smem > 64 * 1024)
     (void)hipFuncSetAttribute((const void*)trimul_proj_kernel<T, PREC>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
@@ -421,9 +507,8 @@ int launch_contract(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t
 template <typename T, int PREC>
 int launch_out(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
   const int64_t NP = round_up(a.N, 32);
-  const int64_t ntile = (a.N + PT - 1) / PT;
-  const size_t smem =
-      ((size_t)a.Ch * (PT + lds_pad<T>()) + (size_t)PT * (a.Ch + lds_pad<T>())) * sizeof(T);
+  const int64_t ntile = (a.N + PTO - 1) / PTO;
+  const size_t smem = out_smem<T>(a);
   if (smem > 64 * 1024)
     (void)hipFuncSetAttribute((const void*)trimul_out_kernel<T, PREC>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
@@ -449,8 +534,9 @@ int check_args(const gnn_trimul_args& a, const char* who) {
     if (((uintptr_t)ptr) % 16 != 0)
       return set_error(GNN_ERR_ARG, "trimul: x, out, weights and workspace must be 16-byte aligned");
   const size_t e = a.dtype == GNN_F32 ? 4 : 2;
-  if ((size_t)PT * (a.C + 16 / e) * e > 160 * 1024 ||
-      ((size_t)a.Ch * (PT + 16 / e) + (size_t)PT * (a.Ch + 16 / e)) * e > 160 * 1024)
+  const size_t proj_lds = (size_t)PT * (a.C + 16 / e) * e + (2 * (size_t)a.C + PT) * 4;
+  const size_t out_lds = ((size_t)a.Ch * (PTO + 16 / e) + (size_t)PTO * (a.Ch + 16 / e)) * e + 2 * (size_t)a.Ch * 4;
+  if (proj_lds > 160 * 1024 || out_lds > 160 * 1024)
     return set_error(GNN_ERR_UNSUPPORTED, "trimul: channel count too large for the LDS tiles");
   if (a.B * a.N * ((a.N + PT - 1) / PT) >= ((int64_t)1 << 31))
     return set_error(GNN_ERR_UNSUPPORTED, "trimul: grid too large");
