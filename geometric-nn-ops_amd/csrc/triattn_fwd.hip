@@ -15,12 +15,19 @@
 //   * O^T = V^T P^T: the probabilities feed the second MFMA straight from the score
 //     registers (P^T is the B operand), and the running-max rescale of O is a per-lane
 //     scalar multiply.
-//   * K (row-major) and V^T are staged per 64-key tile in LDS, shared by the 4 waves;
-//     Q' = bf16(q * scale * log2 e) lives in registers for the whole loop.
-//   * Scores are kept in log2 units (log2 e folded into Q' and into the bias / mask
-//     terms) so p = exp2(s - m) costs one subtract and one v_exp_f32.
-//   * The running max is only moved when a tile raises it by more than 8 (log2 units),
-//     so most tiles skip the O / l rescale; p then stays below 2^8.
+//   * K (row-major), V^T and the [128 query x 64 key] pair-bias tile are staged per key
+//     tile in LDS (16-byte coalesced global loads), shared by the 4 waves; Q' =
+//     bf16(q * scale), rounded like the reference's Q * softmax_scale, lives in registers.
+//   * For 16-bit inputs the pair bias is added by the MFMA unit: one extra 32x32x16 step
+//     per 16 keys multiplies an identity fragment (rows = keys) by the bias fragment read
+//     from LDS (cols = queries), so no VALU work is spent on the bias. fp32 inputs add it
+//     on the VALU.
+//   * p = exp2(s * log2 e - m * log2 e) is one FMA and one v_exp_f32 per score (rows with
+//     no live key use the exact (s - m) * log2 e, since m is then the -1e9 sentinel); the
+//     row sum is taken on the rounded probabilities with v_dot2 (16-bit inputs), so the
+//     normaliser matches what the PV product consumes.
+//   * The running max is only moved when a tile raises it by more than 8 ln 2, so most
+//     tiles skip the O / l rescale; p then stays below 2^8.
 //   * Key tiles whose keys are all masked are skipped when the row has at least one
 //     live key (their probabilities are exactly 0 either way). Rows with no live key
 //     are computed in full, reproducing the finite-sentinel result of the reference.
@@ -41,7 +48,7 @@ constexpr int KT = 64;   // keys per LDS tile
 constexpr int NTHREADS = 256;
 constexpr int MAX_TILES = 512;  // N <= 32768
 constexpr float LOG2E = 1.4426950408889634f;
-constexpr float RESCALE_THRESHOLD = 8.0f;  // log2 units
+constexpr float RESCALE_THRESHOLD = 8.0f / LOG2E;  // natural-log units: p <= 2^8
 
 template <typename T, int DP>
 struct Smem {
@@ -49,8 +56,13 @@ struct Smem {
   static constexpr int VPAD = 4;
   static constexpr int KROW = DP + KPAD;
   static constexpr int VROW = KT + VPAD;
-  T k[KT * KROW];
-  T vt[DP * VROW];
+  static constexpr int BROW = KT + KPAD;  // bias tile row pitch (16 B of padding)
+  static constexpr int STAGE_BYTES = (KT * KROW + DP * VROW + QB * BROW) * (int)sizeof(T);
+  // two stages (one barrier per key tile) when they fit in 80 KB, else one
+  static constexpr int NBUF = 2 * STAGE_BYTES <= 80 * 1024 ? 2 : 1;
+  T k[NBUF][KT * KROW];
+  T vt[NBUF][DP * VROW];
+  T bias[NBUF][QB * BROW];
   uint64_t tile_live[MAX_TILES];  // bit j: key tile*64+j is < N and unmasked
   uint16_t tile_list[MAX_TILES];
   int ntiles_run;
@@ -64,12 +76,22 @@ __device__ __forceinline__ typename TypeOps<T>::V8 frag_from_acc(const f32x16& p
   return TypeOps<T>::from_f32(x);
 }
 
-// Sum of the values the MFMA will actually consume (the rounded probabilities), so the
-// normaliser matches the numerator exactly.
-template <typename T>
-__device__ __forceinline__ float frag_sum(const typename TypeOps<T>::V8& v) {
-  f32x8 f = TypeOps<T>::to_f32(v);
-  return ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
+// Adds the 8 probabilities of a fragment (as rounded for the MFMA, so the normaliser
+// matches the numerator) to acc: two-element dot products with 1 for 16-bit types.
+__device__ __forceinline__ float rowsum_add(const bf16x8& v, float acc) {
+  const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{v[e], v[e + 1]}, one, acc, false);
+  return acc;
+}
+__device__ __forceinline__ float rowsum_add(const f16x8& v, float acc) {
+  const f16x2 one = {(f16)1.0f, (f16)1.0f};
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) acc = __builtin_amdgcn_fdot2(f16x2{v[e], v[e + 1]}, one, acc, false);
+  return acc;
+}
+__device__ __forceinline__ float rowsum_add(const f32x8& v, float acc) {
+  return acc + (((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7])));
 }
 
 template <typename T, int PREC, int DP>
@@ -106,7 +128,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
   const T* __restrict__ biasp =
       has_bias ? (const T*)a.bias + b * a.bias_stride[0] + h * a.bias_stride[1] : nullptr;
   const int64_t bsi = a.bias_stride[2];
-  const float mask_add = a.mask_value * LOG2E;
+  const float mask_add = a.mask_value;
 
   // ---- per-row key liveness: one 64-bit word per key tile, and the list of tiles to run.
   if (wave == 0) {
@@ -139,7 +161,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
   const int q0 = qb * QB + wave * 32;
   const int myq = q0 + l32;
   const bool qvalid = myq < N;
-  const float qscale = a.scale * LOG2E;
+  const float qscale = a.scale;
   V8 qf[DP / 16];
 #pragma unroll
   for (int t = 0; t < DP / 16; ++t) {
@@ -160,6 +182,14 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
   float m = -INFINITY;
   float lsum = 0.f;
 
+  // identity A-fragments for the bias MFMA: element e of lane group g in step t is key
+  // 16t + 8g + e; row l32 of the identity holds a 1 there iff l32 is that key.
+  V8 idf[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) idf[t][e] = TypeOps<T>::from_f32(l32 == 16 * t + 8 * g + e ? 1.f : 0.f);
+
   __syncthreads();
   const int nrun = sm.ntiles_run;
   const bool row_dead = sm.row_dead != 0;
@@ -167,8 +197,19 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
   // ---- K / V^T tile staging: each thread moves CH chunks of 8 elements of K and of V.
   constexpr int CPK = DP / 8;                  // chunks per key
   constexpr int CH = KT * CPK / NTHREADS;      // chunks per thread
-  V8 kreg[CH], vreg[CH];
+  constexpr int BCH = QB * KT / 8 / NTHREADS;  // bias chunks per thread
+  V8 kreg[CH], vreg[CH], breg[BCH];
   auto load_tile = [&](int t) {
+    if (has_bias) {
+#pragma unroll
+      for (int i = 0; i < BCH; ++i) {
+        const int c = tid + i * NTHREADS;
+        const int q = qb * QB + c / (KT / 8);
+        const int key = t * KT + (c % (KT / 8)) * 8;
+        // keys up to the next multiple of 8 stay inside the row pitch (host guarantees it)
+        breg[i] = (q < N && key < N) ? load8(biasp + (int64_t)q * bsi + key) : zero8<T>();
+      }
+    }
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + i * NTHREADS;
@@ -183,25 +224,33 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
       }
     }
   };
-  auto store_tile = [&]() {
+  auto store_tile = [&](int buf) {
+    if (has_bias) {
+#pragma unroll
+      for (int i = 0; i < BCH; ++i) {
+        const int c = tid + i * NTHREADS;
+        store8(&sm.bias[buf][(c / (KT / 8)) * S::BROW + (c % (KT / 8)) * 8], breg[i]);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + i * NTHREADS;
       const int kl = c / CPK;
       const int d0 = (c % CPK) * 8;
-      store8(&sm.k[kl * S::KROW + d0], kreg[i]);
+      store8(&sm.k[buf][kl * S::KROW + d0], kreg[i]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sm.vt[(d0 + e) * S::VROW + kl] = vreg[i][e];
+      for (int e = 0; e < 8; ++e) sm.vt[buf][(d0 + e) * S::VROW + kl] = vreg[i][e];
     }
   };
 
   if (nrun > 0) {
     load_tile(sm.tile_list[0]);
-    store_tile();
+    store_tile(0);
   }
   __syncthreads();
 
   for (int it = 0; it < nrun; ++it) {
+    const int cur = S::NBUF == 2 ? (it & 1) : 0;
     const int t = sm.tile_list[it];
     const bool has_next = it + 1 < nrun;
     if (has_next) load_tile(sm.tile_list[it + 1]);
@@ -212,6 +261,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
     const uint64_t valid = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
     const bool all_live = live == ~0ull;  // every one of the 64 keys exists and is kept
 
+    // S^T tile (+ bias): sc[sub][r] is key kbase + sub*32 + 8*(r/4) + 4g + r%4, query myq.
     f32x16 sc[2];
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
@@ -219,32 +269,26 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
       for (int r = 0; r < 16; ++r) sc[sub][r] = 0.f;
 #pragma unroll
       for (int kk = 0; kk < DP / 16; ++kk) {
-        const V8 kf = *reinterpret_cast<const V8*>(&sm.k[(sub * 32 + l32) * S::KROW + 16 * kk + 8 * g]);
+        const V8 kf = *reinterpret_cast<const V8*>(&sm.k[cur][(sub * 32 + l32) * S::KROW + 16 * kk + 8 * g]);
         Mma<T, MP>::step(sc[sub], kf, qf[kk]);
+      }
+      if (has_bias) {
+        const T* brow = &sm.bias[cur][(wave * 32 + l32) * S::BROW + sub * 32];
+        if constexpr (sizeof(T) == 2) {
+#pragma unroll
+          for (int t2 = 0; t2 < 2; ++t2)
+            Mma<T, MP>::step(sc[sub], idf[t2], *reinterpret_cast<const V8*>(brow + 16 * t2 + 8 * g));
+        } else {
+#pragma unroll
+          for (int rg = 0; rg < 4; ++rg) {
+            const f32x4 bv = TypeOps<T>::to_f32(load4(brow + 8 * rg + 4 * g));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sc[sub][4 * rg + e] += bv[e];
+          }
+        }
       }
     }
 
-    // bias, mask, out-of-range keys; sc[sub][r] is key kbase + sub*32 + 8*(r/4) + 4g + r%4.
-    if (has_bias && qvalid) {
-      const T* brow = biasp + (int64_t)myq * bsi + kbase;
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-        for (int rg = 0; rg < 4; ++rg) {
-          const int kl = sub * 32 + 8 * rg + 4 * g;
-          if (kbase + kl + 3 < N) {
-            const f32x4 bv = TypeOps<T>::to_f32(load4(brow + kl));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sc[sub][4 * rg + e] = __builtin_fmaf(bv[e], LOG2E, sc[sub][4 * rg + e]);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (kbase + kl + e < N)
-                sc[sub][4 * rg + e] =
-                    __builtin_fmaf(TypeOps<T>::to_f32(brow[kl + e]), LOG2E, sc[sub][4 * rg + e]);
-          }
-        }
-    }
     if (!all_live) {
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
@@ -267,7 +311,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
     mt = pair_max(mt);
     if (__any(mt > m + RESCALE_THRESHOLD)) {
       const float mnew = fmaxf(m, mt);
-      const float alpha = fast_exp2(m - mnew);  // 0 on the first tile (m = -inf)
+      const float alpha = fast_exp2((m - mnew) * LOG2E);  // 0 on the first tile (m = -inf)
       m = mnew;
       lsum *= alpha;
 #pragma unroll
@@ -276,14 +320,22 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
         for (int r = 0; r < 16; ++r) o[c][r] *= alpha;
     }
     V8 pf[2][2];
+    const float nm = -m * LOG2E;
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
+      if (sizeof(T) == 2 && !row_dead) {
+        // residual of the folded FMA is below half an ulp of s * log2 e; after the 16-bit
+        // rounding of p the row maximum still maps to exactly 1
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sc[sub][r] = fast_exp2(sc[sub][r] - m);
+        for (int r = 0; r < 16; ++r) sc[sub][r] = fast_exp2(__builtin_fmaf(sc[sub][r], LOG2E, nm));
+      } else {  // fp32, or m is the collapsed sentinel: subtract first so s - m is exact
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[sub][r] = fast_exp2((sc[sub][r] - m) * LOG2E);
+      }
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         pf[sub][kk] = frag_from_acc<T>(sc[sub], kk);
-        lsum += frag_sum<T>(pf[sub][kk]);
+        lsum = rowsum_add(pf[sub][kk], lsum);
       }
     }
 
@@ -295,7 +347,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
       for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          const T* vrow = &sm.vt[(32 * c + l32) * S::VROW + sub * 32 + 16 * kk + 4 * g];
+          const T* vrow = &sm.vt[cur][(32 * c + l32) * S::VROW + sub * 32 + 16 * kk + 4 * g];
           const typename TypeOps<T>::V4 lo = load4(vrow);
           const typename TypeOps<T>::V4 hi = load4(vrow + 8);
           V8 vf;
@@ -307,11 +359,16 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
           Mma<T, MP>::step(o[c], vf, pf[sub][kk]);
         }
 
-    __syncthreads();
-    if (has_next) store_tile();
-    __syncthreads();
+    if constexpr (S::NBUF == 2) {
+      // the other stage was last read in the previous iteration, before its barrier
+      if (has_next) store_tile(cur ^ 1);
+      __syncthreads();
+    } else {
+      __syncthreads();
+      if (has_next) store_tile(0);
+      __syncthreads();
+    }
   }
-  (void)row_dead;
 
   // ---- normalise and store. o[c][r] is O[myq][32c + 8*(r/4) + 4g + r%4].
   const float ltot = pair_sum(lsum);
@@ -330,8 +387,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
         }
       }
     if (a.lse && g == 0) {
-      // natural-log lse of the logits: (m + log2 l) / log2 e
-      a.lse[((bs * H + h) * (int64_t)N) + myq] = (m + __log2f(ltot)) * (1.0f / LOG2E);
+      // natural-log lse of the logits
+      a.lse[((bs * H + h) * (int64_t)N) + myq] = m + __log2f(ltot) * (1.0f / LOG2E);
     }
   }
 }
