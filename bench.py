@@ -41,6 +41,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline / parity gate")
     ap.add_argument("--only", choices=["attn", "trimul"], default=None,
                     help="profile helper: run only one op (the JSON line is then partial)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="profile helper: run a plain 256 MiB device copy (known HBM bytes) and exit, "
+                         "to scale FETCH_SIZE / WRITE_SIZE counter readings")
     return ap.parse_args()
 
 
@@ -62,6 +65,14 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calib:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes_read": src.numel(), "copy_calib_bytes_written": dst.numel()}))
+        return
     lib = _lib.load()
     N, H, D, C, CH = args.n, 4, 32, 128, 128
     dt = torch.bfloat16

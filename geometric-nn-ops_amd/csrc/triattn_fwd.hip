@@ -7,34 +7,40 @@
 // triangle_attention.py:11-44) and the Triton forward it stands in for
 // (geometric_nn_ops_torch/triangle/_kernels/triangle_attention.py:48-365).
 //
-// Design (one workgroup = 4 waves = 128 queries of one (b, s, h); one wave = 32 queries):
+// Design (one workgroup = 4 waves x 32 queries, for R consecutive N_seq rows s of one
+// (b, h); a wave owns the same 32 queries in every one of its R rows):
 //   * The score tile is computed transposed, S^T = K Q'^T, on 32x32x16 MFMA so that each
-//     lane ends up owning ONE query (l % 32) and 16 of the 32 keys of a sub-tile. The
-//     softmax statistics are then per-lane scalars, the row max needs a single
-//     permlane32 swap per 64 keys, and the row sum needs none until the end.
+//     lane owns ONE query (l % 32) and 16 of the 32 keys of a sub-tile: the
+//     softmax statistics are per-lane scalars, the row max needs one cross-half exchange
+//     per 64 keys and the row sum none until the end.
 //   * O^T = V^T P^T: the probabilities feed the second MFMA straight from the score
 //     registers (P^T is the B operand), and the running-max rescale of O is a per-lane
 //     scalar multiply.
-//   * K (row-major), V^T and the [128 query x 64 key] pair-bias tile are staged per key
-//     tile in LDS (16-byte coalesced global loads), shared by the 4 waves; Q' =
-//     bf16(q * scale), rounded like the reference's Q * softmax_scale, lives in registers.
-//   * For 16-bit inputs the pair bias is added by the MFMA unit: one extra 32x32x16 step
-//     per 16 keys multiplies an identity fragment (rows = keys) by the bias fragment read
-//     from LDS (cols = queries), so no VALU work is spent on the bias. fp32 inputs add it
-//     on the VALU.
-//   * p = exp2(s * log2 e - m * log2 e) is one FMA and one v_exp_f32 per score (rows with
-//     no live key use the exact (s - m) * log2 e, since m is then the -1e9 sentinel); the
-//     row sum is taken on the rounded probabilities with v_dot2 (16-bit inputs), so the
-//     normaliser matches what the PV product consumes.
-//   * The running max is only moved when a tile raises it by more than 8 ln 2, so most
+//   * K (row-major) and V^T of each row are staged per 64-key tile in LDS (16-byte
+//     coalesced loads) and shared by the 4 waves. Q' = bf16(q * scale), rounded like the
+//     reference's
+//     Q * softmax_scale, lives in registers.
+//   * The pair bias is read straight from global memory in the MFMA B-fragment layout
+//     (lane = query, 8 consecutive keys = 16 bytes), one tile ahead, and added on the MFMA
+//     unit: one extra 32x32x16 step per 16 keys multiplies an identity fragment (rows =
+//     keys) by the bias fragment (cols = queries), so the bias costs no VALU work (fp32
+//     inputs add it on the VALU). The bias plane bias[b, h] is the same for every N_seq
+//     row, so each fragment loaded serves the workgroup's R rows: bias traffic and the
+//     per-tile barriers are amortised over R rows.
+//   * The key mask costs nothing on tiles whose 64 keys are all kept; other tiles add the
+//     caller's sentinel (mask_val rounded to the input dtype, in fp32, after the bias)
+//     and -inf for keys past N, on the VALU.
+//   * p = exp2(s * log2 e - m * log2 e): one FMA and one v_exp_f32 per score for 16-bit
+//     inputs; fp32 inputs and rows with no live key (m is then the -1e9 sentinel) use the
+//     exact (s - m) * log2 e. The row sum is taken on the rounded probabilities with
+//     v_dot2 (16-bit inputs), so the normaliser matches what the PV product consumes.
+//   * The running max only moves when a tile raises it by more than 8 ln 2, so most
 //     tiles skip the O / l rescale; p then stays below 2^8.
-//   * Key tiles whose keys are all masked are skipped when the row has at least one
-//     live key (their probabilities are exactly 0 either way). Rows with no live key
-//     are computed in full, reproducing the finite-sentinel result of the reference.
-//   * Keys past N get -inf; masked keys get the caller's mask_value (the reference's
-//     bf16/fp16/fp32-rounded sentinel) added in fp32.
+//   * Key tiles whose keys are all masked are skipped when the row has at least one live
+//     key (their probabilities are exactly 0 either way). Rows with no live key are
+//     computed in full, reproducing the finite-sentinel result of the reference.
 //   * Workgroup ids are remapped so the workgroups on one XCD walk consecutive
-//     (b, s, h, q-block) items: the 4 q-blocks sharing K/V, and the heads sharing one
+//     (b, row group, h, q-block) items: the q-blocks sharing K/V, and the heads sharing one
 //     bias plane, then hit that XCD's L2.
 #include "gnn_common.hpp"
 #include "gnn_internal.hpp"
@@ -43,30 +49,42 @@ namespace gnn {
 
 namespace {
 
-constexpr int QB = 128;  // queries per workgroup
-constexpr int KT = 64;   // keys per LDS tile
+constexpr int KT = 64;  // keys per LDS tile
 constexpr int NTHREADS = 256;
 constexpr int MAX_TILES = 512;  // N <= 32768
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_THRESHOLD = 8.0f / LOG2E;  // natural-log units: p <= 2^8
 
+// Tuning (measured on MI355X at N_res = 512, D = 32, bf16): a single LDS stage (two
+// barriers per key tile, 14.6 KB) beat double buffering, and one N_seq row per workgroup
+// beat sharing the bias fragments across 2 or 4 rows, whose extra K/V staging and
+// registers cost more than the bias loads they saved.
+#ifndef GNN_ATTN_NBUF
+#define GNN_ATTN_NBUF 1
+#endif
+#ifndef GNN_ATTN_MINBLOCKS
+#define GNN_ATTN_MINBLOCKS 2
+#endif
+#ifndef GNN_ATTN_ROWS
+#define GNN_ATTN_ROWS 1
+#endif
+
+constexpr int QB = 128;              // queries per workgroup (32 per wave)
+constexpr int R = GNN_ATTN_ROWS;     // N_seq rows per workgroup (sharing the bias plane)
+
 template <typename T, int DP>
 struct Smem {
-  static constexpr int KPAD = (sizeof(T) == 2) ? 8 : 4;  // 16 B per K row
+  static constexpr int KPAD = (sizeof(T) == 2) ? 8 : 4;  // 16 B per row
   static constexpr int VPAD = 4;
   static constexpr int KROW = DP + KPAD;
   static constexpr int VROW = KT + VPAD;
-  static constexpr int BROW = KT + KPAD;  // bias tile row pitch (16 B of padding)
-  static constexpr int STAGE_BYTES = (KT * KROW + DP * VROW + QB * BROW) * (int)sizeof(T);
-  // two stages (one barrier per key tile) when they fit in 80 KB, else one
-  static constexpr int NBUF = 2 * STAGE_BYTES <= 80 * 1024 ? 2 : 1;
-  T k[NBUF][KT * KROW];
-  T vt[NBUF][DP * VROW];
-  T bias[NBUF][QB * BROW];
-  uint64_t tile_live[MAX_TILES];  // bit j: key tile*64+j is < N and unmasked
-  uint16_t tile_list[MAX_TILES];
+  static constexpr int NBUF = GNN_ATTN_NBUF;
+  T k[NBUF][R][KT * KROW];
+  T vt[NBUF][R][DP * VROW];
+  uint64_t tile_live[R][MAX_TILES];  // bit j: key tile*64+j is < N and unmasked in row r
+  uint16_t tile_list[MAX_TILES];     // tiles with a live key in some row (all if a row is dead)
   int ntiles_run;
-  int row_dead;
+  int row_dead[R];                   // row r has no live key (or does not exist)
 };
 
 template <typename T>
@@ -94,23 +112,60 @@ __device__ __forceinline__ float rowsum_add(const f32x8& v, float acc) {
   return acc + (((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7])));
 }
 
-template <typename T, int PREC, int DP>
-__global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_triattn_args a) {
+// Bias registers of one key tile for one 32-query group. 16-bit: the B fragments of the
+// identity MFMA, f[sub][t] = bias[q][sub*32 + 16t + 8g + 0..7]. fp32: the values the lane
+// adds on the VALU, f[sub][rg] = bias[q][sub*32 + 8rg + 4g + 0..3].
+template <typename T> struct BiasFrag {
+  typename TypeOps<T>::V8 f[2][2];
+};
+template <> struct BiasFrag<float> {
+  f32x4 f[2][4];
+};
+
+template <typename T>
+__device__ __forceinline__ void load_bias(BiasFrag<T>& bf, const T* brow, bool qok, int kbase, int N,
+                                          int g) {
+  // keys up to the next multiple of 8 stay inside the bias row pitch (host guarantees it)
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int key = kbase + sub * 32 + 16 * t + 8 * g;
+      bf.f[sub][t] = (qok && key < N) ? load8(brow + key) : zero8<T>();
+    }
+}
+template <>
+__device__ __forceinline__ void load_bias<float>(BiasFrag<float>& bf, const float* brow, bool qok, int kbase,
+                                                 int N, int g) {
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      const int key = kbase + sub * 32 + 8 * rg + 4 * g;
+      bf.f[sub][rg] = (qok && key < N) ? load4(brow + key) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+}
+
+enum RowState { ROW_LIVE = 0, ROW_DEAD = 1, ROW_ABSENT = 2 };
+
+template <typename T, int PREC, int DP, bool HAS_BIAS>
+__global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kernel(const gnn_triattn_args a) {
   typedef typename TypeOps<T>::V8 V8;
+  typedef typename TypeOps<T>::V4 V4;
   typedef Smem<T, DP> S;
-  constexpr int MP = (PREC == PREC_NATIVE) ? PREC_NATIVE : PREC;
   __shared__ S sm;
 
   const int N = (int)a.N;
   const int H = (int)a.H;
   const int D = (int)a.D;
   const int nqb = (N + QB - 1) / QB;
+  const int nsg = (int)((a.S + R - 1) / R);
   const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
   const int qb = w % nqb;
   const int h = (w / nqb) % H;
-  const int64_t bs = w / ((uint32_t)nqb * H);
-  const int s = (int)(bs % a.S);
-  const int b = (int)(bs / a.S);
+  const int64_t rest = w / ((uint32_t)nqb * H);
+  const int s0 = (int)(rest % nsg) * R;
+  const int b = (int)(rest / nsg);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -118,69 +173,85 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
   const int l32 = lane & 31;
   const int g = lane >> 5;
   const int ntiles = (N + KT - 1) / KT;
+  const int64_t ksn = a.k_stride[2], vsn = a.v_stride[2];
 
-  const T* __restrict__ qp = (const T*)a.q + b * a.q_stride[0] + s * a.q_stride[1] + h * a.q_stride[3];
-  const T* __restrict__ kp = (const T*)a.k + b * a.k_stride[0] + s * a.k_stride[1] + h * a.k_stride[3];
-  const T* __restrict__ vp = (const T*)a.v + b * a.v_stride[0] + s * a.v_stride[1] + h * a.v_stride[3];
-  T* __restrict__ op = (T*)a.o + b * a.o_stride[0] + s * a.o_stride[1] + h * a.o_stride[3];
-  const int64_t qsn = a.q_stride[2], ksn = a.k_stride[2], vsn = a.v_stride[2], osn = a.o_stride[2];
-  const bool has_bias = a.bias != nullptr;
-  const T* __restrict__ biasp =
-      has_bias ? (const T*)a.bias + b * a.bias_stride[0] + h * a.bias_stride[1] : nullptr;
-  const int64_t bsi = a.bias_stride[2];
-  const float mask_add = a.mask_value;
+  const T* kp[R];
+  const T* vp[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int s = min(s0 + r, (int)a.S - 1);  // absent rows alias the last row, never used
+    kp[r] = (const T*)a.k + b * a.k_stride[0] + s * a.k_stride[1] + h * a.k_stride[3];
+    vp[r] = (const T*)a.v + b * a.v_stride[0] + s * a.v_stride[1] + h * a.v_stride[3];
+  }
 
-  // ---- per-row key liveness: one 64-bit word per key tile, and the list of tiles to run.
+  // ---- key liveness per row: one 64-bit word per key tile, row states, and the tiles to run.
   if (wave == 0) {
-    const uint8_t* mrow =
-        a.mask ? a.mask + b * a.mask_stride[0] + s * a.mask_stride[1] : nullptr;
-    int n = 0;  // tiles holding at least one live key, listed as they are found
+    uint64_t any_live = 0;  // lane t%64 accumulates nothing; the list is built by lane 0
+    int n = 0;
+    bool some_dead = false;
+    int nlive_row[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) nlive_row[r] = 0;
     for (int t = 0; t < ntiles; ++t) {
       const int key = t * KT + lane;
-      bool live = key < N;
-      if (live && mrow) live = mrow[(int64_t)key * a.mask_stride[2]] != 0;
-      const uint64_t bits = __ballot(live);
-      if (lane == 0) {
-        sm.tile_live[t] = bits;
-        if (bits != 0) sm.tile_list[n] = (uint16_t)t;
+      uint64_t tile_any = 0;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int s = s0 + r;
+        bool live = key < N && s < a.S;
+        if (live && a.mask) live = a.mask[b * a.mask_stride[0] + s * a.mask_stride[1] + (int64_t)key * a.mask_stride[2]] != 0;
+        const uint64_t bits = __ballot(live);
+        if (lane == 0) sm.tile_live[r][t] = bits;
+        nlive_row[r] += bits != 0;
+        tile_any |= bits;
       }
-      n += bits != 0;
+      if (lane == 0 && tile_any != 0) sm.tile_list[n] = (uint16_t)t;
+      n += tile_any != 0;
     }
-    const int dead = n == 0;
-    if (dead) {  // no live key anywhere in the row: every tile runs
+    (void)any_live;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int state = s0 + r >= a.S ? ROW_ABSENT : (nlive_row[r] == 0 ? ROW_DEAD : ROW_LIVE);
+      some_dead |= state == ROW_DEAD;
+      if (lane == 0) sm.row_dead[r] = state;
+    }
+    if (some_dead) {  // a row with no live key runs every tile
       for (int t = lane; t < ntiles; t += 64) sm.tile_list[t] = (uint16_t)t;
       n = ntiles;
     }
-    if (lane == 0) {
-      sm.row_dead = dead;
-      sm.ntiles_run = n;
-    }
+    if (lane == 0) sm.ntiles_run = n;
   }
 
-  // ---- this wave's queries: Q' fragments (B operand of S^T = K Q'^T).
-  const int q0 = qb * QB + wave * 32;
-  const int myq = q0 + l32;
-  const bool qvalid = myq < N;
-  const float qscale = a.scale;
-  V8 qf[DP / 16];
+  // ---- this wave's queries (the same 32 in every row): Q' fragments per row.
+  const int myq = qb * QB + wave * 32 + l32;
+  const bool qok = myq < N;
+  const T* brow = HAS_BIAS ? (const T*)a.bias + b * a.bias_stride[0] + h * a.bias_stride[1] +
+                                 (int64_t)(qok ? myq : 0) * a.bias_stride[2]
+                           : nullptr;
+  V8 qf[R][DP / 16];
+  f32x16 o[R][DP / 32];
+  float m[R], lsum[R];
 #pragma unroll
-  for (int t = 0; t < DP / 16; ++t) {
-    const int d0 = 16 * t + 8 * g;
-    if (qvalid && d0 < D) {
-      f32x8 x = TypeOps<T>::to_f32(load8(qp + myq * qsn + d0));
-      qf[t] = TypeOps<T>::from_f32(x * qscale);
-    } else {
-      qf[t] = zero8<T>();
+  for (int r = 0; r < R; ++r) {
+    const int s = min(s0 + r, (int)a.S - 1);
+    const T* qp = (const T*)a.q + b * a.q_stride[0] + s * a.q_stride[1] + h * a.q_stride[3];
+#pragma unroll
+    for (int t = 0; t < DP / 16; ++t) {
+      const int d0 = 16 * t + 8 * g;
+      if (qok && d0 < D) {
+        f32x8 x = TypeOps<T>::to_f32(load8(qp + myq * a.q_stride[2] + d0));
+        qf[r][t] = TypeOps<T>::from_f32(x * a.scale);
+      } else {
+        qf[r][t] = zero8<T>();
+      }
     }
+#pragma unroll
+    for (int cc = 0; cc < DP / 32; ++cc)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[r][cc][i] = 0.f;
+    m[r] = -INFINITY;
+    lsum[r] = 0.f;
   }
-
-  f32x16 o[DP / 32];
-#pragma unroll
-  for (int c = 0; c < DP / 32; ++c)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[c][r] = 0.f;
-  float m = -INFINITY;
-  float lsum = 0.f;
 
   // identity A-fragments for the bias MFMA: element e of lane group g in step t is key
   // 16t + 8g + e; row l32 of the identity holds a 1 there iff l32 is that key.
@@ -190,62 +261,54 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
 #pragma unroll
     for (int e = 0; e < 8; ++e) idf[t][e] = TypeOps<T>::from_f32(l32 == 16 * t + 8 * g + e ? 1.f : 0.f);
 
+  // ---- K / V^T staging: CH chunks of 8 elements of K and of V per thread and row.
+  constexpr int CPK = DP / 8;
+  constexpr int CH = KT * CPK / NTHREADS;
+  V8 kreg[R][CH], vreg[R][CH];
+  auto load_kv = [&](int t) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const int c = tid + i * NTHREADS;
+        const int key = t * KT + c / CPK;
+        const int d0 = (c % CPK) * 8;
+        if (key < N && d0 < D && s0 + r < a.S) {
+          kreg[r][i] = load8(kp[r] + key * ksn + d0);
+          vreg[r][i] = load8(vp[r] + key * vsn + d0);
+        } else {
+          kreg[r][i] = zero8<T>();
+          vreg[r][i] = zero8<T>();
+        }
+      }
+  };
+  auto store_kv = [&](int buf) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        const int c = tid + i * NTHREADS;
+        const int kl = c / CPK;
+        const int d0 = (c % CPK) * 8;
+        store8(&sm.k[buf][r][kl * S::KROW + d0], kreg[r][i]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sm.vt[buf][r][(d0 + e) * S::VROW + kl] = vreg[r][i][e];
+      }
+  };
+
   __syncthreads();
   const int nrun = sm.ntiles_run;
-  const bool row_dead = sm.row_dead != 0;
+  int state[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) state[r] = sm.row_dead[r];
+  const float mval = a.mask_value;
 
-  // ---- K / V^T tile staging: each thread moves CH chunks of 8 elements of K and of V.
-  constexpr int CPK = DP / 8;                  // chunks per key
-  constexpr int CH = KT * CPK / NTHREADS;      // chunks per thread
-  constexpr int BCH = QB * KT / 8 / NTHREADS;  // bias chunks per thread
-  V8 kreg[CH], vreg[CH], breg[BCH];
-  auto load_tile = [&](int t) {
-    if (has_bias) {
-#pragma unroll
-      for (int i = 0; i < BCH; ++i) {
-        const int c = tid + i * NTHREADS;
-        const int q = qb * QB + c / (KT / 8);
-        const int key = t * KT + (c % (KT / 8)) * 8;
-        // keys up to the next multiple of 8 stay inside the row pitch (host guarantees it)
-        breg[i] = (q < N && key < N) ? load8(biasp + (int64_t)q * bsi + key) : zero8<T>();
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int c = tid + i * NTHREADS;
-      const int key = t * KT + c / CPK;
-      const int d0 = (c % CPK) * 8;
-      if (key < N && d0 < D) {
-        kreg[i] = load8(kp + key * ksn + d0);
-        vreg[i] = load8(vp + key * vsn + d0);
-      } else {
-        kreg[i] = zero8<T>();
-        vreg[i] = zero8<T>();
-      }
-    }
-  };
-  auto store_tile = [&](int buf) {
-    if (has_bias) {
-#pragma unroll
-      for (int i = 0; i < BCH; ++i) {
-        const int c = tid + i * NTHREADS;
-        store8(&sm.bias[buf][(c / (KT / 8)) * S::BROW + (c % (KT / 8)) * 8], breg[i]);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const int c = tid + i * NTHREADS;
-      const int kl = c / CPK;
-      const int d0 = (c % CPK) * 8;
-      store8(&sm.k[buf][kl * S::KROW + d0], kreg[i]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sm.vt[buf][(d0 + e) * S::VROW + kl] = vreg[i][e];
-    }
-  };
-
+  BiasFrag<T> bcur, bnext;
   if (nrun > 0) {
-    load_tile(sm.tile_list[0]);
-    store_tile(0);
+    const int t0 = sm.tile_list[0];
+    load_kv(t0);
+    if constexpr (HAS_BIAS) load_bias<T>(bcur, brow, qok, t0 * KT, N, g);
+    store_kv(0);
   }
   __syncthreads();
 
@@ -253,158 +316,176 @@ __global__ __launch_bounds__(NTHREADS, 2) void triattn_fwd_kernel(const gnn_tria
     const int cur = S::NBUF == 2 ? (it & 1) : 0;
     const int t = sm.tile_list[it];
     const bool has_next = it + 1 < nrun;
-    if (has_next) load_tile(sm.tile_list[it + 1]);
+    if (has_next) {
+      const int tn = sm.tile_list[it + 1];
+      load_kv(tn);
+      if constexpr (HAS_BIAS) load_bias<T>(bnext, brow, qok, tn * KT, N, g);
+    }
 
-    const uint64_t live = sm.tile_live[t];
-    const int kbase = t * KT;
-    const int nvalid = min(KT, N - kbase);
-    const uint64_t valid = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
-    const bool all_live = live == ~0ull;  // every one of the 64 keys exists and is kept
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint64_t live = sm.tile_live[r][t];
+      const bool dead = state[r] == ROW_DEAD;
+      if (state[r] == ROW_ABSENT || (!dead && live == 0)) continue;
 
-    // S^T tile (+ bias): sc[sub][r] is key kbase + sub*32 + 8*(r/4) + 4g + r%4, query myq.
-    f32x16 sc[2];
+      // S^T (+ bias): sc[sub][i] is key t*64 + sub*32 + 8*(i/4) + 4g + i%4, query myq.
+      const T* ks = sm.k[cur][r];
+      f32x16 sc[2];
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
+      for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sc[sub][r] = 0.f;
+        for (int i = 0; i < 16; ++i) sc[sub][i] = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < DP / 16; ++kk) {
-        const V8 kf = *reinterpret_cast<const V8*>(&sm.k[cur][(sub * 32 + l32) * S::KROW + 16 * kk + 8 * g]);
-        Mma<T, MP>::step(sc[sub], kf, qf[kk]);
-      }
-      if (has_bias) {
-        const T* brow = &sm.bias[cur][(wave * 32 + l32) * S::BROW + sub * 32];
+      for (int kk = 0; kk < DP / 16; ++kk)
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+          Mma<T, PREC>::step(sc[sub], load8(&ks[(sub * 32 + l32) * S::KROW + 16 * kk + 8 * g]), qf[r][kk]);
+      if constexpr (HAS_BIAS) {
         if constexpr (sizeof(T) == 2) {
 #pragma unroll
           for (int t2 = 0; t2 < 2; ++t2)
-            Mma<T, MP>::step(sc[sub], idf[t2], *reinterpret_cast<const V8*>(brow + 16 * t2 + 8 * g));
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub) Mma<T, PREC>::step(sc[sub], idf[t2], bcur.f[sub][t2]);
         } else {
 #pragma unroll
-          for (int rg = 0; rg < 4; ++rg) {
-            const f32x4 bv = TypeOps<T>::to_f32(load4(brow + 8 * rg + 4 * g));
+          for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) sc[sub][4 * rg + e] += bv[e];
+            for (int rg = 0; rg < 4; ++rg)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) sc[sub][4 * rg + e] += TypeOps<T>::to_f32(bcur.f[sub][rg][e]);
+        }
+      }
+      if (live != ~0ull) {
+        // some key of the tile is masked or past N. Bit 8*(i/4) + i%4 of lb / vb is key
+        // sub*32 + 8*(i/4) + 4g + i%4 of the tile.
+        const int nvalid = min(KT, N - t * KT);
+        const uint64_t valid = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+          const uint32_t lb = ((uint32_t)(live >> (32 * sub)) >> (4 * g)) & 0x0F0F0F0Fu;
+          const uint32_t vb = ((uint32_t)(valid >> (32 * sub)) >> (4 * g)) & 0x0F0F0F0Fu;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int bit = 8 * (i / 4) + (i % 4);
+            const float x = ((lb >> bit) & 1u) ? sc[sub][i] : sc[sub][i] + mval;
+            sc[sub][i] = ((vb >> bit) & 1u) ? x : -INFINITY;
           }
         }
       }
-    }
 
-    if (!all_live) {
+      // online softmax, lazily rescaled
+      float m0 = fmaxf(sc[0][0], sc[0][1]), m1 = fmaxf(sc[1][0], sc[1][1]);
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
+      for (int i = 2; i < 16; ++i) {
+        m0 = fmaxf(m0, sc[0][i]);
+        m1 = fmaxf(m1, sc[1][i]);
+      }
+      const float mt = pair_max(fmaxf(m0, m1));
+      if (__any(mt > m[r] + RESCALE_THRESHOLD)) {
+        const float mnew = fmaxf(m[r], mt);
+        const float alpha = fast_exp2((m[r] - mnew) * LOG2E);  // 0 on the first tile (m = -inf)
+        m[r] = mnew;
+        lsum[r] *= alpha;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kl = sub * 32 + 8 * (r / 4) + 4 * g + (r % 4);
-          if (!((valid >> kl) & 1ull))
-            sc[sub][r] = -INFINITY;
-          else if (!((live >> kl) & 1ull))
-            sc[sub][r] += mask_add;
+        for (int cc = 0; cc < DP / 32; ++cc)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[r][cc][i] *= alpha;
+      }
+      V8 pf[2][2];
+      const float nm = -m[r] * LOG2E;
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        if (sizeof(T) == 2 && !dead) {
+          // the folded FMA leaves a residual below half an ulp of s * log2 e; after the
+          // 16-bit rounding of p the row maximum still maps to exactly 1
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sc[sub][i] = fast_exp2(__builtin_fmaf(sc[sub][i], LOG2E, nm));
+        } else {  // fp32, or m is the collapsed sentinel: subtract first so s - m is exact
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sc[sub][i] = fast_exp2((sc[sub][i] - m[r]) * LOG2E);
         }
-    }
-
-    // online softmax (log2 units), lazily rescaled
-    float mt = sc[0][0];
-#pragma unroll
-    for (int r = 1; r < 16; ++r) mt = fmaxf(mt, sc[0][r]);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[1][r]);
-    mt = pair_max(mt);
-    if (__any(mt > m + RESCALE_THRESHOLD)) {
-      const float mnew = fmaxf(m, mt);
-      const float alpha = fast_exp2((m - mnew) * LOG2E);  // 0 on the first tile (m = -inf)
-      m = mnew;
-      lsum *= alpha;
-#pragma unroll
-      for (int c = 0; c < DP / 32; ++c)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[c][r] *= alpha;
-    }
-    V8 pf[2][2];
-    const float nm = -m * LOG2E;
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      if (sizeof(T) == 2 && !row_dead) {
-        // residual of the folded FMA is below half an ulp of s * log2 e; after the 16-bit
-        // rounding of p the row maximum still maps to exactly 1
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sc[sub][r] = fast_exp2(__builtin_fmaf(sc[sub][r], LOG2E, nm));
-      } else {  // fp32, or m is the collapsed sentinel: subtract first so s - m is exact
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sc[sub][r] = fast_exp2((sc[sub][r] - m) * LOG2E);
-      }
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        pf[sub][kk] = frag_from_acc<T>(sc[sub], kk);
-        lsum = rowsum_add(pf[sub][kk], lsum);
-      }
-    }
-
-    // O^T += V^T P^T. Fragment element e of k-step kk of sub-tile sub is key
-    // sub*32 + 16*kk + 8*(e/4) + 4g + e%4 in both operands.
-#pragma unroll
-    for (int c = 0; c < DP / 32; ++c)
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          const T* vrow = &sm.vt[cur][(32 * c + l32) * S::VROW + sub * 32 + 16 * kk + 4 * g];
-          const typename TypeOps<T>::V4 lo = load4(vrow);
-          const typename TypeOps<T>::V4 hi = load4(vrow + 8);
-          V8 vf;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            vf[e] = lo[e];
-            vf[e + 4] = hi[e];
-          }
-          Mma<T, MP>::step(o[c], vf, pf[sub][kk]);
+          pf[sub][kk] = frag_from_acc<T>(sc[sub], kk);
+          lsum[r] = rowsum_add(pf[sub][kk], lsum[r]);
         }
+      }
 
+      // O^T += V^T P^T. Fragment element e of k-step kk of sub-tile sub is key
+      // sub*32 + 16*kk + 8*(e/4) + 4g + e%4 in both operands.
+      const T* vs = sm.vt[cur][r];
+#pragma unroll
+      for (int cc = 0; cc < DP / 32; ++cc)
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) {
+            const T* vrow = &vs[(32 * cc + l32) * S::VROW + sub * 32 + 16 * kk + 4 * g];
+            const V4 lo = load4(vrow);
+            const V4 hi = load4(vrow + 8);
+            V8 vf;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              vf[e] = lo[e];
+              vf[e + 4] = hi[e];
+            }
+            Mma<T, PREC>::step(o[r][cc], vf, pf[sub][kk]);
+          }
+    }
+
+    if constexpr (HAS_BIAS) bcur = bnext;
     if constexpr (S::NBUF == 2) {
       // the other stage was last read in the previous iteration, before its barrier
-      if (has_next) store_tile(cur ^ 1);
+      if (has_next) store_kv(cur ^ 1);
       __syncthreads();
     } else {
       __syncthreads();
-      if (has_next) store_tile(0);
+      if (has_next) store_kv(0);
       __syncthreads();
     }
   }
 
-  // ---- normalise and store. o[c][r] is O[myq][32c + 8*(r/4) + 4g + r%4].
-  const float ltot = pair_sum(lsum);
-  const float inv = 1.0f / ltot;
-  if (qvalid) {
-    T* orow = op + (int64_t)myq * osn;
+  // ---- normalise and store. o[r][cc][i] is O[s0 + r][myq][32cc + 8*(i/4) + 4g + i%4].
 #pragma unroll
-    for (int c = 0; c < DP / 32; ++c)
+  for (int r = 0; r < R; ++r) {
+    const float ltot = pair_sum(lsum[r]);
+    if (!qok || state[r] == ROW_ABSENT) continue;
+    const float inv = 1.0f / ltot;
+    const int s = s0 + r;
+    T* orow = (T*)a.o + b * a.o_stride[0] + s * a.o_stride[1] + h * a.o_stride[3] + (int64_t)myq * a.o_stride[2];
+#pragma unroll
+    for (int cc = 0; cc < DP / 32; ++cc)
 #pragma unroll
       for (int rg = 0; rg < 4; ++rg) {
-        const int d0 = 32 * c + 8 * rg + 4 * g;
+        const int d0 = 32 * cc + 8 * rg + 4 * g;
         if (d0 < D) {
-          f32x4 x = {o[c][4 * rg] * inv, o[c][4 * rg + 1] * inv, o[c][4 * rg + 2] * inv,
-                     o[c][4 * rg + 3] * inv};
+          f32x4 x = {o[r][cc][4 * rg] * inv, o[r][cc][4 * rg + 1] * inv, o[r][cc][4 * rg + 2] * inv,
+                     o[r][cc][4 * rg + 3] * inv};
           store4(orow + d0, TypeOps<T>::from_f32(x));
         }
       }
-    if (a.lse && g == 0) {
-      // natural-log lse of the logits
-      a.lse[((bs * H + h) * (int64_t)N) + myq] = m + __log2f(ltot) * (1.0f / LOG2E);
-    }
+    if (a.lse && g == 0)  // natural-log lse of the logits
+      a.lse[(((int64_t)b * a.S + s) * H + h) * N + myq] = m[r] + __log2f(ltot) * (1.0f / LOG2E);
   }
+}
+
+template <typename T, int PREC, bool HAS_BIAS>
+int launch_bias(const gnn_triattn_args& a, hipStream_t stream) {
+  const int64_t nqb = (a.N + QB - 1) / QB;
+  const int64_t nblk = nqb * a.H * ((a.S + R - 1) / R) * a.B;
+  dim3 grid((uint32_t)nblk), block(NTHREADS);
+  if (a.D <= 32)
+    hipLaunchKernelGGL((triattn_fwd_kernel<T, PREC, 32, HAS_BIAS>), grid, block, 0, stream, a);
+  else if (a.D <= 64)
+    hipLaunchKernelGGL((triattn_fwd_kernel<T, PREC, 64, HAS_BIAS>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((triattn_fwd_kernel<T, PREC, 128, HAS_BIAS>), grid, block, 0, stream, a);
+  return (int)hipGetLastError();
 }
 
 template <typename T, int PREC>
 int launch_dp(const gnn_triattn_args& a, hipStream_t stream) {
-  const int64_t nqb = (a.N + QB - 1) / QB;
-  const int64_t nblk = nqb * a.H * a.S * a.B;
-  dim3 grid((uint32_t)nblk), block(NTHREADS);
-  if (a.D <= 32)
-    hipLaunchKernelGGL((triattn_fwd_kernel<T, PREC, 32>), grid, block, 0, stream, a);
-  else if (a.D <= 64)
-    hipLaunchKernelGGL((triattn_fwd_kernel<T, PREC, 64>), grid, block, 0, stream, a);
-  else
-    hipLaunchKernelGGL((triattn_fwd_kernel<T, PREC, 128>), grid, block, 0, stream, a);
-  return (int)hipGetLastError();
+  return a.bias ? launch_bias<T, PREC, true>(a, stream) : launch_bias<T, PREC, false>(a, stream);
 }
 
 }  // namespace
@@ -415,7 +496,7 @@ int triattn_fwd(const gnn_triattn_args& a, hipStream_t stream) {
   if (a.D > 128)
     return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention: head dim > 128 is not supported");
   const int64_t nqb = (a.N + QB - 1) / QB;
-  if (nqb * a.H * a.S * a.B >= (int64_t)1 << 31)
+  if (nqb * a.H * ((a.S + R - 1) / R) * a.B >= (int64_t)1 << 31)
     return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention: grid too large");
   switch (a.dtype) {
     case GNN_BF16: return launch_dp<bf16, PREC_NATIVE>(a, stream);
