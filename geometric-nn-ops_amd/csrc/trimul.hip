@@ -34,13 +34,44 @@ __device__ __forceinline__ float ld_or(const void* p, int64_t i, float dflt) {
   return p ? TypeOps<T>::to_f32(((const T*)p)[i]) : dflt;
 }
 
-__device__ __forceinline__ float sigmoid_acc(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// sigmoid(x) = 1 / (1 + 2^(-x log2 e)) with the hardware exp2 and reciprocal (about 1 ulp
+// each), instead of an IEEE division sequence per element. x -> -inf gives rcp(inf) = 0,
+// x -> +inf gives rcp(1) = 1.
+__device__ __forceinline__ float sigmoid_acc(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
 
 // Row pitch (elements) of the LDS pixel tiles: 16 B of padding keeps the fragment reads
 // of consecutive rows on distinct banks.
 template <typename T>
 __host__ __device__ constexpr int lds_pad() {
   return (int)(16 / sizeof(T));
+}
+
+// Orders LDS accesses of the lanes of one wave (a wave executes its LDS operations in
+// order; this keeps the compiler from moving them across the exchange).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Per-wave epilogue staging tile of the projection stage: max(32 x (64 + pad), 64 x (32 + pad)).
+template <typename T>
+__host__ __device__ constexpr int proj_ebuf_elems() {
+  return (32 * (64 + lds_pad<T>()) > 64 * (32 + lds_pad<T>())) ? 32 * (64 + lds_pad<T>())
+                                                                 : 64 * (32 + lds_pad<T>());
+}
+// LDS of the projection stage: z tile [PT][C + pad] (T), LN gamma / beta [C] and the mask
+// of the tile [PT] (fp32), then 4 staging tiles (T), each region 16-byte aligned.
+template <typename T>
+__host__ __device__ inline size_t proj_ebuf_offset(int C) {
+  const size_t head = (size_t)PT * (C + lds_pad<T>()) * sizeof(T) + (2 * (size_t)C + PT) * sizeof(float);
+  return (head + 15) / 16 * 16;
+}
+template <typename T>
+__device__ __forceinline__ T* proj_ebuf(unsigned char* smem, int C) {
+  return reinterpret_cast<T*>(smem + proj_ebuf_offset<T>(C));
 }
 
 // ============================== stage 1: LN-in + projections ==============================
@@ -50,7 +81,10 @@ __host__ __device__ constexpr int lds_pad() {
 // its gate g_in share the unit so the epilogue can combine them), or 32 channels of the
 // output gate. Weight fragments are read once per pair of 32-pixel sub-tiles.
 template <typename T, int PREC>
-__global__ __launch_bounds__(NT, 2) void trimul_proj_kernel(const gnn_trimul_args a, int64_t NP,
+#ifndef GNN_PROJ_MINBLOCKS
+#define GNN_PROJ_MINBLOCKS 2
+#endif
+__global__ __launch_bounds__(NT, GNN_PROJ_MINBLOCKS) void trimul_proj_kernel(const gnn_trimul_args a, int64_t NP,
                                                             size_t off_a, size_t off_b,
                                                             size_t off_g) {
   typedef typename TypeOps<T>::V8 V8;
@@ -155,51 +189,79 @@ __global__ __launch_bounds__(NT, 2) void trimul_proj_kernel(const gnn_trimul_arg
   const T* __restrict__ wp = (const T*)a.p_in_w;
   const T* __restrict__ wg = (const T*)a.g_in_w;
   const T* __restrict__ wgo = (const T*)a.g_out_w;
+  // wave-private staging tile for the epilogues (32 channels x 64 pixels, or 64 x 32)
+  T* ebuf = proj_ebuf<T>(smem_raw, C) + wave * proj_ebuf_elems<T>();
+  constexpr int ER = 64 + lds_pad<T>();  // [32 channel rows][64 pixels] (a / b)
+  constexpr int EG = 32 + lds_pad<T>();  // [64 pixel rows][32 channels] (g)
 
   for (int u = wave; u < nunits; u += 4) {
     if (u < npg) {
-      // acc[s][.] = [pixel][channel] tiles: row = pixel 32*sub + 8*(r/4) + 4g + r%4, col = channel
+      // acc[s] = [pixel][channel] tiles: row = pixel 32*s + 8*(r/4) + 4g + r%4, col = channel
       const int ch = 32 * u + l32;  // channel of the 2*Ch projection held by this lane
       const float bp = ld_or<T>(a.p_in_b, ch, 0.f);
       const float bg = ld_or<T>(a.g_in_b, ch, 0.f);
-      T* dst = ch < Ch ? a_cm : b_cm;
-      const int chh = ch < Ch ? ch : ch - Ch;
-      T* drow = dst + (((int64_t)b * Ch + chh) * N + row) * NP + c0;
       const T* wprow = wp + (int64_t)ch * C + 8 * g;
       const T* wgrow = wg + (int64_t)ch * C + 8 * g;
-      for (int sp = 0; sp < PT / 32; sp += 2) {
-        f32x16 accp[2], accg[2];
+      // weight fragments of up to KCH k-steps stay in registers across the pixel sub-tiles
+      constexpr int KCH = sizeof(T) == 2 ? 8 : 4;
+      V8 wpf[KCH], wgf[KCH];
+      auto load_w = [&](int kc) {
 #pragma unroll
-        for (int s = 0; s < 2; ++s)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) accp[s][r] = accg[s][r] = 0.f;
-        for (int k = 0; k < nk; ++k) {
-          const V8 wpf = load8(wprow + 16 * k);
-          const V8 wgf = load8(wgrow + 16 * k);
-#pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            const V8 zf = load8(&zs[(32 * (sp + s) + l32) * ZR + 16 * k + 8 * g]);
-            Mma<T, PREC>::step(accp[s], zf, wpf);
-            Mma<T, PREC>::step(accg[s], zf, wgf);
+        for (int j = 0; j < KCH; ++j)
+          if (kc + j < nk) {
+            wpf[j] = load8(wprow + 16 * (kc + j));
+            wgf[j] = load8(wgrow + 16 * (kc + j));
           }
-        }
+      };
+      if (nk <= KCH) load_w(0);
+      for (int sp = 0; sp < PT / 32; sp += 2) {
 #pragma unroll
-        for (int s = 0; s < 2; ++s)
+        for (int s2 = 0; s2 < 2; ++s2) {
+          f32x16 accp, accg;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) accp[r] = accg[r] = 0.f;
+          for (int kc = 0; kc < nk; kc += KCH) {
+            if (nk > KCH) load_w(kc);
+#pragma unroll
+            for (int j = 0; j < KCH; ++j) {
+              if (kc + j >= nk) break;
+              const V8 zf = load8(&zs[(32 * (sp + s2) + l32) * ZR + 16 * (kc + j) + 8 * g]);
+              Mma<T, PREC>::step(accp, zf, wpf[j]);
+              Mma<T, PREC>::step(accg, zf, wgf[j]);
+            }
+          }
+          // gated, masked values -> staging tile [channel l32][pixel]
 #pragma unroll
           for (int rg = 0; rg < 4; ++rg) {
-            const int pl = 32 * (sp + s) + 8 * rg + 4 * g;
+            const int pt = 32 * s2 + 8 * rg + 4 * g;  // pixel within the sub-tile pair
             f32x4 v;
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              v[e] = (accp[s][4 * rg + e] + bp) * sigmoid_acc(accg[s][4 * rg + e] + bg) * mk[pl + e];
-            if (c0 + pl + 3 < N) {
-              store4(drow + pl, TypeOps<T>::from_f32(v));
-            } else {
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                if (c0 + pl + e < N) drow[pl + e] = TypeOps<T>::from_f32(v[e]);
-            }
+              v[e] = (accp[4 * rg + e] + bp) * sigmoid_acc(accg[4 * rg + e] + bg) * mk[32 * sp + pt + e];
+            store4(&ebuf[l32 * ER + pt], TypeOps<T>::from_f32(v));
           }
+        }
+        wave_lds_sync();
+        // 16-byte stores, 8 lanes per 128-byte channel row segment
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int c = lane + 64 * i;
+          const int crow = c / 8, p0 = (c % 8) * 8;
+          const int chg = 32 * u + crow;
+          T* dst = chg < Ch ? a_cm : b_cm;
+          const int chh = chg < Ch ? chg : chg - Ch;
+          const int pl = 32 * sp + p0;
+          T* drow = dst + (((int64_t)b * Ch + chh) * N + row) * NP + c0 + pl;
+          const V8 val = load8(&ebuf[crow * ER + p0]);
+          if (c0 + pl + 8 <= N) {
+            store8(drow, val);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (c0 + pl + e < N) drow[e] = val[e];
+          }
+        }
+        wave_lds_sync();
       }
     } else {
       // acc[s] = [channel][pixel]: row = channel c00 + 8*(r/4) + 4g + r%4, col = pixel
@@ -208,33 +270,48 @@ __global__ __launch_bounds__(NT, 2) void trimul_proj_kernel(const gnn_trimul_arg
 #pragma unroll
       for (int r = 0; r < 16; ++r) bgo[r] = ld_or<T>(a.g_out_b, c00 + 8 * (r / 4) + 4 * g + (r % 4), 0.f);
       const T* wrow = wgo + (int64_t)(c00 + l32) * C + 8 * g;
+      constexpr int KCH = sizeof(T) == 2 ? 8 : 4;
+      V8 wf[KCH];
+      auto load_w = [&](int kc) {
+#pragma unroll
+        for (int j = 0; j < KCH; ++j)
+          if (kc + j < nk) wf[j] = load8(wrow + 16 * (kc + j));
+      };
+      if (nk <= KCH) load_w(0);
       for (int sp = 0; sp < PT / 32; sp += 2) {
-        f32x16 acc[2];
 #pragma unroll
-        for (int s = 0; s < 2; ++s)
+        for (int s2 = 0; s2 < 2; ++s2) {
+          f32x16 acc;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[s][r] = 0.f;
-        for (int k = 0; k < nk; ++k) {
-          const V8 wf = load8(wrow + 16 * k);
+          for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+          for (int kc = 0; kc < nk; kc += KCH) {
+            if (nk > KCH) load_w(kc);
 #pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            const V8 zf = load8(&zs[(32 * (sp + s) + l32) * ZR + 16 * k + 8 * g]);
-            Mma<T, PREC>::step(acc[s], wf, zf);
+            for (int j = 0; j < KCH; ++j) {
+              if (kc + j >= nk) break;
+              const V8 zf = load8(&zs[(32 * (sp + s2) + l32) * ZR + 16 * (kc + j) + 8 * g]);
+              Mma<T, PREC>::step(acc, wf[j], zf);
+            }
           }
-        }
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const int pl = 32 * (sp + s) + l32;
-          if (c0 + pl >= N) continue;
-          T* grow = gout + pix_index(pl) * C + c00 + 4 * g;
+          // sigmoid -> staging tile [pixel][channel]
 #pragma unroll
           for (int rg = 0; rg < 4; ++rg) {
             f32x4 v;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = sigmoid_acc(acc[s][4 * rg + e] + bgo[4 * rg + e]);
-            store4(grow + 8 * rg, TypeOps<T>::from_f32(v));
+            for (int e = 0; e < 4; ++e) v[e] = sigmoid_acc(acc[4 * rg + e] + bgo[4 * rg + e]);
+            store4(&ebuf[(32 * s2 + l32) * EG + 8 * rg + 4 * g], TypeOps<T>::from_f32(v));
           }
         }
+        wave_lds_sync();
+        // 16-byte stores, 4 lanes per 64-byte pixel row segment
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int c = lane + 64 * i;
+          const int px = c / 4, k0 = (c % 4) * 8;
+          const int pl = 32 * sp + px;
+          if (c0 + pl < N) store8(gout + pix_index(pl) * C + c00 + k0, load8(&ebuf[px * EG + k0]));
+        }
+        wave_lds_sync();
       }
     }
   }
@@ -470,7 +547,7 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
 
 template <typename T>
 size_t proj_smem(const gnn_trimul_args& a) {
-  return (size_t)PT * (a.C + lds_pad<T>()) * sizeof(T) + (2 * (size_t)a.C + PT) * sizeof(float);
+  return proj_ebuf_offset<T>((int)a.C) + 4 * (size_t)proj_ebuf_elems<T>() * sizeof(T);
 }
 
 template <typename T>
@@ -534,7 +611,8 @@ int check_args(const gnn_trimul_args& a, const char* who) {
     if (((uintptr_t)ptr) % 16 != 0)
       return set_error(GNN_ERR_ARG, "trimul: x, out, weights and workspace must be 16-byte aligned");
   const size_t e = a.dtype == GNN_F32 ? 4 : 2;
-  const size_t proj_lds = (size_t)PT * (a.C + 16 / e) * e + (2 * (size_t)a.C + PT) * 4;
+  const size_t proj_lds = (size_t)PT * (a.C + 16 / e) * e + (2 * (size_t)a.C + PT) * 4 + 16 +
+                          4 * (size_t)(e == 2 ? proj_ebuf_elems<bf16>() : proj_ebuf_elems<float>()) * e;
   const size_t out_lds = ((size_t)a.Ch * (PTO + 16 / e) + (size_t)PTO * (a.Ch + 16 / e)) * e + 2 * (size_t)a.Ch * 4;
   if (proj_lds > 160 * 1024 || out_lds > 160 * 1024)
     return set_error(GNN_ERR_UNSUPPORTED, "trimul: channel count too large for the LDS tiles");
