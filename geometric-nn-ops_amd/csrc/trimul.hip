@@ -140,19 +140,23 @@ __global__ __launch_bounds__(NT, GNN_PROJ_MINBLOCKS) void trimul_proj_kernel(con
   }
   __syncthreads();
 
-  // ---- LayerNorm in place, 2 threads per pixel (fp32 statistics, biased variance)
+  // ---- LayerNorm in place (fp32 statistics, biased variance). Thread = (pixel tid % 128,
+  // channel half tid / 128), so the lanes of a wave read 64 different rows at one column
+  // (conflict-free); the two halves' partial sums meet in LDS (the staging area, idle now).
   {
-    const int pl = tid >> 1, half = tid & 1;
+    const int pl = tid & (PT - 1), half = tid / PT;
     const int k0 = half * (C / 2);
     T* zrow = &zs[pl * ZR];
+    float* red = reinterpret_cast<float*>(proj_ebuf<T>(smem_raw, C));  // [2 stats][2 halves][PT]
     float sum = 0.f;
     for (int k = k0; k < k0 + C / 2; k += 8) {
       const f32x8 v = TypeOps<T>::to_f32(load8(zrow + k));
 #pragma unroll
       for (int e = 0; e < 8; ++e) sum += v[e];
     }
-    sum += __shfl_xor(sum, 1);
-    const float mean = sum / (float)C;
+    red[half * PT + pl] = sum;
+    __syncthreads();
+    const float mean = (red[pl] + red[PT + pl]) / (float)C;
     float sq = 0.f;
     for (int k = k0; k < k0 + C / 2; k += 8) {
       const f32x8 v = TypeOps<T>::to_f32(load8(zrow + k));
@@ -162,8 +166,9 @@ __global__ __launch_bounds__(NT, GNN_PROJ_MINBLOCKS) void trimul_proj_kernel(con
         sq += d * d;
       }
     }
-    sq += __shfl_xor(sq, 1);
-    const float rstd = 1.0f / sqrtf(sq / (float)C + a.eps);
+    red[2 * PT + half * PT + pl] = sq;
+    __syncthreads();
+    const float rstd = 1.0f / sqrtf((red[2 * PT + pl] + red[3 * PT + pl]) / (float)C + a.eps);
     for (int k = k0; k < k0 + C / 2; k += 8) {
       f32x8 v = TypeOps<T>::to_f32(load8(zrow + k));
       const f32x4 w0 = *reinterpret_cast<const f32x4*>(lnw + k);
@@ -454,6 +459,7 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
   T* zs = ot + (size_t)Ch * OR;
   float* lnw = reinterpret_cast<float*>(zs + (size_t)PTO * ZR);
   float* lnb = lnw + Ch;
+  float* red = lnb + Ch;  // [2 stats][4 quarters][PTO] partial sums
 
   const int ntile = (N + PTO - 1) / PTO;
   const int ct = blockIdx.x % ntile;
@@ -478,23 +484,27 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
   }
   __syncthreads();
 
-  // ---- LayerNorm over channels: 4 threads per pixel, each a quarter of the channels
+  // ---- LayerNorm over channels. Thread = (pixel tid % 64, channel quarter tid / 64): the
+  // lanes of a wave read 64 consecutive pixels of one channel row (conflict-free); the
+  // quarters' partial sums meet in LDS.
   {
-    const int pl = tid >> 2, qtr = tid & 3;
+    const int pl = tid & (PTO - 1), qtr = tid / PTO;
     const int k0 = qtr * (Ch / 4), k1 = k0 + Ch / 4;
     float sum = 0.f;
     for (int k = k0; k < k1; ++k) sum += TypeOps<T>::to_f32(ot[k * OR + pl]);
-    sum += __shfl_xor(sum, 1);
-    sum += __shfl_xor(sum, 2);
-    const float mean = sum / (float)Ch;
+    red[qtr * PTO + pl] = sum;
+    __syncthreads();
+    const float mean = ((red[pl] + red[PTO + pl]) + (red[2 * PTO + pl] + red[3 * PTO + pl])) / (float)Ch;
     float sq = 0.f;
     for (int k = k0; k < k1; ++k) {
       const float d = TypeOps<T>::to_f32(ot[k * OR + pl]) - mean;
       sq += d * d;
     }
-    sq += __shfl_xor(sq, 1);
-    sq += __shfl_xor(sq, 2);
-    const float rstd = 1.0f / sqrtf(sq / (float)Ch + a.eps);
+    float* red2 = red + 4 * PTO;
+    red2[qtr * PTO + pl] = sq;
+    __syncthreads();
+    const float var = ((red2[pl] + red2[PTO + pl]) + (red2[2 * PTO + pl] + red2[3 * PTO + pl])) / (float)Ch;
+    const float rstd = 1.0f / sqrtf(var + a.eps);
     for (int k = k0; k < k1; k += 8) {
       f32x8 v;
 #pragma unroll
@@ -553,7 +563,7 @@ size_t proj_smem(const gnn_trimul_args& a) {
 template <typename T>
 size_t out_smem(const gnn_trimul_args& a) {
   return ((size_t)a.Ch * (PTO + lds_pad<T>()) + (size_t)PTO * (a.Ch + lds_pad<T>())) * sizeof(T) +
-         2 * (size_t)a.Ch * sizeof(float);
+         (2 * (size_t)a.Ch + 8 * PTO) * sizeof(float);
 }
 
 template <typename T, int PREC>
@@ -613,7 +623,8 @@ int check_args(const gnn_trimul_args& a, const char* who) {
   const size_t e = a.dtype == GNN_F32 ? 4 : 2;
   const size_t proj_lds = (size_t)PT * (a.C + 16 / e) * e + (2 * (size_t)a.C + PT) * 4 + 16 +
                           4 * (size_t)(e == 2 ? proj_ebuf_elems<bf16>() : proj_ebuf_elems<float>()) * e;
-  const size_t out_lds = ((size_t)a.Ch * (PTO + 16 / e) + (size_t)PTO * (a.Ch + 16 / e)) * e + 2 * (size_t)a.Ch * 4;
+  const size_t out_lds =
+      ((size_t)a.Ch * (PTO + 16 / e) + (size_t)PTO * (a.Ch + 16 / e)) * e + (2 * (size_t)a.Ch + 8 * PTO) * 4;
   if (proj_lds > 160 * 1024 || out_lds > 160 * 1024)
     return set_error(GNN_ERR_UNSUPPORTED, "trimul: channel count too large for the LDS tiles");
   if (a.B * a.N * ((a.N + PT - 1) / PT) >= ((int64_t)1 << 31))
