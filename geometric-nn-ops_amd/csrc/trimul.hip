@@ -440,23 +440,56 @@ __global__ __launch_bounds__(NT, 2) void trimul_contract_kernel(const T* __restr
 }
 
 // ============================== stage 3: LN-out + p_out + gate ============================
-// One workgroup = PTO pixels of one row of the pair grid. The channel-major o tile is
-// loaded with 16-byte rows, normalised per pixel (4 threads per pixel reading down the
-// channel columns), written back pixel-major, then multiplied by p_out on MFMA with the
-// gate applied in the epilogue (8-byte loads of g, 8-byte stores of out).
+// One workgroup = PTO consecutive pixels of one row of the pair grid; their g and out rows
+// form one contiguous block of PTO * C elements (pixel-major). The channel-major o tile is
+// loaded with 16-byte rows and normalised per pixel (lanes walk consecutive pixels of one
+// channel row), then p_out runs on MFMA in passes of OPC output channels, one 32-channel
+// tile per wave. A pass writes the linear output, rounded to T as the reference's linear
+// layer does, into an LDS tile; the workgroup then streams the tile out with 16-byte g loads
+// and 16-byte out stores over the contiguous block, multiplying in fp32 and rounding once.
+// The g chunk of a pass is loaded into registers one pass ahead (the first before the o
+// tile), so its latency hides behind the LayerNorm / the previous pass.
 constexpr int PTO = 64;
+constexpr int OPC = 128;                  // output channels per pass (4 waves x 32)
+constexpr int OCH = PTO * OPC / 8 / NT;  // 8-element chunks per thread per pass
+
+// LDS of the output stage: region 1 = the raw o tile [Ch][PTO + pad], reused after the
+// LayerNorm as the pass tile [PTO][OPC + pad]; then the normalised tile [PTO][Ch + pad] (T),
+// LN gamma / beta [Ch] and the LayerNorm partial sums [2][4][PTO] (fp32).
+__host__ __device__ inline size_t out_region1_elems(int64_t Ch, int pad) {
+  const int64_t o = Ch * (PTO + pad), y = (int64_t)PTO * (OPC + pad);
+  return (size_t)(o > y ? o : y);
+}
+__host__ __device__ inline size_t out_lds_bytes(int64_t Ch, size_t elem) {
+  const int pad = (int)(16 / elem);
+  return (out_region1_elems(Ch, pad) + (size_t)PTO * (Ch + pad)) * elem + (2 * (size_t)Ch + 8 * PTO) * 4;
+}
+
+// Chunk i of a thread = 8 output channels (c8) of one pixel (px) of the pass's
+// [PTO][W] sub-block, W = 8 * W8 channels; consecutive threads take consecutive chunks.
+template <typename T>
+__device__ __forceinline__ void out_load_g(typename TypeOps<T>::V8 (&gr)[OCH], const T* __restrict__ gblk,
+                                           int C, int c0, int W8, int npix, int tid) {
+#pragma unroll
+  for (int i = 0; i < OCH; ++i) {
+    const int idx = tid + i * NT, px = idx / W8, c8 = idx - px * W8;
+    gr[i] = zero8<T>();
+    if (idx < PTO * W8 && px < npix) gr[i] = load8(gblk + (int64_t)px * C + c0 + 8 * c8);
+  }
+}
 
 template <typename T, int PREC>
 __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args a, int64_t NP,
                                                            size_t off_g, size_t off_o) {
   typedef typename TypeOps<T>::V8 V8;
-  typedef typename TypeOps<T>::V4 V4;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int C = (int)a.C, Ch = (int)a.Ch, N = (int)a.N;
   const int OR = PTO + lds_pad<T>();  // raw o tile [Ch][OR]
   const int ZR = Ch + lds_pad<T>();   // normalised tile [PTO][ZR]
+  const int YR = OPC + lds_pad<T>();  // pass tile [PTO][YR]
   T* ot = reinterpret_cast<T*>(smem_raw);
-  T* zs = ot + (size_t)Ch * OR;
+  T* ys = ot;  // the o tile is dead once the LayerNorm has written zs
+  T* zs = ot + out_region1_elems(Ch, lds_pad<T>());
   float* lnw = reinterpret_cast<float*>(zs + (size_t)PTO * ZR);
   float* lnb = lnw + Ch;
   float* red = lnb + Ch;  // [2 stats][4 quarters][PTO] partial sums
@@ -466,11 +499,16 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
   const int p = (blockIdx.x / ntile) % N;
   const int b = blockIdx.x / (ntile * N);
   const int q0 = ct * PTO;
+  const int npix = N - q0 < PTO ? N - q0 : PTO;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
 
   const T* __restrict__ ocm = (const T*)((const unsigned char*)a.workspace + off_o);
-  const T* __restrict__ gg = (const T*)((const unsigned char*)a.workspace + off_g);
-  T* __restrict__ out = (T*)a.out;
+  const int64_t blk = (((int64_t)b * N + p) * N + q0) * C;
+  const T* __restrict__ gblk = (const T*)((const unsigned char*)a.workspace + off_g) + blk;
+  T* __restrict__ oblk = (T*)a.out + blk;
+
+  V8 gr[OCH];
+  out_load_g<T>(gr, gblk, C, 0, (C < OPC ? C : OPC) / 8, npix, tid);
 
   for (int c = tid; c < Ch; c += NT) {
     lnw[c] = ld_or<T>(a.ln_out_w, c, 1.f);
@@ -515,42 +553,55 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
   }
   __syncthreads();
 
-  // ---- out = (z Wpo^T + bpo) * g. acc[s] = [cout][pixel]: row = cout 32ctile + 8(r/4) + 4g + r%4
+  // ---- out = (z Wpo^T + bpo) * g, in passes of OPC output channels.
+  // acc[s] = [cout][pixel]: cout = c0 + 32 wave + 8(r/4) + 4g + r%4, pixel = 32s + l32.
   const T* __restrict__ wpo = (const T*)a.p_out_w;
   const int nk = Ch / 16;
-  for (int ctile = wave; ctile < C / 32; ctile += 4) {
-    const int cbase = 32 * ctile + 4 * g;
-    float bpo[16];
+  for (int c0 = 0; c0 < C; c0 += OPC) {
+    const int W = C - c0 < OPC ? C - c0 : OPC;
+    if (32 * wave < W) {
+      const int cw = c0 + 32 * wave;
+      float bpo[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) bpo[r] = ld_or<T>(a.p_out_b, cbase + 8 * (r / 4) + (r % 4), 0.f);
-    const T* wrow = wpo + (int64_t)(32 * ctile + l32) * Ch + 8 * g;
-    f32x16 acc[PTO / 32];
+      for (int r = 0; r < 16; ++r) bpo[r] = ld_or<T>(a.p_out_b, cw + 4 * g + 8 * (r / 4) + (r % 4), 0.f);
+      const T* wrow = wpo + (int64_t)(cw + l32) * Ch + 8 * g;
+      f32x16 acc[PTO / 32];
 #pragma unroll
-    for (int s = 0; s < PTO / 32; ++s)
+      for (int s = 0; s < PTO / 32; ++s)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[s][r] = 0.f;
-    for (int k = 0; k < nk; ++k) {
-      const V8 wf = load8(wrow + 16 * k);
+        for (int r = 0; r < 16; ++r) acc[s][r] = 0.f;
+      for (int k = 0; k < nk; ++k) {
+        const V8 wf = load8(wrow + 16 * k);
 #pragma unroll
-      for (int s = 0; s < PTO / 32; ++s) {
-        const V8 zf = load8(&zs[(32 * s + l32) * ZR + 16 * k + 8 * g]);
-        Mma<T, PREC>::step(acc[s], wf, zf);
+        for (int s = 0; s < PTO / 32; ++s) {
+          const V8 zf = load8(&zs[(32 * s + l32) * ZR + 16 * k + 8 * g]);
+          Mma<T, PREC>::step(acc[s], wf, zf);
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < PTO / 32; ++s)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          f32x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = acc[s][4 * rg + e] + bpo[4 * rg + e];
+          store4(&ys[(32 * s + l32) * YR + 32 * wave + 8 * rg + 4 * g], TypeOps<T>::from_f32(v));
+        }
+    }
+    __syncthreads();
+    const int W8 = W / 8;
+#pragma unroll
+    for (int i = 0; i < OCH; ++i) {
+      const int idx = tid + i * NT, px = idx / W8, c8 = idx - px * W8;
+      if (idx < PTO * W8 && px < npix) {
+        const f32x8 y = TypeOps<T>::to_f32(load8(&ys[px * YR + 8 * c8]));
+        store8(oblk + (int64_t)px * C + c0 + 8 * c8, TypeOps<T>::from_f32(y * TypeOps<T>::to_f32(gr[i])));
       }
     }
-#pragma unroll
-    for (int s = 0; s < PTO / 32; ++s) {
-      const int q = q0 + 32 * s + l32;
-      if (q >= N) continue;
-      const int64_t pix = ((int64_t)b * N + p) * N + q;
-#pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        const int64_t off = pix * C + cbase + 8 * rg;
-        const f32x4 gv = TypeOps<T>::to_f32(load4(gg + off));
-        f32x4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (acc[s][4 * rg + e] + bpo[4 * rg + e]) * gv[e];
-        store4(out + off, TypeOps<T>::from_f32(v));
-      }
+    if (c0 + OPC < C) {
+      __syncthreads();  // the next pass rewrites ys
+      const int Wn = C - c0 - OPC < OPC ? C - c0 - OPC : OPC;
+      out_load_g<T>(gr, gblk, C, c0 + OPC, Wn / 8, npix, tid);
     }
   }
 }
@@ -562,8 +613,7 @@ size_t proj_smem(const gnn_trimul_args& a) {
 
 template <typename T>
 size_t out_smem(const gnn_trimul_args& a) {
-  return ((size_t)a.Ch * (PTO + lds_pad<T>()) + (size_t)PTO * (a.Ch + lds_pad<T>())) * sizeof(T) +
-         (2 * (size_t)a.Ch + 8 * PTO) * sizeof(float);
+  return out_lds_bytes(a.Ch, sizeof(T));
 }
 
 template <typename T, int PREC>
@@ -623,8 +673,7 @@ int check_args(const gnn_trimul_args& a, const char* who) {
   const size_t e = a.dtype == GNN_F32 ? 4 : 2;
   const size_t proj_lds = (size_t)PT * (a.C + 16 / e) * e + (2 * (size_t)a.C + PT) * 4 + 16 +
                           4 * (size_t)(e == 2 ? proj_ebuf_elems<bf16>() : proj_ebuf_elems<float>()) * e;
-  const size_t out_lds =
-      ((size_t)a.Ch * (PTO + 16 / e) + (size_t)PTO * (a.Ch + 16 / e)) * e + (2 * (size_t)a.Ch + 8 * PTO) * 4;
+  const size_t out_lds = out_lds_bytes(a.Ch, e);
   if (proj_lds > 160 * 1024 || out_lds > 160 * 1024)
     return set_error(GNN_ERR_UNSUPPORTED, "trimul: channel count too large for the LDS tiles");
   if (a.B * a.N * ((a.N + PT - 1) / PT) >= ((int64_t)1 << 31))
