@@ -25,7 +25,8 @@ namespace gnn {
 namespace {
 
 constexpr int NT = 256;  // threads per workgroup (4 waves)
-constexpr int PT = 128;  // pixels per workgroup in the projection / output stages
+constexpr int PT = 128;  // pixels per workgroup in the projection stage
+constexpr int LDB = 8;   // tile loads kept in flight per thread (issued before their LDS stores)
 
 __host__ __device__ inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
@@ -129,14 +130,22 @@ __global__ __launch_bounds__(NT, GNN_PROJ_MINBLOCKS) void trimul_proj_kernel(con
     mk[pl] = mval;
   }
 
-  // ---- x tile (PT pixels x C channels) into LDS
+  // ---- x tile (PT pixels x C channels) into LDS, LDB 16-byte loads in flight per thread
   const T* __restrict__ x = (const T*)a.x;
   const int cpp = C / 8;
-  for (int c = tid; c < PT * cpp; c += NT) {
-    const int pl = c / cpp, k0 = (c % cpp) * 8;
-    V8 v = zero8<T>();
-    if (c0 + pl < N) v = load8(x + pix_index(pl) * C + k0);
-    store8(&zs[pl * ZR + k0], v);
+  for (int cb = 0; cb < PT * cpp; cb += LDB * NT) {
+    V8 v[LDB];
+#pragma unroll
+    for (int i = 0; i < LDB; ++i) {
+      const int c = cb + tid + i * NT, pl = c / cpp, k0 = (c % cpp) * 8;
+      v[i] = zero8<T>();
+      if (c < PT * cpp && c0 + pl < N) v[i] = load8(x + pix_index(pl) * C + k0);
+    }
+#pragma unroll
+    for (int i = 0; i < LDB; ++i) {
+      const int c = cb + tid + i * NT, pl = c / cpp, k0 = (c % cpp) * 8;
+      if (c < PT * cpp) store8(&zs[pl * ZR + k0], v[i]);
+    }
   }
   __syncthreads();
 
@@ -514,11 +523,19 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
     lnw[c] = ld_or<T>(a.ln_out_w, c, 1.f);
     lnb[c] = ld_or<T>(a.ln_out_b, c, 0.f);
   }
-  for (int c = tid; c < Ch * (PTO / 8); c += NT) {
-    const int ch = c / (PTO / 8), k0 = (c % (PTO / 8)) * 8;
-    V8 v = zero8<T>();
-    if (q0 + k0 < N) v = load8(ocm + (((int64_t)b * Ch + ch) * N + p) * NP + q0 + k0);
-    store8(&ot[ch * OR + k0], v);
+  for (int cb = 0; cb < Ch * (PTO / 8); cb += LDB * NT) {
+    V8 v[LDB];
+#pragma unroll
+    for (int i = 0; i < LDB; ++i) {
+      const int c = cb + tid + i * NT, ch = c / (PTO / 8), k0 = (c % (PTO / 8)) * 8;
+      v[i] = zero8<T>();
+      if (c < Ch * (PTO / 8) && q0 + k0 < N) v[i] = load8(ocm + (((int64_t)b * Ch + ch) * N + p) * NP + q0 + k0);
+    }
+#pragma unroll
+    for (int i = 0; i < LDB; ++i) {
+      const int c = cb + tid + i * NT, ch = c / (PTO / 8), k0 = (c % (PTO / 8)) * 8;
+      if (c < Ch * (PTO / 8)) store8(&ot[ch * OR + k0], v[i]);
+    }
   }
   __syncthreads();
 
