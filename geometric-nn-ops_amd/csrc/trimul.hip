@@ -20,12 +20,13 @@
 #include "gnn_common.hpp"
 #include "gnn_internal.hpp"
 
+#include <algorithm>
+
 namespace gnn {
 
 namespace {
 
 constexpr int NT = 256;  // threads per workgroup (4 waves)
-constexpr int PT = 128;  // pixels per workgroup in the projection stage
 constexpr int LDB = 8;   // tile loads kept in flight per thread (issued before their LDS stores)
 
 __host__ __device__ inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
@@ -57,168 +58,228 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Per-wave epilogue staging tile of the projection stage: max(32 x (64 + pad), 64 x (32 + pad)).
+// ============================== stage 1: LN-in + projections ==============================
+// Persistent kernel: PW waves per workgroup, as many workgroups as fit on the device at
+// once, each looping over pixel tiles of PTP pixels along one row ('outgoing') or column
+// ('incoming') of the pair grid. Work per tile: the 2*Ch gated projection in units of 32
+// channels (p and its gate g_in together, over all PTP pixels), and the output gate g_out
+// in items of 32 channels x 32 pixels. Wave w takes projection units w, w + PW, ... and
+// gate items w, w + PW, ...; while a wave's unit does not change between tiles (C = Ch =
+// 128: one unit of each kind per wave) its weight fragments and biases stay in registers
+// for the whole launch.
+//
+// The x of the next tile is loaded into registers while the current tile's MFMAs and
+// epilogues run, 8 threads per pixel, each holding up to XM 8-channel chunks of it. A thread
+// reduces its chunks to a LayerNorm partial (mean, M2); after one barrier it merges the
+// pixel's 8 partials (the pairwise update of Chan, Golub and LeVeque: exact for the
+// combined mean and sum of squared deviations), normalises its chunks and writes z into the
+// single LDS tile, which a second barrier hands to the next iteration.
+constexpr int PW = 8;          // waves per projection workgroup
+constexpr int PNT = 64 * PW;   // threads per projection workgroup
+constexpr int PTP = 64;        // pixels per tile
+constexpr int PSUB = PTP / 32; // 32-pixel sub-tiles per tile
+
+// Epilogue staging of a projection unit: [32 channels][SPT * 32 pixels] (128-byte channel
+// rows), reused as [32 pixels][32 channels] by the gate items.
+template <typename T>
+__host__ __device__ constexpr int proj_spt() {
+  return sizeof(T) == 2 ? 2 : 1;
+}
+template <typename T>
+__host__ __device__ constexpr int proj_er() {
+  return 32 * proj_spt<T>() + lds_pad<T>();
+}
 template <typename T>
 __host__ __device__ constexpr int proj_ebuf_elems() {
-  return (32 * (64 + lds_pad<T>()) > 64 * (32 + lds_pad<T>())) ? 32 * (64 + lds_pad<T>())
-                                                                 : 64 * (32 + lds_pad<T>());
-}
-// LDS of the projection stage: z tile [PT][C + pad] (T), LN gamma / beta [C] and the mask
-// of the tile [PT] (fp32), then 4 staging tiles (T), each region 16-byte aligned.
-template <typename T>
-__host__ __device__ inline size_t proj_ebuf_offset(int C) {
-  const size_t head = (size_t)PT * (C + lds_pad<T>()) * sizeof(T) + (2 * (size_t)C + PT) * sizeof(float);
-  return (head + 15) / 16 * 16;
-}
-template <typename T>
-__device__ __forceinline__ T* proj_ebuf(unsigned char* smem, int C) {
-  return reinterpret_cast<T*>(smem + proj_ebuf_offset<T>(C));
+  return 32 * proj_er<T>();
 }
 
-// ============================== stage 1: LN-in + projections ==============================
-// One workgroup = PT pixels along one row ('outgoing') or column ('incoming') of the pair
-// grid. LDS holds the x tile (normalised in place to z), the LayerNorm parameters and the
-// tile's mask values. Work units per wave: 32 channels of the 2*Ch gated projection (p and
-// its gate g_in share the unit so the epilogue can combine them), or 32 channels of the
-// output gate. Weight fragments are read once per pair of 32-pixel sub-tiles.
-template <typename T, int PREC>
-#ifndef GNN_PROJ_MINBLOCKS
-#define GNN_PROJ_MINBLOCKS 2
-#endif
-__global__ __launch_bounds__(NT, GNN_PROJ_MINBLOCKS) void trimul_proj_kernel(const gnn_trimul_args a, int64_t NP,
-                                                            size_t off_a, size_t off_b,
-                                                            size_t off_g) {
+// LDS of the projection stage (byte offsets, 16-byte aligned): z tile [PTP][C + pad] (T),
+// one staging tile per wave (T), LayerNorm partials [8][PTP] (float2), LN gamma / beta [C]
+// and the tile's mask values [PTP] (fp32).
+struct ProjLds {
+  size_t zs, ebuf, red, lnw, mk, total;
+};
+template <typename T>
+__host__ __device__ inline ProjLds proj_lds(int64_t C) {
+  ProjLds L;
+  L.zs = 0;
+  L.ebuf = ((size_t)PTP * (C + lds_pad<T>()) * sizeof(T) + 15) / 16 * 16;
+  L.red = L.ebuf + (size_t)PW * proj_ebuf_elems<T>() * sizeof(T);
+  L.lnw = L.red + 8 * (size_t)PTP * 2 * sizeof(float);
+  L.mk = L.lnw + ((2 * (size_t)C * sizeof(float) + 15) / 16 * 16);
+  L.total = L.mk + PTP * sizeof(float);
+  return L;
+}
+
+// Tile t of the projection stage. Outgoing tiles step along a row of the pair grid first,
+// incoming tiles along the column index, so concurrently running workgroups read
+// neighbouring memory. Local pixel pl of a tile is pair-grid pixel (row, c0 + pl) for
+// 'outgoing' and (c0 + pl, row) for 'incoming'.
+struct PTile {
+  int b, row, c0;
+};
+__device__ __forceinline__ PTile proj_tile(int64_t t, int N, bool outgoing) {
+  const int ntp = (N + PTP - 1) / PTP;
+  PTile r;
+  if (outgoing) {
+    r.c0 = (int)(t % ntp) * PTP;
+    const int64_t rest = t / ntp;
+    r.row = (int)(rest % N);
+    r.b = (int)(rest / N);
+  } else {
+    r.row = (int)(t % N);
+    const int64_t rest = t / N;
+    r.c0 = (int)(rest % ntp) * PTP;
+    r.b = (int)(rest / ntp);
+  }
+  return r;
+}
+__device__ __forceinline__ int64_t proj_pix(const PTile& tl, int pl, int N, bool outgoing) {
+  const int cpos = tl.c0 + pl;
+  const int pp = outgoing ? tl.row : cpos;
+  const int qq = outgoing ? cpos : tl.row;
+  return ((int64_t)tl.b * N + pp) * N + qq;
+}
+template <typename T>
+__device__ __forceinline__ float proj_mask(const gnn_trimul_args& a, const PTile& tl, int pl, int N,
+                                           bool outgoing) {
+  if (!a.mask || tl.c0 + pl >= N) return 1.f;
+  const int cpos = tl.c0 + pl;
+  const int pp = outgoing ? tl.row : cpos;
+  const int qq = outgoing ? cpos : tl.row;
+  return TypeOps<T>::to_f32(
+      ((const T*)a.mask)[tl.b * a.mask_stride[0] + pp * a.mask_stride[1] + qq * a.mask_stride[2]]);
+}
+
+// Chunks of x per thread that the tile load must hold: ceil(C / 64), rounded up to 2, 4, 8.
+__host__ __device__ inline int proj_xm(int64_t C) { return C <= 128 ? 2 : C <= 256 ? 4 : 8; }
+
+template <typename T, int PREC, int XM>
+__global__ __launch_bounds__(PNT, 1) void trimul_proj_kernel(const gnn_trimul_args a, int64_t NP,
+                                                             size_t off_a, size_t off_b,
+                                                             size_t off_g) {
   typedef typename TypeOps<T>::V8 V8;
-  typedef typename TypeOps<T>::V4 V4;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int C = (int)a.C, Ch = (int)a.Ch, N = (int)a.N;
+  const ProjLds Ld = proj_lds<T>(C);
   const int ZR = C + lds_pad<T>();
-  T* zs = reinterpret_cast<T*>(smem_raw);                                   // [PT][ZR]
-  float* lnw = reinterpret_cast<float*>(smem_raw + (size_t)PT * ZR * sizeof(T));  // [C]
-  float* lnb = lnw + C;                                                      // [C]
-  float* mk = lnb + C;                                                       // [PT]
-
-  const int ntile = (N + PT - 1) / PT;
-  const int ct = blockIdx.x % ntile;
-  const int row = (blockIdx.x / ntile) % N;
-  const int b = blockIdx.x / (ntile * N);
-  const int c0 = ct * PT;
+  constexpr int SPT = proj_spt<T>();
+  constexpr int ER = proj_er<T>();       // unit staging [32 channels][ER]
+  constexpr int EG = 32 + lds_pad<T>();  // gate staging [32 pixels][EG]
+  constexpr int KCH = sizeof(T) == 2 ? 8 : 4;  // k-steps of weight fragments held in registers
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
-  const bool outgoing = a.outgoing != 0;
+  T* zs = reinterpret_cast<T*>(smem_raw + Ld.zs);
+  T* ebuf = reinterpret_cast<T*>(smem_raw + Ld.ebuf) + wave * proj_ebuf_elems<T>();
+  float2* red = reinterpret_cast<float2*>(smem_raw + Ld.red);
+  float* lnw = reinterpret_cast<float*>(smem_raw + Ld.lnw);
+  float* lnb = lnw + C;
+  float* mk = reinterpret_cast<float*>(smem_raw + Ld.mk);
 
-  // pixel (pp, qq) of local pixel index pl: outgoing walks row `row`, incoming column `row`
-  auto pix_index = [&](int pl) -> int64_t {
-    const int cpos = c0 + pl;
-    const int pp = outgoing ? row : cpos;
-    const int qq = outgoing ? cpos : row;
-    return ((int64_t)b * N + pp) * N + qq;
+  const bool outgoing = a.outgoing != 0;
+  const int64_t ntiles = (int64_t)a.B * N * ((N + PTP - 1) / PTP);
+  typedef PTile Tile;
+  auto tile_of = [&](int64_t t) -> Tile { return proj_tile(t, N, outgoing); };
+  auto pix_index = [&](const Tile& tl, int pl) -> int64_t { return proj_pix(tl, pl, N, outgoing); };
+
+  // ---- tile load + LayerNorm, thread = (pixel xpl, part xpart) holding chunks xpart + 8j
+  const int xpl = tid >> 3, xpart = tid & 7, cpp = C / 8;
+  V8 xr[XM];
+  float mreg = 1.f;
+  auto load_x = [&](const Tile& tl) {
+    const bool in = tl.c0 + xpl < N;
+    const T* src = (const T*)a.x + (in ? pix_index(tl, xpl) * C : 0);
+#pragma unroll
+    for (int j = 0; j < XM; ++j) {
+      const int ci = xpart + 8 * j;
+      xr[j] = zero8<T>();
+      if (in && ci < cpp) xr[j] = load8(src + 8 * ci);
+    }
+    if (tid < PTP) mreg = proj_mask<T>(a, tl, tid, N, outgoing);
+  };
+  auto ln_partial = [&]() {
+    float s = 0.f, n = 0.f;
+#pragma unroll
+    for (int j = 0; j < XM; ++j)
+      if (xpart + 8 * j < cpp) {
+        const f32x8 v = TypeOps<T>::to_f32(xr[j]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += v[e];
+        n += 8.f;
+      }
+    const float mean = n > 0.f ? s / n : 0.f;
+    float m2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < XM; ++j)
+      if (xpart + 8 * j < cpp) {
+        const f32x8 v = TypeOps<T>::to_f32(xr[j]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = v[e] - mean;
+          m2 += d * d;
+        }
+      }
+    red[xpart * PTP + xpl] = make_float2(mean, m2);
+  };
+  auto ln_finish = [&]() {
+    float2 pr[8];
+    float nj[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pr[j] = red[j * PTP + xpl];
+      nj[j] = cpp > j ? 8.f * (float)((cpp - j + 7) / 8) : 0.f;  // elements held by part j
+    }
+    float mean = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mean += nj[j] * pr[j].x;
+    mean /= (float)C;
+    float m2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float d = pr[j].x - mean;
+      m2 += pr[j].y + nj[j] * d * d;
+    }
+    const float rstd = 1.0f / sqrtf(m2 / (float)C + a.eps);
+#pragma unroll
+    for (int j = 0; j < XM; ++j) {
+      const int ci = xpart + 8 * j;
+      if (ci < cpp) {
+        f32x8 v = TypeOps<T>::to_f32(xr[j]);
+        const f32x4 w0 = *reinterpret_cast<const f32x4*>(lnw + 8 * ci);
+        const f32x4 w1 = *reinterpret_cast<const f32x4*>(lnw + 8 * ci + 4);
+        const f32x4 b0 = *reinterpret_cast<const f32x4*>(lnb + 8 * ci);
+        const f32x4 b1 = *reinterpret_cast<const f32x4*>(lnb + 8 * ci + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = (v[e] - mean) * rstd * w0[e] + b0[e];
+          v[e + 4] = (v[e + 4] - mean) * rstd * w1[e] + b1[e];
+        }
+        store8(&zs[xpl * ZR + 8 * ci], TypeOps<T>::from_f32(v));
+      }
+    }
+    if (tid < PTP) mk[tid] = mreg;
   };
 
-  for (int c = tid; c < C; c += NT) {
-    lnw[c] = ld_or<T>(a.ln_in_w, c, 1.f);
-    lnb[c] = ld_or<T>(a.ln_in_b, c, 0.f);
-  }
-  for (int pl = tid; pl < PT; pl += NT) {
-    float mval = 1.f;
-    if (a.mask && c0 + pl < N) {
-      const int cpos = c0 + pl;
-      const int pp = outgoing ? row : cpos;
-      const int qq = outgoing ? cpos : row;
-      mval = TypeOps<T>::to_f32(
-          ((const T*)a.mask)[b * a.mask_stride[0] + pp * a.mask_stride[1] + qq * a.mask_stride[2]]);
-    }
-    mk[pl] = mval;
-  }
-
-  // ---- x tile (PT pixels x C channels) into LDS, LDB 16-byte loads in flight per thread
-  const T* __restrict__ x = (const T*)a.x;
-  const int cpp = C / 8;
-  for (int cb = 0; cb < PT * cpp; cb += LDB * NT) {
-    V8 v[LDB];
-#pragma unroll
-    for (int i = 0; i < LDB; ++i) {
-      const int c = cb + tid + i * NT, pl = c / cpp, k0 = (c % cpp) * 8;
-      v[i] = zero8<T>();
-      if (c < PT * cpp && c0 + pl < N) v[i] = load8(x + pix_index(pl) * C + k0);
-    }
-#pragma unroll
-    for (int i = 0; i < LDB; ++i) {
-      const int c = cb + tid + i * NT, pl = c / cpp, k0 = (c % cpp) * 8;
-      if (c < PT * cpp) store8(&zs[pl * ZR + k0], v[i]);
-    }
-  }
-  __syncthreads();
-
-  // ---- LayerNorm in place (fp32 statistics, biased variance). Thread = (pixel tid % 128,
-  // channel half tid / 128), so the lanes of a wave read 64 different rows at one column
-  // (conflict-free); the two halves' partial sums meet in LDS (the staging area, idle now).
-  {
-    const int pl = tid & (PT - 1), half = tid / PT;
-    const int k0 = half * (C / 2);
-    T* zrow = &zs[pl * ZR];
-    float* red = reinterpret_cast<float*>(proj_ebuf<T>(smem_raw, C));  // [2 stats][2 halves][PT]
-    float sum = 0.f;
-    for (int k = k0; k < k0 + C / 2; k += 8) {
-      const f32x8 v = TypeOps<T>::to_f32(load8(zrow + k));
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sum += v[e];
-    }
-    red[half * PT + pl] = sum;
-    __syncthreads();
-    const float mean = (red[pl] + red[PT + pl]) / (float)C;
-    float sq = 0.f;
-    for (int k = k0; k < k0 + C / 2; k += 8) {
-      const f32x8 v = TypeOps<T>::to_f32(load8(zrow + k));
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float d = v[e] - mean;
-        sq += d * d;
-      }
-    }
-    red[2 * PT + half * PT + pl] = sq;
-    __syncthreads();
-    const float rstd = 1.0f / sqrtf((red[2 * PT + pl] + red[3 * PT + pl]) / (float)C + a.eps);
-    for (int k = k0; k < k0 + C / 2; k += 8) {
-      f32x8 v = TypeOps<T>::to_f32(load8(zrow + k));
-      const f32x4 w0 = *reinterpret_cast<const f32x4*>(lnw + k);
-      const f32x4 w1 = *reinterpret_cast<const f32x4*>(lnw + k + 4);
-      const f32x4 b0 = *reinterpret_cast<const f32x4*>(lnb + k);
-      const f32x4 b1 = *reinterpret_cast<const f32x4*>(lnb + k + 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[e] = (v[e] - mean) * rstd * w0[e] + b0[e];
-        v[e + 4] = (v[e + 4] - mean) * rstd * w1[e] + b1[e];
-      }
-      store8(zrow + k, TypeOps<T>::from_f32(v));
-    }
-  }
-  __syncthreads();
-
-  const int npg = 2 * Ch / 32;
-  const int nunits = npg + C / 32;
+  // ---- projections of one tile
   const int nk = C / 16;
+  const int npg = 2 * Ch / 32, ngo = C / 32;
   T* __restrict__ a_cm = (T*)((unsigned char*)a.workspace + off_a);
   T* __restrict__ b_cm = (T*)((unsigned char*)a.workspace + off_b);
   T* __restrict__ gout = (T*)((unsigned char*)a.workspace + off_g);
   const T* __restrict__ wp = (const T*)a.p_in_w;
   const T* __restrict__ wg = (const T*)a.g_in_w;
   const T* __restrict__ wgo = (const T*)a.g_out_w;
-  // wave-private staging tile for the epilogues (32 channels x 64 pixels, or 64 x 32)
-  T* ebuf = proj_ebuf<T>(smem_raw, C) + wave * proj_ebuf_elems<T>();
-  constexpr int ER = 64 + lds_pad<T>();  // [32 channel rows][64 pixels] (a / b)
-  constexpr int EG = 32 + lds_pad<T>();  // [64 pixel rows][32 channels] (g)
+  V8 wpf[KCH], wgf[KCH], wof[KCH];
+  float bp = 0.f, bg = 0.f, bgo[16];
+  int wp_unit = -1, wo_unit = -1;
 
-  for (int u = wave; u < nunits; u += 4) {
-    if (u < npg) {
-      // acc[s] = [pixel][channel] tiles: row = pixel 32*s + 8*(r/4) + 4g + r%4, col = channel
-      const int ch = 32 * u + l32;  // channel of the 2*Ch projection held by this lane
-      const float bp = ld_or<T>(a.p_in_b, ch, 0.f);
-      const float bg = ld_or<T>(a.g_in_b, ch, 0.f);
+  auto compute = [&](const Tile& tl) {
+    // gated projection units: acc = [pixel][channel], row = pixel 32s + 8(r/4) + 4g + r%4,
+    // col = channel 32u + l32; staged as [channel][pixel] for 128-byte row stores
+    for (int u = wave; u < npg; u += PW) {
+      const int ch = 32 * u + l32;
       const T* wprow = wp + (int64_t)ch * C + 8 * g;
       const T* wgrow = wg + (int64_t)ch * C + 8 * g;
-      // weight fragments of up to KCH k-steps stay in registers across the pixel sub-tiles
-      constexpr int KCH = sizeof(T) == 2 ? 8 : 4;
-      V8 wpf[KCH], wgf[KCH];
       auto load_w = [&](int kc) {
 #pragma unroll
         for (int j = 0; j < KCH; ++j)
@@ -227,107 +288,395 @@ __global__ __launch_bounds__(NT, GNN_PROJ_MINBLOCKS) void trimul_proj_kernel(con
             wgf[j] = load8(wgrow + 16 * (kc + j));
           }
       };
-      if (nk <= KCH) load_w(0);
-      for (int sp = 0; sp < PT / 32; sp += 2) {
+      if (u != wp_unit) {
+        bp = ld_or<T>(a.p_in_b, ch, 0.f);
+        bg = ld_or<T>(a.g_in_b, ch, 0.f);
+        if (nk <= KCH) load_w(0);
+        wp_unit = u;
+      }
+      for (int s0 = 0; s0 < PSUB; s0 += SPT) {
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
+        for (int s2 = 0; s2 < SPT; ++s2) {
+          const int s = s0 + s2;
           f32x16 accp, accg;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) accp[r] = accg[r] = 0.f;
+          for (int r = 0; r < 16; ++r) {
+            accp[r] = bp;
+            accg[r] = bg;
+          }
           for (int kc = 0; kc < nk; kc += KCH) {
             if (nk > KCH) load_w(kc);
 #pragma unroll
             for (int j = 0; j < KCH; ++j) {
               if (kc + j >= nk) break;
-              const V8 zf = load8(&zs[(32 * (sp + s2) + l32) * ZR + 16 * (kc + j) + 8 * g]);
+              const V8 zf = load8(&zs[(32 * s + l32) * ZR + 16 * (kc + j) + 8 * g]);
               Mma<T, PREC>::step(accp, zf, wpf[j]);
               Mma<T, PREC>::step(accg, zf, wgf[j]);
             }
           }
-          // gated, masked values -> staging tile [channel l32][pixel]
 #pragma unroll
           for (int rg = 0; rg < 4; ++rg) {
-            const int pt = 32 * s2 + 8 * rg + 4 * g;  // pixel within the sub-tile pair
+            const int pt = 8 * rg + 4 * g;  // pixel within the sub-tile
+            const f32x4 m4 = *reinterpret_cast<const f32x4*>(&mk[32 * s + pt]);
             f32x4 v;
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              v[e] = (accp[4 * rg + e] + bp) * sigmoid_acc(accg[4 * rg + e] + bg) * mk[32 * sp + pt + e];
-            store4(&ebuf[l32 * ER + pt], TypeOps<T>::from_f32(v));
+            for (int e = 0; e < 4; ++e) v[e] = accp[4 * rg + e] * sigmoid_acc(accg[4 * rg + e]) * m4[e];
+            store4(&ebuf[l32 * ER + 32 * s2 + pt], TypeOps<T>::from_f32(v));
           }
         }
         wave_lds_sync();
-        // 16-byte stores, 8 lanes per 128-byte channel row segment
+        // 16-byte stores, 4 * SPT lanes per channel row of 32 * SPT pixels
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 2 * SPT; ++i) {
           const int c = lane + 64 * i;
-          const int crow = c / 8, p0 = (c % 8) * 8;
+          const int crow = c / (4 * SPT), p0 = (c % (4 * SPT)) * 8;
           const int chg = 32 * u + crow;
           T* dst = chg < Ch ? a_cm : b_cm;
           const int chh = chg < Ch ? chg : chg - Ch;
-          const int pl = 32 * sp + p0;
-          T* drow = dst + (((int64_t)b * Ch + chh) * N + row) * NP + c0 + pl;
+          const int pl = 32 * s0 + p0;
+          T* drow = dst + (((int64_t)tl.b * Ch + chh) * N + tl.row) * NP + tl.c0 + pl;
           const V8 val = load8(&ebuf[crow * ER + p0]);
-          if (c0 + pl + 8 <= N) {
+          if (tl.c0 + pl + 8 <= N) {
             store8(drow, val);
           } else {
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-              if (c0 + pl + e < N) drow[e] = val[e];
+              if (tl.c0 + pl + e < N) drow[e] = val[e];
           }
-        }
-        wave_lds_sync();
-      }
-    } else {
-      // acc[s] = [channel][pixel]: row = channel c00 + 8*(r/4) + 4g + r%4, col = pixel
-      const int c00 = 32 * (u - npg);
-      float bgo[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) bgo[r] = ld_or<T>(a.g_out_b, c00 + 8 * (r / 4) + 4 * g + (r % 4), 0.f);
-      const T* wrow = wgo + (int64_t)(c00 + l32) * C + 8 * g;
-      constexpr int KCH = sizeof(T) == 2 ? 8 : 4;
-      V8 wf[KCH];
-      auto load_w = [&](int kc) {
-#pragma unroll
-        for (int j = 0; j < KCH; ++j)
-          if (kc + j < nk) wf[j] = load8(wrow + 16 * (kc + j));
-      };
-      if (nk <= KCH) load_w(0);
-      for (int sp = 0; sp < PT / 32; sp += 2) {
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          f32x16 acc;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-          for (int kc = 0; kc < nk; kc += KCH) {
-            if (nk > KCH) load_w(kc);
-#pragma unroll
-            for (int j = 0; j < KCH; ++j) {
-              if (kc + j >= nk) break;
-              const V8 zf = load8(&zs[(32 * (sp + s2) + l32) * ZR + 16 * (kc + j) + 8 * g]);
-              Mma<T, PREC>::step(acc, wf[j], zf);
-            }
-          }
-          // sigmoid -> staging tile [pixel][channel]
-#pragma unroll
-          for (int rg = 0; rg < 4; ++rg) {
-            f32x4 v;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = sigmoid_acc(acc[4 * rg + e] + bgo[4 * rg + e]);
-            store4(&ebuf[(32 * s2 + l32) * EG + 8 * rg + 4 * g], TypeOps<T>::from_f32(v));
-          }
-        }
-        wave_lds_sync();
-        // 16-byte stores, 4 lanes per 64-byte pixel row segment
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int c = lane + 64 * i;
-          const int px = c / 4, k0 = (c % 4) * 8;
-          const int pl = 32 * sp + px;
-          if (c0 + pl < N) store8(gout + pix_index(pl) * C + c00 + k0, load8(&ebuf[px * EG + k0]));
         }
         wave_lds_sync();
       }
     }
+    // output-gate items (unit uo, sub-tile s): acc = [channel][pixel], row = channel
+    // 32uo + 8(r/4) + 4g + r%4, col = pixel 32s + l32; staged as [pixel][channel]
+    for (int it = wave; it < ngo * PSUB; it += PW) {
+      const int uo = it % ngo, s = it / ngo;
+      const int c00 = 32 * uo;
+      const T* wrow = wgo + (int64_t)(c00 + l32) * C + 8 * g;
+      auto load_w = [&](int kc) {
+#pragma unroll
+        for (int j = 0; j < KCH; ++j)
+          if (kc + j < nk) wof[j] = load8(wrow + 16 * (kc + j));
+      };
+      if (uo != wo_unit) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) bgo[r] = ld_or<T>(a.g_out_b, c00 + 8 * (r / 4) + 4 * g + (r % 4), 0.f);
+        if (nk <= KCH) load_w(0);
+        wo_unit = uo;
+      }
+      f32x16 acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = bgo[r];
+      for (int kc = 0; kc < nk; kc += KCH) {
+        if (nk > KCH) load_w(kc);
+#pragma unroll
+        for (int j = 0; j < KCH; ++j) {
+          if (kc + j >= nk) break;
+          const V8 zf = load8(&zs[(32 * s + l32) * ZR + 16 * (kc + j) + 8 * g]);
+          Mma<T, PREC>::step(acc, wof[j], zf);
+        }
+      }
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = sigmoid_acc(acc[4 * rg + e]);
+        store4(&ebuf[l32 * EG + 8 * rg + 4 * g], TypeOps<T>::from_f32(v));
+      }
+      wave_lds_sync();
+      // 16-byte stores, 4 lanes per 32-channel pixel row segment
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int c = lane + 64 * i;
+        const int px = c / 4, k0 = (c % 4) * 8;
+        const int pl = 32 * s + px;
+        if (tl.c0 + pl < N) store8(gout + pix_index(tl, pl) * C + c00 + k0, load8(&ebuf[px * EG + k0]));
+      }
+      wave_lds_sync();
+    }
+  };
+
+  for (int c = tid; c < C; c += PNT) {
+    lnw[c] = ld_or<T>(a.ln_in_w, c, 1.f);
+    lnb[c] = ld_or<T>(a.ln_in_b, c, 0.f);
+  }
+  int64_t t = blockIdx.x;
+  if (t >= ntiles) return;  // uniform over the workgroup
+  Tile cur = tile_of(t);
+  load_x(cur);
+  ln_partial();
+  __syncthreads();
+  ln_finish();
+  __syncthreads();
+  for (; t < ntiles; t += gridDim.x) {
+    const int64_t tn = t + gridDim.x;
+    const bool has_next = tn < ntiles;  // uniform over the workgroup
+    Tile nxt = cur;
+    if (has_next) {
+      nxt = tile_of(tn);
+      load_x(nxt);
+    }
+    compute(cur);
+    if (has_next) ln_partial();
+    __syncthreads();  // z / mask of this tile consumed, partials of the next one published
+    if (has_next) ln_finish();
+    __syncthreads();
+    cur = nxt;
+  }
+}
+
+// ---- stage 1, fixed-width variant: 16-bit types with C = CK in {64, 128} ----------------
+// Same work split and tile order as trimul_proj_kernel, with C known at compile time so the
+// k loops unroll and a wave's gate MFMAs and second sub-tile can overlap the first
+// sub-tile's epilogue. Differences: the output-gate weights and biases live in LDS (loaded
+// once per workgroup), gate items stage through a tile of their own, the z tile is
+// double-buffered and the LayerNorm is wave-local (the 8 threads of a pixel are lanes of
+// one wave and reduce with cross-lane shuffles: the same two-pass mean / variance), so a
+// tile costs one barrier.
+template <int CK>
+struct ProjFastLds {
+  static constexpr int ZR = CK + 8;  // z and gate-weight row pitch (16-bit elements)
+  static constexpr int ER = 72;      // unit staging [32 channels][64 pixels + 8]
+  static constexpr int EG = 40;      // gate staging [32 pixels][32 channels + 8]
+  static constexpr size_t zs = 0;                                  // [2][PTP][ZR]
+  static constexpr size_t wgo = zs + 2 * (size_t)PTP * ZR * 2;     // [CK][ZR]
+  static constexpr size_t ebuf = wgo + (size_t)CK * ZR * 2;        // [PW][32][ER]
+  static constexpr size_t gbuf = ebuf + (size_t)PW * 32 * ER * 2;  // [PW][32][EG]
+  static constexpr size_t bgo = gbuf + (size_t)PW * 32 * EG * 2;   // [CK] fp32
+  static constexpr size_t lnw = bgo + (size_t)CK * 4;              // gamma, beta [2][CK] fp32
+  static constexpr size_t mk = lnw + 2 * (size_t)CK * 4;           // [2][PTP] fp32
+  static constexpr size_t total = mk + 2 * (size_t)PTP * 4;
+};
+
+template <typename T, int CK>
+__global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trimul_args a, int64_t NP,
+                                                                  size_t off_a, size_t off_b,
+                                                                  size_t off_g) {
+  static_assert(sizeof(T) == 2 && (CK == 64 || CK == 128), "fixed-width projection: 16-bit, C in {64, 128}");
+  typedef typename TypeOps<T>::V8 V8;
+  typedef ProjFastLds<CK> LD;
+  constexpr int ZR = LD::ZR, ER = LD::ER, EG = LD::EG;
+  constexpr int NKS = CK / 16;  // k-steps
+  constexpr int XMF = CK / 64;  // x chunks per thread (8 threads per pixel)
+  constexpr int NGI = CK / 16;  // gate items (CK / 32 units x 2 sub-tiles), at most one per wave
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int Ch = (int)a.Ch, N = (int)a.N;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
+  T* zs = reinterpret_cast<T*>(smem_raw + LD::zs);
+  T* wgo_s = reinterpret_cast<T*>(smem_raw + LD::wgo);
+  T* ebuf = reinterpret_cast<T*>(smem_raw + LD::ebuf) + wave * 32 * ER;
+  T* gbuf = reinterpret_cast<T*>(smem_raw + LD::gbuf) + wave * 32 * EG;
+  float* bgo_s = reinterpret_cast<float*>(smem_raw + LD::bgo);
+  float* lnw = reinterpret_cast<float*>(smem_raw + LD::lnw);
+  float* lnb = lnw + CK;
+  float* mk = reinterpret_cast<float*>(smem_raw + LD::mk);
+  const bool outgoing = a.outgoing != 0;
+  const int64_t ntiles = (int64_t)a.B * N * ((N + PTP - 1) / PTP);
+
+  // ---- per-workgroup constants
+  {
+    const T* wgo = (const T*)a.g_out_w;
+    for (int c = tid; c < CK * CK / 8; c += PNT) {
+      const int r = c / (CK / 8), k0 = (c % (CK / 8)) * 8;
+      store8(&wgo_s[r * ZR + k0], load8(wgo + r * CK + k0));
+    }
+    for (int c = tid; c < CK; c += PNT) {
+      bgo_s[c] = ld_or<T>(a.g_out_b, c, 0.f);
+      lnw[c] = ld_or<T>(a.ln_in_w, c, 1.f);
+      lnb[c] = ld_or<T>(a.ln_in_b, c, 0.f);
+    }
+  }
+
+  // ---- tile load + wave-local LayerNorm: thread = (pixel xpl, part xpart), chunks xpart + 8j
+  const int xpl = tid >> 3, xpart = tid & 7;
+  V8 xr[XMF];
+  float mreg = 1.f;
+  auto load_x = [&](const PTile& tl) {
+    const bool in = tl.c0 + xpl < N;
+    const T* src = (const T*)a.x + (in ? proj_pix(tl, xpl, N, outgoing) * CK : 0);
+#pragma unroll
+    for (int j = 0; j < XMF; ++j) xr[j] = in ? load8(src + 8 * (xpart + 8 * j)) : zero8<T>();
+    if (tid < PTP) mreg = proj_mask<T>(a, tl, tid, N, outgoing);
+  };
+  auto ln_store = [&](int nb) {
+    f32x8 v[XMF];
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < XMF; ++j) {
+      v[j] = TypeOps<T>::to_f32(xr[j]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += v[j][e];
+    }
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    const float mean = s * (1.0f / CK);
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < XMF; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = v[j][e] - mean;
+        q += d * d;
+      }
+    q += __shfl_xor(q, 1);
+    q += __shfl_xor(q, 2);
+    q += __shfl_xor(q, 4);
+    const float rstd = 1.0f / sqrtf(q * (1.0f / CK) + a.eps);
+#pragma unroll
+    for (int j = 0; j < XMF; ++j) {
+      const int k = 8 * (xpart + 8 * j);
+      const f32x4 w0 = *reinterpret_cast<const f32x4*>(lnw + k);
+      const f32x4 w1 = *reinterpret_cast<const f32x4*>(lnw + k + 4);
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(lnb + k);
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(lnb + k + 4);
+      f32x8 z;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        z[e] = (v[j][e] - mean) * rstd * w0[e] + b0[e];
+        z[e + 4] = (v[j][e + 4] - mean) * rstd * w1[e] + b1[e];
+      }
+      store8(&zs[(nb * PTP + xpl) * ZR + k], TypeOps<T>::from_f32(z));
+    }
+    if (tid < PTP) mk[nb * PTP + tid] = mreg;
+  };
+
+  // ---- projections of one tile
+  const int npg = 2 * Ch / 32;
+  T* __restrict__ a_cm = (T*)((unsigned char*)a.workspace + off_a);
+  T* __restrict__ b_cm = (T*)((unsigned char*)a.workspace + off_b);
+  T* __restrict__ gout = (T*)((unsigned char*)a.workspace + off_g);
+  V8 wpf[NKS], wgf[NKS];
+  float bp = 0.f, bg = 0.f;
+  int wp_unit = -1;
+  const bool has_go = wave < NGI;
+  const int uo = wave % (CK / 32), so = wave / (CK / 32);  // this wave's gate item
+
+  auto compute = [&](const PTile& tl, int cb) {
+    const T* z = zs + cb * PTP * ZR;
+    const float* m = mk + cb * PTP;
+    // gate item: acc = [channel][pixel], row = channel 32uo + 8(r/4) + 4g + r%4, col = pixel
+    // 32so + l32. Its MFMAs go first; the epilogue comes after the unit's.
+    f32x16 accgo;
+    if (has_go) {
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bgo_s[32 * uo + 8 * rg + 4 * g]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) accgo[4 * rg + e] = b4[e];
+      }
+#pragma unroll
+      for (int k = 0; k < NKS; ++k) {
+        const V8 wf = load8(&wgo_s[(32 * uo + l32) * ZR + 16 * k + 8 * g]);
+        const V8 zf = load8(&z[(32 * so + l32) * ZR + 16 * k + 8 * g]);
+        Mma<T, PREC_NATIVE>::step(accgo, wf, zf);
+      }
+    }
+    // gated projection units: acc = [pixel][channel], row = pixel 32s + 8(r/4) + 4g + r%4,
+    // col = channel 32u + l32; staged as [channel][pixel] for 128-byte row stores
+    for (int u = wave; u < npg; u += PW) {
+      const int ch = 32 * u + l32;
+      if (u != wp_unit) {
+        const T* wprow = (const T*)a.p_in_w + (int64_t)ch * CK + 8 * g;
+        const T* wgrow = (const T*)a.g_in_w + (int64_t)ch * CK + 8 * g;
+#pragma unroll
+        for (int k = 0; k < NKS; ++k) {
+          wpf[k] = load8(wprow + 16 * k);
+          wgf[k] = load8(wgrow + 16 * k);
+        }
+        bp = ld_or<T>(a.p_in_b, ch, 0.f);
+        bg = ld_or<T>(a.g_in_b, ch, 0.f);
+        wp_unit = u;
+      }
+      f32x16 accp[PSUB], accg[PSUB];
+#pragma unroll
+      for (int s = 0; s < PSUB; ++s) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          accp[s][r] = bp;
+          accg[s][r] = bg;
+        }
+#pragma unroll
+        for (int k = 0; k < NKS; ++k) {
+          const V8 zf = load8(&z[(32 * s + l32) * ZR + 16 * k + 8 * g]);
+          Mma<T, PREC_NATIVE>::step(accp[s], zf, wpf[k]);
+          Mma<T, PREC_NATIVE>::step(accg[s], zf, wgf[k]);
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < PSUB; ++s)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const int pt = 32 * s + 8 * rg + 4 * g;  // pixel within the tile
+          const f32x4 m4 = *reinterpret_cast<const f32x4*>(&m[pt]);
+          f32x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = accp[s][4 * rg + e] * sigmoid_acc(accg[s][4 * rg + e]) * m4[e];
+          store4(&ebuf[l32 * ER + pt], TypeOps<T>::from_f32(v));
+        }
+      wave_lds_sync();
+      // 16-byte stores, 8 lanes per 64-pixel channel row
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = lane + 64 * i;
+        const int crow = c / 8, p0 = (c % 8) * 8;
+        const int chg = 32 * u + crow;
+        T* dst = chg < Ch ? a_cm : b_cm;
+        const int chh = chg < Ch ? chg : chg - Ch;
+        T* drow = dst + (((int64_t)tl.b * Ch + chh) * N + tl.row) * NP + tl.c0 + p0;
+        const V8 val = load8(&ebuf[crow * ER + p0]);
+        if (tl.c0 + p0 + 8 <= N) {
+          store8(drow, val);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (tl.c0 + p0 + e < N) drow[e] = val[e];
+        }
+      }
+      wave_lds_sync();
+    }
+    if (has_go) {
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = sigmoid_acc(accgo[4 * rg + e]);
+        store4(&gbuf[l32 * EG + 8 * rg + 4 * g], TypeOps<T>::from_f32(v));
+      }
+      wave_lds_sync();
+      // 16-byte stores, 4 lanes per 32-channel pixel row segment
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int c = lane + 64 * i;
+        const int px = c / 4, k0 = (c % 4) * 8;
+        const int pl = 32 * so + px;
+        if (tl.c0 + pl < N)
+          store8(gout + proj_pix(tl, pl, N, outgoing) * CK + 32 * uo + k0, load8(&gbuf[px * EG + k0]));
+      }
+    }
+  };
+
+  int64_t t = blockIdx.x;
+  if (t >= ntiles) return;  // uniform over the workgroup
+  PTile cur = proj_tile(t, N, outgoing);
+  load_x(cur);
+  __syncthreads();  // LN parameters and gate weights in LDS
+  ln_store(0);
+  __syncthreads();
+  int cb = 0;
+  for (; t < ntiles; t += gridDim.x) {
+    const int64_t tn = t + gridDim.x;
+    const bool has_next = tn < ntiles;  // uniform over the workgroup
+    PTile nxt = cur;
+    if (has_next) {
+      nxt = proj_tile(tn, N, outgoing);
+      load_x(nxt);
+    }
+    compute(cur, cb);
+    if (has_next) ln_store(cb ^ 1);
+    __syncthreads();  // tile cb consumed by every wave, tile cb ^ 1 complete
+    cb ^= 1;
+    cur = nxt;
   }
 }
 
@@ -624,26 +973,60 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
 }
 
 template <typename T>
-size_t proj_smem(const gnn_trimul_args& a) {
-  return proj_ebuf_offset<T>((int)a.C) + 4 * (size_t)proj_ebuf_elems<T>() * sizeof(T);
-}
-
-template <typename T>
 size_t out_smem(const gnn_trimul_args& a) {
   return out_lds_bytes(a.Ch, sizeof(T));
 }
 
+// Resident workgroups of a persistent kernel: occupancy x CU count, at least 1.
+int persistent_grid(const void* fn, int threads, size_t smem) {
+  int dev = 0, ncu = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu < 1)
+    ncu = 1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, smem) != hipSuccess || per_cu < 1)
+    per_cu = 1;
+  return ncu * per_cu;
+}
+
+template <typename T, int PREC, int XM>
+int launch_proj_xm(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
+  const int64_t NP = round_up(a.N, 32);
+  const int64_t ntiles = a.B * a.N * ((a.N + PTP - 1) / PTP);
+  const size_t smem = proj_lds<T>(a.C).total;
+  const void* fn = (const void*)trimul_proj_kernel<T, PREC, XM>;
+  if (smem > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  const int64_t grid = std::min<int64_t>(ntiles, persistent_grid(fn, PNT, smem));
+  hipLaunchKernelGGL((trimul_proj_kernel<T, PREC, XM>), dim3((uint32_t)grid), dim3(PNT), smem, st, a, NP,
+                     L.off_a, L.off_b, L.off_g);
+  return (int)hipGetLastError();
+}
+
+template <typename T, int CK>
+int launch_proj_fast(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
+  const int64_t NP = round_up(a.N, 32);
+  const int64_t ntiles = a.B * a.N * ((a.N + PTP - 1) / PTP);
+  constexpr size_t smem = ProjFastLds<CK>::total;
+  const void* fn = (const void*)trimul_proj_fast_kernel<T, CK>;
+  (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  const int64_t grid = std::min<int64_t>(ntiles, persistent_grid(fn, PNT, smem));
+  hipLaunchKernelGGL((trimul_proj_fast_kernel<T, CK>), dim3((uint32_t)grid), dim3(PNT), smem, st, a, NP,
+                     L.off_a, L.off_b, L.off_g);
+  return (int)hipGetLastError();
+}
+
 template <typename T, int PREC>
 int launch_proj(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
-  const int64_t NP = round_up(a.N, 32);
-  const int64_t ntile = (a.N + PT - 1) / PT;
-  const size_t smem = proj_smem<T>(a);
-  if (smem > 64 * 1024)
-    (void)hipFuncSetAttribute((const void*)trimul_proj_kernel<T, PREC>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-  hipLaunchKernelGGL((trimul_proj_kernel<T, PREC>), dim3((uint32_t)(a.B * a.N * ntile)), dim3(NT),
-                     smem, st, a, NP, L.off_a, L.off_b, L.off_g);
-  return (int)hipGetLastError();
+  if constexpr (sizeof(T) == 2) {
+    if (a.C == 128) return launch_proj_fast<T, 128>(a, L, st);
+    if (a.C == 64) return launch_proj_fast<T, 64>(a, L, st);
+  }
+  switch (proj_xm(a.C)) {
+    case 2: return launch_proj_xm<T, PREC, 2>(a, L, st);
+    case 4: return launch_proj_xm<T, PREC, 4>(a, L, st);
+    default:
+      if constexpr (sizeof(T) == 2) return launch_proj_xm<T, PREC, 8>(a, L, st);
+      return set_error(GNN_ERR_UNSUPPORTED, "trimul: fp32 c_z above 256 is not supported");
+  }
 }
 
 template <typename T, int PREC>
@@ -688,12 +1071,13 @@ int check_args(const gnn_trimul_args& a, const char* who) {
     if (((uintptr_t)ptr) % 16 != 0)
       return set_error(GNN_ERR_ARG, "trimul: x, out, weights and workspace must be 16-byte aligned");
   const size_t e = a.dtype == GNN_F32 ? 4 : 2;
-  const size_t proj_lds = (size_t)PT * (a.C + 16 / e) * e + (2 * (size_t)a.C + PT) * 4 + 16 +
-                          4 * (size_t)(e == 2 ? proj_ebuf_elems<bf16>() : proj_ebuf_elems<float>()) * e;
+  if (e == 4 && (a.C > 256 || a.Ch > 256))
+    return set_error(GNN_ERR_UNSUPPORTED, "trimul: fp32 c_z and c_hidden above 256 are not supported");
+  const size_t proj_bytes = e == 2 ? proj_lds<bf16>(a.C).total : proj_lds<float>(a.C).total;
   const size_t out_lds = out_lds_bytes(a.Ch, e);
-  if (proj_lds > 160 * 1024 || out_lds > 160 * 1024)
+  if (proj_bytes > 160 * 1024 || out_lds > 160 * 1024)
     return set_error(GNN_ERR_UNSUPPORTED, "trimul: channel count too large for the LDS tiles");
-  if (a.B * a.N * ((a.N + PT - 1) / PT) >= ((int64_t)1 << 31))
+  if (a.B * a.N * ((a.N + PTO - 1) / PTO) >= ((int64_t)1 << 31))
     return set_error(GNN_ERR_UNSUPPORTED, "trimul: grid too large");
   const TrimulLayout L = trimul_layout(a.B, a.N, a.C, a.Ch, a.dtype);
   if (!a.workspace || a.workspace_bytes < L.total)
