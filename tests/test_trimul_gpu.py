@@ -125,8 +125,10 @@ def test_block_padded(direction, true_length):
 
 
 @DIRECTIONS
-@pytest.mark.parametrize("channels", [96, 128, 256])
+@pytest.mark.parametrize("channels", [64, 96, 128, 256, 320, 512])
 def test_channel_widths(direction, channels):
+    """64 and 128 take the fixed-width projection kernel, the others the general one (up to
+    8 x chunks per thread at 512)."""
     w = trimul_weights(channels, channels, torch.bfloat16, seed=17)
     x, mask = pair_input(1, 24, channels, torch.bfloat16, seed=18)
     assert_close_to_oracle("out", hip(x, direction, mask, w), oracle(x, direction, mask, w),
@@ -134,11 +136,34 @@ def test_channel_widths(direction, channels):
 
 
 @DIRECTIONS
-def test_hidden_differs_from_channels(direction):
-    w = trimul_weights(64, 32, torch.bfloat16, seed=19)
-    x, mask = pair_input(1, 24, 64, torch.bfloat16, seed=20)
+@pytest.mark.parametrize("c_z,c_hidden", [(64, 32), (128, 256), (128, 32), (256, 64), (32, 160)])
+def test_hidden_differs_from_channels(direction, c_z, c_hidden):
+    """c_hidden = 256 gives a wave two projection units (weights reloaded per tile); 32 leaves
+    waves idle."""
+    w = trimul_weights(c_z, c_hidden, torch.bfloat16, seed=19)
+    x, mask = pair_input(1, 24, c_z, torch.bfloat16, seed=20)
     assert_close_to_oracle("out", hip(x, direction, mask, w), oracle(x, direction, mask, w),
                            Tolerance(1 - 1e-4, 2e-2))
+
+
+@DIRECTIONS
+@pytest.mark.parametrize("channels", [64, 128])
+def test_fixed_width_fp16(direction, channels):
+    w = trimul_weights(channels, channels, torch.float16, seed=21, biases=True)
+    x, mask = pair_input(1, 40, channels, torch.float16, seed=22)
+    assert_close_to_oracle("out", hip(x, direction, mask, w), oracle(x, direction, mask, w),
+                           Tolerance(1 - 1e-4, 1e-2))
+
+
+@DIRECTIONS
+@pytest.mark.parametrize("precision", ["ieee", "tf32"])
+@pytest.mark.parametrize("channels", [128, 256])
+def test_fp32_channel_widths(direction, precision, channels):
+    w = trimul_weights(channels, channels, torch.float32, seed=23, biases=True)
+    x, mask = pair_input(1, 24, channels, torch.float32, seed=24)
+    with matmul_precision(precision):
+        got = hip(x, direction, mask, w)
+    assert_close_to_oracle("out", got, oracle(x, direction, mask, w), TRIMUL_TOL[torch.float32, precision])
 
 
 @DIRECTIONS
