@@ -338,10 +338,12 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_kernel(const gnn_trimul_ar
           const V8 val = load8(&ebuf[crow * ER + p0]);
           if (tl.c0 + pl + 8 <= N) {
             store8(drow, val);
-          } else {
+          } else if (tl.c0 + pl < NP) {  // row tail: pixels N .. NP-1 are written as zeros
+            V8 v = val;
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-              if (tl.c0 + pl + e < N) drow[e] = val[e];
+              if (tl.c0 + pl + e >= N) v[e] = TypeOps<T>::from_f32(0.f);
+            store8(drow, v);
           }
         }
         wave_lds_sync();
@@ -627,10 +629,12 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
         const V8 val = load8(&ebuf[crow * ER + p0]);
         if (tl.c0 + p0 + 8 <= N) {
           store8(drow, val);
-        } else {
+        } else if (tl.c0 + p0 < NP) {  // row tail: pixels N .. NP-1 are written as zeros
+          V8 v = val;
 #pragma unroll
           for (int e = 0; e < 8; ++e)
-            if (tl.c0 + p0 + e < N) drow[e] = val[e];
+            if (tl.c0 + p0 + e >= N) v[e] = TypeOps<T>::from_f32(0.f);
+          store8(drow, v);
         }
       }
       wave_lds_sync();
@@ -972,6 +976,150 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
   }
 }
 
+// ---- stage 2, 16-bit types: 128 x 256 tiles fed by a 3-stage global->LDS DMA pipeline ----
+// Workgroup tile: 128 rows of A (i) x 256 rows of B (j); wave (wm, wn) of the 2 x 2 grid owns
+// 64 i x 128 j as 2 x 4 accumulators of 32 x 32, computed as O^T blocks (rows = j) so a lane
+// holds 4 consecutive j of one i per register group. k advances in stages of 32 (64 bytes per
+// row): every wave issues global_load_lds_dwordx4 for its share of the stage two stages
+// ahead of the one it multiplies, so operands never pass through registers. Within a stage
+// row r keeps its four 16-byte chunks XOR-swizzled by (r / 4) % 4, which makes the fragment
+// reads (16 consecutive rows, one chunk each) hit 16 distinct bank groups. The K range runs
+// to NP = round_up(N, 32): the projection stage writes zeros into columns N .. NP-1 of a and b.
+// Rows past N are loaded from row N-1 (their outputs are never stored). The finished tile is
+// staged in LDS and written with 16-byte row stores.
+struct ContractDma {
+  static constexpr int BM = 128, BN = 256, BK = 32, STAGES = 3;
+  static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;  // 24 KB
+  static constexpr int SP = BN + 8;                       // epilogue row pitch (elements)
+  static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;  // 72 KB, also holds the 128 x SP tile
+  static_assert(BM * SP * 2 <= LDS_BYTES, "epilogue tile must fit the stage buffers");
+};
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <typename T>
+__global__ __launch_bounds__(NT, 2) void trimul_contract_dma_kernel(const T* __restrict__ A,
+                                                                    const T* __restrict__ Bm,
+                                                                    T* __restrict__ O, int N,
+                                                                    int64_t NP) {
+  static_assert(sizeof(T) == 2, "16-bit operands");
+  typedef typename TypeOps<T>::V8 V8;
+  typedef typename TypeOps<T>::V4 V4;
+  typedef ContractDma Cfg;
+  __shared__ __align__(16) unsigned char smem[Cfg::LDS_BYTES];
+
+  const int nti = (N + Cfg::BM - 1) / Cfg::BM;
+  const int ntj = (N + Cfg::BN - 1) / Cfg::BN;
+  const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
+  const int tj = w % ntj;
+  const int ti = (w / ntj) % nti;
+  const int64_t plane = w / ((uint32_t)ntj * nti);
+  const int64_t poff = plane * N * NP;
+  const T* Ap = A + poff;
+  const T* Bp = Bm + poff;
+  T* Op = O + poff;
+  const int i0 = ti * Cfg::BM, j0 = tj * Cfg::BN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // DMA source addresses of this lane: instruction q of a wave fills 16 rows x 64 bytes;
+  // lane -> (row lane / 4, physical chunk lane % 4) holding logical chunk p ^ ((row / 4) % 4).
+  const int drow = lane >> 2, dphys = lane & 3;
+  const T* asrc[2];
+  const T* bsrc[4];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int r = 32 * wave + 16 * q + drow;
+    const int c = dphys ^ ((r >> 2) & 3);
+    asrc[q] = Ap + (int64_t)min(i0 + r, N - 1) * NP + 8 * c;
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = 64 * wave + 16 * q + drow;
+    const int c = dphys ^ ((r >> 2) & 3);
+    bsrc[q] = Bp + (int64_t)min(j0 + r, N - 1) * NP + 8 * c;
+  }
+  auto issue = [&](int kt) {
+    unsigned char* st = smem + (kt % Cfg::STAGES) * Cfg::STAGE_BYTES;
+    const int k0 = kt * Cfg::BK;
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      __builtin_amdgcn_global_load_lds((const void*)(asrc[q] + k0),
+                                       (lds_void_t*)(st + (32 * wave + 16 * q) * 64), 16, 0, 0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      __builtin_amdgcn_global_load_lds((const void*)(bsrc[q] + k0),
+                                       (lds_void_t*)(st + Cfg::A_BYTES + (64 * wave + 16 * q) * 64), 16, 0,
+                                       0);
+  };
+  // fragment (row r, logical chunk c) of a stage operand
+  auto frag = [&](const unsigned char* base, int r, int c) -> V8 {
+    return *reinterpret_cast<const V8*>(base + r * 64 + ((c ^ ((r >> 2) & 3)) << 4));
+  };
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int y = 0; y < 4; ++y)
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[y][x][r] = 0.f;
+
+  const int nkt = (int)(NP / Cfg::BK);
+  issue(0);
+  if (nkt > 1) issue(1);
+  for (int kt = 0; kt < nkt; ++kt) {
+    // This wave's DMA of stage kt is its oldest outstanding one (6 instructions per stage)
+    // and its fragment reads of stage kt - 1 have returned; after the barrier every wave's
+    // stage kt has landed and stage (kt + 2) % 3 is no longer read. A plain s_barrier (with a
+    // compiler memory clobber) replaces __syncthreads, whose fence would also wait for the
+    // DMA of stage kt + 1.
+    if (kt + 1 < nkt)
+      __builtin_amdgcn_s_waitcnt(0x076);  // vmcnt(6) lgkmcnt(0)
+    else
+      __builtin_amdgcn_s_waitcnt(0x070);  // vmcnt(0) lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+    if (kt + 2 < nkt) issue(kt + 2);
+    const unsigned char* sa = smem + (kt % Cfg::STAGES) * Cfg::STAGE_BYTES;
+    const unsigned char* sb = sa + Cfg::A_BYTES;
+#pragma unroll
+    for (int kk = 0; kk < Cfg::BK / 16; ++kk) {
+      V8 af[2], bf[4];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) af[x] = frag(sa, 64 * wm + 32 * x + l32, 2 * kk + g);
+#pragma unroll
+      for (int y = 0; y < 4; ++y) bf[y] = frag(sb, 128 * wn + 32 * y + l32, 2 * kk + g);
+#pragma unroll
+      for (int y = 0; y < 4; ++y)
+#pragma unroll
+        for (int x = 0; x < 2; ++x) Mma<T, PREC_NATIVE>::step(acc[y][x], bf[y], af[x]);
+    }
+  }
+  __syncthreads();  // stage buffers become the output tile
+
+  // acc[y][x][r] = o[i = i0 + 64wm + 32x + l32][j = j0 + 128wn + 32y + 8(r/4) + 4g + r%4]
+  T* ot = reinterpret_cast<T*>(smem);
+#pragma unroll
+  for (int y = 0; y < 4; ++y)
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const f32x4 v = {acc[y][x][4 * rg], acc[y][x][4 * rg + 1], acc[y][x][4 * rg + 2], acc[y][x][4 * rg + 3]};
+        store4(&ot[(64 * wm + 32 * x + l32) * Cfg::SP + 128 * wn + 32 * y + 8 * rg + 4 * g],
+               TypeOps<T>::from_f32(v));
+      }
+  __syncthreads();
+  constexpr int CPR = Cfg::BN / 8;  // 16-byte chunks per output row
+#pragma unroll 4
+  for (int c = tid; c < Cfg::BM * CPR; c += NT) {
+    const int r = c / CPR, cj = (c % CPR) * 8;
+    if (i0 + r < N && j0 + cj < N) store8(Op + (int64_t)(i0 + r) * NP + j0 + cj, load8(&ot[r * Cfg::SP + cj]));
+  }
+}
+
 template <typename T>
 size_t out_smem(const gnn_trimul_args& a) {
   return out_lds_bytes(a.Ch, sizeof(T));
@@ -1032,6 +1180,15 @@ int launch_proj(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st)
 template <typename T, int PREC>
 int launch_contract(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
   const int64_t NP = round_up(a.N, 32);
+  unsigned char* wsp = (unsigned char*)a.workspace;
+  if constexpr (sizeof(T) == 2) {
+    typedef ContractDma D;
+    const int64_t nblk = a.B * a.Ch * ((a.N + D::BM - 1) / D::BM) * ((a.N + D::BN - 1) / D::BN);
+    hipLaunchKernelGGL((trimul_contract_dma_kernel<T>), dim3((uint32_t)nblk), dim3(NT), 0, st,
+                       (const T*)(wsp + L.off_a), (const T*)(wsp + L.off_b), (T*)(wsp + L.off_o), (int)a.N,
+                       NP);
+    return (int)hipGetLastError();
+  }
   typedef ContractCfg<T> Cfg;
   const int64_t nblk = a.B * a.Ch * ((a.N + Cfg::BM - 1) / Cfg::BM) * ((a.N + Cfg::BN - 1) / Cfg::BN);
   unsigned char* ws = (unsigned char*)a.workspace;
