@@ -15,8 +15,10 @@
 //   out      (stage 3)  LN_out over the Ch channels of each pixel (the channel-major o tile
 //                       is read down its columns in LDS), then out = (LN(o) Wpo^T + bpo) * g.
 //
-// Workspace (element type = input dtype): a, b, o are [B, Ch, N, NP] with a row pitch
-// NP = round_up(N, 32) so every row is 16-byte aligned; g is [B, N, N, C].
+// Workspace (element type = input dtype), NP = round_up(N, 32): o is [B, Ch, N, NP] (16-byte
+// aligned rows); g is [B, N, N, C]; a and b hold the same N x NP matrix per channel, k-blocked
+// as [B, Ch, NP / 32, N, 32] for 16-bit types (zeros in columns N .. NP-1) and row-major
+// [B, Ch, N, NP] for fp32.
 #include "gnn_common.hpp"
 #include "gnn_internal.hpp"
 
@@ -48,6 +50,18 @@ __device__ __forceinline__ float sigmoid_acc(float x) {
 template <typename T>
 __host__ __device__ constexpr int lds_pad() {
   return (int)(16 / sizeof(T));
+}
+
+// Element offset of (plane, row i, column k) in the a / b operands of the contraction
+// (plane = batch * Ch + channel, k < NP). 16-bit types: k-blocked [plane][NP / 32][N][32], so
+// that one 32-column pipeline stage of a block of rows is a single contiguous range;
+// fp32: row-major [plane][N][NP].
+template <typename T>
+__host__ __device__ inline int64_t ab_offset(int64_t plane, int row, int k, int N, int64_t NP) {
+  if constexpr (sizeof(T) == 2)
+    return ((plane * (NP / 32) + k / 32) * N + row) * 32 + (k % 32);
+  else
+    return (plane * N + row) * NP + k;
 }
 
 // Orders LDS accesses of the lanes of one wave (a wave executes its LDS operations in
@@ -334,7 +348,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_kernel(const gnn_trimul_ar
           T* dst = chg < Ch ? a_cm : b_cm;
           const int chh = chg < Ch ? chg : chg - Ch;
           const int pl = 32 * s0 + p0;
-          T* drow = dst + (((int64_t)tl.b * Ch + chh) * N + tl.row) * NP + tl.c0 + pl;
+          T* drow = dst + ab_offset<T>((int64_t)tl.b * Ch + chh, tl.row, tl.c0 + pl, N, NP);
           const V8 val = load8(&ebuf[crow * ER + p0]);
           if (tl.c0 + pl + 8 <= N) {
             store8(drow, val);
@@ -625,7 +639,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
         const int chg = 32 * u + crow;
         T* dst = chg < Ch ? a_cm : b_cm;
         const int chh = chg < Ch ? chg : chg - Ch;
-        T* drow = dst + (((int64_t)tl.b * Ch + chh) * N + tl.row) * NP + tl.c0 + p0;
+        T* drow = dst + ab_offset<T>((int64_t)tl.b * Ch + chh, tl.row, tl.c0 + p0, N, NP);
         const V8 val = load8(&ebuf[crow * ER + p0]);
         if (tl.c0 + p0 + 8 <= N) {
           store8(drow, val);
@@ -1016,10 +1030,11 @@ __global__ __launch_bounds__(NT, 2) void trimul_contract_dma_kernel(const T* __r
   const int ti = (w / ntj) % nti;
   const int64_t plane = w / ((uint32_t)ntj * nti);
   const int64_t poff = plane * N * NP;
-  const T* Ap = A + poff;
+  const T* Ap = A + poff;  // k-blocked operands: stage kt of row r at ((kt * N) + r) * 32
   const T* Bp = Bm + poff;
   T* Op = O + poff;
   const int i0 = ti * Cfg::BM, j0 = tj * Cfg::BN;
+  const int64_t stage_stride = (int64_t)N * Cfg::BK;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
   const int wm = wave >> 1, wn = wave & 1;
@@ -1033,17 +1048,17 @@ __global__ __launch_bounds__(NT, 2) void trimul_contract_dma_kernel(const T* __r
   for (int q = 0; q < 2; ++q) {
     const int r = 32 * wave + 16 * q + drow;
     const int c = dphys ^ ((r >> 2) & 3);
-    asrc[q] = Ap + (int64_t)min(i0 + r, N - 1) * NP + 8 * c;
+    asrc[q] = Ap + (int64_t)min(i0 + r, N - 1) * Cfg::BK + 8 * c;
   }
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int r = 64 * wave + 16 * q + drow;
     const int c = dphys ^ ((r >> 2) & 3);
-    bsrc[q] = Bp + (int64_t)min(j0 + r, N - 1) * NP + 8 * c;
+    bsrc[q] = Bp + (int64_t)min(j0 + r, N - 1) * Cfg::BK + 8 * c;
   }
   auto issue = [&](int kt) {
     unsigned char* st = smem + (kt % Cfg::STAGES) * Cfg::STAGE_BYTES;
-    const int k0 = kt * Cfg::BK;
+    const int64_t k0 = kt * stage_stride;
 #pragma unroll
     for (int q = 0; q < 2; ++q)
       __builtin_amdgcn_global_load_lds((const void*)(asrc[q] + k0),
@@ -1084,18 +1099,24 @@ __global__ __launch_bounds__(NT, 2) void trimul_contract_dma_kernel(const T* __r
     if (kt + 2 < nkt) issue(kt + 2);
     const unsigned char* sa = smem + (kt % Cfg::STAGES) * Cfg::STAGE_BYTES;
     const unsigned char* sb = sa + Cfg::A_BYTES;
+    // all fragment reads of the stage first, so their latency is exposed once per stage
+    constexpr int KS = Cfg::BK / 16;
+    V8 af[KS][2], bf[KS][4];
 #pragma unroll
-    for (int kk = 0; kk < Cfg::BK / 16; ++kk) {
-      V8 af[2], bf[4];
+    for (int kk = 0; kk < KS; ++kk) {
 #pragma unroll
-      for (int x = 0; x < 2; ++x) af[x] = frag(sa, 64 * wm + 32 * x + l32, 2 * kk + g);
+      for (int x = 0; x < 2; ++x) af[kk][x] = frag(sa, 64 * wm + 32 * x + l32, 2 * kk + g);
 #pragma unroll
-      for (int y = 0; y < 4; ++y) bf[y] = frag(sb, 128 * wn + 32 * y + l32, 2 * kk + g);
+      for (int y = 0; y < 4; ++y) bf[kk][y] = frag(sb, 128 * wn + 32 * y + l32, 2 * kk + g);
+    }
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
       for (int y = 0; y < 4; ++y)
 #pragma unroll
-        for (int x = 0; x < 2; ++x) Mma<T, PREC_NATIVE>::step(acc[y][x], bf[y], af[x]);
-    }
+        for (int x = 0; x < 2; ++x) Mma<T, PREC_NATIVE>::step(acc[y][x], bf[kk][y], af[kk][x]);
+    __builtin_amdgcn_sched_group_barrier(0x100, 6 * KS, 0);  // the LDS reads, in order
+    __builtin_amdgcn_sched_group_barrier(0x008, 8 * KS, 0);  // then the MFMAs
   }
   __syncthreads();  // stage buffers become the output tile
 

@@ -128,11 +128,13 @@ typedef struct gnn_trimul_args {
 
 /* Workspace size in bytes for one call (a, b, the output gate and o, each in the
  * input dtype), and the byte offsets of those four regions:
- *   off[0] a  channel-major [B, Ch, N, NP]  (incoming: stored transposed per channel)
- *   off[1] b  channel-major [B, Ch, N, NP]  (same)
+ *   off[0] a  channel-major, (i, k) of channel c (incoming: stored transposed per channel);
+ *             bf16 / fp16: k-blocked [B, Ch, NP/32, N, 32], columns N .. NP-1 zero;
+ *             fp32: row-major [B, Ch, N, NP]
+ *   off[1] b  the same for b
  *   off[2] g  pixel-major   [B, N, N, C]    sigmoid(z Wg_out^T + bg_out)
  *   off[3] o  channel-major [B, Ch, N, NP]  the contraction output
- * where NP = N rounded up to a multiple of 32 is the row pitch (columns >= N unused).
+ * where NP = N rounded up to a multiple of 32 (the row pitch; columns >= N of o unused).
  * No reference counterpart: the reference allocates its intermediates through torch
  * (trimul.py:253, :308). */
 size_t gnn_trimul_workspace_bytes(int64_t B, int64_t N, int64_t C, int64_t Ch, int32_t dtype,

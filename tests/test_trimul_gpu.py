@@ -66,7 +66,8 @@ def test_accuracy(direction, dtype, precision):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
 def test_stages_against_oracle(direction, dtype):
     """Each kernel's output region of the workspace against the oracle's intermediate:
-    a, b (channel-major, transposed per channel for 'incoming'), g and o."""
+    a, b (channel-major, transposed per channel for 'incoming'; k-blocked for 16-bit types,
+    zero in the row padding), g and o."""
     from geometric_nn_ops_torch.triangle._kernels import trimul as K
 
     B, N, C, Ch = 2, 40, 64, 32
@@ -88,8 +89,16 @@ def test_stages_against_oracle(direction, dtype):
 
     st = O.trimul_stages(to_np(x), direction, to_np(mask), **np_weights(w))
     tol = TRIMUL_TOL[dtype, "ieee"]
-    a_cm = region(0, (B, Ch, N, NP))[..., :N]
-    b_cm = region(1, (B, Ch, N, NP))[..., :N]
+    def operand(i):
+        if dtype == torch.float32:  # row-major [B, Ch, N, NP]
+            return region(i, (B, Ch, N, NP))
+        # 16-bit: k-blocked [B, Ch, NP / 32, N, 32]
+        return region(i, (B, Ch, NP // 32, N, 32)).permute(0, 1, 3, 2, 4).reshape(B, Ch, N, NP)
+
+    a_full, b_full = operand(0), operand(1)
+    if dtype != torch.float32:  # the contraction runs K to NP: columns N .. NP-1 must be zero
+        assert torch.count_nonzero(a_full[..., N:]) == 0 and torch.count_nonzero(b_full[..., N:]) == 0
+    a_cm, b_cm = a_full[..., :N], b_full[..., :N]
     o_cm = region(3, (B, Ch, N, NP))[..., :N]
     perm = (0, 2, 3, 1) if direction == "outgoing" else (0, 3, 2, 1)
     assert_close_to_oracle("a", a_cm.permute(*perm), st["a"], tol)
