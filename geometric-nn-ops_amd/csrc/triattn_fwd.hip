@@ -122,16 +122,26 @@ template <> struct BiasFrag<float> {
   f32x4 f[2][4];
 };
 
+// brow is the bias row of the lane's query (row 0 for queries past N, whose results are
+// never stored). Keys of a tile that reaches past N are zero-filled; inside the row pitch
+// either way (the host pads it to a multiple of 8).
 template <typename T>
 __device__ __forceinline__ void load_bias(BiasFrag<T>& bf, const T* brow, bool qok, int kbase, int N,
                                           int g) {
-  // keys up to the next multiple of 8 stay inside the bias row pitch (host guarantees it)
+  (void)qok;
+  if (kbase + KT <= N) {
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) bf.f[sub][t] = load8(brow + kbase + sub * 32 + 16 * t + 8 * g);
+    return;
+  }
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int key = kbase + sub * 32 + 16 * t + 8 * g;
-      bf.f[sub][t] = (qok && key < N) ? load8(brow + key) : zero8<T>();
+      bf.f[sub][t] = key < N ? load8(brow + key) : zero8<T>();
     }
 }
 template <>
@@ -266,6 +276,7 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
   constexpr int CH = KT * CPK / NTHREADS;
   V8 kreg[R][CH], vreg[R][CH];
   auto load_kv = [&](int t) {
+    const bool full = t * KT + KT <= N && DP == D;  // no key past N, no padded head dim
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -273,7 +284,10 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
         const int c = tid + i * NTHREADS;
         const int key = t * KT + c / CPK;
         const int d0 = (c % CPK) * 8;
-        if (key < N && d0 < D && s0 + r < a.S) {
+        if (full && (R == 1 || s0 + r < a.S)) {
+          kreg[r][i] = load8(kp[r] + key * ksn + d0);
+          vreg[r][i] = load8(vp[r] + key * vsn + d0);
+        } else if (key < N && d0 < D && s0 + r < a.S) {
           kreg[r][i] = load8(kp[r] + key * ksn + d0);
           vreg[r][i] = load8(vp[r] + key * vsn + d0);
         } else {
@@ -303,23 +317,28 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
   for (int r = 0; r < R; ++r) state[r] = sm.row_dead[r];
   const float mval = a.mask_value;
 
-  BiasFrag<T> bcur, bnext;
+  BiasFrag<T> bias0, bias1;
   if (nrun > 0) {
     const int t0 = sm.tile_list[0];
     load_kv(t0);
-    if constexpr (HAS_BIAS) load_bias<T>(bcur, brow, qok, t0 * KT, N, g);
+    if constexpr (HAS_BIAS) load_bias<T>(bias0, brow, qok, t0 * KT, N, g);
     store_kv(0);
   }
   __syncthreads();
 
+  // lane l ^ 32 for the pair maximum, as a ds_bpermute byte index (loop invariant)
+  const int xlane = (lane ^ 32) << 2;
+
   for (int it = 0; it < nrun; ++it) {
+    BiasFrag<T>& bc = bias0;
+    BiasFrag<T>& bn = bias1;
     const int cur = S::NBUF == 2 ? (it & 1) : 0;
     const int t = sm.tile_list[it];
     const bool has_next = it + 1 < nrun;
     if (has_next) {
       const int tn = sm.tile_list[it + 1];
       load_kv(tn);
-      if constexpr (HAS_BIAS) load_bias<T>(bnext, brow, qok, tn * KT, N, g);
+      if constexpr (HAS_BIAS) load_bias<T>(bn, brow, qok, tn * KT, N, g);
     }
 
 #pragma unroll
@@ -345,14 +364,14 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
 #pragma unroll
           for (int t2 = 0; t2 < 2; ++t2)
 #pragma unroll
-            for (int sub = 0; sub < 2; ++sub) Mma<T, PREC>::step(sc[sub], idf[t2], bcur.f[sub][t2]);
+            for (int sub = 0; sub < 2; ++sub) Mma<T, PREC>::step(sc[sub], idf[t2], bc.f[sub][t2]);
         } else {
 #pragma unroll
           for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg)
 #pragma unroll
-              for (int e = 0; e < 4; ++e) sc[sub][4 * rg + e] += TypeOps<T>::to_f32(bcur.f[sub][rg][e]);
+              for (int e = 0; e < 4; ++e) sc[sub][4 * rg + e] += TypeOps<T>::to_f32(bc.f[sub][rg][e]);
         }
       }
       if (live != ~0ull) {
@@ -380,7 +399,8 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
         m0 = fmaxf(m0, sc[0][i]);
         m1 = fmaxf(m1, sc[1][i]);
       }
-      const float mt = pair_max(fmaxf(m0, m1));
+      const float mh = fmaxf(m0, m1);
+      const float mt = fmaxf(mh, __int_as_float(__builtin_amdgcn_ds_bpermute(xlane, __float_as_int(mh))));
       if (__any(mt > m[r] + RESCALE_THRESHOLD)) {
         const float mnew = fmaxf(m[r], mt);
         const float alpha = fast_exp2((m[r] - mnew) * LOG2E);  // 0 on the first tile (m = -inf)
@@ -433,7 +453,7 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
           }
     }
 
-    if constexpr (HAS_BIAS) bcur = bnext;
+    if constexpr (HAS_BIAS) bias0 = bias1;
     if constexpr (S::NBUF == 2) {
       // the other stage was last read in the previous iteration, before its barrier
       if (has_next) store_kv(cur ^ 1);
