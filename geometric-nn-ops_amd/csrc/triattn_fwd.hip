@@ -75,12 +75,16 @@ constexpr int R = GNN_ATTN_ROWS;     // N_seq rows per workgroup (sharing the bi
 template <typename T, int DP>
 struct Smem {
   static constexpr int KPAD = (sizeof(T) == 2) ? 8 : 4;  // 16 B per row
-  static constexpr int VPAD = 4;
   static constexpr int KROW = DP + KPAD;
-  static constexpr int VROW = KT + VPAD;
+  // 16-bit types keep V as [key][d] and read V^T fragments with ds_read_b64_tr_b16: a row
+  // pitch of 64 B modulo 256 B puts the four 64-byte row windows of one read pass on
+  // disjoint banks. fp32 stores V^T [d][key].
+  static constexpr bool VTR = sizeof(T) == 2;
+  static constexpr int VROW = VTR ? (DP == 32 ? 32 : DP + 32) : KT + 4;
+  static constexpr int VSIZE = VTR ? KT * VROW : DP * VROW;
   static constexpr int NBUF = GNN_ATTN_NBUF;
   T k[NBUF][R][KT * KROW];
-  T vt[NBUF][R][DP * VROW];
+  T vt[NBUF][R][VSIZE];
   uint64_t tile_live[R][MAX_TILES];  // bit j: key tile*64+j is < N and unmasked in row r
   uint16_t tile_list[MAX_TILES];     // tiles with a live key in some row (all if a row is dead)
   int ntiles_run;
@@ -92,6 +96,17 @@ __device__ __forceinline__ typename TypeOps<T>::V8 frag_from_acc(const f32x16& p
   f32x8 x = {p[8 * t + 0], p[8 * t + 1], p[8 * t + 2], p[8 * t + 3],
              p[8 * t + 4], p[8 * t + 5], p[8 * t + 6], p[8 * t + 7]};
   return TypeOps<T>::from_f32(x);
+}
+
+// ds_read_b64_tr_b16 (gfx950): within each group of 16 lanes, lane r supplies the address
+// of 4 consecutive 16-bit elements (row r of a 16 x 4 block) and lane i receives element
+// i % 4 of rows i / 4, 4 + i / 4, 8 + i / 4 and 12 + i / 4.
+template <typename T>
+__device__ __forceinline__ typename TypeOps<T>::V4 tr_read4(const T* p) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(__attribute__((address_space(3))) const T*)p);
+  return __builtin_bit_cast(typename TypeOps<T>::V4, v);
 }
 
 // Adds the 8 probabilities of a fragment (as rounded for the MFMA, so the normaliser
@@ -305,10 +320,21 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
         const int kl = c / CPK;
         const int d0 = (c % CPK) * 8;
         store8(&sm.k[buf][r][kl * S::KROW + d0], kreg[r][i]);
+        if constexpr (S::VTR) {
+          store8(&sm.vt[buf][r][kl * S::VROW + d0], vreg[r][i]);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sm.vt[buf][r][(d0 + e) * S::VROW + kl] = vreg[r][i][e];
+          for (int e = 0; e < 8; ++e) sm.vt[buf][r][(d0 + e) * S::VROW + kl] = vreg[r][i][e];
+        }
       }
   };
+  // V^T A fragment (16-bit types) of k-step kk of sub-tile sub, head-dim block cc: lane l
+  // gets d = 32cc + l % 32 and keys sub*32 + 16kk + 8h + 4g + e (element 4h + e). Each
+  // ds_read_b64_tr_b16 hands the 16 lanes of a group a 16 (d) x 4 (key) block: lane r of the
+  // group addresses key kb + r / 4, d 16 * ((l / 16) % 2) + 4 * (r % 4) .. + 3, and receives
+  // the 4 keys of column d = l % 16 of that block.
+  const int tr_r = lane & 15;
+  const int tr_off = (tr_r >> 2) * S::VROW + 16 * ((lane >> 4) & 1) + 4 * (tr_r & 3);
 
   __syncthreads();
   const int nrun = sm.ntiles_run;
@@ -440,9 +466,16 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
         for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
           for (int kk = 0; kk < 2; ++kk) {
-            const T* vrow = &vs[(32 * cc + l32) * S::VROW + sub * 32 + 16 * kk + 4 * g];
-            const V4 lo = load4(vrow);
-            const V4 hi = load4(vrow + 8);
+            V4 lo, hi;
+            if constexpr (S::VTR) {
+              const T* vb = &vs[(sub * 32 + 16 * kk + 4 * g) * S::VROW + 32 * cc + tr_off];
+              lo = tr_read4<T>(vb);
+              hi = tr_read4<T>(vb + 8 * S::VROW);
+            } else {
+              const T* vrow = &vs[(32 * cc + l32) * S::VROW + sub * 32 + 16 * kk + 4 * g];
+              lo = load4(vrow);
+              hi = load4(vrow + 8);
+            }
             V8 vf;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
