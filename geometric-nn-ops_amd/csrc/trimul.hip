@@ -885,6 +885,18 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
 
   V8 gr[OCH];
   out_load_g<T>(gr, gblk, C, 0, (C < OPC ? C : OPC) / 8, npix, tid);
+  // p_out fragments of this wave's first 32-channel tile, first KPF k-steps, loaded now so
+  // their latency overlaps the o tile load and the LayerNorm
+  constexpr int KPF = sizeof(T) == 2 ? 8 : 4;
+  const T* __restrict__ wpo = (const T*)a.p_out_w;
+  const int nk = Ch / 16;
+  V8 wpf[KPF];
+  if (32 * wave < C) {
+    const T* wrow0 = wpo + (int64_t)(32 * wave + l32) * Ch + 8 * g;
+#pragma unroll
+    for (int k = 0; k < KPF; ++k)
+      if (k < nk) wpf[k] = load8(wrow0 + 16 * k);
+  }
 
   for (int c = tid; c < Ch; c += NT) {
     lnw[c] = ld_or<T>(a.ln_out_w, c, 1.f);
@@ -906,41 +918,61 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
   }
   __syncthreads();
 
-  // ---- LayerNorm over channels. Thread = (pixel tid % 64, channel quarter tid / 64): the
-  // lanes of a wave read 64 consecutive pixels of one channel row (conflict-free); the
-  // quarters' partial sums meet in LDS.
+  // ---- LayerNorm over channels. Thread = (pixel pair pp = tid % 32, channel part
+  // tid / 32 of Ch / 8 channels): 32-bit LDS reads of two neighbouring pixels, the lanes of a
+  // wave covering 64 consecutive pixels of one channel row; the parts' partial sums meet in
+  // LDS. Two passes (mean, then squared deviations), as F.layer_norm.
   {
-    const int pl = tid & (PTO - 1), qtr = tid / PTO;
-    const int k0 = qtr * (Ch / 4), k1 = k0 + Ch / 4;
-    float sum = 0.f;
-    for (int k = k0; k < k1; ++k) sum += TypeOps<T>::to_f32(ot[k * OR + pl]);
-    red[qtr * PTO + pl] = sum;
+    const int pp = tid & 31, part = tid >> 5;
+    const int kc = Ch / 8, k0 = part * kc;
+    typedef T T2 __attribute__((ext_vector_type(2)));
+    auto pair = [&](int k) -> f32x2 {
+      return __builtin_convertvector(*reinterpret_cast<const T2*>(&ot[k * OR + 2 * pp]), f32x2);
+    };
+    float2* red2 = reinterpret_cast<float2*>(red);  // [8 parts][32 pairs]
+    f32x2 s2 = {0.f, 0.f};
+    for (int k = k0; k < k0 + kc; ++k) s2 += pair(k);
+    red2[part * 32 + pp] = make_float2(s2[0], s2[1]);
     __syncthreads();
-    const float mean = ((red[pl] + red[PTO + pl]) + (red[2 * PTO + pl] + red[3 * PTO + pl])) / (float)Ch;
-    float sq = 0.f;
-    for (int k = k0; k < k1; ++k) {
-      const float d = TypeOps<T>::to_f32(ot[k * OR + pl]) - mean;
-      sq += d * d;
-    }
-    float* red2 = red + 4 * PTO;
-    red2[qtr * PTO + pl] = sq;
-    __syncthreads();
-    const float var = ((red2[pl] + red2[PTO + pl]) + (red2[2 * PTO + pl] + red2[3 * PTO + pl])) / (float)Ch;
-    const float rstd = 1.0f / sqrtf(var + a.eps);
-    for (int k = k0; k < k1; k += 8) {
-      f32x8 v;
+    f32x2 mean = {0.f, 0.f};
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        v[e] = (TypeOps<T>::to_f32(ot[(k + e) * OR + pl]) - mean) * rstd * lnw[k + e] + lnb[k + e];
-      store8(&zs[pl * ZR + k], TypeOps<T>::from_f32(v));
+    for (int j = 0; j < 8; ++j) {
+      const float2 v = red2[j * 32 + pp];
+      mean += f32x2{v.x, v.y};
+    }
+    mean *= 1.0f / (float)Ch;
+    f32x2 q2 = {0.f, 0.f};
+    for (int k = k0; k < k0 + kc; ++k) {
+      const f32x2 d = pair(k) - mean;
+      q2 += d * d;
+    }
+    __syncthreads();  // every part has read the sums
+    red2[part * 32 + pp] = make_float2(q2[0], q2[1]);
+    __syncthreads();
+    f32x2 var = {0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float2 v = red2[j * 32 + pp];
+      var += f32x2{v.x, v.y};
+    }
+    const float rs0 = 1.0f / sqrtf(var[0] * (1.0f / (float)Ch) + a.eps);
+    const float rs1 = 1.0f / sqrtf(var[1] * (1.0f / (float)Ch) + a.eps);
+    for (int k = k0; k < k0 + kc; k += 8) {
+      f32x8 v0, v1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const f32x2 x = pair(k + e);
+        v0[e] = (x[0] - mean[0]) * rs0 * lnw[k + e] + lnb[k + e];
+        v1[e] = (x[1] - mean[1]) * rs1 * lnw[k + e] + lnb[k + e];
+      }
+      store8(&zs[(2 * pp) * ZR + k], TypeOps<T>::from_f32(v0));
+      store8(&zs[(2 * pp + 1) * ZR + k], TypeOps<T>::from_f32(v1));
     }
   }
   __syncthreads();
 
   // ---- out = (z Wpo^T + bpo) * g, in passes of OPC output channels.
   // acc[s] = [cout][pixel]: cout = c0 + 32 wave + 8(r/4) + 4g + r%4, pixel = 32s + l32.
-  const T* __restrict__ wpo = (const T*)a.p_out_w;
-  const int nk = Ch / 16;
   for (int c0 = 0; c0 < C; c0 += OPC) {
     const int W = C - c0 < OPC ? C - c0 : OPC;
     if (32 * wave < W) {
@@ -954,7 +986,18 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
       for (int s = 0; s < PTO / 32; ++s)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[s][r] = 0.f;
-      for (int k = 0; k < nk; ++k) {
+      if (c0 == 0) {
+#pragma unroll
+        for (int k = 0; k < KPF; ++k) {
+          if (k >= nk) break;
+#pragma unroll
+          for (int s = 0; s < PTO / 32; ++s) {
+            const V8 zf = load8(&zs[(32 * s + l32) * ZR + 16 * k + 8 * g]);
+            Mma<T, PREC>::step(acc[s], wpf[k], zf);
+          }
+        }
+      }
+      for (int k = c0 == 0 ? KPF : 0; k < nk; ++k) {
         const V8 wf = load8(wrow + 16 * k);
 #pragma unroll
         for (int s = 0; s < PTO / 32; ++s) {
