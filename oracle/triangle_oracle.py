@@ -166,6 +166,40 @@ def trimul(x, direction="outgoing", mask=None, *, eps=1e-5, dtype=np.float64, **
     return trimul_stages(x, direction, mask, eps=eps, dtype=dtype, **w)["out"]
 
 
+def trimul_grid(x, direction="outgoing", mask=None, rows=(0,), cols=(0,), *, eps=1e-5,
+                dtype=np.float64, **w) -> np.ndarray:
+    """``trimul(...)[..., rows, :, :][..., :, cols, :]`` computed from the rows / columns of
+    x those pixels depend on, for checking sizes where the full N^3 product is too slow on
+    the CPU. Same math as trimul_stages (_reference/trimul.py:57-97): out[i, j] needs
+    a[i, k] and b[j, k] for all k ('outgoing', rows i and j of the pair grid) or a[k, i] and
+    b[k, j] ('incoming', columns), plus the gate of pixel (i, j) itself."""
+    outgoing = is_outgoing(direction)
+    x = np.asarray(x, dtype=dtype)
+    rows, cols = list(rows), list(cols)
+    c_hidden = np.asarray(w["p_in_weight"]).shape[0] // 2
+    m = None if mask is None else np.broadcast_to(np.asarray(mask, dtype=dtype), x.shape[:-1])
+
+    def gated(sel_x, sel_m):
+        z = layer_norm(sel_x, w.get("norm_in_weight"), w.get("norm_in_bias"), eps, dtype=dtype)
+        p = linear(z, w["p_in_weight"], w.get("p_in_bias"), dtype=dtype) * sigmoid(
+            linear(z, w["g_in_weight"], w.get("g_in_bias"), dtype=dtype))
+        return p if sel_m is None else p * sel_m[..., None]
+
+    if outgoing:  # [..., R, N, 2Ch] from rows, contract over the column index k
+        pr = gated(x[..., rows, :, :], None if m is None else m[..., rows, :])
+        pc = gated(x[..., cols, :, :], None if m is None else m[..., cols, :])
+        o = np.einsum("...ikc,...jkc->...ijc", pr[..., :c_hidden], pc[..., c_hidden:])
+    else:  # [..., N, R, 2Ch] from columns, contract over the row index k
+        pr = gated(x[..., :, rows, :], None if m is None else m[..., :, rows])
+        pc = gated(x[..., :, cols, :], None if m is None else m[..., :, cols])
+        o = np.einsum("...kic,...kjc->...ijc", pr[..., :c_hidden], pc[..., c_hidden:])
+    on = layer_norm(o, w.get("norm_out_weight"), w.get("norm_out_bias"), eps, dtype=dtype)
+    xg = x[..., rows, :, :][..., :, cols, :]
+    zg = layer_norm(xg, w.get("norm_in_weight"), w.get("norm_in_bias"), eps, dtype=dtype)
+    g = sigmoid(linear(zg, w["g_out_weight"], w.get("g_out_bias"), dtype=dtype))
+    return linear(on, w["p_out_weight"], w.get("p_out_bias"), dtype=dtype) * g
+
+
 # ------------------------------------------------------------------------- metrics
 def rel_fro(a, b) -> float:
     """``||a - b|| / ||b||`` in fp64; ``b`` is the reference (testutil/metrics.py:40-47)."""

@@ -257,6 +257,20 @@ def test_trimul_stages_are_consistent():
     np.testing.assert_allclose(st["out"], O.linear(st["on"], w["p_out_weight"]) * st["g"])
 
 
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_trimul_grid_is_the_full_oracle_sampled(direction):
+    """The sampled-pixel oracle used at large N equals the full oracle at those pixels
+    (rows and columns repeated and unsorted on purpose; batched; masked; with biases)."""
+    r = RNG(29)
+    w = _weights(r, 8, 4, biases=True)
+    x = r.standard_normal((2, 7, 7, 8))
+    mask = (r.random((2, 7, 7)) < 0.7).astype(float)
+    rows, cols = [5, 0, 5, 3], [6, 2, 0]
+    full = O.trimul(x, direction, mask, **w)
+    grid = O.trimul_grid(x, direction, mask, rows, cols, **w)
+    np.testing.assert_allclose(grid, full[:, rows][:, :, cols], rtol=1e-12, atol=1e-12)
+
+
 # --------------------------------------------- oracle vs the product's torch fallback (fp64)
 def test_oracle_agrees_with_torch_fallback():
     """Two independent restatements (numpy loops-free oracle here, torch einsum in the
