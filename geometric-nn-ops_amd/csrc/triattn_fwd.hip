@@ -290,21 +290,51 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
   constexpr int CPK = DP / 8;
   constexpr int CH = KT * CPK / NTHREADS;
   V8 kreg[R][CH], vreg[R][CH];
+  // chunk i of this thread: key kl[i] of the tile, head-dim columns dc[i] .. + 7; the
+  // per-lane address parts are loop invariant
+  int kl[CH], dc[CH];
+  int64_t koff[CH], voff[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int c = tid + i * NTHREADS;
+    kl[i] = c / CPK;
+    dc[i] = (c % CPK) * 8;
+    koff[i] = (int64_t)kl[i] * ksn + dc[i];
+    voff[i] = (int64_t)kl[i] * vsn + dc[i];
+  }
   auto load_kv = [&](int t) {
-    const bool full = t * KT + KT <= N && DP == D;  // no key past N, no padded head dim
+    if (DP == D && (R == 1 || s0 + R <= a.S)) {
+      if (t * KT + KT <= N) {  // full tile: tile base (uniform) + lane part
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const T* kt = kp[r] + (int64_t)t * KT * ksn;
+          const T* vt = vp[r] + (int64_t)t * KT * vsn;
+#pragma unroll
+          for (int i = 0; i < CH; ++i) {
+            kreg[r][i] = load8(kt + koff[i]);
+            vreg[r][i] = load8(vt + voff[i]);
+          }
+        }
+      } else {  // keys past N read row N-1: finite data whose scores become -inf, p = 0
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int i = 0; i < CH; ++i) {
+            const int key = min(t * KT + kl[i], N - 1);
+            kreg[r][i] = load8(kp[r] + (int64_t)key * ksn + dc[i]);
+            vreg[r][i] = load8(vp[r] + (int64_t)key * vsn + dc[i]);
+          }
+      }
+      return;
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int i = 0; i < CH; ++i) {
-        const int c = tid + i * NTHREADS;
-        const int key = t * KT + c / CPK;
-        const int d0 = (c % CPK) * 8;
-        if (full && (R == 1 || s0 + r < a.S)) {
-          kreg[r][i] = load8(kp[r] + key * ksn + d0);
-          vreg[r][i] = load8(vp[r] + key * vsn + d0);
-        } else if (key < N && d0 < D && s0 + r < a.S) {
-          kreg[r][i] = load8(kp[r] + key * ksn + d0);
-          vreg[r][i] = load8(vp[r] + key * vsn + d0);
+        const int key = t * KT + kl[i];
+        if (key < N && dc[i] < D && s0 + r < a.S) {
+          kreg[r][i] = load8(kp[r] + (int64_t)key * ksn + dc[i]);
+          vreg[r][i] = load8(vp[r] + (int64_t)key * vsn + dc[i]);
         } else {
           kreg[r][i] = zero8<T>();
           vreg[r][i] = zero8<T>();
@@ -343,7 +373,7 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
   for (int r = 0; r < R; ++r) state[r] = sm.row_dead[r];
   const float mval = a.mask_value;
 
-  BiasFrag<T> bias0, bias1;
+  BiasFrag<T> bias0;  // this tile's fragments; refilled with the next tile's once used
   if (nrun > 0) {
     const int t0 = sm.tile_list[0];
     load_kv(t0);
@@ -357,15 +387,12 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
 
   for (int it = 0; it < nrun; ++it) {
     BiasFrag<T>& bc = bias0;
-    BiasFrag<T>& bn = bias1;
     const int cur = S::NBUF == 2 ? (it & 1) : 0;
     const int t = sm.tile_list[it];
     const bool has_next = it + 1 < nrun;
-    if (has_next) {
-      const int tn = sm.tile_list[it + 1];
-      load_kv(tn);
-      if constexpr (HAS_BIAS) load_bias<T>(bn, brow, qok, tn * KT, N, g);
-    }
+    const int tn = has_next ? sm.tile_list[it + 1] : t;
+    if (has_next) load_kv(tn);
+    bool bias_next = false;  // bc already holds the next tile's bias
 
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -398,6 +425,10 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
             for (int rg = 0; rg < 4; ++rg)
 #pragma unroll
               for (int e = 0; e < 4; ++e) sc[sub][4 * rg + e] += TypeOps<T>::to_f32(bc.f[sub][rg][e]);
+        }
+        if (R == 1 && has_next) {  // the next tile's fragments, as early as possible
+          load_bias<T>(bc, brow, qok, tn * KT, N, g);
+          bias_next = true;
         }
       }
       if (live != ~0ull) {
@@ -486,7 +517,7 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
           }
     }
 
-    if constexpr (HAS_BIAS) bias0 = bias1;
+    if (HAS_BIAS && has_next && !bias_next) load_bias<T>(bc, brow, qok, tn * KT, N, g);
     if constexpr (S::NBUF == 2) {
       // the other stage was last read in the previous iteration, before its barrier
       if (has_next) store_kv(cur ^ 1);

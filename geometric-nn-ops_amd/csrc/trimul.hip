@@ -1033,40 +1033,54 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
   }
 }
 
-// ---- stage 2, 16-bit types: 128 x 256 tiles fed by a 3-stage global->LDS DMA pipeline ----
-// Workgroup tile: 128 rows of A (i) x 256 rows of B (j); wave (wm, wn) of the 2 x 2 grid owns
-// 64 i x 128 j as 2 x 4 accumulators of 32 x 32, computed as O^T blocks (rows = j) so a lane
-// holds 4 consecutive j of one i per register group. k advances in stages of 32 (64 bytes per
-// row): every wave issues global_load_lds_dwordx4 for its share of the stage two stages
-// ahead of the one it multiplies, so operands never pass through registers. Within a stage
-// row r keeps its four 16-byte chunks XOR-swizzled by (r / 4) % 4, which makes the fragment
-// reads (16 consecutive rows, one chunk each) hit 16 distinct bank groups. The K range runs
-// to NP = round_up(N, 32): the projection stage writes zeros into columns N .. NP-1 of a and b.
-// Rows past N are loaded from row N-1 (their outputs are never stored). The finished tile is
-// staged in LDS and written with 16-byte row stores.
+// ---- stage 2, 16-bit types: BM x 256 tiles fed by a global->LDS DMA pipeline -------------
+// Workgroup tile: BM rows of A (i) x 256 rows of B (j), BM = 128 (4 waves, 3 stages) or 256
+// (8 waves, 4 stages); wave (wm, wn) of the (BM / 64) x 2 grid owns 64 i x 128 j as 2 x 4
+// accumulators of 32 x 32, computed as O^T blocks (rows = j) so a lane holds 4 consecutive j
+// of one i per register group. k advances in stages of 32 (64 bytes per row): every wave
+// issues global_load_lds_dwordx4 for its share of a stage STAGES - 1 stages ahead of the one
+// it multiplies, so operands never pass through registers. Within a stage row r keeps its
+// four 16-byte chunks XOR-swizzled by (r / 4) % 4, which makes the fragment reads (16
+// consecutive rows, one chunk each) hit 16 distinct bank groups. The K range runs to NP =
+// round_up(N, 32): the projection stage writes zeros into columns N .. NP-1 of a and b. Rows
+// past N are loaded from row N-1 (their outputs are never stored). The finished tile is
+// staged in LDS, 128 rows at a time, and written with 16-byte row stores. The larger tile
+// halves the L2 -> LDS bytes per flop, which bound the 128-row tile.
+template <int BM>
 struct ContractDma {
-  static constexpr int BM = 128, BN = 256, BK = 32, STAGES = 3;
+  static constexpr int BN = 256, BK = 32;
+  static constexpr int NW = BM / 32;                      // waves
+  static constexpr int NTH = 64 * NW;                     // threads
+  static constexpr int STAGES = BM == 256 ? 4 : 3;
   static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
-  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;  // 24 KB
-  static constexpr int SP = BN + 8;                       // epilogue row pitch (elements)
-  static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;  // 72 KB, also holds the 128 x SP tile
-  static_assert(BM * SP * 2 <= LDS_BYTES, "epilogue tile must fit the stage buffers");
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int QA = BM / 16 / NW, QB = BN / 16 / NW;  // DMA instructions per wave
+  static constexpr int QPS = QA + QB;                          // ... per stage
+  static constexpr int SP = BN + 8;                            // epilogue row pitch (elements)
+  static constexpr int EROWS = 128;                            // epilogue rows per pass
+  static constexpr int LDS_BYTES = STAGES * STAGE_BYTES;
+  static_assert(EROWS * SP * 2 <= LDS_BYTES, "epilogue pass must fit the stage buffers");
+  static_assert(QA * 16 * NW == BM && QB * 16 * NW == BN, "DMA split");
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-template <typename T>
-__global__ __launch_bounds__(NT, 2) void trimul_contract_dma_kernel(const T* __restrict__ A,
-                                                                    const T* __restrict__ Bm,
-                                                                    T* __restrict__ O, int N,
-                                                                    int64_t NP) {
+template <int N_>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N_ >= 0 && N_ < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x070 | N_);  // vmcnt(N_) expcnt(7) lgkmcnt(0)
+}
+
+template <typename T, int BM>
+__global__ __launch_bounds__(ContractDma<BM>::NTH, BM == 256 ? 1 : 2) void trimul_contract_dma_kernel(
+    const T* __restrict__ A, const T* __restrict__ Bm, T* __restrict__ O, int N, int64_t NP) {
   static_assert(sizeof(T) == 2, "16-bit operands");
   typedef typename TypeOps<T>::V8 V8;
-  typedef typename TypeOps<T>::V4 V4;
-  typedef ContractDma Cfg;
+  typedef ContractDma<BM> Cfg;
+  constexpr int NTH = Cfg::NTH;
   __shared__ __align__(16) unsigned char smem[Cfg::LDS_BYTES];
 
-  const int nti = (N + Cfg::BM - 1) / Cfg::BM;
+  const int nti = (N + BM - 1) / BM;
   const int ntj = (N + Cfg::BN - 1) / Cfg::BN;
   const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
   const int tj = w % ntj;
@@ -1076,7 +1090,7 @@ __global__ __launch_bounds__(NT, 2) void trimul_contract_dma_kernel(const T* __r
   const T* Ap = A + poff;  // k-blocked operands: stage kt of row r at ((kt * N) + r) * 32
   const T* Bp = Bm + poff;
   T* Op = O + poff;
-  const int i0 = ti * Cfg::BM, j0 = tj * Cfg::BN;
+  const int i0 = ti * BM, j0 = tj * Cfg::BN;
   const int64_t stage_stride = (int64_t)N * Cfg::BK;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
@@ -1085,17 +1099,17 @@ __global__ __launch_bounds__(NT, 2) void trimul_contract_dma_kernel(const T* __r
   // DMA source addresses of this lane: instruction q of a wave fills 16 rows x 64 bytes;
   // lane -> (row lane / 4, physical chunk lane % 4) holding logical chunk p ^ ((row / 4) % 4).
   const int drow = lane >> 2, dphys = lane & 3;
-  const T* asrc[2];
-  const T* bsrc[4];
+  const T* asrc[Cfg::QA];
+  const T* bsrc[Cfg::QB];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int r = 32 * wave + 16 * q + drow;
+  for (int q = 0; q < Cfg::QA; ++q) {
+    const int r = 16 * Cfg::QA * wave + 16 * q + drow;
     const int c = dphys ^ ((r >> 2) & 3);
     asrc[q] = Ap + (int64_t)min(i0 + r, N - 1) * Cfg::BK + 8 * c;
   }
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int r = 64 * wave + 16 * q + drow;
+  for (int q = 0; q < Cfg::QB; ++q) {
+    const int r = 16 * Cfg::QB * wave + 16 * q + drow;
     const int c = dphys ^ ((r >> 2) & 3);
     bsrc[q] = Bp + (int64_t)min(j0 + r, N - 1) * Cfg::BK + 8 * c;
   }
@@ -1103,14 +1117,14 @@ __global__ __launch_bounds__(NT, 2) void trimul_contract_dma_kernel(const T* __r
     unsigned char* st = smem + (kt % Cfg::STAGES) * Cfg::STAGE_BYTES;
     const int64_t k0 = kt * stage_stride;
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
+    for (int q = 0; q < Cfg::QA; ++q)
       __builtin_amdgcn_global_load_lds((const void*)(asrc[q] + k0),
-                                       (lds_void_t*)(st + (32 * wave + 16 * q) * 64), 16, 0, 0);
+                                       (lds_void_t*)(st + (16 * Cfg::QA * wave + 16 * q) * 64), 16, 0, 0);
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int q = 0; q < Cfg::QB; ++q)
       __builtin_amdgcn_global_load_lds((const void*)(bsrc[q] + k0),
-                                       (lds_void_t*)(st + Cfg::A_BYTES + (64 * wave + 16 * q) * 64), 16, 0,
-                                       0);
+                                       (lds_void_t*)(st + Cfg::A_BYTES + (16 * Cfg::QB * wave + 16 * q) * 64),
+                                       16, 0, 0);
   };
   // fragment (row r, logical chunk c) of a stage operand
   auto frag = [&](const unsigned char* base, int r, int c) -> V8 {
@@ -1126,20 +1140,24 @@ __global__ __launch_bounds__(NT, 2) void trimul_contract_dma_kernel(const T* __r
       for (int r = 0; r < 16; ++r) acc[y][x][r] = 0.f;
 
   const int nkt = (int)(NP / Cfg::BK);
-  issue(0);
-  if (nkt > 1) issue(1);
+#pragma unroll
+  for (int st = 0; st < Cfg::STAGES - 1; ++st)
+    if (st < nkt) issue(st);
   for (int kt = 0; kt < nkt; ++kt) {
-    // This wave's DMA of stage kt is its oldest outstanding one (6 instructions per stage)
-    // and its fragment reads of stage kt - 1 have returned; after the barrier every wave's
-    // stage kt has landed and stage (kt + 2) % 3 is no longer read. A plain s_barrier (with a
-    // compiler memory clobber) replaces __syncthreads, whose fence would also wait for the
-    // DMA of stage kt + 1.
-    if (kt + 1 < nkt)
-      __builtin_amdgcn_s_waitcnt(0x076);  // vmcnt(6) lgkmcnt(0)
+    // This wave's DMA of stage kt is its oldest outstanding one (QPS instructions per stage,
+    // later stages issued after it) and its fragment reads of stage kt - 1 have returned;
+    // after the barrier every wave's stage kt has landed and stage (kt - 1) % STAGES is no
+    // longer read. A plain s_barrier (with a compiler memory clobber) replaces
+    // __syncthreads, whose fence would also wait for the DMA of the later stages.
+    const int ahead = min(Cfg::STAGES - 2, nkt - 1 - kt);  // stages issued after kt
+    if (ahead >= 2)
+      wait_vm_lgkm0<2 * Cfg::QPS>();
+    else if (ahead == 1)
+      wait_vm_lgkm0<Cfg::QPS>();
     else
-      __builtin_amdgcn_s_waitcnt(0x070);  // vmcnt(0) lgkmcnt(0)
+      wait_vm_lgkm0<0>();
     asm volatile("s_barrier" ::: "memory");
-    if (kt + 2 < nkt) issue(kt + 2);
+    if (kt + Cfg::STAGES - 1 < nkt) issue(kt + Cfg::STAGES - 1);
     const unsigned char* sa = smem + (kt % Cfg::STAGES) * Cfg::STAGE_BYTES;
     const unsigned char* sb = sa + Cfg::A_BYTES;
     // all fragment reads of the stage first, so their latency is exposed once per stage
@@ -1161,26 +1179,33 @@ __global__ __launch_bounds__(NT, 2) void trimul_contract_dma_kernel(const T* __r
     __builtin_amdgcn_sched_group_barrier(0x100, 6 * KS, 0);  // the LDS reads, in order
     __builtin_amdgcn_sched_group_barrier(0x008, 8 * KS, 0);  // then the MFMAs
   }
-  __syncthreads();  // stage buffers become the output tile
 
   // acc[y][x][r] = o[i = i0 + 64wm + 32x + l32][j = j0 + 128wn + 32y + 8(r/4) + 4g + r%4]
   T* ot = reinterpret_cast<T*>(smem);
-#pragma unroll
-  for (int y = 0; y < 4; ++y)
-#pragma unroll
-    for (int x = 0; x < 2; ++x)
-#pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        const f32x4 v = {acc[y][x][4 * rg], acc[y][x][4 * rg + 1], acc[y][x][4 * rg + 2], acc[y][x][4 * rg + 3]};
-        store4(&ot[(64 * wm + 32 * x + l32) * Cfg::SP + 128 * wn + 32 * y + 8 * rg + 4 * g],
-               TypeOps<T>::from_f32(v));
-      }
-  __syncthreads();
   constexpr int CPR = Cfg::BN / 8;  // 16-byte chunks per output row
+#pragma unroll
+  for (int ep = 0; ep < BM / Cfg::EROWS; ++ep) {
+    __syncthreads();  // stage buffers (or the previous pass) free
+    if ((wm >> 1) == ep) {
+#pragma unroll
+      for (int y = 0; y < 4; ++y)
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int rg = 0; rg < 4; ++rg) {
+            const f32x4 v = {acc[y][x][4 * rg], acc[y][x][4 * rg + 1], acc[y][x][4 * rg + 2],
+                             acc[y][x][4 * rg + 3]};
+            store4(&ot[(64 * (wm & 1) + 32 * x + l32) * Cfg::SP + 128 * wn + 32 * y + 8 * rg + 4 * g],
+                   TypeOps<T>::from_f32(v));
+          }
+    }
+    __syncthreads();
 #pragma unroll 4
-  for (int c = tid; c < Cfg::BM * CPR; c += NT) {
-    const int r = c / CPR, cj = (c % CPR) * 8;
-    if (i0 + r < N && j0 + cj < N) store8(Op + (int64_t)(i0 + r) * NP + j0 + cj, load8(&ot[r * Cfg::SP + cj]));
+    for (int c = tid; c < Cfg::EROWS * CPR; c += NTH) {
+      const int r = c / CPR, cj = (c % CPR) * 8;
+      const int i = i0 + Cfg::EROWS * ep + r;
+      if (i < N && j0 + cj < N) store8(Op + (int64_t)i * NP + j0 + cj, load8(&ot[r * Cfg::SP + cj]));
+    }
   }
 }
 
@@ -1241,17 +1266,23 @@ int launch_proj(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st)
   }
 }
 
+template <typename T, int BM>
+int launch_contract_dma(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st, int64_t NP) {
+  typedef ContractDma<BM> D;
+  const int64_t nblk = a.B * a.Ch * ((a.N + BM - 1) / BM) * ((a.N + D::BN - 1) / D::BN);
+  unsigned char* wsp = (unsigned char*)a.workspace;
+  hipLaunchKernelGGL((trimul_contract_dma_kernel<T, BM>), dim3((uint32_t)nblk), dim3(D::NTH), 0, st,
+                     (const T*)(wsp + L.off_a), (const T*)(wsp + L.off_b), (T*)(wsp + L.off_o), (int)a.N, NP);
+  return (int)hipGetLastError();
+}
+
 template <typename T, int PREC>
 int launch_contract(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
   const int64_t NP = round_up(a.N, 32);
-  unsigned char* wsp = (unsigned char*)a.workspace;
   if constexpr (sizeof(T) == 2) {
-    typedef ContractDma D;
-    const int64_t nblk = a.B * a.Ch * ((a.N + D::BM - 1) / D::BM) * ((a.N + D::BN - 1) / D::BN);
-    hipLaunchKernelGGL((trimul_contract_dma_kernel<T>), dim3((uint32_t)nblk), dim3(NT), 0, st,
-                       (const T*)(wsp + L.off_a), (const T*)(wsp + L.off_b), (T*)(wsp + L.off_o), (int)a.N,
-                       NP);
-    return (int)hipGetLastError();
+    // 256-row tiles once N fills them (half the L2 -> LDS bytes per flop), 128 below
+    if (a.N >= 512) return launch_contract_dma<T, 256>(a, L, st, NP);
+    return launch_contract_dma<T, 128>(a, L, st, NP);
   }
   typedef ContractCfg<T> Cfg;
   const int64_t nblk = a.B * a.Ch * ((a.N + Cfg::BM - 1) / Cfg::BM) * ((a.N + Cfg::BN - 1) / Cfg::BN);
