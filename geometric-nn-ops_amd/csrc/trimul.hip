@@ -838,7 +838,7 @@ __host__ __device__ inline size_t out_region1_elems(int64_t Ch, int pad) {
 }
 __host__ __device__ inline size_t out_lds_bytes(int64_t Ch, size_t elem) {
   const int pad = (int)(16 / elem);
-  return (out_region1_elems(Ch, pad) + (size_t)PTO * (Ch + pad)) * elem + (2 * (size_t)Ch + 8 * PTO) * 4;
+  return (out_region1_elems(Ch, pad) + (size_t)PTO * (Ch + pad)) * elem + (2 * (size_t)Ch + 8 * PTO + OPC) * 4;
 }
 
 // Chunk i of a thread = 8 output channels (c8) of one pixel (px) of the pass's
@@ -868,7 +868,8 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
   T* zs = ot + out_region1_elems(Ch, lds_pad<T>());
   float* lnw = reinterpret_cast<float*>(zs + (size_t)PTO * ZR);
   float* lnb = lnw + Ch;
-  float* red = lnb + Ch;  // [2 stats][4 quarters][PTO] partial sums
+  float* red = lnb + Ch;        // LayerNorm partial sums [8 * PTO]
+  float* bpo_s = red + 8 * PTO;  // p_out bias of the current pass [OPC]
 
   const int ntile = (N + PTO - 1) / PTO;
   const int ct = blockIdx.x % ntile;
@@ -902,6 +903,7 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
     lnw[c] = ld_or<T>(a.ln_out_w, c, 1.f);
     lnb[c] = ld_or<T>(a.ln_out_b, c, 0.f);
   }
+  for (int c = tid; c < (C < OPC ? C : OPC); c += NT) bpo_s[c] = ld_or<T>(a.p_out_b, c, 0.f);
   for (int cb = 0; cb < Ch * (PTO / 8); cb += LDB * NT) {
     V8 v[LDB];
 #pragma unroll
@@ -978,8 +980,17 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
     if (32 * wave < W) {
       const int cw = c0 + 32 * wave;
       float bpo[16];
+      if (c0 == 0) {  // first pass: from LDS
 #pragma unroll
-      for (int r = 0; r < 16; ++r) bpo[r] = ld_or<T>(a.p_out_b, cw + 4 * g + 8 * (r / 4) + (r % 4), 0.f);
+        for (int rg = 0; rg < 4; ++rg) {
+          const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bpo_s[32 * wave + 8 * rg + 4 * g]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bpo[4 * rg + e] = b4[e];
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) bpo[r] = ld_or<T>(a.p_out_b, cw + 4 * g + 8 * (r / 4) + (r % 4), 0.f);
+      }
       const T* wrow = wpo + (int64_t)(cw + l32) * Ch + 8 * g;
       f32x16 acc[PTO / 32];
 #pragma unroll
