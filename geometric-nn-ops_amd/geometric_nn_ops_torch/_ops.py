@@ -1,0 +1,78 @@
+"""The HIP forward kernels registered as torch operators (``torch.ops.gnn_amd.*``).
+
+Each operator calls the C ABI through the host launchers in ``triangle/_kernels`` and has
+a shape-only fake implementation, so ``torch.compile`` traces it as one opaque node (no
+graph break on the ctypes call) and FakeTensor / meta tracing works without a GPU. The
+public ``triangle_attention`` and ``triangle_multiplicative_update`` dispatch their kernel
+path through these operators; the differentiable torch path stays outside them (the
+operators are forward-only, like the reference's Triton kernels).
+
+Registration follows the boundary the reference's callers bind
+(geometric_nn_ops_torch/triangle/_triattn.py:96, _trimul.py:87).
+"""
+
+from typing import Optional
+
+import torch
+
+__all__ = ["triangle_attention_fwd", "trimul_fwd"]
+
+
+@torch.library.custom_op("gnn_amd::triangle_attention_fwd", mutates_args=())
+def triangle_attention_fwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    bias: Optional[torch.Tensor],
+    mask: Optional[torch.Tensor],
+    scale: Optional[float],
+) -> torch.Tensor:
+    """Canonical 5D ``[B, N_seq, N_res, H, D]`` q / k / v (any strides), bias
+    ``[B, 1, H, N, N]``, bool mask ``[B, N_seq, 1, 1, N]``; returns a fresh contiguous
+    tensor of q's shape and dtype."""
+    from .triangle._kernels.triangle_attention import triangle_attention_hip
+
+    return triangle_attention_hip(q, k, v, bias=bias, mask=mask, scale=scale)
+
+
+@triangle_attention_fwd.register_fake
+def _triangle_attention_fwd_fake(q, k, v, bias, mask, scale):
+    return q.new_empty(q.shape)
+
+
+@torch.library.custom_op("gnn_amd::trimul_fwd", mutates_args=())
+def trimul_fwd(
+    x: torch.Tensor,
+    direction: str,
+    mask: Optional[torch.Tensor],
+    norm_in_weight: Optional[torch.Tensor],
+    norm_in_bias: Optional[torch.Tensor],
+    p_in_weight: torch.Tensor,
+    p_in_bias: Optional[torch.Tensor],
+    g_in_weight: torch.Tensor,
+    g_in_bias: Optional[torch.Tensor],
+    norm_out_weight: Optional[torch.Tensor],
+    norm_out_bias: Optional[torch.Tensor],
+    p_out_weight: torch.Tensor,
+    p_out_bias: Optional[torch.Tensor],
+    g_out_weight: torch.Tensor,
+    g_out_bias: Optional[torch.Tensor],
+    eps: float,
+) -> torch.Tensor:
+    """``[*, N, N, C_z]`` in, a fresh contiguous tensor of the same shape and dtype out."""
+    from .triangle._kernels.trimul import trimul_hip
+
+    return trimul_hip(
+        x, direction, mask, eps=eps,
+        norm_in_weight=norm_in_weight, norm_in_bias=norm_in_bias,
+        p_in_weight=p_in_weight, p_in_bias=p_in_bias,
+        g_in_weight=g_in_weight, g_in_bias=g_in_bias,
+        norm_out_weight=norm_out_weight, norm_out_bias=norm_out_bias,
+        p_out_weight=p_out_weight, p_out_bias=p_out_bias,
+        g_out_weight=g_out_weight, g_out_bias=g_out_bias,
+    )
+
+
+@trimul_fwd.register_fake
+def _trimul_fwd_fake(x, direction, mask, *weights_and_eps):
+    return x.new_empty(x.shape)

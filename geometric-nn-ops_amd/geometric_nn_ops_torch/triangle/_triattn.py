@@ -5,7 +5,8 @@ Shape and dtype normalisation follow geometric_nn_ops_torch/triangle/_triattn.py
 N_seq axis, bias and mask are broadcast to ``[B, 1, H, N, N]`` / ``[B, N_seq, 1, 1, N]``,
 fp64 is computed in fp32, and the output has the input's shape and dtype.
 
-Dispatch: the gfx950 HIP kernel serves every forward-only call on a HIP device.
+Dispatch: the gfx950 HIP kernel serves every forward-only call on a HIP device, through
+the ``gnn_amd::triangle_attention_fwd`` operator (``geometric_nn_ops_torch._ops``).
 Calls that need a backward (grad enabled and some input requires grad), CPU tensors and
 head dims above the kernel's tile take the differentiable torch path instead -- the
 reference has no such path and runs its Triton kernel for all of them. There is no
@@ -14,8 +15,8 @@ fallback when the HIP library is missing: a GPU call then raises.
 
 import torch
 
+from .. import _ops
 from ._kernels import triangle_attention as _hip
-from ._kernels.triangle_attention import triangle_attention_hip
 from ._reference.triangle_attention import triangle_attention_torch
 
 _KERNEL_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
@@ -88,14 +89,12 @@ def triangle_attention(
         return o.to(orig_dtype).reshape(orig_shape)
 
     compute_dtype = orig_dtype if orig_dtype in _KERNEL_DTYPES else torch.float32
-    o = triangle_attention_hip(
+    o = _ops.triangle_attention_fwd(
         q.to(compute_dtype),
         k.to(compute_dtype),
         v.to(compute_dtype),
-        bias=None if bias is None else bias.to(compute_dtype),
-        mask=mask,
-        scale=scale,
-        dynamic=dynamic,
-        use_exp2=use_exp2,
+        None if bias is None else bias.to(compute_dtype),
+        mask,
+        scale,
     )
     return o.to(orig_dtype).reshape(orig_shape)

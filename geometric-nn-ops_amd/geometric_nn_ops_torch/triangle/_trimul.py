@@ -8,7 +8,8 @@ Dispatch follows the reference's rule (_trimul.py:31-36): the torch path runs wh
 backward could run (grad enabled and x or a weight requires grad), the tensor is not on
 a HIP device, or its dtype has no kernel; it also runs for channel counts the kernels do
 not tile (c_z or c_hidden not a multiple of 32, or above 512). Otherwise the HIP kernels
-run. A missing HIP library is an error on GPU tensors, never a silent fallback.
+run, through the ``gnn_amd::trimul_fwd`` operator (``geometric_nn_ops_torch._ops``). A
+missing HIP library is an error on GPU tensors, never a silent fallback.
 
 ``p_in_weight`` / ``g_in_weight`` are the concatenated ``[a; b]`` projections
 (``[2 * C_hidden, C_z]``).
@@ -16,8 +17,8 @@ run. A missing HIP library is an error on GPU tensors, never a silent fallback.
 
 import torch
 
+from .. import _ops
 from ._kernels import trimul as _hip
-from ._kernels.trimul import trimul_hip
 from ._reference.trimul import trimul_torch
 
 __all__ = ["triangle_multiplicative_update"]
@@ -82,5 +83,6 @@ def triangle_multiplicative_update(
         g_out_weight=g_out_weight,
         g_out_bias=g_out_bias,
     )
-    impl = trimul_torch if _needs_torch_path(x, weights.items()) else trimul_hip
-    return impl(x, direction, mask, eps=eps, **weights)
+    if _needs_torch_path(x, weights.items()):
+        return trimul_torch(x, direction, mask, eps=eps, **weights)
+    return _ops.trimul_fwd(x, direction, mask, eps=eps, **weights)

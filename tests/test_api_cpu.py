@@ -12,6 +12,7 @@ import torch
 from geometric_nn_ops_torch import _precision
 from geometric_nn_ops_torch.triangle import triangle_attention, triangle_multiplicative_update
 from geometric_nn_ops_torch.triangle import _trimul, _triattn
+from geometric_nn_ops_torch.triangle._kernels import trimul as _kt
 from geometric_nn_ops_torch.triangle._masking import mask_val, masked_key_bias, rounded_mask_value
 from helpers import attention_inputs, key_mask, np_weights, pair_input, to_np, trimul_weights
 from oracle import triangle_oracle as O
@@ -157,7 +158,7 @@ def test_unsupported_configs_use_the_torch_path(config):
     if config == "weights_require_grad":
         w = {k: v.requires_grad_() for k, v in w.items()}
     with mock.patch.object(_trimul, "trimul_torch", wraps=_trimul.trimul_torch) as ref, \
-            mock.patch.object(_trimul, "trimul_hip", wraps=_trimul.trimul_hip) as kern:
+            mock.patch.object(_kt, "trimul_hip", wraps=_kt.trimul_hip) as kern:
         triangle_multiplicative_update(x, "outgoing", mask, **w)
     assert ref.called and not kern.called
 
@@ -181,3 +182,22 @@ def test_kernel_dispatch_rule_for_gpu_tensors():
     with torch.no_grad():
         assert not _trimul._needs_torch_path(FakeCuda(), w_req.items())
     assert _trimul._needs_torch_path(FakeCuda(), {"p_in_weight": torch.zeros(96, 128)}.items())
+
+
+def test_operators_have_fake_implementations():
+    """The gnn_amd operators trace under FakeTensorMode without a GPU or the HIP library
+    (what torch.compile relies on): shapes and dtypes of the results."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    import geometric_nn_ops_torch._ops  # noqa: F401  (registers the operators)
+
+    with FakeTensorMode():
+        q = torch.empty(1, 3, 16, 4, 32, dtype=torch.bfloat16)
+        o = torch.ops.gnn_amd.triangle_attention_fwd(q, q, q, None, None, None)
+        assert o.shape == q.shape and o.dtype == q.dtype
+        x = torch.empty(2, 16, 16, 64, dtype=torch.float16)
+        pw, ow, gw = torch.empty(64, 64, dtype=x.dtype), torch.empty(64, 32, dtype=x.dtype), torch.empty(64, 64, dtype=x.dtype)
+        out = torch.ops.gnn_amd.trimul_fwd(x, "outgoing", None, None, None, pw, None, pw, None, None, None, ow, None,
+                                           gw, None, 1e-5)
+        assert out.shape == x.shape and out.dtype == x.dtype
+

@@ -57,15 +57,18 @@ def _trimul_stage(z, direction, w, tol, rel_fro_max, rows, cols):
 
 
 def _attention_stage(z, w, ending, tol, rel_fro_max, rows):
-    """Rows s of the pair stream (columns for the ending node) attend along their other axis;
-    q / k / v / bias are projections of the (transposed) stream."""
+    """Starting node: rows s of the pair stream attend along their columns. Ending node: the
+    same on the transposed stream, passed as transpose(1, 2) views of q / k / v and a
+    transpose(-1, -2) view of the bias (no copies), the output transposed back."""
     from geometric_nn_ops_torch.triangle import triangle_attention
 
     B, N = z.shape[0], z.shape[1]
-    zz = z.transpose(1, 2).contiguous() if ending else z
     with torch.no_grad():
-        q, k, v = ((zz @ w[n]).view(B, N, N, H, D) for n in ("q", "k", "v"))
-        bias = (zz @ w["b"]).permute(0, 3, 1, 2).unsqueeze(1)  # [B, 1, H, N, N], a strided view
+        q, k, v = ((z @ w[n]).view(B, N, N, H, D) for n in ("q", "k", "v"))
+        bias = (z @ w["b"]).permute(0, 3, 1, 2).unsqueeze(1)  # [B, 1, H, N, N], a strided view
+        if ending:
+            q, k, v = (t.transpose(1, 2) for t in (q, k, v))
+            bias = bias.transpose(-1, -2)
         o = triangle_attention(q, k, v, bias, None, D**-0.5)
     want = O.triangle_attention(to_np(q[:, rows]), to_np(k[:, rows]), to_np(v[:, rows]), to_np(bias), None,
                                 D**-0.5)

@@ -282,9 +282,10 @@ def test_tf32_changes_the_result():
 @contextlib.contextmanager
 def dispatch_spy():
     from geometric_nn_ops_torch.triangle import _trimul
+    from geometric_nn_ops_torch.triangle._kernels import trimul as _kt
 
     with mock.patch.object(_trimul, "trimul_torch", wraps=_trimul.trimul_torch) as ref, \
-            mock.patch.object(_trimul, "trimul_hip", wraps=_trimul.trimul_hip) as kern:
+            mock.patch.object(_kt, "trimul_hip", wraps=_kt.trimul_hip) as kern:
         yield ref, kern
 
 
