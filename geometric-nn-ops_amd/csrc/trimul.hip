@@ -854,12 +854,14 @@ __device__ __forceinline__ void out_load_g(typename TypeOps<T>::V8 (&gr)[OCH], c
   }
 }
 
-template <typename T, int PREC>
+// CK / CHK: c_z / c_hidden fixed at compile time (0 = taken from the arguments), so the
+// common 128 / 128 instantiation folds its loop bounds, chunk divisions and address strides.
+template <typename T, int PREC, int CK, int CHK>
 __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args a, int64_t NP,
                                                            size_t off_g, size_t off_o) {
   typedef typename TypeOps<T>::V8 V8;
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  const int C = (int)a.C, Ch = (int)a.Ch, N = (int)a.N;
+  const int C = CK ? CK : (int)a.C, Ch = CHK ? CHK : (int)a.Ch, N = (int)a.N;
   const int OR = PTO + lds_pad<T>();  // raw o tile [Ch][OR]
   const int ZR = Ch + lds_pad<T>();   // normalised tile [PTO][ZR]
   const int YR = OPC + lds_pad<T>();  // pass tile [PTO][YR]
@@ -1304,17 +1306,22 @@ int launch_contract(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t
   return (int)hipGetLastError();
 }
 
-template <typename T, int PREC>
-int launch_out(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
+template <typename T, int PREC, int CK, int CHK>
+int launch_out_w(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
   const int64_t NP = round_up(a.N, 32);
   const int64_t ntile = (a.N + PTO - 1) / PTO;
   const size_t smem = out_smem<T>(a);
-  if (smem > 64 * 1024)
-    (void)hipFuncSetAttribute((const void*)trimul_out_kernel<T, PREC>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-  hipLaunchKernelGGL((trimul_out_kernel<T, PREC>), dim3((uint32_t)(a.B * a.N * ntile)), dim3(NT),
+  const void* fn = (const void*)trimul_out_kernel<T, PREC, CK, CHK>;
+  if (smem > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  hipLaunchKernelGGL((trimul_out_kernel<T, PREC, CK, CHK>), dim3((uint32_t)(a.B * a.N * ntile)), dim3(NT),
                      smem, st, a, NP, L.off_g, L.off_o);
   return (int)hipGetLastError();
+}
+
+template <typename T, int PREC>
+int launch_out(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
+  if (a.C == 128 && a.Ch == 128) return launch_out_w<T, PREC, 128, 128>(a, L, st);
+  return launch_out_w<T, PREC, 0, 0>(a, L, st);
 }
 
 int check_args(const gnn_trimul_args& a, const char* who) {
