@@ -464,7 +464,7 @@ struct ProjFastLds {
   static constexpr size_t total = mk + 2 * (size_t)PTP * 4;
 };
 
-template <typename T, int CK>
+template <typename T, int CK, int CHK>  // CHK: c_hidden at compile time, 0 = from the arguments
 __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trimul_args a, int64_t NP,
                                                                   size_t off_a, size_t off_b,
                                                                   size_t off_g) {
@@ -476,7 +476,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
   constexpr int XMF = CK / 64;  // x chunks per thread (8 threads per pixel)
   constexpr int NGI = CK / 16;  // gate items (CK / 32 units x 2 sub-tiles), at most one per wave
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  const int Ch = (int)a.Ch, N = (int)a.N;
+  const int Ch = CHK ? CHK : (int)a.Ch, N = (int)a.N;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
   T* zs = reinterpret_cast<T*>(smem_raw + LD::zs);
   T* wgo_s = reinterpret_cast<T*>(smem_raw + LD::wgo);
@@ -1251,15 +1251,15 @@ int launch_proj_xm(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t 
   return (int)hipGetLastError();
 }
 
-template <typename T, int CK>
+template <typename T, int CK, int CHK>
 int launch_proj_fast(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
   const int64_t NP = round_up(a.N, 32);
   const int64_t ntiles = a.B * a.N * ((a.N + PTP - 1) / PTP);
   constexpr size_t smem = ProjFastLds<CK>::total;
-  const void* fn = (const void*)trimul_proj_fast_kernel<T, CK>;
+  const void* fn = (const void*)trimul_proj_fast_kernel<T, CK, CHK>;
   (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   const int64_t grid = std::min<int64_t>(ntiles, persistent_grid(fn, PNT, smem));
-  hipLaunchKernelGGL((trimul_proj_fast_kernel<T, CK>), dim3((uint32_t)grid), dim3(PNT), smem, st, a, NP,
+  hipLaunchKernelGGL((trimul_proj_fast_kernel<T, CK, CHK>), dim3((uint32_t)grid), dim3(PNT), smem, st, a, NP,
                      L.off_a, L.off_b, L.off_g);
   return (int)hipGetLastError();
 }
@@ -1267,8 +1267,9 @@ int launch_proj_fast(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_
 template <typename T, int PREC>
 int launch_proj(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
   if constexpr (sizeof(T) == 2) {
-    if (a.C == 128) return launch_proj_fast<T, 128>(a, L, st);
-    if (a.C == 64) return launch_proj_fast<T, 64>(a, L, st);
+    if (a.C == 128 && a.Ch == 128) return launch_proj_fast<T, 128, 128>(a, L, st);
+    if (a.C == 128) return launch_proj_fast<T, 128, 0>(a, L, st);
+    if (a.C == 64) return launch_proj_fast<T, 64, 0>(a, L, st);
   }
   switch (proj_xm(a.C)) {
     case 2: return launch_proj_xm<T, PREC, 2>(a, L, st);
