@@ -16,6 +16,16 @@ int set_error(int code, const char* msg) {
   return code;
 }
 
+int persistent_grid(const void* fn, int threads, size_t smem) {
+  int dev = 0, ncu = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu < 1)
+    ncu = 1;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, smem) != hipSuccess || per_cu < 1)
+    per_cu = 1;
+  return ncu * per_cu;
+}
+
 static int hip_status(hipError_t e, const char* who) {
   if (e == hipSuccess) return GNN_OK;
   char buf[256];

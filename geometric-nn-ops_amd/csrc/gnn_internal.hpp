@@ -10,6 +10,10 @@ namespace gnn {
 // Records `msg` as this thread's last error and returns `code`.
 int set_error(int code, const char* msg);
 
+// Resident workgroups of a persistent kernel on the current device: occupancy x CU count,
+// at least 1.
+int persistent_grid(const void* fn, int threads, size_t smem);
+
 int triattn_fwd(const gnn_triattn_args& a, hipStream_t stream);
 
 // Workspace layout shared by the three trimul stages (byte offsets, see the C header).

@@ -1227,17 +1227,6 @@ size_t out_smem(const gnn_trimul_args& a) {
   return out_lds_bytes(a.Ch, sizeof(T));
 }
 
-// Resident workgroups of a persistent kernel: occupancy x CU count, at least 1.
-int persistent_grid(const void* fn, int threads, size_t smem) {
-  int dev = 0, ncu = 0, per_cu = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu < 1)
-    ncu = 1;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, smem) != hipSuccess || per_cu < 1)
-    per_cu = 1;
-  return ncu * per_cu;
-}
-
 template <typename T, int PREC, int XM>
 int launch_proj_xm(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
   const int64_t NP = round_up(a.N, 32);
