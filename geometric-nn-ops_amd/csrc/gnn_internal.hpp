@@ -16,6 +16,11 @@ int persistent_grid(const void* fn, int threads, size_t smem);
 
 int triattn_fwd(const gnn_triattn_args& a, hipStream_t stream);
 
+// Row-resident attention (16-bit inputs, head dim <= 32, bounded N_res): the whole row of
+// K and V staged in LDS, no barrier in the key loop.
+bool triattn_row_applicable(const gnn_triattn_args& a);
+int triattn_row_fwd(const gnn_triattn_args& a, hipStream_t stream);
+
 // Workspace layout shared by the three trimul stages (byte offsets, see the C header).
 struct TrimulLayout {
   size_t off_a, off_b, off_g, off_o, total;

@@ -582,6 +582,7 @@ int triattn_fwd(const gnn_triattn_args& a, hipStream_t stream) {
   const int64_t nqb = (a.N + QB - 1) / QB;
   if (nqb * a.H * ((a.S + R - 1) / R) * a.B >= (int64_t)1 << 31)
     return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention: grid too large");
+  if (triattn_row_applicable(a)) return triattn_row_fwd(a, stream);
   switch (a.dtype) {
     case GNN_BF16: return launch_dp<bf16, PREC_NATIVE>(a, stream);
     case GNN_F16: return launch_dp<f16, PREC_NATIVE>(a, stream);

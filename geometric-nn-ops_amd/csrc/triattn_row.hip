@@ -1,0 +1,457 @@
+// Triangle attention forward for gfx950, row-resident variant: 16-bit inputs, head dim
+// <= 32, N_res <= ROW_MAX_N.
+//
+// Same mathematics as the tiled kernel (triattn_fwd.hip) and the reference forward
+// (geometric_nn_ops_torch/triangle/_kernels/triangle_attention.py:48-365, torch form
+// geometric_nn_ops_torch/triangle/_reference/triangle_attention.py:11-44):
+//   o[b,s,i,h,:] = sum_j softmax_j(l_ij) v[b,s,j,h,:],
+//   l_ij = bf16(q * scale) . k_j + bias[b,h,i,j] + mask_bias[b,s,j].
+//
+// What changes is the schedule. At D = 32 one (b, s, h) row of K and V is N * 128 bytes
+// (64 KB at N = 512), so a workgroup stages the WHOLE row of K and V in LDS once and its
+// waves then sweep every key tile with no barrier at all:
+//   * one workgroup per (b, s, h); its NW waves take the row's 32-query blocks round robin;
+//   * K rows are 64 bytes with the four 16-byte chunks XOR-swizzled by (key / 4) % 4, so the
+//     32-lane fragment reads of QK^T hit 16 distinct bank groups; V keeps [key][d] rows for
+//     the ds_read_b64_tr_b16 V^T fragments of PV (a 64-byte pitch puts the four row windows
+//     of one read pass on disjoint banks);
+//   * software pipelining inside each wave: the QK^T (and bias) MFMAs of key tile t+1 are
+//     issued before the softmax of tile t, so the matrix unit works on tile t+1 while the
+//     VALU exponentiates tile t; the pair-bias fragments of tile t+2 are requested from
+//     global memory (L2: the plane bias[b, h] is shared by every N_seq row) one tile ahead
+//     of their MFMA;
+//   * logical workgroup order (b, h, s) with s fastest, remapped so each XCD walks a
+//     contiguous range: the workgroups of one XCD share one bias plane in their L2.
+// The per-tile arithmetic (transposed score tile S^T = K Q'^T on 32x32x16 MFMA, bias added
+// by MFMA against an identity fragment, lazy rescale with threshold 8 ln 2, exp2 with the
+// folded FMA, v_dot2 row sums on the rounded probabilities, masked-key sentinel, all-masked
+// rows reproducing mean(v)) is the tiled kernel's, so both paths give identical results.
+#include "gnn_common.hpp"
+#include "gnn_internal.hpp"
+
+namespace gnn {
+
+namespace {
+
+constexpr int KT = 64;                 // keys per tile
+constexpr int ROW_BYTES = 64;          // one key row of K or V: 32 x 16-bit
+constexpr int TILE_BYTES = KT * ROW_BYTES;
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float RESCALE_THRESHOLD = 8.0f / LOG2E;
+
+#ifndef GNN_ROW_WAVES
+#define GNN_ROW_WAVES 8
+#endif
+#ifndef GNN_ROW_MINBLOCKS
+#define GNN_ROW_MINBLOCKS 2
+#endif
+#ifndef GNN_ROW_SETPRIO
+#define GNN_ROW_SETPRIO 1
+#endif
+#ifndef GNN_ROW_MAX_N
+#define GNN_ROW_MAX_N 1024
+#endif
+#ifndef GNN_ROW_HEADS_FIRST_BYTES
+#define GNN_ROW_HEADS_FIRST_BYTES (8 << 20)
+#endif
+constexpr int64_t ROW_HEADS_FIRST_BYTES = GNN_ROW_HEADS_FIRST_BYTES;
+constexpr int NW = GNN_ROW_WAVES;
+constexpr int NT = NW * 64;
+constexpr int ROW_MAX_TILES = (GNN_ROW_MAX_N + KT - 1) / KT;
+
+struct RowHdr {
+  uint64_t tile_live[ROW_MAX_TILES];  // bit j: key t*64+j is < N and unmasked
+  uint16_t tile_list[ROW_MAX_TILES];  // tiles to run (all of them when the row is dead)
+  int nrun;
+  int dead;  // the row has no live key
+  int full;  // every key < N is live (no masked key): tiles run in order, liveness is arithmetic
+};
+constexpr int HDR_BYTES = (int)((sizeof(RowHdr) + 255) / 256 * 256);
+
+size_t row_smem_bytes(int64_t N) {
+  const int64_t ntiles = (N + KT - 1) / KT;
+  return HDR_BYTES + 2 * (size_t)ntiles * TILE_BYTES;
+}
+
+template <typename T> struct BiasFragR {
+  typename TypeOps<T>::V8 f[2][2];  // f[sub][t] = bias[q][tile*64 + sub*32 + 16t + 8g + 0..7]
+};
+
+template <typename T>
+__device__ __forceinline__ void load_bias_row(BiasFragR<T>& bf, const T* brow, int kbase, int N, int g) {
+  if (kbase + KT <= N) {
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) bf.f[sub][t] = load8(brow + kbase + sub * 32 + 16 * t + 8 * g);
+    return;
+  }
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int key = kbase + sub * 32 + 16 * t + 8 * g;
+      bf.f[sub][t] = key < N ? load8(brow + key) : zero8<T>();
+    }
+}
+
+__device__ __forceinline__ float rowsum_add_r(const bf16x8& v, float acc) {
+  const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{v[e], v[e + 1]}, one, acc, false);
+  return acc;
+}
+__device__ __forceinline__ float rowsum_add_r(const f16x8& v, float acc) {
+  const f16x2 one = {(f16)1.0f, (f16)1.0f};
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) acc = __builtin_amdgcn_fdot2(f16x2{v[e], v[e + 1]}, one, acc, false);
+  return acc;
+}
+
+// max / sum over the lane pair (l, l ^ 32) with gfx950's v_permlane32_swap (no LDS trip)
+__device__ __forceinline__ float pair_max_swap(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum_swap(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <typename T>
+__device__ __forceinline__ typename TypeOps<T>::V4 tr_read4_r(const unsigned char* p) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4i16*)(__attribute__((address_space(3))) const unsigned char*)p);
+  return __builtin_bit_cast(typename TypeOps<T>::V4, v);
+}
+
+template <typename T, bool HAS_BIAS>
+__global__ __launch_bounds__(NT, GNN_ROW_MINBLOCKS) void triattn_row_kernel(const gnn_triattn_args a) {
+  typedef typename TypeOps<T>::V8 V8;
+  typedef typename TypeOps<T>::V4 V4;
+  extern __shared__ __align__(256) unsigned char smem_raw[];
+  RowHdr& hdr = *reinterpret_cast<RowHdr*>(smem_raw);
+
+  const int N = (int)a.N;
+  const int H = (int)a.H;
+  const int D = (int)a.D;
+  const int S = (int)a.S;
+  const int ntiles = (N + KT - 1) / KT;
+  unsigned char* ks = smem_raw + HDR_BYTES;
+  unsigned char* vs = ks + ntiles * TILE_BYTES;
+
+  // Logical order: heads fastest when all H bias planes of a batch fit one XCD's L2
+  // together (the XCD then reads whole 4-head key rows of K and V), rows fastest otherwise
+  // (an XCD then keeps a single bias plane).
+  const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
+  int s, h;
+  if (a.H * a.N * a.N * (int64_t)sizeof(T) <= ROW_HEADS_FIRST_BYTES) {
+    h = (int)(w % (uint32_t)H);
+    s = (int)((w / (uint32_t)H) % (uint32_t)S);
+  } else {
+    s = (int)(w % (uint32_t)S);
+    h = (int)((w / (uint32_t)S) % (uint32_t)H);
+  }
+  const int b = (int)(w / ((uint32_t)S * H));
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+
+  const int64_t ksn = a.k_stride[2], vsn = a.v_stride[2];
+  const T* kp = (const T*)a.k + b * a.k_stride[0] + s * a.k_stride[1] + h * a.k_stride[3];
+  const T* vp = (const T*)a.v + b * a.v_stride[0] + s * a.v_stride[1] + h * a.v_stride[3];
+
+  // ---- stage the row's K (swizzled) and V into LDS.
+  if (D == 32) {
+    // global_load_lds_dwordx4: one instruction moves 16 key rows (1 KB) straight into LDS,
+    // lane l filling bytes 16 l .. 16 l + 15, i.e. row l / 4, physical chunk l % 4. For K that
+    // slot holds logical chunk (l % 4) ^ ((row / 4) % 4), and (row / 4) % 4 = (l / 16) % 4
+    // because blocks start at multiples of 16 rows. Rows past N repeat row N - 1: finite
+    // values whose scores are masked to -inf (p = 0).
+    const int lrow = lane >> 2, lch = lane & 3;
+    const int kch = lch ^ ((lane >> 4) & 3);
+    const int nblk16 = ntiles * (KT / 16);
+    for (int q = wave; q < nblk16; q += NW) {
+      const int r = min(16 * q + lrow, N - 1);
+      __builtin_amdgcn_global_load_lds((const void*)(kp + (int64_t)r * ksn + 8 * kch),
+                                       (__attribute__((address_space(3))) void*)(ks + q * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vp + (int64_t)r * vsn + 8 * lch),
+                                       (__attribute__((address_space(3))) void*)(vs + q * 1024), 16, 0, 0);
+    }
+  } else {
+    // D < 32: through registers, so that columns D .. 31 are zero. Chunk c = key c / 4,
+    // columns 8 (c % 4) .. + 7; rows past N are zero.
+    constexpr int U = 4;
+    const int nchunks = ntiles * KT * 4;
+    for (int base = 0; base < nchunks; base += NT * U) {
+      V8 kr[U], vr[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = base + u * NT + tid;
+        const int key = c >> 2, d0 = (c & 3) * 8;
+        if (c < nchunks && key < N && d0 < D) {
+          kr[u] = load8(kp + (int64_t)key * ksn + d0);
+          vr[u] = load8(vp + (int64_t)key * vsn + d0);
+        } else {
+          kr[u] = zero8<T>();
+          vr[u] = zero8<T>();
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = base + u * NT + tid;
+        if (c < nchunks) {
+          const int key = c >> 2, cc = c & 3;
+          store8((T*)(ks + key * ROW_BYTES + 16 * (cc ^ ((key >> 2) & 3))), kr[u]);
+          store8((T*)(vs + key * ROW_BYTES + 16 * cc), vr[u]);
+        }
+      }
+    }
+  }
+
+  // ---- key liveness of the row (wave 0) and the tiles to run.
+  if (wave == 0) {
+    int n = 0;
+    bool full = true;
+    for (int t = 0; t < ntiles; ++t) {
+      const int key = t * KT + lane;
+      const bool valid = key < N;
+      bool live = valid;
+      if (live && a.mask) live = a.mask[b * a.mask_stride[0] + s * a.mask_stride[1] + (int64_t)key * a.mask_stride[2]] != 0;
+      const uint64_t bits = __ballot(live);
+      full &= bits == __ballot(valid);
+      if (lane == 0) {
+        hdr.tile_live[t] = bits;
+        if (bits != 0) hdr.tile_list[n] = (uint16_t)t;
+      }
+      n += bits != 0;
+    }
+    const bool dead = n == 0;
+    if (dead)
+      for (int t = lane; t < ntiles; t += 64) hdr.tile_list[t] = (uint16_t)t;
+    if (lane == 0) {
+      hdr.nrun = dead ? ntiles : n;
+      hdr.dead = dead;
+      hdr.full = full;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): this wave's LDS DMA has landed
+  __syncthreads();
+  const int nrun = hdr.nrun;
+  const bool dead = hdr.dead != 0;
+  const bool full = hdr.full != 0;
+  const float mval = a.mask_value;
+
+  // identity A-fragments for the bias MFMA (element e of lane group g in step t is key
+  // 16t + 8g + e of the 32-key sub-tile; row l32 holds a 1 there iff l32 is that key)
+  V8 idf[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) idf[t][e] = TypeOps<T>::from_f32(l32 == 16 * t + 8 * g + e ? 1.f : 0.f);
+
+  // per-lane LDS offsets: K fragment of k-step kk for key row l32 of a 32-key sub-tile
+  // (the swizzle term (key / 4) % 4 only depends on l32), and the V^T transposed-read base.
+  int koff[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) koff[kk] = l32 * ROW_BYTES + 16 * ((2 * kk + g) ^ ((l32 >> 2) & 3));
+  const int tr_r = lane & 15;
+  int tr_off = ((tr_r >> 2) * 32 + 16 * ((lane >> 4) & 1) + 4 * (tr_r & 3)) * 2 + 4 * g * ROW_BYTES;
+
+  const int nqb = (N + 31) / 32;
+  for (int qblk = wave; qblk < nqb; qblk += NW) {
+    // The first tiles' LDS reads are the same for every query block; keeping the compiler
+    // from hoisting them out of this loop keeps their registers free for the key loop.
+    asm volatile("" : "+v"(koff[0]), "+v"(koff[1]), "+v"(tr_off));
+    const int myq = qblk * 32 + l32;
+    const bool qok = myq < N;
+    V8 qf[2];
+    {
+      const T* qp = (const T*)a.q + b * a.q_stride[0] + s * a.q_stride[1] + h * a.q_stride[3] +
+                    (int64_t)(qok ? myq : 0) * a.q_stride[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int d0 = 16 * t + 8 * g;
+        if (qok && d0 < D) {
+          f32x8 x = TypeOps<T>::to_f32(load8(qp + d0));
+          qf[t] = TypeOps<T>::from_f32(x * a.scale);
+        } else {
+          qf[t] = zero8<T>();
+        }
+      }
+    }
+    const T* brow = HAS_BIAS ? (const T*)a.bias + b * a.bias_stride[0] + h * a.bias_stride[1] +
+                                   (int64_t)(qok ? myq : 0) * a.bias_stride[2]
+                             : nullptr;
+    f32x16 o;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] = 0.f;
+    float m = -INFINITY, lsum = 0.f;
+    BiasFragR<T> bb;
+
+    // S^T (+ bias) of tile t into acc: acc[sub][i] is key t*64 + sub*32 + 8*(i/4) + 4g + i%4.
+    auto qk = [&](f32x16 (&acc)[2], int t) {
+      const unsigned char* kt = ks + t * TILE_BYTES;
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[sub][i] = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+          Mma<T, PREC_NATIVE>::step(acc[sub], load8((const T*)(kt + sub * 32 * ROW_BYTES + koff[kk])), qf[kk]);
+      if constexpr (HAS_BIAS) {
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+          for (int sub = 0; sub < 2; ++sub) Mma<T, PREC_NATIVE>::step(acc[sub], idf[t2], bb.f[sub][t2]);
+      }
+    };
+
+    // mask, online softmax and O^T += V^T P^T for the scores of tile t
+    auto softmax_pv = [&](f32x16 (&sc)[2], int t, uint64_t live) {
+      if (live != ~0ull) {
+        const int nvalid = min(KT, N - t * KT);
+        const uint64_t valid = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+          const uint32_t lb = ((uint32_t)(live >> (32 * sub)) >> (4 * g)) & 0x0F0F0F0Fu;
+          const uint32_t vb = ((uint32_t)(valid >> (32 * sub)) >> (4 * g)) & 0x0F0F0F0Fu;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int bit = 8 * (i / 4) + (i % 4);
+            const float x = ((lb >> bit) & 1u) ? sc[sub][i] : sc[sub][i] + mval;
+            sc[sub][i] = ((vb >> bit) & 1u) ? x : -INFINITY;
+          }
+        }
+      }
+      float m0 = fmaxf(sc[0][0], sc[0][1]), m1 = fmaxf(sc[1][0], sc[1][1]);
+#pragma unroll
+      for (int i = 2; i < 16; ++i) {
+        m0 = fmaxf(m0, sc[0][i]);
+        m1 = fmaxf(m1, sc[1][i]);
+      }
+      const float mh = fmaxf(m0, m1);
+      const float mt = pair_max_swap(mh);
+      if (__any(mt > m + RESCALE_THRESHOLD)) {
+        const float mnew = fmaxf(m, mt);
+        const float alpha = fast_exp2((m - mnew) * LOG2E);  // 0 on the first tile (m = -inf)
+        m = mnew;
+        lsum *= alpha;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[i] *= alpha;
+      }
+      const float nm = -m * LOG2E;
+      // per 32-key half: exponentiate, round to the MFMA type, accumulate the row sum and
+      // O^T += V^T P^T. Fragment element e of k-step kk of half sub is key
+      // sub*32 + 16kk + 8(e/4) + 4g + e%4 in both operands.
+      const unsigned char* vt = vs + t * TILE_BYTES;
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        if (!dead) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sc[sub][i] = fast_exp2(__builtin_fmaf(sc[sub][i], LOG2E, nm));
+        } else {  // m is the collapsed sentinel: subtract first so s - m is exact
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sc[sub][i] = fast_exp2((sc[sub][i] - m) * LOG2E);
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          f32x8 x = {sc[sub][8 * kk + 0], sc[sub][8 * kk + 1], sc[sub][8 * kk + 2], sc[sub][8 * kk + 3],
+                     sc[sub][8 * kk + 4], sc[sub][8 * kk + 5], sc[sub][8 * kk + 6], sc[sub][8 * kk + 7]};
+          const V8 pf = TypeOps<T>::from_f32(x);
+          lsum = rowsum_add_r(pf, lsum);
+          const unsigned char* vb = vt + (sub * 32 + 16 * kk) * ROW_BYTES + tr_off;
+          const V4 lo = tr_read4_r<T>(vb);
+          const V4 hi = tr_read4_r<T>(vb + 8 * ROW_BYTES);
+          V8 vf;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            vf[e] = lo[e];
+            vf[e + 4] = hi[e];
+          }
+          Mma<T, PREC_NATIVE>::step(o, vf, pf);
+        }
+      }
+    };
+
+#if GNN_ROW_SETPRIO
+#define ROW_PRIO_HI() __builtin_amdgcn_s_setprio(1)
+#define ROW_PRIO_LO() __builtin_amdgcn_s_setprio(0)
+#else
+#define ROW_PRIO_HI()
+#define ROW_PRIO_LO()
+#endif
+    if (full) {
+      // no masked key: tiles in order, liveness from N alone (no LDS reads in the loop)
+      if constexpr (HAS_BIAS) load_bias_row<T>(bb, brow, 0, N, g);
+      for (int t = 0; t < ntiles; ++t) {
+        f32x16 sc[2];
+        ROW_PRIO_HI();
+        qk(sc, t);
+        ROW_PRIO_LO();
+        if (HAS_BIAS && t + 1 < ntiles) load_bias_row<T>(bb, brow, (t + 1) * KT, N, g);
+        const int nvalid = N - t * KT;
+        softmax_pv(sc, t, nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull));
+      }
+    } else {
+      if constexpr (HAS_BIAS) load_bias_row<T>(bb, brow, hdr.tile_list[0] * KT, N, g);
+      for (int it = 0; it < nrun; ++it) {
+        const int t = hdr.tile_list[it];
+        f32x16 sc[2];
+        ROW_PRIO_HI();
+        qk(sc, t);
+        ROW_PRIO_LO();
+        if (HAS_BIAS && it + 1 < nrun) load_bias_row<T>(bb, brow, hdr.tile_list[it + 1] * KT, N, g);
+        softmax_pv(sc, t, hdr.tile_live[t]);
+      }
+    }
+
+    // ---- normalise and store. o[i] is O[myq][8*(i/4) + 4g + i%4].
+    const float ltot = pair_sum_swap(lsum);
+    if (qok) {
+      const float inv = 1.0f / ltot;
+      T* orow = (T*)a.o + b * a.o_stride[0] + s * a.o_stride[1] + h * a.o_stride[3] + (int64_t)myq * a.o_stride[2];
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int d0 = 8 * rg + 4 * g;
+        if (d0 < D) {
+          f32x4 x = {o[4 * rg] * inv, o[4 * rg + 1] * inv, o[4 * rg + 2] * inv, o[4 * rg + 3] * inv};
+          store4(orow + d0, TypeOps<T>::from_f32(x));
+        }
+      }
+      if (a.lse && g == 0)
+        a.lse[(((int64_t)b * a.S + s) * H + h) * N + myq] = m + __log2f(ltot) * (1.0f / LOG2E);
+    }
+  }
+}
+
+template <typename T, bool HAS_BIAS>
+int launch_row(const gnn_triattn_args& a, hipStream_t stream) {
+  const size_t smem = row_smem_bytes(a.N);
+  const void* fn = (const void*)triattn_row_kernel<T, HAS_BIAS>;
+  if (smem > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  const int64_t nblk = a.B * a.S * a.H;
+  hipLaunchKernelGGL((triattn_row_kernel<T, HAS_BIAS>), dim3((uint32_t)nblk), dim3(NT), smem, stream, a);
+  return (int)hipGetLastError();
+}
+
+}  // namespace
+
+bool triattn_row_applicable(const gnn_triattn_args& a) {
+  return (a.dtype == GNN_BF16 || a.dtype == GNN_F16) && a.D <= 32 && a.N <= GNN_ROW_MAX_N && a.N >= 1 &&
+         a.B * a.S * a.H < ((int64_t)1 << 31);
+}
+
+int triattn_row_fwd(const gnn_triattn_args& a, hipStream_t stream) {
+  if (a.dtype == GNN_BF16) return a.bias ? launch_row<bf16, true>(a, stream) : launch_row<bf16, false>(a, stream);
+  return a.bias ? launch_row<f16, true>(a, stream) : launch_row<f16, false>(a, stream);
+}
+
+}  // namespace gnn
