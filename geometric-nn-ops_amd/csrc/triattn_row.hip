@@ -15,13 +15,19 @@
 //     32-lane fragment reads of QK^T hit 16 distinct bank groups; V keeps [key][d] rows for
 //     the ds_read_b64_tr_b16 V^T fragments of PV (a 64-byte pitch puts the four row windows
 //     of one read pass on disjoint banks);
-//   * software pipelining inside each wave: the QK^T (and bias) MFMAs of key tile t+1 are
-//     issued before the softmax of tile t, so the matrix unit works on tile t+1 while the
-//     VALU exponentiates tile t; the pair-bias fragments of tile t+2 are requested from
-//     global memory (L2: the plane bias[b, h] is shared by every N_seq row) one tile ahead
-//     of their MFMA;
-//   * logical workgroup order (b, h, s) with s fastest, remapped so each XCD walks a
-//     contiguous range: the workgroups of one XCD share one bias plane in their L2.
+//   * K and V arrive by global_load_lds (global -> LDS without registers) when D = 32;
+//   * the pair-bias fragments of tile t+1 are requested from global memory (L2: the plane
+//     bias[b, h] is shared by every N_seq row) while tile t is computed;
+//   * the pair maximum of the online softmax uses v_permlane32_swap (no LDS round trip), and
+//     rows without a masked key run their tiles in order with arithmetic liveness, so the
+//     key loop reads nothing from LDS but K and V;
+//   * logical workgroup order (b, s, h) with heads fastest when the H bias planes of a batch
+//     fit one XCD's L2 together (whole 4-head key rows of K and V then stay on one XCD),
+//     (b, h, s) otherwise (one bias plane per XCD), remapped so each XCD walks a contiguous
+//     range.
+// Measured alternatives not kept: 4 waves per workgroup (the staging then is not amortised),
+// and software pipelining the QK^T of the next tile (or 32-key half tile) ahead of the
+// softmax (the extra score registers cost occupancy and it measured slower).
 // The per-tile arithmetic (transposed score tile S^T = K Q'^T on 32x32x16 MFMA, bias added
 // by MFMA against an identity fragment, lazy rescale with threshold 8 ln 2, exp2 with the
 // folded FMA, v_dot2 row sums on the rounded probabilities, masked-key sentinel, all-masked
