@@ -21,10 +21,11 @@
 //   * the pair maximum of the online softmax uses v_permlane32_swap (no LDS round trip), and
 //     rows without a masked key run their tiles in order with arithmetic liveness, so the
 //     key loop reads nothing from LDS but K and V;
-//   * logical workgroup order (b, s, h) with heads fastest when the H bias planes of a batch
-//     fit one XCD's L2 together (whole 4-head key rows of K and V then stay on one XCD),
-//     (b, h, s) otherwise (one bias plane per XCD), remapped so each XCD walks a contiguous
-//     range.
+//   * logical workgroup order (b, head pair, s, head in pair), remapped so each XCD walks a
+//     contiguous range: the two heads of a pair share the 128-byte lines of the K and V rows
+//     and an XCD's L2 holds just their two bias planes (248 MB fetched from beyond L2 per
+//     launch at N = 512 against 309 MB with all four heads fastest). Odd H falls back to heads
+//     fastest (when the planes fit the L2 together) or rows fastest.
 // Measured alternatives not kept: 4 waves per workgroup (the staging then is not amortised),
 // and software pipelining the QK^T of the next tile (or 32-key half tile) ahead of the
 // softmax (the extra score registers cost occupancy and it measured slower).
@@ -61,6 +62,10 @@ constexpr float RESCALE_THRESHOLD = 8.0f / LOG2E;
 #define GNN_ROW_HEADS_FIRST_BYTES (8 << 20)
 #endif
 constexpr int64_t ROW_HEADS_FIRST_BYTES = GNN_ROW_HEADS_FIRST_BYTES;
+#ifndef GNN_ROW_HEAD_PAIRS
+#define GNN_ROW_HEAD_PAIRS 1
+#endif
+constexpr bool ROW_HEAD_PAIRS = GNN_ROW_HEAD_PAIRS;
 constexpr int NW = GNN_ROW_WAVES;
 constexpr int NT = NW * 64;
 constexpr int ROW_MAX_TILES = (GNN_ROW_MAX_N + KT - 1) / KT;
@@ -153,7 +158,13 @@ __global__ __launch_bounds__(NT, GNN_ROW_MINBLOCKS) void triattn_row_kernel(cons
   // (an XCD then keeps a single bias plane).
   const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
   int s, h;
-  if (a.H * a.N * a.N * (int64_t)sizeof(T) <= ROW_HEADS_FIRST_BYTES) {
+  if (ROW_HEAD_PAIRS && H % 2 == 0) {
+    // head pairs fastest: the two heads of a pair share the 128-byte lines of K and V rows
+    // (D = 32, 16-bit), and an XCD keeps only their two bias planes
+    const uint32_t hi = w & 1u, rest = w >> 1;
+    s = (int)(rest % (uint32_t)S);
+    h = 2 * (int)((rest / (uint32_t)S) % (uint32_t)(H / 2)) + (int)hi;
+  } else if (a.H * a.N * a.N * (int64_t)sizeof(T) <= ROW_HEADS_FIRST_BYTES) {
     h = (int)(w % (uint32_t)H);
     s = (int)((w / (uint32_t)H) % (uint32_t)S);
   } else {
