@@ -108,6 +108,22 @@ __device__ __forceinline__ typename TypeOps<T>::V8 zero8() {
   return TypeOps<T>::from_f32(f32x8{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f});
 }
 
+// 8 bias values from key `key` on, with the ones at keys >= N replaced by zero: the
+// identity-fragment MFMA that adds the bias multiplies every loaded value (0 * x for the
+// other keys), so padding past N must not hold a NaN or an infinity.
+template <typename T>
+__device__ __forceinline__ typename TypeOps<T>::V8 load8_bias_tail(const T* row, int key, int N) {
+  if (key >= N) return zero8<T>();
+  typename TypeOps<T>::V8 x = load8(row + key);
+  if (key + 8 > N) {
+    const T zero = TypeOps<T>::from_f32(0.f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (key + e >= N) x[e] = zero;
+  }
+  return x;
+}
+
 // ---- 32x32 tile, one K=16 step ----------------------------------------------------------
 // acc[row, col] += sum_k A[row, k] * B[k, col] over the 16 k of this step, with both
 // operands given as fragments (see the file comment).

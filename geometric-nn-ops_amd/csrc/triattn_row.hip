@@ -102,7 +102,7 @@ __device__ __forceinline__ void load_bias_row(BiasFragR<T>& bf, const T* brow, i
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int key = kbase + sub * 32 + 16 * t + 8 * g;
-      bf.f[sub][t] = key < N ? load8(brow + key) : zero8<T>();
+      bf.f[sub][t] = load8_bias_tail<T>(brow, key, N);
     }
 }
 
