@@ -107,6 +107,20 @@ int gnn_trimul_contract(const gnn_trimul_args* args, void* stream) {
 }
 int gnn_trimul_out(const gnn_trimul_args* args, void* stream) { return trimul_stage(args, stream, 4); }
 
+int gnn_pair_bias_proj(const gnn_pair_bias_args* args, void* stream) {
+  if (!args) return set_error(GNN_ERR_ARG, "pair_bias_proj: args is NULL");
+  const gnn_pair_bias_args& a = *args;
+  if (!a.z || !a.proj_w || !a.out)
+    return set_error(GNN_ERR_ARG, "pair_bias_proj: z, proj_w and out are required");
+  if (a.B < 1 || a.U < 1 || a.V < 1 || a.Zc < 1 || a.H < 1)
+    return set_error(GNN_ERR_ARG, "pair_bias_proj: B, U, V, c_z and H must be positive");
+  if (!aligned(a.z, 16))
+    return set_error(GNN_ERR_ARG, "pair_bias_proj: z must be 16-byte aligned");
+  int rc = pair_bias_proj(a, (hipStream_t)stream);
+  if (rc < 0) return rc;
+  return hip_status((hipError_t)rc, "pair_bias_proj");
+}
+
 const char* gnn_last_error(void) { return g_last_error.c_str(); }
 
 const char* gnn_version(void) { return "0.1.0 gfx950"; }

@@ -31,4 +31,6 @@ int trimul_proj(const gnn_trimul_args& a, hipStream_t stream);
 int trimul_contract(const gnn_trimul_args& a, hipStream_t stream);
 int trimul_out(const gnn_trimul_args& a, hipStream_t stream);
 
+int pair_bias_proj(const gnn_pair_bias_args& a, hipStream_t stream);
+
 }  // namespace gnn

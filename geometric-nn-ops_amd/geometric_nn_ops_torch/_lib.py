@@ -87,6 +87,25 @@ class TrimulArgs(ctypes.Structure):
     ]
 
 
+class PairBiasArgs(ctypes.Structure):
+    """Mirror of ``gnn_pair_bias_args``."""
+
+    _fields_ = [
+        ("z", ctypes.c_void_p),
+        ("ln_w", ctypes.c_void_p),
+        ("proj_w", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("B", ctypes.c_int64),
+        ("U", ctypes.c_int64),
+        ("V", ctypes.c_int64),
+        ("Zc", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("out_stride", I64x3),
+        ("eps", ctypes.c_float),
+        ("dtype", ctypes.c_int32),
+    ]
+
+
 # Every symbol include/gnn_triangle.h declares, with its ctypes signature.
 _SIGNATURES = {
     "gnn_triattn_fwd": (ctypes.c_int, [ctypes.POINTER(TriAttnArgs), ctypes.c_void_p]),
@@ -99,6 +118,7 @@ _SIGNATURES = {
     "gnn_trimul_proj": (ctypes.c_int, [ctypes.POINTER(TrimulArgs), ctypes.c_void_p]),
     "gnn_trimul_contract": (ctypes.c_int, [ctypes.POINTER(TrimulArgs), ctypes.c_void_p]),
     "gnn_trimul_out": (ctypes.c_int, [ctypes.POINTER(TrimulArgs), ctypes.c_void_p]),
+    "gnn_pair_bias_proj": (ctypes.c_int, [ctypes.POINTER(PairBiasArgs), ctypes.c_void_p]),
     "gnn_last_error": (ctypes.c_char_p, []),
     "gnn_version": (ctypes.c_char_p, []),
 }

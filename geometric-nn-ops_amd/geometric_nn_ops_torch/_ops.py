@@ -15,7 +15,7 @@ from typing import Optional
 
 import torch
 
-__all__ = ["triangle_attention_fwd", "trimul_fwd"]
+__all__ = ["triangle_attention_fwd", "trimul_fwd", "attention_pair_bias_fwd"]
 
 
 @torch.library.custom_op("gnn_amd::triangle_attention_fwd", mutates_args=())
@@ -76,3 +76,47 @@ def trimul_fwd(
 @trimul_fwd.register_fake
 def _trimul_fwd_fake(x, direction, mask, *weights_and_eps):
     return x.new_empty(x.shape)
+
+
+@torch.library.custom_op("gnn_amd::attention_pair_bias_fwd", mutates_args=())
+def attention_pair_bias_fwd(
+    s: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    z: torch.Tensor,
+    proj_g_weight: torch.Tensor,
+    proj_o_weight: torch.Tensor,
+    proj_z_weight: Optional[torch.Tensor],
+    ln_z_weight: Optional[torch.Tensor],
+    proj_g_bias: Optional[torch.Tensor],
+    proj_o_bias: Optional[torch.Tensor],
+    mask: Optional[torch.Tensor],
+    scale: Optional[float],
+    inf: Optional[float],
+    eps: float,
+    z_is_projected: bool,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(out [BM, U, D], pz [B, H, U, V])``; with ``z_is_projected`` the second output is an
+    empty tensor (the caller already holds the bias)."""
+    from .triangle._kernels.attention_pair_bias import attention_pair_bias_hip
+
+    out, pz = attention_pair_bias_hip(
+        s, q, k, v, z, proj_g_weight=proj_g_weight, proj_o_weight=proj_o_weight,
+        proj_z_weight=proj_z_weight, ln_z_weight=ln_z_weight, proj_g_bias=proj_g_bias,
+        proj_o_bias=proj_o_bias, mask=mask, scale=scale, inf=inf, eps=eps,
+        z_is_projected=z_is_projected,
+    )
+    if z_is_projected:
+        return out, z.new_empty((0,))
+    return out, pz.contiguous()
+
+
+@attention_pair_bias_fwd.register_fake
+def _attention_pair_bias_fwd_fake(s, q, k, v, z, proj_g_weight, proj_o_weight, proj_z_weight, ln_z_weight,
+                                  proj_g_bias, proj_o_bias, mask, scale, inf, eps, z_is_projected):
+    BM, H, U, _ = q.shape
+    out = s.new_empty((BM, U, proj_o_weight.shape[0]))
+    if z_is_projected:
+        return out, z.new_empty((0,))
+    return out, z.new_empty((z.shape[0], H, U, k.shape[2]))

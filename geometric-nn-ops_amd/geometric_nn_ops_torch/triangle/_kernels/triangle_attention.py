@@ -43,7 +43,7 @@ def _prepare(t: torch.Tensor) -> torch.Tensor:
 
 
 def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=False, use_exp2=False,
-                           lse=None):
+                           lse=None, mask_value=None):
     """Triangle attention forward on the canonical 5D layout.
 
     q/k/v ``[B, N_seq, N_res, H, D]`` (bf16, fp16 or fp32, on a HIP device); bias
@@ -51,7 +51,9 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
     ``None``. ``dynamic`` is accepted for API parity and has no effect (N is always a
     runtime argument); ``use_exp2`` likewise (the kernel always evaluates the softmax in
     base 2). ``lse``, if given, is a float32 ``[B, N_seq, H, N_res]`` tensor that receives
-    the natural-log log-sum-exp of each query's logits.
+    the natural-log log-sum-exp of each query's logits. ``mask_value`` overrides the logit
+    offset of masked keys (default: the dtype's sentinel rounded to the dtype, as the
+    reference launcher applies it).
     """
     del dynamic, use_exp2
     lib = _lib.load()
@@ -85,7 +87,7 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
             # unit key stride and a query pitch that is a multiple of 8 elements; keys
             # past N in the padded pitch are never read
             pitch = (N + 7) // 8 * 8
-            padded = torch.empty((B, 1, H, N, pitch), device=bias.device, dtype=bias.dtype)
+            padded = torch.zeros((B, 1, H, N, pitch), device=bias.device, dtype=bias.dtype)
             padded[..., :N] = bias
             bias = padded
         args.bias = bias.data_ptr()
@@ -99,7 +101,7 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
         assert lse.shape == (B, S, H, N) and lse.dtype == torch.float32 and lse.is_contiguous()
         args.lse = lse.data_ptr()
     args.scale = float(scale)
-    args.mask_value = rounded_mask_value(q.dtype)
+    args.mask_value = rounded_mask_value(q.dtype) if mask_value is None else float(mask_value)
     args.dtype = _lib.DTYPE_CODE[q.dtype]
     precision = _precision.matmul_precision(fp32_operands=q.dtype == torch.float32)
     args.precision = _lib.PRECISION_CODE[precision]

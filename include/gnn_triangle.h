@@ -27,6 +27,8 @@
  *                        (geometric_nn_ops_torch/triangle/_reference/trimul.py:44-54, called
  *                        from trimul.py:442)
  *   gnn_trimul_out    -> triton_layernorm(o) + p_out linear + the o*g gate (trimul.py:443-448)
+ *   gnn_pair_bias_proj -> _project_pair_bias of attention_pair_bias
+ *                        (geometric_nn_ops_torch/triangle/_reference/attention_pair_bias.py:17-22)
  */
 #ifndef GNN_TRIANGLE_H
 #define GNN_TRIANGLE_H
@@ -154,6 +156,32 @@ int gnn_trimul_contract(const gnn_trimul_args* args, void* stream);
 /* Stage 3: LayerNorm-out + p_out projection, multiplied by the gate g.
  * Replaces trimul.py:443-448. */
 int gnn_trimul_out(const gnn_trimul_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Pair-bias projection of attention with pair bias:
+ *   out[b, h, u, v] = sum_c LN(z[b, u, v, :])[c] * proj_w[h, c]
+ *   LN(x) = (x - mean) / sqrt(var + eps) * ln_w   (biased variance, no beta; the result is
+ *   rounded to the input dtype before the projection, as F.layer_norm returns it)
+ * z contiguous [B, U, V, Zc]; proj_w contiguous [H, Zc]; ln_w [Zc] or NULL (ones); out
+ * [B, H, U, V] by strides (v stride 1), all in the input dtype. Zc a multiple of 8 and at
+ * most 256, H * Zc at most 8192.
+ */
+typedef struct gnn_pair_bias_args {
+  const void* z;
+  const void* ln_w;
+  const void* proj_w;
+  void* out;
+  int64_t B, U, V, Zc, H;
+  int64_t out_stride[3]; /* b, h, u (v stride must be 1) */
+  float eps;
+  int32_t dtype; /* enum gnn_dtype, shared by every tensor */
+} gnn_pair_bias_args;
+
+/* Replaces _project_pair_bias (geometric_nn_ops_torch/triangle/_reference/
+ * attention_pair_bias.py:17-22: F.layer_norm + F.linear + permute to [B, H, U, V]), the
+ * pair-rep half of attention_pair_bias (triangle/_attention_pair_bias.py:11-98); the
+ * attention itself runs on gnn_triattn_fwd with N_seq = the multiplicity. */
+int gnn_pair_bias_proj(const gnn_pair_bias_args* args, void* stream);
 
 /* Message for the last failing call on this thread ("" if none). */
 const char* gnn_last_error(void);

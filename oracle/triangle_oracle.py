@@ -11,6 +11,9 @@ Reference files followed (paths relative to AMDResearch/geometric-nn-ops):
                                         geometric_nn_ops_torch/triangle/_reference/trimul.py:27-97
   * layer_norm semantics                torch.nn.functional.layer_norm (biased variance,
                                         1/sqrt(var + eps)), called at _reference/trimul.py:85,94
+  * attention_pair_bias (pair-bias projection, multiplicity broadcast, key mask with a
+    caller-given magnitude, gate from s, output projection)
+                                        geometric_nn_ops_torch/triangle/_reference/attention_pair_bias.py:17-89
 
 Everything is computed in ``dtype`` (float64 by default). How each function is pinned
 (tests/test_oracle.py): triangle_attention against a pure-Python loop softmax-attention
@@ -19,7 +22,11 @@ mean(v), masked keys are bit-invariant to noise, fully masked rows give mean(v))
 combine against pure-Python triple loops for both directions; layer_norm against its
 closed-form moments and the zero-vector -> beta case; trimul end to end against the
 N = 1 closed form and the fully-masked constant field; mask_val against the reference's
-stated sentinel values.
+stated sentinel values; attention_pair_bias against a pure-Python per-element loop at tiny
+sizes, against triangle_attention with N_seq = the multiplicity (the shared-bias
+identity), and the reference's known answers (masked keys ignored, cached bias equal to the
+recomputed one, copies with equal inputs equal, a per-batch mask equal to its per-copy
+repetition).
 """
 
 from __future__ import annotations
@@ -217,3 +224,58 @@ def cos(a, b) -> float:
     if na == 0 and nb == 0:
         return 1.0
     return float(a @ b / max(na * nb, 1e-300))
+
+
+# ------------------------------- attention with pair bias (_reference/attention_pair_bias.py)
+def pair_bias_projection(z, ln_z_weight, proj_z_weight, eps=1e-5, *, dtype=np.float64) -> np.ndarray:
+    """``z [B, U, V, Zc]`` -> per-head bias ``[B, H, U, V]``: LayerNorm over ``Zc`` with no
+    beta, then the bias-free projection to H heads (attention_pair_bias.py:17-22)."""
+    zc = layer_norm(z, ln_z_weight, None, eps, dtype=dtype)
+    pz = linear(zc, proj_z_weight, None, dtype=dtype)  # [B, U, V, H]
+    return np.ascontiguousarray(np.transpose(pz, (0, 3, 1, 2)))
+
+
+def attention_pair_bias(s, q, k, v, z, *, proj_g_weight, proj_o_weight, proj_z_weight=None,
+                        ln_z_weight=None, proj_g_bias=None, proj_o_bias=None, mask=None,
+                        scale=None, inf=None, eps=1e-5, z_is_projected=False,
+                        return_z_proj=False, dtype=np.float64):
+    """Attention with pair bias (attention_pair_bias.py:25-89).
+
+    q ``[B*M, H, U, DH]``, k / v ``[B*M, H, V, DH]``, s ``[B*M, U, H*DH]``; z the pair rep
+    ``[B, U, V, Zc]`` (or the projected bias ``[B, H, U, V]`` with ``z_is_projected``);
+    mask ``[B, V]`` or ``[B*M, V]`` with 1 = keep, pushing masked logits down by ``inf``
+    (``None``: the dtype's mask_val). Returns ``(out [B*M, U, H*DH], bias or None)``.
+    """
+    q = np.asarray(q, dtype=dtype)
+    k = np.asarray(k, dtype=dtype)
+    v = np.asarray(v, dtype=dtype)
+    BM, H, U, DH = q.shape
+    V = k.shape[2]
+    B = np.asarray(z).shape[0]
+    if BM % B != 0:
+        raise ValueError(f"q batch {BM} is not a multiple of z batch {B}")
+    M = BM // B
+    if scale is None:
+        scale = DH ** -0.5
+    pz = np.asarray(z, dtype=dtype) if z_is_projected else pair_bias_projection(
+        z, ln_z_weight, proj_z_weight, eps, dtype=dtype)
+    qm = q.reshape(B, M, H, U, DH)
+    km = k.reshape(B, M, H, V, DH)
+    vm = v.reshape(B, M, H, V, DH)
+    logits = (qm @ np.swapaxes(km, -1, -2)) * dtype(scale) + pz[:, None]  # [B, M, H, U, V]
+    if mask is not None:
+        mask = np.asarray(mask, dtype=dtype)
+        if mask.shape[0] == B:
+            keep = mask.reshape(B, 1, 1, 1, V)
+        elif mask.shape[0] == BM:
+            keep = mask.reshape(B, M, 1, 1, V)
+        else:
+            raise ValueError(f"mask batch {mask.shape[0]} must be B={B} or BM={BM}")
+        if inf is None:
+            inf = mask_val("float64" if dtype == np.float64 else "float32")
+        logits = logits + (keep - 1.0) * dtype(inf)
+    o = _softmax(logits, -1) @ vm  # [B, M, H, U, DH]
+    o = np.transpose(o.reshape(BM, H, U, DH), (0, 2, 1, 3)).reshape(BM, U, H * DH)
+    g = sigmoid(linear(s, proj_g_weight, proj_g_bias, dtype=dtype))
+    out = linear(o * g, proj_o_weight, proj_o_bias, dtype=dtype)
+    return out, (pz if return_z_proj else None)

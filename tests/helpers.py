@@ -31,6 +31,12 @@ TRIANGLE_ATTENTION_TOL = {
     (torch.float16, "ieee"): Tolerance(1.0 - 1e-4, 2e-2),
     (torch.bfloat16, "ieee"): Tolerance(1.0 - 1e-4, 5e-2),
 }
+ATTENTION_PAIR_BIAS_TOL = {
+    (torch.float32, "ieee"): Tolerance(1.0 - 1e-5, 2e-3),
+    (torch.float32, "tf32"): Tolerance(1.0 - 1e-5, 3e-3),
+    (torch.float16, "ieee"): Tolerance(1.0 - 1e-4, 5e-3),
+    (torch.bfloat16, "ieee"): Tolerance(1.0 - 1e-4, 2e-2),
+}
 # The build's own bar for 16-bit inputs: relative Frobenius <= 1e-2 against the
 # fp32/fp64 reference on identical inputs.
 NORTH_STAR_REL_FRO = 1e-2
@@ -117,3 +123,32 @@ def assert_close_to_oracle(name, got, want, tol: Tolerance, *, rel_fro_max=None)
     assert c >= tol.cos_min, f"{name}: cos {c:.7f} < {tol.cos_min}"
     assert f <= bound, f"{name}: rel-fro {f:.3e} > {bound:.1e} (max-abs {np.abs(g - want).max():.3e})"
     return c, f
+
+
+def apb_inputs(b, m, h, u, v, dh, zc, dtype=torch.float32, *, seed=0, biases=False, device="cpu"):
+    """Attention-with-pair-bias op tensors (the reference's testutil/attention_pair_bias.py:
+    make_op_tensors layout): s, pre-projected q/k/v, pair rep z and the weights."""
+    g = gen(seed)
+    d = h * dh
+    t = {
+        "s": randn((b * m, u, d), g=g),
+        "q": randn((b * m, h, u, dh), g=g),
+        "k": randn((b * m, h, v, dh), g=g),
+        "v": randn((b * m, h, v, dh), g=g),
+        "z": randn((b, u, v, zc), g=g),
+        "proj_z_weight": randn((h, zc), g=g, scale=zc ** -0.5),
+        "ln_z_weight": 1.0 + 0.1 * randn((zc,), g=g),
+        "proj_g_weight": randn((d, d), g=g, scale=d ** -0.5),
+        "proj_o_weight": randn((d, d), g=g, scale=d ** -0.5),
+    }
+    if biases:
+        t["proj_g_bias"] = randn((d,), g=g, scale=0.1)
+        t["proj_o_bias"] = randn((d,), g=g, scale=0.1)
+    return {k: x.to(dtype).to(device) for k, x in t.items()}
+
+
+def apb_key_mask(batch, v, *, seed=0, frac_keep=0.9, dtype=torch.float32, device="cpu"):
+    """``[batch, V]`` 0 / 1 key mask, key 0 always kept."""
+    m = torch.rand(batch, v, generator=gen(seed)) < frac_keep
+    m[:, 0] = True
+    return m.to(dtype).to(device)

@@ -201,3 +201,58 @@ def test_operators_have_fake_implementations():
                                            gw, None, 1e-5)
         assert out.shape == x.shape and out.dtype == x.dtype
 
+
+
+# ---------------------------------------------------------------- attention with pair bias
+def test_attention_pair_bias_signature_matches_the_reference():
+    """_attention_pair_bias.py:11-30: positional s, q, k, v, z, then keyword-only options."""
+    from geometric_nn_ops_torch.triangle import attention_pair_bias
+
+    sig = inspect.signature(attention_pair_bias)
+    names = list(sig.parameters)
+    assert names[:5] == ["s", "q", "k", "v", "z"]
+    assert names[5:] == ["proj_g_weight", "proj_o_weight", "proj_z_weight", "ln_z_weight", "proj_g_bias",
+                         "proj_o_bias", "mask", "scale", "inf", "eps", "z_is_projected", "return_z_proj"]
+    assert all(sig.parameters[n].kind is inspect.Parameter.KEYWORD_ONLY for n in names[5:])
+    assert sig.parameters["eps"].default == 1e-5 and sig.parameters["inf"].default is None
+
+
+@pytest.mark.parametrize("mask_kind", [None, "batch", "copy"])
+def test_attention_pair_bias_cpu_matches_oracle(mask_kind):
+    from geometric_nn_ops_torch.triangle import attention_pair_bias
+    from helpers import apb_inputs, apb_key_mask
+
+    t = apb_inputs(2, 2, 3, 10, 10, 8, 16, seed=4, biases=True)
+    mask = None if mask_kind is None else apb_key_mask(2 if mask_kind == "batch" else 4, 10, seed=6, frac_keep=0.6)
+    out, pz = attention_pair_bias(**t, mask=mask, inf=1e6, return_z_proj=True)
+    want, want_pz = O.attention_pair_bias(**{k: to_np(v) for k, v in t.items()},
+                                          mask=None if mask is None else to_np(mask), inf=1e6, return_z_proj=True)
+    assert O.rel_fro(to_np(out), want) < 1e-5 and O.rel_fro(to_np(pz), want_pz) < 1e-5
+    cached, none = attention_pair_bias(**{**t, "z": pz}, mask=mask, inf=1e6, z_is_projected=True)
+    assert none is None and torch.equal(cached, out)
+
+
+def test_attention_pair_bias_errors():
+    from geometric_nn_ops_torch.triangle import attention_pair_bias
+    from helpers import apb_inputs
+
+    t = apb_inputs(2, 2, 2, 6, 6, 8, 8, seed=1)
+    with pytest.raises(ValueError, match="multiple of z batch"):
+        attention_pair_bias(**{**t, "z": torch.randn(3, 6, 6, 8)})
+    with pytest.raises(ValueError, match="must be B=2 or BM=4"):
+        attention_pair_bias(**t, mask=torch.ones(3, 6))
+
+
+def test_attention_pair_bias_operator_fake():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    import geometric_nn_ops_torch._ops  # noqa: F401
+
+    with FakeTensorMode():
+        s = torch.empty(6, 16, 32, dtype=torch.bfloat16)
+        q = torch.empty(6, 4, 16, 8, dtype=torch.bfloat16)
+        z = torch.empty(2, 16, 16, 24, dtype=torch.bfloat16)
+        w = torch.empty(32, 32, dtype=torch.bfloat16)
+        out, pz = torch.ops.gnn_amd.attention_pair_bias_fwd(s, q, q, q, z, w, w, torch.empty(4, 24, dtype=s.dtype),
+                                                             None, None, None, None, None, None, 1e-5, False)
+        assert out.shape == (6, 16, 32) and pz.shape == (2, 4, 16, 16)

@@ -48,10 +48,13 @@ def _c_layout():
     int main(void) {
       printf("gnn_triattn_args %zu\n", sizeof(gnn_triattn_args));
       printf("gnn_trimul_args %zu\n", sizeof(gnn_trimul_args));
+      printf("gnn_pair_bias_args %zu\n", sizeof(gnn_pair_bias_args));
       P(gnn_triattn_args, lse) P(gnn_triattn_args, D) P(gnn_triattn_args, bias_stride)
       P(gnn_triattn_args, mask_stride) P(gnn_triattn_args, scale) P(gnn_triattn_args, precision)
       P(gnn_trimul_args, mask_stride) P(gnn_trimul_args, workspace_bytes) P(gnn_trimul_args, Ch)
       P(gnn_trimul_args, eps) P(gnn_trimul_args, precision)
+      P(gnn_pair_bias_args, out) P(gnn_pair_bias_args, H) P(gnn_pair_bias_args, out_stride)
+      P(gnn_pair_bias_args, eps) P(gnn_pair_bias_args, dtype)
       return 0;
     }
     """
@@ -67,11 +70,14 @@ def test_ctypes_structs_match_c_layout(tmp_path):
                                                                 check=True).stdout.splitlines())
     assert int(lines["gnn_triattn_args"]) == ctypes.sizeof(_lib.TriAttnArgs)
     assert int(lines["gnn_trimul_args"]) == ctypes.sizeof(_lib.TrimulArgs)
+    assert int(lines["gnn_pair_bias_args"]) == ctypes.sizeof(_lib.PairBiasArgs)
+    classes = {"gnn_triattn_args": _lib.TriAttnArgs, "gnn_trimul_args": _lib.TrimulArgs,
+               "gnn_pair_bias_args": _lib.PairBiasArgs}
     for key, val in lines.items():
         if "." not in key:
             continue
         struct, field = key.split(".")
-        cls = _lib.TriAttnArgs if struct == "gnn_triattn_args" else _lib.TrimulArgs
+        cls = classes[struct]
         assert getattr(cls, field).offset == int(val), key
 
 
@@ -131,3 +137,25 @@ def test_missing_library_raises(monkeypatch, tmp_path):
     monkeypatch.delenv("GNN_HIP_LIB")
     monkeypatch.setattr(_lib, "_lib", None)
     _lib.load()
+
+
+def test_pair_bias_argument_errors():
+    lib = _lib.load()
+    assert lib.gnn_pair_bias_proj(None, None) == _lib.GNN_ERR_ARG
+    a = _lib.PairBiasArgs()
+    assert lib.gnn_pair_bias_proj(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    assert b"required" in lib.gnn_last_error()
+    a.z = a.proj_w = a.out = 4096
+    a.B, a.U, a.V, a.H = 1, 8, 8, 4
+    a.Zc = 0
+    assert lib.gnn_pair_bias_proj(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    assert b"positive" in lib.gnn_last_error()
+    a.Zc = 12
+    assert lib.gnn_pair_bias_proj(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
+    assert b"multiple of 8" in lib.gnn_last_error()
+    a.Zc, a.H = 256, 64
+    assert lib.gnn_pair_bias_proj(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
+    assert b"8192" in lib.gnn_last_error()
+    a.z = 4100
+    assert lib.gnn_pair_bias_proj(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    assert b"aligned" in lib.gnn_last_error()

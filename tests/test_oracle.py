@@ -293,3 +293,142 @@ def test_oracle_agrees_with_torch_fallback():
     for direction in ("outgoing", "incoming"):
         got = trimul_torch(t(x), direction, t(m), **{kk: t(vv) for kk, vv in w.items()}).numpy()
         np.testing.assert_allclose(got, O.trimul(x, direction, m, **w), rtol=1e-11, atol=1e-11)
+
+
+# ------------------------------------------------------------- attention with pair bias
+def _apb_inputs(B=2, M=2, H=2, U=3, V=3, DH=2, Zc=4, seed=0, biases=True):
+    rng = np.random.default_rng(seed)
+    D = H * DH
+    t = {
+        "s": rng.standard_normal((B * M, U, D)),
+        "q": rng.standard_normal((B * M, H, U, DH)),
+        "k": rng.standard_normal((B * M, H, V, DH)),
+        "v": rng.standard_normal((B * M, H, V, DH)),
+        "z": rng.standard_normal((B, U, V, Zc)),
+        "proj_z_weight": rng.standard_normal((H, Zc)) * Zc ** -0.5,
+        "ln_z_weight": 1.0 + 0.1 * rng.standard_normal(Zc),
+        "proj_g_weight": rng.standard_normal((D, D)) * D ** -0.5,
+        "proj_o_weight": rng.standard_normal((D, D)) * D ** -0.5,
+    }
+    if biases:
+        t["proj_g_bias"] = 0.1 * rng.standard_normal(D)
+        t["proj_o_bias"] = 0.1 * rng.standard_normal(D)
+    return t
+
+
+def _apb_loops(t, mask=None, scale=None, inf=1e18, eps=1e-5):
+    """Element-by-element restatement in pure Python (math module only)."""
+    s, q, k, v, z = (t[n].tolist() for n in ("s", "q", "k", "v", "z"))
+    BM, H, U, DH = t["q"].shape
+    V = t["k"].shape[2]
+    B, Zc = t["z"].shape[0], t["z"].shape[3]
+    M = BM // B
+    D = H * DH
+    scale = DH ** -0.5 if scale is None else scale
+    wz, lw = t["proj_z_weight"].tolist(), t["ln_z_weight"].tolist()
+    wg, wo = t["proj_g_weight"].tolist(), t["proj_o_weight"].tolist()
+    bg = t.get("proj_g_bias", np.zeros(D)).tolist()
+    bo = t.get("proj_o_bias", np.zeros(D)).tolist()
+    bias = [[[[0.0] * V for _ in range(U)] for _ in range(H)] for _ in range(B)]
+    for b in range(B):
+        for u in range(U):
+            for j in range(V):
+                x = z[b][u][j]
+                mu = sum(x) / Zc
+                var = sum((e - mu) ** 2 for e in x) / Zc
+                zn = [(e - mu) / math.sqrt(var + eps) * lw[c] for c, e in enumerate(x)]
+                for h in range(H):
+                    bias[b][h][u][j] = sum(zn[c] * wz[h][c] for c in range(Zc))
+    out = [[[0.0] * D for _ in range(U)] for _ in range(BM)]
+    for n in range(BM):
+        b = n // M
+        o = [[0.0] * D for _ in range(U)]
+        for h in range(H):
+            for u in range(U):
+                logit = []
+                for j in range(V):
+                    l_ = sum(q[n][h][u][d] * k[n][h][j][d] for d in range(DH)) * scale + bias[b][h][u][j]
+                    if mask is not None:
+                        keep = mask[b][j] if len(mask) == B else mask[n][j]
+                        l_ += (keep - 1.0) * inf
+                    logit.append(l_)
+                mx = max(logit)
+                e = [math.exp(x - mx) for x in logit]
+                tot = sum(e)
+                for d in range(DH):
+                    o[u][h * DH + d] = sum(e[j] / tot * v[n][h][j][d] for j in range(V))
+        for u in range(U):
+            gated = [o[u][c] / (1.0 + math.exp(-(sum(s[n][u][i] * wg[c][i] for i in range(D)) + bg[c])))
+                     for c in range(D)]
+            for c in range(D):
+                out[n][u][c] = sum(gated[i] * wo[c][i] for i in range(D)) + bo[c]
+    return np.array(out), np.array(bias)
+
+
+@pytest.mark.parametrize("mask_kind", [None, "batch", "copy"])
+def test_attention_pair_bias_matches_loops(mask_kind):
+    t = _apb_inputs()
+    B, M, V = 2, 2, 3
+    mask = None
+    if mask_kind == "batch":
+        mask = np.array([[1.0, 0.0, 1.0], [1.0, 1.0, 0.0]])
+    elif mask_kind == "copy":
+        mask = np.array([[1.0, 0.0, 1.0], [0.0, 1.0, 1.0], [1.0, 1.0, 0.0], [1.0, 0.0, 0.0]])
+    out, pz = O.attention_pair_bias(**t, mask=mask, scale=0.7, inf=30.0, return_z_proj=True)
+    want, want_pz = _apb_loops(t, None if mask is None else mask.tolist(), scale=0.7, inf=30.0)
+    np.testing.assert_allclose(pz, want_pz, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(out, want, rtol=1e-11, atol=1e-12)
+    assert out.shape == (B * M, 3, 4) and V == 3
+
+
+def test_attention_pair_bias_is_triangle_attention_with_multiplicity_rows():
+    """The attention core equals triangle attention with N_seq = M: q [B*M, H, U, DH] is the
+    canonical [B, M, U, H, DH] by a permutation, the bias is shared across the M rows."""
+    B, M, H, U, DH, Zc = 2, 3, 2, 5, 4, 6
+    t = _apb_inputs(B=B, M=M, H=H, U=U, V=U, DH=DH, Zc=Zc, seed=3, biases=False)
+    D = H * DH
+    t["proj_g_weight"] = np.zeros((D, D))  # gate = 1/2
+    t["proj_o_weight"] = 2.0 * np.eye(D)   # out = o
+    keep = (np.random.default_rng(5).random((B, U)) < 0.7).astype(np.float64)
+    keep[:, 0] = 1.0
+    out, pz = O.attention_pair_bias(**t, mask=keep, return_z_proj=True)
+    canon = lambda a: np.transpose(a.reshape(B, M, H, U, DH), (0, 1, 3, 2, 4))  # noqa: E731
+    o = O.triangle_attention(canon(t["q"]), canon(t["k"]), canon(t["v"]), bias=pz,
+                             mask=keep.astype(bool)[:, None, None, None, :])
+    np.testing.assert_allclose(out, o.reshape(B * M, U, D), rtol=1e-12, atol=1e-12)
+
+
+def test_attention_pair_bias_known_answers():
+    t = _apb_inputs(B=2, M=3, H=2, U=4, V=4, DH=3, Zc=5, seed=7)
+    mask = np.ones((2, 4))
+    mask[0, 2] = mask[1, 1] = 0.0
+    out, pz = O.attention_pair_bias(**t, mask=mask, return_z_proj=True)
+    # masked keys: v (and k) noise there changes nothing
+    noisy = dict(t)
+    for name in ("v", "k"):
+        a = t[name].copy().reshape(2, 3, 2, 4, 3)
+        a[0, :, :, 2] += 1e3
+        a[1, :, :, 1] -= 1e3
+        noisy[name] = a.reshape(t[name].shape)
+    np.testing.assert_array_equal(O.attention_pair_bias(**noisy, mask=mask)[0], out)
+    # the cached bias reproduces the uncached call exactly
+    cached, _ = O.attention_pair_bias(**{**t, "z": pz}, mask=mask, z_is_projected=True)
+    np.testing.assert_array_equal(cached, out)
+    # a per-batch mask equals its per-copy repetition
+    np.testing.assert_array_equal(O.attention_pair_bias(**t, mask=np.repeat(mask, 3, axis=0))[0], out)
+    # copies with equal inputs give equal outputs; batch elements differ
+    same = dict(t)
+    for name in ("s", "q", "k", "v"):
+        g = t[name].reshape(2, 3, *t[name].shape[1:])
+        same[name] = np.broadcast_to(g[:, :1], g.shape).reshape(t[name].shape).copy()
+    o2 = O.attention_pair_bias(**same)[0].reshape(2, 3, 4, 6)
+    np.testing.assert_array_equal(o2[:, 1], o2[:, 0])
+    assert not np.array_equal(o2[0, 0], o2[1, 0])
+    # zero q and a zero pair bias: uniform attention, o = mean(v)
+    flat = {**t, "q": np.zeros_like(t["q"]), "z": np.zeros((2, 2, 4, 4))}
+    base = O.attention_pair_bias(**flat, z_is_projected=True)[0]
+    o_mean = np.transpose(t["v"].mean(axis=2, keepdims=True).repeat(4, axis=2), (0, 2, 1, 3)).reshape(6, 4, 6)
+    g = 1.0 / (1.0 + np.exp(-(t["s"] @ t["proj_g_weight"].T + t["proj_g_bias"])))
+    np.testing.assert_allclose(base, (o_mean * g) @ t["proj_o_weight"].T + t["proj_o_bias"], rtol=1e-12)
+    with pytest.raises(ValueError, match="multiple"):
+        O.attention_pair_bias(**{**t, "z": t["z"][:1].repeat(4, axis=0)})

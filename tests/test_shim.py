@@ -1,0 +1,151 @@
+"""The cuequivariance_ops_torch shim (geometric-nn-ops_amd/cuequivariance_ops_torch), after
+the reference's hipequivariance_ops_torch/tests: import surface and deep-imported constants
+(test_import_compat.py), the installation guard, cueq's triangle-attention layout and rank,
+the trimul precision policy (test_precision_check.py) and the attention_pair_bias argument
+mapping. cuequivariance_torch itself is not installed here, so the shim's functions are
+called directly; the GPU cases check they give exactly what the public ops give."""
+
+import importlib
+import warnings
+from unittest import mock
+
+import pytest
+import torch
+
+import cuequivariance_ops_torch as cueq
+from cuequivariance_ops_torch import _guard
+from geometric_nn_ops_torch.triangle import attention_pair_bias, triangle_attention, triangle_multiplicative_update
+from helpers import apb_inputs, apb_key_mask, pair_input, trimul_weights
+
+# the package rebinds the submodule names to the functions, as cueq's callers expect
+tmu_module = importlib.import_module("cuequivariance_ops_torch.triangle_multiplicative_update")
+
+
+class fp32_precision:
+    def __init__(self, value):
+        self.value = value
+
+    def __enter__(self):
+        self.old = torch.backends.cuda.matmul.fp32_precision
+        torch.backends.cuda.matmul.fp32_precision = self.value
+
+    def __exit__(self, *exc):
+        torch.backends.cuda.matmul.fp32_precision = self.old
+
+
+def test_import_surface():
+    assert set(cueq.__all__) == {"attention_pair_bias", "triangle_attention", "triangle_multiplicative_update",
+                                 "TriMulPrecision"}
+    from cuequivariance_ops_torch.attention_pair_bias_torch import CUEQ_ATTENTION_PAIR_BIAS_FALLBACK_THRESHOLD
+    from cuequivariance_ops_torch.triangle_attention import CUEQ_TRIATTN_FALLBACK_THRESHOLD
+    from cuequivariance_ops_torch.triangle_multiplicative_update import CUEQ_TRIMUL_FALLBACK_THRESHOLD
+
+    assert CUEQ_TRIATTN_FALLBACK_THRESHOLD > 0 and CUEQ_TRIMUL_FALLBACK_THRESHOLD > 0
+    assert CUEQ_ATTENTION_PAIR_BIAS_FALLBACK_THRESHOLD > 1 << 30
+    assert [m.value for m in cueq.TriMulPrecision] == [-1, 0, 1, 2, 3]
+
+
+def test_guard_rejects_the_real_wheel_and_warns_on_version():
+    with mock.patch.object(_guard, "installed", return_value={"cuequivariance-ops-torch-cu12", "torch"}):
+        with pytest.raises(RuntimeError, match="cuequivariance-ops-torch-cu12"):
+            _guard.check()
+    with mock.patch.object(_guard, "installed", return_value={"torch"}), \
+            mock.patch.object(_guard.metadata, "version", return_value="0.8.0"):
+        with pytest.warns(RuntimeWarning, match="0.9.1"):
+            _guard.check()
+    with mock.patch.object(_guard, "installed", return_value={"torch"}), \
+            mock.patch.object(_guard.metadata, "version", return_value="0.9.1"), warnings.catch_warnings():
+        warnings.simplefilter("error")
+        _guard.check()
+
+
+def _cueq_attention_inputs(device="cpu", dtype=torch.float32, batch=True):
+    g = torch.Generator().manual_seed(0)
+    B, N, H, S, D = 1, 3, 4, 24, 16
+    shape = (B, N, H, S, D) if batch else (N, H, S, D)
+    q, k, v = (torch.randn(*shape, generator=g).to(device, dtype) for _ in range(3))
+    bias = (0.3 * torch.randn(1, 1, H, S, S, generator=g)).to(device, dtype)
+    mask = torch.rand(*((B,) if batch else ()), N, 1, 1, S, generator=g) < 0.8
+    mask[..., 0] = True
+    return q, k, v, bias, mask.to(device)
+
+
+def test_triangle_attention_layout_and_rank():
+    q, k, v, bias, mask = _cueq_attention_inputs()
+    out = cueq.triangle_attention(q, k, v, bias, mask=mask.float(), scale=0.3)
+    swap = lambda t: t.transpose(-2, -3)  # noqa: E731
+    want = swap(triangle_attention(swap(q), swap(k), swap(v), bias, mask, 0.3))
+    assert out.shape == q.shape and torch.equal(out, want)
+    qb, kb, vb, bb, mb = _cueq_attention_inputs(batch=False)
+    out4 = cueq.triangle_attention(qb, kb, vb, bb[0], mask=mb)
+    assert out4.dim() == 5 and out4.shape[0] == 1
+    with pytest.raises(NotImplementedError, match="return_aux"):
+        cueq.triangle_attention(q, k, v, bias, return_aux=True)
+
+
+def test_trimul_precision_policy():
+    check = tmu_module.check_precision
+    with fp32_precision("ieee"), warnings.catch_warnings():
+        warnings.simplefilter("error")
+        for ok in (None, "none", "DEFAULT", cueq.TriMulPrecision.NONE, 0, "ieee", cueq.TriMulPrecision.IEEE, 3):
+            check(ok)
+    with fp32_precision("ieee"), pytest.warns(UserWarning, match="full fp32"):
+        check("tf32")
+    with fp32_precision("tf32"):
+        check("tf32")
+        check(cueq.TriMulPrecision.TF32)
+        with pytest.raises(ValueError, match="fp32_precision"):
+            check("ieee")
+        with pytest.raises(ValueError):
+            check(cueq.TriMulPrecision.TF32x3)
+
+
+def test_trimul_matches_the_public_op_on_cpu():
+    x, mask = pair_input(1, 12, 32, torch.float32, seed=2)
+    w = trimul_weights(32, 32, torch.float32, seed=3, biases=True)
+    out = cueq.triangle_multiplicative_update(x, "incoming", mask, precision="default", **w)
+    assert torch.equal(out, triangle_multiplicative_update(x, "incoming", mask, **w))
+
+
+def test_attention_pair_bias_argument_mapping():
+    t = apb_inputs(2, 2, 4, 12, 12, 8, 16, seed=5, biases=True)
+    mask = apb_key_mask(2, 12, seed=6, frac_keep=0.6)
+    kw = dict(mask=mask, num_heads=4, w_proj_z=t["proj_z_weight"], w_proj_g=t["proj_g_weight"],
+              w_proj_o=t["proj_o_weight"], w_ln_z=t["ln_z_weight"], b_proj_g=t["proj_g_bias"],
+              b_proj_o=t["proj_o_bias"])
+    out, pz = cueq.attention_pair_bias(t["s"], t["q"], t["k"], t["v"], t["z"], **kw)
+    want, want_pz = attention_pair_bias(t["s"], t["q"], t["k"], t["v"], t["z"], proj_g_weight=t["proj_g_weight"],
+                                        proj_o_weight=t["proj_o_weight"], proj_z_weight=t["proj_z_weight"],
+                                        ln_z_weight=t["ln_z_weight"], proj_g_bias=t["proj_g_bias"],
+                                        proj_o_bias=t["proj_o_bias"], mask=mask, inf=1e6, return_z_proj=True)
+    assert torch.equal(out, want) and torch.equal(pz, want_pz)
+    with pytest.warns(UserWarning, match="b_ln_z is ignored"):
+        cueq.attention_pair_bias(t["s"], t["q"], t["k"], t["v"], t["z"], **kw, b_ln_z=torch.ones(16))
+    with pytest.raises(ValueError, match="num_heads=3"):
+        cueq.attention_pair_bias(t["s"], t["q"], t["k"], t["v"], t["z"], **{**kw, "num_heads": 3})
+    cached, _ = cueq.attention_pair_bias(t["s"], t["q"], t["k"], t["v"], pz, **kw, is_cached_z_proj=True)
+    assert torch.equal(cached, out)
+
+
+@pytest.mark.gpu
+def test_shim_runs_the_hip_kernels_exactly():
+    q, k, v, bias, mask = _cueq_attention_inputs("cuda", torch.bfloat16)
+    swap = lambda t: t.transpose(-2, -3)  # noqa: E731
+    with torch.no_grad():
+        out = cueq.triangle_attention(q, k, v, bias, mask=mask)
+        want = swap(triangle_attention(swap(q), swap(k), swap(v), bias, mask))
+    assert torch.equal(out, want)
+    x, m = pair_input(1, 40, 64, torch.bfloat16, seed=2, device="cuda")
+    w = trimul_weights(64, 64, torch.bfloat16, seed=3, device="cuda")
+    with torch.no_grad():
+        assert torch.equal(cueq.triangle_multiplicative_update(x, "outgoing", m, **w),
+                           triangle_multiplicative_update(x, "outgoing", m, **w))
+    t = {k_: v_.to("cuda", torch.bfloat16) for k_, v_ in apb_inputs(1, 2, 4, 32, 32, 16, 16, seed=9).items()}
+    with torch.no_grad():
+        out, pz = cueq.attention_pair_bias(t["s"], t["q"], t["k"], t["v"], t["z"], None, 4, t["proj_z_weight"],
+                                           t["proj_g_weight"], t["proj_o_weight"], t["ln_z_weight"])
+        want, want_pz = attention_pair_bias(t["s"], t["q"], t["k"], t["v"], t["z"],
+                                            proj_g_weight=t["proj_g_weight"], proj_o_weight=t["proj_o_weight"],
+                                            proj_z_weight=t["proj_z_weight"], ln_z_weight=t["ln_z_weight"],
+                                            inf=1e6, return_z_proj=True)
+    assert torch.equal(out, want) and torch.equal(pz, want_pz)

@@ -340,3 +340,26 @@ def test_config_c4_n768_ragged():
     rows = [0, 5, int(lengths.argmin()), int(lengths.argmax()), 400, 767]
     _rows_vs_oracle(t, mask, rows, D**-0.5, TRIANGLE_ATTENTION_TOL[torch.bfloat16, "ieee"],
                     rel_fro_max=NORTH_STAR_REL_FRO)
+
+
+@DTYPES
+@pytest.mark.parametrize("n", [100, 37], ids=["n100", "n37"])
+def test_bias_pitch_padding_does_not_reach_valid_keys(dtype, n):
+    """A bias view whose row pitch runs past N (here filled with NaN there) gives exactly the
+    result of a contiguous bias: the 16-bit kernels add the bias with an identity-fragment
+    MFMA, so a padding value loaded with the last keys must be zeroed, not just masked."""
+    from geometric_nn_ops_torch.triangle import triangle_attention
+
+    B, S, H, D = 1, 3, 2, 32
+    t = attention_inputs(B, S, n, H, D, dtype, seed=13, bias_scale=0.5, device=DEV)
+    pitch = (n + 7) // 8 * 8
+    storage = torch.full((B, 1, H, n, pitch), float("nan"), device=DEV, dtype=dtype)
+    storage[..., :n] = t["bias"]
+    padded = storage[..., :n]
+    assert padded.stride(-2) == pitch and pitch > n
+    mask = key_mask(B, S, n, seed=3, device=DEV)
+    with torch.no_grad():
+        got = triangle_attention(t["q"], t["k"], t["v"], padded, mask)
+        want = triangle_attention(t["q"], t["k"], t["v"], t["bias"].contiguous(), mask)
+    assert torch.isfinite(got).all()
+    torch.testing.assert_close(got, want, rtol=0, atol=0)
