@@ -77,6 +77,32 @@ int gnn_triattn_fwd(const gnn_triattn_args* args, void* stream) {
   return hip_status((hipError_t)rc, "triangle_attention");
 }
 
+int gnn_triattn_bwd(const gnn_triattn_bwd_args* args, void* stream) {
+  if (!args) return set_error(GNN_ERR_ARG, "triangle_attention backward: args is NULL");
+  const gnn_triattn_bwd_args& a = *args;
+  if (!a.q || !a.k || !a.v || !a.o || !a.dout || !a.lse || !a.dq || !a.dk || !a.dv || !a.delta)
+    return set_error(GNN_ERR_ARG, "triangle_attention backward: q, k, v, o, dout, lse, dq, dk, dv and delta are required");
+  if (a.B < 1 || a.S < 1 || a.N < 1 || a.H < 1 || a.D < 1)
+    return set_error(GNN_ERR_ARG, "triangle_attention backward: B, N_seq, N_res, H and D must be positive");
+  if (a.D % 8 != 0)
+    return set_error(GNN_ERR_ARG, "triangle_attention backward: D must be a multiple of 8 (pad on the host)");
+  const int64_t* st[5] = {a.q_stride, a.k_stride, a.v_stride, a.o_stride, a.do_stride};
+  const void* ptr[5] = {a.q, a.k, a.v, a.o, a.dout};
+  for (int t = 0; t < 5; ++t) {
+    if (!aligned(ptr[t], 16))
+      return set_error(GNN_ERR_ARG, "triangle_attention backward: q/k/v/o/dout must be 16-byte aligned");
+    for (int d = 0; d < 4; ++d)
+      if (st[t][d] % 8 != 0)
+        return set_error(GNN_ERR_ARG, "triangle_attention backward: q/k/v/o/dout strides must be multiples of 8 elements");
+  }
+  if (a.bias && (a.bias_stride[3] != 1 || a.bias_stride[2] % 8 != 0 || !aligned(a.bias, 16)))
+    return set_error(GNN_ERR_ARG, "triangle_attention backward: bias needs unit key stride, a query stride that is a "
+                                  "multiple of 8 and 16-byte alignment");
+  int rc = triattn_bwd(a, (hipStream_t)stream);
+  if (rc < 0) return rc;
+  return hip_status((hipError_t)rc, "triangle_attention backward");
+}
+
 size_t gnn_trimul_workspace_bytes(int64_t B, int64_t N, int64_t C, int64_t Ch, int32_t dtype,
                                   size_t off[4]) {
   const TrimulLayout L = trimul_layout(B, N, C, Ch, dtype);

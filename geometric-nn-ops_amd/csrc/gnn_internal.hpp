@@ -15,6 +15,7 @@ int set_error(int code, const char* msg);
 int persistent_grid(const void* fn, int threads, size_t smem);
 
 int triattn_fwd(const gnn_triattn_args& a, hipStream_t stream);
+int triattn_bwd(const gnn_triattn_bwd_args& a, hipStream_t stream);
 
 // Row-resident attention (16-bit inputs, head dim <= 32, bounded N_res): the whole row of
 // K and V staged in LDS, no barrier in the key loop.

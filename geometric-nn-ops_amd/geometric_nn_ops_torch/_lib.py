@@ -54,6 +54,45 @@ class TriAttnArgs(ctypes.Structure):
     ]
 
 
+class TriAttnBwdArgs(ctypes.Structure):
+    """Mirror of ``gnn_triattn_bwd_args``."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("dout", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("mask", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("dq", ctypes.c_void_p),
+        ("dk", ctypes.c_void_p),
+        ("dv", ctypes.c_void_p),
+        ("dbias", ctypes.c_void_p),
+        ("delta", ctypes.c_void_p),
+        ("B", ctypes.c_int64),
+        ("S", ctypes.c_int64),
+        ("N", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("D", ctypes.c_int64),
+        ("q_stride", I64x4),
+        ("k_stride", I64x4),
+        ("v_stride", I64x4),
+        ("o_stride", I64x4),
+        ("do_stride", I64x4),
+        ("dq_stride", I64x4),
+        ("dk_stride", I64x4),
+        ("dv_stride", I64x4),
+        ("bias_stride", I64x4),
+        ("mask_stride", I64x3),
+        ("scale", ctypes.c_float),
+        ("mask_value", ctypes.c_float),
+        ("dtype", ctypes.c_int32),
+        ("precision", ctypes.c_int32),
+    ]
+
+
 class TrimulArgs(ctypes.Structure):
     """Mirror of ``gnn_trimul_args``."""
 
@@ -109,6 +148,7 @@ class PairBiasArgs(ctypes.Structure):
 # Every symbol include/gnn_triangle.h declares, with its ctypes signature.
 _SIGNATURES = {
     "gnn_triattn_fwd": (ctypes.c_int, [ctypes.POINTER(TriAttnArgs), ctypes.c_void_p]),
+    "gnn_triattn_bwd": (ctypes.c_int, [ctypes.POINTER(TriAttnBwdArgs), ctypes.c_void_p]),
     "gnn_trimul_workspace_bytes": (
         ctypes.c_size_t,
         [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,

@@ -42,6 +42,19 @@ def _prepare(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+def _prepare_bias(bias: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """``[B, 1, H, N, N]`` bias in ``dtype`` with unit key stride, a query pitch that is a
+    multiple of 8 elements and a 16-byte aligned base (zero padding past N)."""
+    bias = bias.to(dtype)
+    if bias.stride(-1) == 1 and bias.stride(-2) % 8 == 0 and bias.data_ptr() % 16 == 0:
+        return bias
+    B, _, H, N, _ = bias.shape
+    pitch = (N + 7) // 8 * 8
+    padded = torch.zeros((B, 1, H, N, pitch), device=bias.device, dtype=bias.dtype)
+    padded[..., :N] = bias
+    return padded[..., :N]
+
+
 def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=False, use_exp2=False,
                            lse=None, mask_value=None):
     """Triangle attention forward on the canonical 5D layout.
@@ -82,14 +95,7 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
     args.v_stride = _lib.I64x4(*vk.stride()[:4])
     args.o_stride = _lib.I64x4(*o.stride()[:4])
     if bias is not None:
-        bias = bias.to(q.dtype)
-        if not (bias.stride(-1) == 1 and bias.stride(-2) % 8 == 0 and bias.data_ptr() % 16 == 0):
-            # unit key stride and a query pitch that is a multiple of 8 elements; keys
-            # past N in the padded pitch are never read
-            pitch = (N + 7) // 8 * 8
-            padded = torch.zeros((B, 1, H, N, pitch), device=bias.device, dtype=bias.dtype)
-            padded[..., :N] = bias
-            bias = padded
+        bias = _prepare_bias(bias, q.dtype)
         args.bias = bias.data_ptr()
         args.bias_stride = _lib.I64x4(bias.stride(0), bias.stride(2), bias.stride(3), bias.stride(4))
     if mask is not None:
@@ -112,3 +118,59 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
     if Dp != D:
         o = o[..., :D].contiguous()
     return o
+
+
+def backward_supported(q: torch.Tensor) -> bool:
+    """Whether the HIP backward covers these inputs: 16-bit, head dim <= 32 and a multiple of 8."""
+    d = q.shape[-1]
+    return q.dtype in (torch.bfloat16, torch.float16) and d <= 32 and d % 8 == 0
+
+
+def triangle_attention_bwd_hip(q, k, v, o, dout, lse, bias=None, mask=None, scale=None, mask_value=None,
+                               need_dbias=True):
+    """Gradients of the HIP forward: ``(dq, dk, dv, dbias)`` with dq/dk/dv like q and dbias
+    ``[B, 1, H, N, N]`` fp32 (``None`` without a bias or when ``need_dbias`` is false).
+    Replaces EvoformerAttention.backward (triangle_attention.py:1278-1442); ``lse`` is the
+    forward's ``[B, N_seq, H, N]`` natural-log log-sum-exp."""
+    lib = _lib.load()
+    B, S, N, H, D = q.shape
+    if scale is None:
+        scale = D**-0.5
+    qk, kk, vk, ok, dk_ = (_prepare(t) for t in (q, k, v, o, dout.to(q.dtype)))
+    assert qk.shape[-1] == D, "the HIP backward needs a head dim that is a multiple of 8"
+    dq = torch.empty((B, S, N, H, D), device=q.device, dtype=q.dtype)
+    dk = torch.empty_like(dq)
+    dv = torch.empty_like(dq)
+    delta = torch.empty((B, S, H, N), device=q.device, dtype=torch.float32)
+    a = _lib.TriAttnBwdArgs()
+    a.q, a.k, a.v, a.o, a.dout = qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), ok.data_ptr(), dk_.data_ptr()
+    a.lse = lse.contiguous().data_ptr()
+    a.dq, a.dk, a.dv, a.delta = dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr()
+    a.B, a.S, a.N, a.H, a.D = B, S, N, H, D
+    a.q_stride = _lib.I64x4(*qk.stride()[:4])
+    a.k_stride = _lib.I64x4(*kk.stride()[:4])
+    a.v_stride = _lib.I64x4(*vk.stride()[:4])
+    a.o_stride = _lib.I64x4(*ok.stride()[:4])
+    a.do_stride = _lib.I64x4(*dk_.stride()[:4])
+    a.dq_stride = _lib.I64x4(*dq.stride()[:4])
+    a.dk_stride = _lib.I64x4(*dk.stride()[:4])
+    a.dv_stride = _lib.I64x4(*dv.stride()[:4])
+    dbias = None
+    if bias is not None:
+        bias = _prepare_bias(bias, q.dtype)
+        a.bias = bias.data_ptr()
+        a.bias_stride = _lib.I64x4(bias.stride(0), bias.stride(2), bias.stride(3), bias.stride(4))
+        if need_dbias:
+            dbias = torch.empty((B, 1, H, N, N), device=q.device, dtype=torch.float32)
+            a.dbias = dbias.data_ptr()
+    if mask is not None:
+        a.mask = mask.data_ptr()
+        a.mask_stride = _lib.I64x3(mask.stride(0), mask.stride(1), mask.stride(4))
+    a.scale = float(scale)
+    a.mask_value = rounded_mask_value(q.dtype) if mask_value is None else float(mask_value)
+    a.dtype = _lib.DTYPE_CODE[q.dtype]
+    a.precision = _lib.GNN_PREC_IEEE
+    with torch.cuda.device(q.device):
+        rc = lib.gnn_triattn_bwd(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(q.device)))
+    _lib.check(rc, "gnn_triattn_bwd")
+    return dq, dk, dv, dbias

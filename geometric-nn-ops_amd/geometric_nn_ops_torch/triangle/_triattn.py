@@ -7,10 +7,12 @@ fp64 is computed in fp32, and the output has the input's shape and dtype.
 
 Dispatch: the gfx950 HIP kernel serves every forward-only call on a HIP device, through
 the ``gnn_amd::triangle_attention_fwd`` operator (``geometric_nn_ops_torch._ops``).
-Calls that need a backward (grad enabled and some input requires grad), CPU tensors and
-head dims above the kernel's tile take the differentiable torch path instead -- the
-reference has no such path and runs its Triton kernel for all of them. There is no
-fallback when the HIP library is missing: a GPU call then raises.
+Calls that need a backward run the HIP forward (saving the log-sum-exp) and the HIP
+backward kernels (dq, dk, dv and the N_seq-summed pair-bias gradient) for bf16 / fp16 with
+a head dim <= 32 that is a multiple of 8, as the reference runs its Triton forward and
+backward; other grad-requiring calls, CPU tensors and head dims above the forward kernel's
+tile take the differentiable torch path. There is no fallback when the HIP library is
+missing: a GPU call then raises.
 """
 
 import torch
@@ -22,12 +24,38 @@ from ._reference.triangle_attention import triangle_attention_torch
 _KERNEL_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 
 
+def _needs_grad(q, k, v, bias) -> bool:
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, k, v, bias))
+
+
 def _needs_torch_path(q, k, v, bias) -> bool:
     if not q.is_cuda or not _hip.supports(q):
         return True
-    return torch.is_grad_enabled() and any(
-        t is not None and t.requires_grad for t in (q, k, v, bias)
-    )
+    return _needs_grad(q, k, v, bias)
+
+
+class _TriangleAttentionHip(torch.autograd.Function):
+    """HIP forward that keeps the log-sum-exp, HIP backward (reference
+    EvoformerAttention, triangle_attention.py:1091-1442)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, bias, mask, scale):
+        B, S, N, H, _ = q.shape
+        lse = torch.empty((B, S, H, N), device=q.device, dtype=torch.float32)
+        o = _hip.triangle_attention_hip(q, k, v, bias=bias, mask=mask, scale=scale, lse=lse)
+        ctx.save_for_backward(q, k, v, bias, mask, o, lse)
+        ctx.scale = scale
+        ctx.bias_grad = bias is not None and bias.requires_grad
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, bias, mask, o, lse = ctx.saved_tensors
+        dq, dk, dv, dbias = _hip.triangle_attention_bwd_hip(q, k, v, o, do, lse, bias=bias, mask=mask,
+                                                            scale=ctx.scale, need_dbias=ctx.bias_grad)
+        if dbias is not None:
+            dbias = dbias.to(bias.dtype)
+        return dq, dk, dv, dbias, None, None
 
 
 def triangle_attention(
@@ -84,6 +112,10 @@ def triangle_attention(
             mask = mask.reshape(-1, *mask.shape[-4:])
         mask = mask.broadcast_to(batch, n_seq, 1, 1, n_res)
 
+    if q.is_cuda and _needs_grad(q, k, v, bias) and _hip.backward_supported(q) and (
+            k.dtype == q.dtype and v.dtype == q.dtype):
+        o = _TriangleAttentionHip.apply(q, k, v, bias, mask, scale)
+        return o.reshape(orig_shape)
     if _needs_torch_path(q, k, v, bias):
         o = triangle_attention_torch(q, k, v, bias=bias, mask=mask, scale=scale)
         return o.to(orig_dtype).reshape(orig_shape)

@@ -27,6 +27,7 @@
  *                        (geometric_nn_ops_torch/triangle/_reference/trimul.py:44-54, called
  *                        from trimul.py:442)
  *   gnn_trimul_out    -> triton_layernorm(o) + p_out linear + the o*g gate (trimul.py:443-448)
+ *   gnn_triattn_bwd   -> EvoformerAttention.backward (triangle_attention.py:1278-1442)
  *   gnn_pair_bias_proj -> _project_pair_bias of attention_pair_bias
  *                        (geometric_nn_ops_torch/triangle/_reference/attention_pair_bias.py:17-22)
  */
@@ -89,6 +90,51 @@ typedef struct gnn_triattn_args {
 
 /* Replaces the forward launch of EvoformerAttention (triangle_attention.py:1091-1276). */
 int gnn_triattn_fwd(const gnn_triattn_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Triangle attention backward (bf16 / fp16, head dim <= 32).
+ * Given the forward's inputs, its output o, the upstream gradient dout and the forward's
+ * lse (fp32 [B, S, H, N] contiguous, natural log; gnn_triattn_fwd writes it when args->lse
+ * is set), writes dq, dk, dv (input dtype, [B, S, N, H, D] by strides) and, when both bias
+ * and dbias are given, the pair-bias gradient summed over N_seq into dbias (fp32
+ * [B, H, N, N] contiguous). delta is caller-provided fp32 scratch of B * S * H * N floats.
+ * Same layout rules as gnn_triattn_args; scale, mask_value and the mask are the forward's.
+ */
+typedef struct gnn_triattn_bwd_args {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const void* dout;
+  const void* bias;      /* [B,H,N,N] or NULL */
+  const uint8_t* mask;   /* bool [B,S,N] or NULL */
+  const float* lse;      /* fp32 [B,S,H,N] */
+  void* dq;
+  void* dk;
+  void* dv;
+  float* dbias;          /* fp32 [B,H,N,N] or NULL */
+  float* delta;          /* fp32 scratch [B,S,H,N] */
+  int64_t B, S, N, H, D;
+  int64_t q_stride[4];   /* b, s, n, h for every [B,S,N,H,D] tensor (d stride 1) */
+  int64_t k_stride[4];
+  int64_t v_stride[4];
+  int64_t o_stride[4];
+  int64_t do_stride[4];
+  int64_t dq_stride[4];
+  int64_t dk_stride[4];
+  int64_t dv_stride[4];
+  int64_t bias_stride[4]; /* b, h, i, j (j stride must be 1) */
+  int64_t mask_stride[3]; /* b, s, j */
+  float scale;
+  float mask_value;
+  int32_t dtype;
+  int32_t precision;
+} gnn_triattn_bwd_args;
+
+/* Replaces the backward of EvoformerAttention
+ * (geometric_nn_ops_torch/triangle/_kernels/triangle_attention.py:1278-1442: the
+ * _attn_bwd_preprocess, _attn_bwd_dk_dv and _attn_bwd_dbias_dq launches). */
+int gnn_triattn_bwd(const gnn_triattn_bwd_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * Triangle multiplicative update forward (reference math:

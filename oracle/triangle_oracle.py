@@ -11,6 +11,8 @@ Reference files followed (paths relative to AMDResearch/geometric-nn-ops):
                                         geometric_nn_ops_torch/triangle/_reference/trimul.py:27-97
   * layer_norm semantics                torch.nn.functional.layer_norm (biased variance,
                                         1/sqrt(var + eps)), called at _reference/trimul.py:85,94
+  * triangle_attention_grad (dq, dk, dv, N_seq-summed dbias): the autograd of
+    _reference/triangle_attention.py:11-44 written out
   * attention_pair_bias (pair-bias projection, multiplicity broadcast, key mask with a
     caller-given magnitude, gate from s, output projection)
                                         geometric_nn_ops_torch/triangle/_reference/attention_pair_bias.py:17-89
@@ -26,7 +28,8 @@ stated sentinel values; attention_pair_bias against a pure-Python per-element lo
 sizes, against triangle_attention with N_seq = the multiplicity (the shared-bias
 identity), and the reference's known answers (masked keys ignored, cached bias equal to the
 recomputed one, copies with equal inputs equal, a per-batch mask equal to its per-copy
-repetition).
+repetition); triangle_attention_grad against central finite differences of
+triangle_attention (every input, with bias and mask).
 """
 
 from __future__ import annotations
@@ -279,3 +282,34 @@ def attention_pair_bias(s, q, k, v, z, *, proj_g_weight, proj_o_weight, proj_z_w
     g = sigmoid(linear(s, proj_g_weight, proj_g_bias, dtype=dtype))
     out = linear(o * g, proj_o_weight, proj_o_bias, dtype=dtype)
     return out, (pz if return_z_proj else None)
+
+
+# --------------------------------------------- triangle attention gradients (autograd of the
+# reference's triangle_attention_torch, _reference/triangle_attention.py:11-44)
+def triangle_attention_grad(q, k, v, bias, mask, scale, dout, *, dtype=np.float64):
+    """Gradients ``(dq, dk, dv, dbias)`` of ``sum(triangle_attention(...) * dout)`` on the
+    canonical layout; ``dbias`` has the bias's ``[B, 1, H, N, N]`` shape (summed over
+    N_seq, where the bias is broadcast), ``None`` without a bias."""
+    q, k, v, dout = (np.asarray(t, dtype=dtype) for t in (q, k, v, dout))
+    B, S, N, H, D = q.shape
+    if scale is None:
+        scale = D ** -0.5
+    tr = lambda t: np.transpose(t, (0, 1, 3, 2, 4))  # noqa: E731  [B, S, H, N, D]
+    qs, ks, vs, dos = tr(q), tr(k), tr(v), tr(dout)
+    logits = (qs * dtype(scale)) @ np.swapaxes(ks, -1, -2)
+    if bias is not None:
+        bias = np.broadcast_to(np.asarray(bias, dtype=dtype), (B, 1, H, N, N))
+        logits = logits + bias
+    if mask is not None:
+        mask = np.broadcast_to(np.asarray(mask, dtype=bool), (B, S, 1, 1, N))
+        logits = logits + masked_key_bias(mask, dtype, "float64" if dtype == np.float64 else "float32")
+    p = _softmax(logits, -1)                          # [B, S, H, N, N]
+    o = p @ vs
+    dv = np.swapaxes(p, -1, -2) @ dos
+    dp = dos @ np.swapaxes(vs, -1, -2)
+    delta = np.sum(dos * o, axis=-1, keepdims=True)
+    ds = p * (dp - delta)
+    dq = (ds @ ks) * dtype(scale)
+    dk = (np.swapaxes(ds, -1, -2) @ qs) * dtype(scale)
+    dbias = None if bias is None else ds.sum(axis=1, keepdims=True)
+    return tr(dq), tr(dk), tr(dv), dbias

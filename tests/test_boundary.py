@@ -49,12 +49,15 @@ def _c_layout():
       printf("gnn_triattn_args %zu\n", sizeof(gnn_triattn_args));
       printf("gnn_trimul_args %zu\n", sizeof(gnn_trimul_args));
       printf("gnn_pair_bias_args %zu\n", sizeof(gnn_pair_bias_args));
+      printf("gnn_triattn_bwd_args %zu\n", sizeof(gnn_triattn_bwd_args));
       P(gnn_triattn_args, lse) P(gnn_triattn_args, D) P(gnn_triattn_args, bias_stride)
       P(gnn_triattn_args, mask_stride) P(gnn_triattn_args, scale) P(gnn_triattn_args, precision)
       P(gnn_trimul_args, mask_stride) P(gnn_trimul_args, workspace_bytes) P(gnn_trimul_args, Ch)
       P(gnn_trimul_args, eps) P(gnn_trimul_args, precision)
       P(gnn_pair_bias_args, out) P(gnn_pair_bias_args, H) P(gnn_pair_bias_args, out_stride)
       P(gnn_pair_bias_args, eps) P(gnn_pair_bias_args, dtype)
+      P(gnn_triattn_bwd_args, delta) P(gnn_triattn_bwd_args, D) P(gnn_triattn_bwd_args, dv_stride)
+      P(gnn_triattn_bwd_args, mask_stride) P(gnn_triattn_bwd_args, scale) P(gnn_triattn_bwd_args, precision)
       return 0;
     }
     """
@@ -71,8 +74,9 @@ def test_ctypes_structs_match_c_layout(tmp_path):
     assert int(lines["gnn_triattn_args"]) == ctypes.sizeof(_lib.TriAttnArgs)
     assert int(lines["gnn_trimul_args"]) == ctypes.sizeof(_lib.TrimulArgs)
     assert int(lines["gnn_pair_bias_args"]) == ctypes.sizeof(_lib.PairBiasArgs)
+    assert int(lines["gnn_triattn_bwd_args"]) == ctypes.sizeof(_lib.TriAttnBwdArgs)
     classes = {"gnn_triattn_args": _lib.TriAttnArgs, "gnn_trimul_args": _lib.TrimulArgs,
-               "gnn_pair_bias_args": _lib.PairBiasArgs}
+               "gnn_pair_bias_args": _lib.PairBiasArgs, "gnn_triattn_bwd_args": _lib.TriAttnBwdArgs}
     for key, val in lines.items():
         if "." not in key:
             continue
@@ -159,3 +163,23 @@ def test_pair_bias_argument_errors():
     a.z = 4100
     assert lib.gnn_pair_bias_proj(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
     assert b"aligned" in lib.gnn_last_error()
+
+
+def test_triattn_bwd_argument_errors():
+    lib = _lib.load()
+    assert lib.gnn_triattn_bwd(None, None) == _lib.GNN_ERR_ARG
+    a = _lib.TriAttnBwdArgs()
+    assert lib.gnn_triattn_bwd(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    assert b"required" in lib.gnn_last_error()
+    a.q = a.k = a.v = a.o = a.dout = a.lse = a.dq = a.dk = a.dv = a.delta = 4096
+    a.B = a.S = a.N = a.H = 1
+    a.D = 12
+    assert lib.gnn_triattn_bwd(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    assert b"multiple of 8" in lib.gnn_last_error()
+    a.D = 48
+    assert lib.gnn_triattn_bwd(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
+    assert b"head dim" in lib.gnn_last_error()
+    a.D = 32
+    a.dtype = _lib.GNN_F32
+    assert lib.gnn_triattn_bwd(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
+    assert b"bf16 / fp16" in lib.gnn_last_error()

@@ -432,3 +432,36 @@ def test_attention_pair_bias_known_answers():
     np.testing.assert_allclose(base, (o_mean * g) @ t["proj_o_weight"].T + t["proj_o_bias"], rtol=1e-12)
     with pytest.raises(ValueError, match="multiple"):
         O.attention_pair_bias(**{**t, "z": t["z"][:1].repeat(4, axis=0)})
+
+
+# ------------------------------------------------------------- attention gradients
+def test_attention_grad_matches_finite_differences():
+    """Central differences of the (loop-pinned) forward oracle: every entry of dq, dk, dv and
+    of the N_seq-summed dbias."""
+    rng = np.random.default_rng(17)
+    B, S, N, H, D = 2, 2, 5, 2, 3
+    q, k, v = (rng.standard_normal((B, S, N, H, D)) for _ in range(3))
+    bias = 0.5 * rng.standard_normal((B, 1, H, N, N))
+    mask = rng.random((B, S, 1, 1, N)) < 0.7
+    mask[..., 0] = True
+    dout = rng.standard_normal((B, S, N, H, D))
+    scale = 0.6
+    grads = O.triangle_attention_grad(q, k, v, bias, mask, scale, dout)
+    inputs = {"q": q, "k": k, "v": v, "bias": bias}
+
+    def loss(**kw):
+        return float(np.sum(O.triangle_attention(kw["q"], kw["k"], kw["v"], kw["bias"], mask, scale) * dout))
+
+    eps = 1e-6
+    for name, g in zip(("q", "k", "v", "bias"), grads):
+        base = inputs[name]
+        num = np.zeros_like(base)
+        for idx in np.ndindex(base.shape):
+            plus, minus = base.copy(), base.copy()
+            plus[idx] += eps
+            minus[idx] -= eps
+            num[idx] = (loss(**{**inputs, name: plus}) - loss(**{**inputs, name: minus})) / (2 * eps)
+        np.testing.assert_allclose(g, num, rtol=1e-6, atol=1e-8, err_msg=name)
+    # masked keys receive no k / v gradient at all
+    dropped = ~mask[:, :, 0, 0, :]
+    assert np.all(grads[1][dropped] == 0) and np.all(grads[2][dropped] == 0)

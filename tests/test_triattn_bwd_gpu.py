@@ -1,0 +1,105 @@
+"""HIP triangle-attention backward (gnn_triattn_bwd through the public op's autograd)
+against the fp64 oracle gradients (oracle.triangle_attention_grad, pinned by finite
+differences), with the reference's tolerance table (testutil/metrics.py:103-108, which its
+tests apply to the gradients as well) and the structural zero gradients of masked keys."""
+
+import pytest
+import torch
+
+from helpers import TRIANGLE_ATTENTION_TOL, assert_close_to_oracle, attention_inputs, gen, key_mask, to_np
+from oracle import triangle_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+DTYPES = pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+
+
+def run(q, k, v, bias, mask, scale, dout):
+    from geometric_nn_ops_torch.triangle import triangle_attention
+
+    leaves = [t.detach().requires_grad_(True) for t in (q, k, v)]
+    b = None if bias is None else bias.detach().requires_grad_(True)
+    o = triangle_attention(*leaves, b, mask, scale)
+    o.backward(dout)
+    return o, [t.grad for t in leaves], None if b is None else b.grad
+
+
+def check_against_oracle(shape, dtype, *, with_bias=True, with_mask=True, seed=0, scale=None):
+    B, S, N, H, D = shape
+    t = attention_inputs(B, S, N, H, D, dtype, seed=seed, with_bias=with_bias, bias_scale=0.5, device=DEV)
+    mask = key_mask(B, S, N, seed=seed + 1, frac_keep=0.75, device=DEV) if with_mask else None
+    dout = (torch.randn(B, S, N, H, D, generator=gen(seed + 2))).to(DEV, dtype)
+    o, (dq, dk, dv), db = run(t["q"], t["k"], t["v"], t.get("bias"), mask, scale, dout)
+    want = O.triangle_attention_grad(to_np(t["q"]), to_np(t["k"]), to_np(t["v"]),
+                                     None if not with_bias else to_np(t["bias"]),
+                                     None if mask is None else mask.cpu().numpy(), scale, to_np(dout))
+    tol = TRIANGLE_ATTENTION_TOL[dtype, "ieee"]
+    for name, got, ref in zip(("dq", "dk", "dv"), (dq, dk, dv), want[:3]):
+        assert_close_to_oracle(name, got, ref, tol)
+    if with_bias:
+        assert_close_to_oracle("dbias", db, want[3], tol)
+    return mask, (dk, dv)
+
+
+def test_uses_the_hip_backward(monkeypatch):
+    from geometric_nn_ops_torch.triangle._kernels import triangle_attention as K
+
+    calls = []
+    real = K.triangle_attention_bwd_hip
+    monkeypatch.setattr(K, "triangle_attention_bwd_hip", lambda *a, **kw: calls.append(1) or real(*a, **kw))
+    check_against_oracle((1, 2, 32, 2, 32), torch.bfloat16, seed=3)
+    assert calls == [1]
+
+
+@DTYPES
+@pytest.mark.parametrize("shape", [(1, 1, 32, 4, 32), (1, 4, 48, 2, 16), (2, 2, 100, 2, 32), (1, 3, 130, 4, 8),
+                                   (1, 2, 200, 2, 24), (1, 2, 257, 1, 32)],
+                         ids=["n32", "d16", "n100_batched", "n130_d8", "n200_d24", "n257"])
+def test_matches_oracle(shape, dtype):
+    check_against_oracle(shape, dtype, seed=11)
+
+
+@DTYPES
+@pytest.mark.parametrize(("with_bias", "with_mask"), [(False, False), (False, True), (True, False)],
+                         ids=["plain", "mask_only", "bias_only"])
+def test_optional_inputs(dtype, with_bias, with_mask):
+    check_against_oracle((1, 3, 72, 2, 32), dtype, with_bias=with_bias, with_mask=with_mask, seed=5, scale=0.3)
+
+
+@DTYPES
+def test_masked_keys_get_no_key_or_value_gradient(dtype):
+    mask, (dk, dv) = check_against_oracle((1, 3, 96, 2, 32), dtype, seed=21)
+    dropped = ~mask[:, :, 0, 0, :]  # [B, S, N]
+    assert dropped.any()
+    assert torch.all(dk[dropped] == 0) and torch.all(dv[dropped] == 0)
+
+
+def test_ending_node_views():
+    """Ending-node callers pass transposed views (storage [B, N, S, H, D], canonical
+    [B, S, N, H, D] by strides): the backward reads them by strides."""
+    B, S, N, H, D = 1, 3, 64, 2, 32
+    dtype = torch.bfloat16
+    store = attention_inputs(B, N, S, H, D, dtype, seed=31, with_bias=False, device=DEV)
+    q, k, v = (store[x].transpose(1, 2) for x in "qkv")
+    assert not q.is_contiguous()
+    bias = (0.5 * torch.randn(B, 1, H, N, N, generator=gen(32))).to(DEV, dtype)
+    mask = key_mask(B, S, N, seed=33, device=DEV)
+    dout = torch.randn(B, S, N, H, D, generator=gen(34)).to(DEV, dtype)
+    _, (dq, dk, dv), db = run(q, k, v, bias, mask, None, dout)
+    want = O.triangle_attention_grad(to_np(q), to_np(k), to_np(v), to_np(bias), mask.cpu().numpy(), None,
+                                     to_np(dout))
+    tol = TRIANGLE_ATTENTION_TOL[dtype, "ieee"]
+    for name, got, ref in zip(("dq", "dk", "dv", "dbias"), (dq, dk, dv, db), want):
+        assert_close_to_oracle(name, got, ref, tol)
+
+
+def test_headline_rows_bf16():
+    """N_res = 512 (the headline width), 8 N_seq rows, pair bias and ragged masks."""
+    check_against_oracle((1, 8, 512, 4, 32), torch.bfloat16, seed=41)
+
+
+def test_fp32_and_wide_heads_keep_the_torch_gradient():
+    """fp32 inputs and head dims above 32 are differentiated by the torch path."""
+    for dtype, d in ((torch.float32, 32), (torch.bfloat16, 64)):
+        check_against_oracle((1, 2, 40, 2, d), dtype, seed=51)
