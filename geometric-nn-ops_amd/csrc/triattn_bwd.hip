@@ -12,8 +12,8 @@
 // (geometric_nn_ops_torch/triangle/_kernels/triangle_attention.py:548-1087, launched at
 // :1278-1442).
 //
-// Four kernels, every sum owned by one workgroup (no atomics, deterministic):
-//   bwd_delta  Delta = rowsum(dO * O) in fp32.
+// Three kernels (plus an ordered reduction of the dbias splits), every sum owned by one
+// workgroup (no atomics, deterministic):
 //   bwd_dkdv   one wave per 32 keys of a (b, s, h) row, looping over 64-query tiles staged
 //              in LDS. Scores are computed as S = Q' K^T with the KEYS on the lanes, so the
 //              P and dS accumulators already are the A operands of dV += P^T dO and
@@ -21,9 +21,10 @@
 //              LDS tiles through ds_read_b64_tr_b16, in the accumulator's row order.
 //   bwd_dq     the forward's layout (queries on the lanes, K / V tiles in LDS): the dS^T
 //              accumulator is the A operand of dQ += dS K, with K read transposed from LDS.
-//   bwd_dbias  one wave per 32 queries x 64 keys of a (b, h) bias plane, looping over the
-//              N_seq rows and accumulating sum_s dS in fp32 registers; the bias tile is
-//              loaded once into the score accumulator's initial value.
+//              It runs first and also writes Delta = rowsum(dO * O) (fp32) for the others.
+//   bwd_dbias  a 128 x 128 tile of a (b, h) bias plane per workgroup, sweeping a range of
+//              N_seq rows with the row's operands staged in LDS and sum_s dS accumulating in
+//              fp32 registers; the bias tile is loaded once as the scores' initial value.
 // The bias is added to the scores in fp32 exactly as in the forward (bf16 values, fp32
 // sums), and the mask sentinel after it, so P matches the forward's normaliser.
 // 16-bit inputs, head dim <= 32 (padded to a multiple of 8 by the host).
@@ -98,25 +99,6 @@ __device__ __forceinline__ void identity_frags(typename TypeOps<T>::V8 (&idf)[2]
 template <typename T>
 __device__ __forceinline__ typename TypeOps<T>::V8 row8(const T* row, int d0, int D, bool ok) {
   return (ok && d0 < D) ? load8(row + d0) : zero8<T>();
-}
-
-// ------------------------------------------------------------------------- Delta
-template <typename T>
-__global__ __launch_bounds__(BNT) void bwd_delta_kernel(const gnn_triattn_bwd_args a) {
-  const int64_t rows = a.B * a.S * a.N * a.H;
-  const int64_t r = (int64_t)blockIdx.x * BNT + threadIdx.x;
-  if (r >= rows) return;
-  // r enumerates [B, S, H, N] (the lse / Delta layout)
-  const int64_t n = r % a.N, h = (r / a.N) % a.H, s = (r / (a.N * a.H)) % a.S, b = r / (a.N * a.H * a.S);
-  const T* o = (const T*)a.o + b * a.o_stride[0] + s * a.o_stride[1] + n * a.o_stride[2] + h * a.o_stride[3];
-  const T* d = (const T*)a.dout + b * a.do_stride[0] + s * a.do_stride[1] + n * a.do_stride[2] + h * a.do_stride[3];
-  float acc = 0.f;
-  for (int c = 0; c < a.D; c += 8) {
-    const f32x8 x = TypeOps<T>::to_f32(load8(o + c)), y = TypeOps<T>::to_f32(load8(d + c));
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(x[e], y[e], acc);
-  }
-  a.delta[r] = acc;
 }
 
 // ------------------------------------------------------------------------- dK, dV
@@ -299,7 +281,22 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dq_kernel(const gnn_triattn_bwd_ar
   }
   const int64_t lrow = (((int64_t)b * a.S + s) * H + h) * N;
   const float lse = qok ? a.lse[lrow + qi] : INFINITY;  // absent queries: p = 0
-  const float delta = qok ? a.delta[lrow + qi] : 0.f;
+  // Delta = dO . O of this query: the lane pair (g = 0, 1) holds the 32 columns between them
+  float delta;
+  {
+    const T* orow = (const T*)a.o + b * a.o_stride[0] + s * a.o_stride[1] + h * a.o_stride[3] +
+                    (int64_t)(qok ? qi : 0) * a.o_stride[2];
+    float part = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const f32x8 x = TypeOps<T>::to_f32(row8(orow, 16 * kk + 8 * g, D, qok));
+      const f32x8 y = TypeOps<T>::to_f32(dof[kk]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part = __builtin_fmaf(x[e], y[e], part);
+    }
+    delta = part + __shfl_xor(part, 32);
+    if (qok && g == 0) a.delta[lrow + qi] = delta;
+  }
   const float nl = -lse * LOG2E_B;
   V8 idf[2];
   identity_frags<T>(idf, l32, g);
@@ -373,129 +370,188 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dq_kernel(const gnn_triattn_bwd_ar
 }
 
 // ------------------------------------------------------------------------- dbias
-// One wave per (b, h, 32 queries, 64 keys); S and dP as [query][key] (lane = key).
-template <typename T>
-__global__ __launch_bounds__(BNT, 2) void bwd_dbias_kernel(const gnn_triattn_bwd_args a) {
-  typedef typename TypeOps<T>::V8 V8;
-  const int N = (int)a.N, H = (int)a.H, D = (int)a.D;
-  const int nqt = (N + 31) / 32, nkt = (N + 63) / 64;
-  const int64_t tiles = (int64_t)a.B * H * nqt * nkt;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
-  const int64_t t = (int64_t)xcd_remap(blockIdx.x, gridDim.x) * 4 + wave;
-  if (t >= tiles) return;  // whole wave
-  const int kt = (int)(t % nkt);
-  const int qt = (int)((t / nkt) % nqt);
-  const int h = (int)((t / ((int64_t)nkt * nqt)) % H);
-  const int b = (int)(t / ((int64_t)nkt * nqt * H));
-  const int q0 = qt * 32;
-  // this lane's keys: kcol[sub] = k0 + 32 sub + l32
-  int kcol[2];
-  bool kok[2];
-#pragma unroll
-  for (int sub = 0; sub < 2; ++sub) {
-    kcol[sub] = kt * 64 + 32 * sub + l32;
-    kok[sub] = kcol[sub] < N;
-  }
-  // the bias tile as the scores' initial value: element i = query q0 + 8 (i / 4) + 4 g + i % 4
-  f32x16 binit[2];
-  const T* bias_plane = (const T*)a.bias + b * a.bias_stride[0] + h * a.bias_stride[1];
-#pragma unroll
-  for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int qq = q0 + 8 * (i / 4) + 4 * g + (i % 4);
-      binit[sub][i] = (qq < N && kok[sub]) ? TypeOps<T>::to_f32(bias_plane[(int64_t)qq * a.bias_stride[2] + kcol[sub]]) : 0.f;
-    }
-  f32x16 acc[2];
-#pragma unroll
-  for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[sub][i] = 0.f;
+// Eight waves per workgroup own a 128-query x 128-key tile of one (b, h) bias plane; wave w
+// takes queries 32 (w % 4) .. + 31 and keys 64 (w / 4) .. + 63 (two 32-key halves), scores
+// laid out [query][key] with the keys on the lanes. The workgroup sweeps N_seq rows
+// [s_begin, s_end): per row, Q' / dO / K / V of the tile, lse / Delta of its queries and the
+// key-mask term of its keys are staged in LDS (the next row's loads are in flight while the
+// current one is computed), and sum_s dS accumulates in fp32 registers. With more than one
+// N_seq split the partial sums go to the workspace and bwd_dbias_reduce adds them in order.
+constexpr int DB_T = 128;
+constexpr int DB_NT = 512;
+struct DbLds {
+  unsigned char q[DB_T * ROWB];
+  unsigned char d[DB_T * ROWB];
+  unsigned char k[DB_T * ROWB];
+  unsigned char v[DB_T * ROWB];
+  float lse[DB_T];
+  float delta[DB_T];
+  float kb[DB_T];
+};
 
-  const int qa = q0 + l32;  // this lane's query row for the A operands
-  const bool qaok = qa < N;
-  for (int s = 0; s < a.S; ++s) {
-    const T* qr = (const T*)a.q + b * a.q_stride[0] + s * a.q_stride[1] + h * a.q_stride[3] + (int64_t)(qaok ? qa : 0) * a.q_stride[2];
-    const T* dr = (const T*)a.dout + b * a.do_stride[0] + s * a.do_stride[1] + h * a.do_stride[3] + (int64_t)(qaok ? qa : 0) * a.do_stride[2];
+template <typename T>
+__global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_bwd_args a) {
+  typedef typename TypeOps<T>::V8 V8;
+  __shared__ __align__(16) DbLds sm;
+  const int N = (int)a.N, H = (int)a.H, D = (int)a.D, S = (int)a.S;
+  const int nt = (N + DB_T - 1) / DB_T;
+  const int splits = a.dbias_splits > 1 ? a.dbias_splits : 1;
+  const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
+  const int split = w % splits;
+  const int kt = (w / splits) % nt;
+  const int qt = (w / (splits * nt)) % nt;
+  const int64_t bh = w / ((uint32_t)splits * nt * nt);
+  const int h = (int)(bh % H), b = (int)(bh / H);
+  const int per = (S + splits - 1) / splits;
+  const int s_begin = split * per, s_end = min(S, s_begin + per);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
+  const int qw = 32 * (wave & 3), kw = 64 * (wave >> 2);  // wave's rows within the tile
+  const int q0 = qt * DB_T, k0 = kt * DB_T;
+
+  // the bias tile as the scores' initial value: element i of half sub is query
+  // q0 + qw + 8 (i / 4) + 4 g + i % 4, key k0 + kw + 32 sub + l32
+  f32x16 binit[2], acc[2];
+  {
+    const T* plane = (const T*)a.bias + b * a.bias_stride[0] + h * a.bias_stride[1];
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int kj = k0 + kw + 32 * sub + l32;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int qq = q0 + qw + 8 * (i / 4) + 4 * g + (i % 4);
+        binit[sub][i] = (qq < N && kj < N) ? TypeOps<T>::to_f32(plane[(int64_t)qq * a.bias_stride[2] + kj]) : 0.f;
+        acc[sub][i] = 0.f;
+      }
+    }
+  }
+
+  // staging: thread = (row r = tid / 4, chunk c = tid % 4) of each of the four tiles
+  const int sr = tid >> 2, sc4 = tid & 3;
+  V8 pq, pd, pk, pv;
+  float plse = 0.f, pdel = 0.f, pkb = 0.f;
+  auto load_stage = [&](int s) {
+    const int qi = q0 + sr, kj = k0 + sr;
+    const bool qok = qi < N, kok = kj < N;
+    const int64_t qo = (int64_t)b * a.q_stride[0] + (int64_t)s * a.q_stride[1] + (int64_t)h * a.q_stride[3];
+    const int64_t doo = (int64_t)b * a.do_stride[0] + (int64_t)s * a.do_stride[1] + (int64_t)h * a.do_stride[3];
+    const int64_t ko = (int64_t)b * a.k_stride[0] + (int64_t)s * a.k_stride[1] + (int64_t)h * a.k_stride[3];
+    const int64_t vo = (int64_t)b * a.v_stride[0] + (int64_t)s * a.v_stride[1] + (int64_t)h * a.v_stride[3];
+    pq = row8((const T*)a.q + qo + (int64_t)(qok ? qi : 0) * a.q_stride[2], 8 * sc4, D, qok);
+    pd = row8((const T*)a.dout + doo + (int64_t)(qok ? qi : 0) * a.do_stride[2], 8 * sc4, D, qok);
+    pk = row8((const T*)a.k + ko + (int64_t)(kok ? kj : 0) * a.k_stride[2], 8 * sc4, D, kok);
+    pv = row8((const T*)a.v + vo + (int64_t)(kok ? kj : 0) * a.v_stride[2], 8 * sc4, D, kok);
+    if (sc4 == 0) {
+      const int64_t lrow = (((int64_t)b * S + s) * H + h) * N;
+      plse = qok ? a.lse[lrow + qi] : INFINITY;  // absent queries: p = 0
+      pdel = qok ? a.delta[lrow + qi] : 0.f;
+      pkb = !kok ? -INFINITY
+                 : ((a.mask && a.mask[b * a.mask_stride[0] + s * a.mask_stride[1] + (int64_t)kj * a.mask_stride[2]] == 0)
+                        ? a.mask_value
+                        : 0.f);
+    }
+  };
+  auto store_stage = [&]() {
+    *reinterpret_cast<V8*>(sm.q + swz(sr, sc4)) = TypeOps<T>::from_f32(TypeOps<T>::to_f32(pq) * a.scale);
+    *reinterpret_cast<V8*>(sm.d + swz(sr, sc4)) = pd;
+    *reinterpret_cast<V8*>(sm.k + swz(sr, sc4)) = pk;
+    *reinterpret_cast<V8*>(sm.v + swz(sr, sc4)) = pv;
+    if (sc4 == 0) {
+      sm.lse[sr] = plse;
+      sm.delta[sr] = pdel;
+      sm.kb[sr] = pkb;
+    }
+  };
+
+  if (s_begin < s_end) {
+    load_stage(s_begin);
+    store_stage();
+  }
+  __syncthreads();
+  for (int s = s_begin; s < s_end; ++s) {
+    const bool has_next = s + 1 < s_end;
+    if (has_next) load_stage(s + 1);
     V8 qf[2], dof[2];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      qf[kk] = TypeOps<T>::from_f32(TypeOps<T>::to_f32(row8(qr, 16 * kk + 8 * g, D, qaok)) * a.scale);
-      dof[kk] = row8(dr, 16 * kk + 8 * g, D, qaok);
+      qf[kk] = lds_row8<T>(sm.q, qw + l32, 2 * kk + g);
+      dof[kk] = lds_row8<T>(sm.d, qw + l32, 2 * kk + g);
     }
-    const int64_t lrow = (((int64_t)b * a.S + s) * H + h) * N;
     f32x4 l4[4], d4[4];
 #pragma unroll
     for (int rg = 0; rg < 4; ++rg) {
-      const int qq = q0 + 8 * rg + 4 * g;
-      if (qq + 4 <= N) {
-        l4[rg] = *reinterpret_cast<const f32x4*>(a.lse + lrow + qq);
-        d4[rg] = *reinterpret_cast<const f32x4*>(a.delta + lrow + qq);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          l4[rg][e] = qq + e < N ? a.lse[lrow + qq + e] : INFINITY;
-          d4[rg][e] = qq + e < N ? a.delta[lrow + qq + e] : 0.f;
-        }
-      }
+      l4[rg] = *reinterpret_cast<const f32x4*>(&sm.lse[qw + 8 * rg + 4 * g]);
+      d4[rg] = *reinterpret_cast<const f32x4*>(&sm.delta[qw + 8 * rg + 4 * g]);
     }
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
-      const T* kr = (const T*)a.k + b * a.k_stride[0] + s * a.k_stride[1] + h * a.k_stride[3] + (int64_t)(kok[sub] ? kcol[sub] : 0) * a.k_stride[2];
-      const T* vr = (const T*)a.v + b * a.v_stride[0] + s * a.v_stride[1] + h * a.v_stride[3] + (int64_t)(kok[sub] ? kcol[sub] : 0) * a.v_stride[2];
-      f32x16 sc = binit[sub], dp;
+      const int kr = kw + 32 * sub + l32;
+      f32x16 scv = binit[sub], dp;
 #pragma unroll
       for (int i = 0; i < 16; ++i) dp[i] = 0.f;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        Mma<T, PREC_NATIVE>::step(sc, qf[kk], row8(kr, 16 * kk + 8 * g, D, kok[sub]));
-        Mma<T, PREC_NATIVE>::step(dp, dof[kk], row8(vr, 16 * kk + 8 * g, D, kok[sub]));
+        Mma<T, PREC_NATIVE>::step(scv, qf[kk], lds_row8<T>(sm.k, kr, 2 * kk + g));
+        Mma<T, PREC_NATIVE>::step(dp, dof[kk], lds_row8<T>(sm.v, kr, 2 * kk + g));
       }
-      float kb = 0.f;
-      if (!kok[sub]) {
-        kb = -INFINITY;
-      } else if (a.mask && a.mask[b * a.mask_stride[0] + s * a.mask_stride[1] + (int64_t)kcol[sub] * a.mask_stride[2]] == 0) {
-        kb = a.mask_value;
-      }
+      const float kb = sm.kb[kr];
 #pragma unroll
       for (int rg = 0; rg < 4; ++rg)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = 4 * rg + e;
-          const float pv = fast_exp2((sc[i] + kb - l4[rg][e]) * LOG2E_B);
+          const float pv = fast_exp2((scv[i] + kb - l4[rg][e]) * LOG2E_B);
           acc[sub][i] += pv * (dp[i] - d4[rg][e]);
         }
     }
+    __syncthreads();
+    if (has_next) store_stage();
+    __syncthreads();
   }
-  // dbias[b, h, q, k] fp32 [B, H, N, N] contiguous
+  // [B, H, N, N] fp32: the final gradient, or this split's slice of the workspace
+  float* out = (splits > 1 ? a.dbias_ws + (int64_t)split * a.B * H * N * N : a.dbias) + ((int64_t)b * H + h) * N * N;
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub) {
-    if (!kok[sub]) continue;
-    float* out = a.dbias + ((int64_t)b * H + h) * N * N + kcol[sub];
+    const int kj = k0 + kw + 32 * sub + l32;
+    if (kj >= N) continue;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int qq = q0 + 8 * (i / 4) + 4 * g + (i % 4);
-      if (qq < N) out[(int64_t)qq * N] = acc[sub][i];
+      const int qq = q0 + qw + 8 * (i / 4) + 4 * g + (i % 4);
+      if (qq < N) out[(int64_t)qq * N + kj] = acc[sub][i];
     }
+  }
+}
+
+// dbias = sum over the splits of the workspace slices, in split order (deterministic)
+__global__ __launch_bounds__(BNT) void bwd_dbias_reduce_kernel(const gnn_triattn_bwd_args a) {
+  const int64_t n = a.B * a.H * a.N * a.N;
+  for (int64_t i = (int64_t)blockIdx.x * BNT + threadIdx.x; i < n; i += (int64_t)gridDim.x * BNT) {
+    float x = 0.f;
+    for (int c = 0; c < a.dbias_splits; ++c) x += a.dbias_ws[c * n + i];
+    a.dbias[i] = x;
   }
 }
 
 template <typename T>
 int launch_bwd(const gnn_triattn_bwd_args& a, hipStream_t stream) {
-  const int64_t rows = a.B * a.S * a.N * a.H;
-  hipLaunchKernelGGL(bwd_delta_kernel<T>, dim3((uint32_t)((rows + BNT - 1) / BNT)), dim3(BNT), 0, stream, a);
   const int64_t nb128 = (a.N + 127) / 128;
   const dim3 grid((uint32_t)(nb128 * a.H * a.S * a.B));
+  // dq first: it also writes Delta, which dk / dv and dbias read
   if (a.bias) {
-    hipLaunchKernelGGL((bwd_dkdv_kernel<T, true>), grid, dim3(BNT), 0, stream, a);
     hipLaunchKernelGGL((bwd_dq_kernel<T, true>), grid, dim3(BNT), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<T, true>), grid, dim3(BNT), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((bwd_dkdv_kernel<T, false>), grid, dim3(BNT), 0, stream, a);
     hipLaunchKernelGGL((bwd_dq_kernel<T, false>), grid, dim3(BNT), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<T, false>), grid, dim3(BNT), 0, stream, a);
   }
   if (a.bias && a.dbias) {
-    const int64_t tiles = a.B * a.H * ((a.N + 31) / 32) * ((a.N + 63) / 64);
-    hipLaunchKernelGGL(bwd_dbias_kernel<T>, dim3((uint32_t)((tiles + 3) / 4)), dim3(BNT), 0, stream, a);
+    const int64_t nt = (a.N + DB_T - 1) / DB_T;
+    const int splits = a.dbias_splits > 1 ? a.dbias_splits : 1;
+    hipLaunchKernelGGL(bwd_dbias_kernel<T>, dim3((uint32_t)(a.B * a.H * nt * nt * splits)), dim3(DB_NT), 0, stream, a);
+    if (splits > 1) {
+      const int64_t n = a.B * a.H * a.N * a.N;
+      const int64_t blocks = std::min<int64_t>((n + BNT - 1) / BNT, 4096);
+      hipLaunchKernelGGL(bwd_dbias_reduce_kernel, dim3((uint32_t)blocks), dim3(BNT), 0, stream, a);
+    }
   }
   return (int)hipGetLastError();
 }
@@ -503,6 +559,10 @@ int launch_bwd(const gnn_triattn_bwd_args& a, hipStream_t stream) {
 }  // namespace
 
 int triattn_bwd(const gnn_triattn_bwd_args& a, hipStream_t stream) {
+  if (a.bias && a.dbias && a.dbias_splits > 1 && !a.dbias_ws)
+    return set_error(GNN_ERR_ARG, "triangle_attention backward: dbias_splits > 1 needs dbias_ws");
+  if (a.bias && a.dbias && (a.dbias_splits > a.S || a.dbias_splits > 64))
+    return set_error(GNN_ERR_ARG, "triangle_attention backward: dbias_splits must be at most N_seq and 64");
   if (a.D > 32)
     return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention backward: head dim > 32 is not supported");
   if (a.B * a.S * a.H * ((a.N + 127) / 128) >= ((int64_t)1 << 31))

@@ -71,6 +71,8 @@ class TriAttnBwdArgs(ctypes.Structure):
         ("dv", ctypes.c_void_p),
         ("dbias", ctypes.c_void_p),
         ("delta", ctypes.c_void_p),
+        ("dbias_ws", ctypes.c_void_p),
+        ("dbias_splits", ctypes.c_int32),
         ("B", ctypes.c_int64),
         ("S", ctypes.c_int64),
         ("N", ctypes.c_int64),

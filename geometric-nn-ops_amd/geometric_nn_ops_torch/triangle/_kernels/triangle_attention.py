@@ -126,6 +126,13 @@ def backward_supported(q: torch.Tensor) -> bool:
     return q.dtype in (torch.bfloat16, torch.float16) and d <= 32 and d % 8 == 0
 
 
+def dbias_splits(B: int, S: int, N: int, H: int) -> int:
+    """N_seq ranges for the pair-bias gradient: enough 128 x 128 tiles x ranges for about
+    two workgroups per compute unit of an MI355X (256 CUs), at most N_seq and 64."""
+    tiles = B * H * ((N + 127) // 128) ** 2
+    return max(1, min(S, 64, -(-512 // tiles)))
+
+
 def triangle_attention_bwd_hip(q, k, v, o, dout, lse, bias=None, mask=None, scale=None, mask_value=None,
                                need_dbias=True):
     """Gradients of the HIP forward: ``(dq, dk, dv, dbias)`` with dq/dk/dv like q and dbias
@@ -163,6 +170,11 @@ def triangle_attention_bwd_hip(q, k, v, o, dout, lse, bias=None, mask=None, scal
         if need_dbias:
             dbias = torch.empty((B, 1, H, N, N), device=q.device, dtype=torch.float32)
             a.dbias = dbias.data_ptr()
+            splits = dbias_splits(B, S, N, H)
+            a.dbias_splits = splits
+            if splits > 1:
+                ws = torch.empty((splits, B, H, N, N), device=q.device, dtype=torch.float32)
+                a.dbias_ws = ws.data_ptr()
     if mask is not None:
         a.mask = mask.data_ptr()
         a.mask_stride = _lib.I64x3(mask.stride(0), mask.stride(1), mask.stride(4))

@@ -97,7 +97,10 @@ int gnn_triattn_fwd(const gnn_triattn_args* args, void* stream);
  * lse (fp32 [B, S, H, N] contiguous, natural log; gnn_triattn_fwd writes it when args->lse
  * is set), writes dq, dk, dv (input dtype, [B, S, N, H, D] by strides) and, when both bias
  * and dbias are given, the pair-bias gradient summed over N_seq into dbias (fp32
- * [B, H, N, N] contiguous). delta is caller-provided fp32 scratch of B * S * H * N floats.
+ * [B, H, N, N] contiguous). delta is caller-provided fp32 scratch of B * S * H * N floats;
+ * with dbias_splits > 1 the N_seq rows are split into that many ranges whose partial sums
+ * go to dbias_ws (dbias_splits * B * H * N * N floats) and are added in range order, so
+ * the result does not depend on scheduling.
  * Same layout rules as gnn_triattn_args; scale, mask_value and the mask are the forward's.
  */
 typedef struct gnn_triattn_bwd_args {
@@ -114,6 +117,8 @@ typedef struct gnn_triattn_bwd_args {
   void* dv;
   float* dbias;          /* fp32 [B,H,N,N] or NULL */
   float* delta;          /* fp32 scratch [B,S,H,N] */
+  float* dbias_ws;       /* fp32 scratch [dbias_splits,B,H,N,N] when dbias_splits > 1 */
+  int32_t dbias_splits;  /* N_seq ranges summed separately (1..min(N_seq, 64)), then added in order */
   int64_t B, S, N, H, D;
   int64_t q_stride[4];   /* b, s, n, h for every [B,S,N,H,D] tensor (d stride 1) */
   int64_t k_stride[4];

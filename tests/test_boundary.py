@@ -56,7 +56,7 @@ def _c_layout():
       P(gnn_trimul_args, eps) P(gnn_trimul_args, precision)
       P(gnn_pair_bias_args, out) P(gnn_pair_bias_args, H) P(gnn_pair_bias_args, out_stride)
       P(gnn_pair_bias_args, eps) P(gnn_pair_bias_args, dtype)
-      P(gnn_triattn_bwd_args, delta) P(gnn_triattn_bwd_args, D) P(gnn_triattn_bwd_args, dv_stride)
+      P(gnn_triattn_bwd_args, delta) P(gnn_triattn_bwd_args, dbias_splits) P(gnn_triattn_bwd_args, D) P(gnn_triattn_bwd_args, dv_stride)
       P(gnn_triattn_bwd_args, mask_stride) P(gnn_triattn_bwd_args, scale) P(gnn_triattn_bwd_args, precision)
       return 0;
     }
