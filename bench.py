@@ -14,6 +14,8 @@ the dominant kernel and a CPU baseline (the numpy oracle in fp32 on a bounded sa
 the same workload, which also serves as the parity gate before timing). ``cold_ms`` times
 each kernel again after a 512 MiB scratch write (inputs then come from HBM, not from the
 Infinity Cache that holds them in the warm loop); ``value`` is the warm figure.
+``attention_backward`` times one gnn_triattn_bwd call (dq, dk, dv and the pair-bias
+gradient) on the same attention inputs, outside the step.
 """
 
 import argparse
@@ -46,6 +48,7 @@ def parse():
                          "the 256 MB Infinity Cache (0 skips)")
     ap.add_argument("--only", choices=["attn", "trimul"], default=None,
                     help="profile helper: run only one op (the JSON line is then partial)")
+    ap.add_argument("--no-backward", action="store_true", help="skip the attention backward timing")
     ap.add_argument("--copy-calib", action="store_true",
                     help="profile helper: run a plain 256 MiB device copy (known HBM bytes) and exit, "
                          "to scale FETCH_SIZE / WRITE_SIZE counter readings")
@@ -64,6 +67,7 @@ def main():
     import torch
 
     from geometric_nn_ops_torch import _lib
+    from geometric_nn_ops_torch.triangle._kernels import triangle_attention as TA
     from geometric_nn_ops_torch.triangle._kernels import trimul as TK
     from geometric_nn_ops_torch.triangle._masking import rounded_mask_value
     from oracle import triangle_oracle as O
@@ -219,6 +223,48 @@ def main():
                    for name, pairs in cev.items()}
         del scratch
 
+    # ---- attention backward (not part of the step): one gnn_triattn_bwd call on the same
+    # inputs with a synthetic upstream gradient, after a forward that writes the lse
+    backward = None
+    if args.only in (None, "attn") and not args.no_backward:
+        lse = torch.empty((1, N, H, N), device=dev, dtype=torch.float32)
+        a.lse = lse.data_ptr()
+        check(lib.gnn_triattn_fwd(ctypes.byref(a), sh), "attn+lse")
+        a.lse = None
+        dout = rn(1, N, N, H, D).to(dev)
+        grads = [torch.empty_like(qd) for _ in range(3)]
+        dbias = torch.empty((1, H, N, N), device=dev, dtype=torch.float32)
+        delta = torch.empty((1, N, H, N), device=dev, dtype=torch.float32)
+        splits = TA.dbias_splits(1, N, N, H)
+        ws = torch.empty((splits, 1, H, N, N), device=dev, dtype=torch.float32)
+        ba = _lib.TriAttnBwdArgs()
+        ba.q, ba.k, ba.v, ba.o, ba.dout = qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), od.data_ptr(), dout.data_ptr()
+        ba.bias, ba.lse = bd.data_ptr(), lse.data_ptr()
+        ba.dq, ba.dk, ba.dv = (t.data_ptr() for t in grads)
+        ba.dbias, ba.delta, ba.dbias_ws, ba.dbias_splits = dbias.data_ptr(), delta.data_ptr(), ws.data_ptr(), splits
+        ba.B, ba.S, ba.N, ba.H, ba.D = 1, N, N, H, D
+        for name in ("q", "k", "v", "o", "do", "dq", "dk", "dv"):
+            setattr(ba, f"{name}_stride", _lib.I64x4(*qd.stride()[:4]))
+        ba.bias_stride = a.bias_stride
+        ba.scale, ba.mask_value, ba.dtype, ba.precision = a.scale, a.mask_value, a.dtype, a.precision
+        for _ in range(3):
+            check(lib.gnn_triattn_bwd(ctypes.byref(ba), sh), "attn bwd")
+        bev = []
+        for _ in range(10):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            check(lib.gnn_triattn_bwd(ctypes.byref(ba), sh), "attn bwd")
+            e1.record(stream)
+            bev.append((e0, e1))
+        torch.cuda.synchronize()
+        bwd_ms = sorted(e0.elapsed_time(e1) for e0, e1 in bev)[len(bev) // 2]
+        bwd_flops = 10.0 * N * H * N * N * D  # QK^T, dO V^T, P^T dO, dS^T Q', dS K
+        backward = {"kernel": "gnn_triattn_bwd (dq with Delta, dk/dv, dbias over N_seq, ordered split sum)",
+                    "ms": round(bwd_ms, 5), "algorithmic_tflops": round(bwd_flops / (bwd_ms * 1e-3) / 1e12, 2),
+                    "mfma_frac": round(bwd_flops / (bwd_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                    "algorithmic_flops": bwd_flops, "dbias_splits": splits}
+
     # ---- algorithmic FLOPs / bytes per launch
     M = N * N
     e = 2
@@ -290,6 +336,7 @@ def main():
         "triton_reference": "unavailable: the reference's Triton kernels are not installed on the box and "
                             "the reference does not travel to it",
         "wall_s_timed": round(wall, 4),
+        "attention_backward": backward,
     }
     if cpu is not None:
         cpu_tflops = step_flops / cpu["seconds_per_step"] / 1e12

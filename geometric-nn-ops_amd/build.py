@@ -48,36 +48,45 @@ def hipcc() -> str:
     return found
 
 
-def _compile(src: pathlib.Path) -> pathlib.Path:
-    obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: pathlib.Path, build_dir: pathlib.Path = BUILD_DIR, extra=()) -> pathlib.Path:
+    obj = build_dir / (src.stem + ".o")
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> pathlib.Path:
-    BUILD_DIR.mkdir(exist_ok=True)
-    OUT_DIR.mkdir(exist_ok=True)
+def build(jobs: int | None = None, verbose: bool = False, defines=(), out: pathlib.Path | None = None) -> pathlib.Path:
+    """Compile and link the library; ``defines`` (``NAME=VALUE`` strings) select the tuning
+    macros of the kernels, ``out`` writes the library elsewhere (objects then go to a build
+    folder of their own) -- how the measured alternatives in the kernels' comments are built."""
+    lib = LIB if out is None else pathlib.Path(out).resolve()
+    build_dir = BUILD_DIR if not defines and out is None else BUILD_DIR.with_name(BUILD_DIR.name + "_" + lib.stem)
+    build_dir.mkdir(exist_ok=True)
+    lib.parent.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     jobs = jobs or min(len(sources), os.cpu_count() or 1, 16)
+    extra = [f"-D{d}" for d in defines]
     with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
-        objs = list(pool.map(_compile, sources))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = list(pool.map(lambda src: _compile(src, build_dir, extra), sources))
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {lib}")
+    return lib
 
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("--define", action="append", default=[], metavar="NAME=VALUE",
+                    help="kernel tuning macro, e.g. GNN_ROW_MAX_N=0 (tiled attention only)")
+    ap.add_argument("--out", default=None, help="library path (default: the package's _lib/libgnn_hip.so)")
     args = ap.parse_args()
-    build(args.jobs, verbose=True)
+    build(args.jobs, verbose=True, defines=args.define, out=args.out)
     sys.exit(0)
