@@ -27,8 +27,11 @@
 //     launch at N = 512 against 309 MB with all four heads fastest). Odd H falls back to heads
 //     fastest (when the planes fit the L2 together) or rows fastest.
 // Measured alternatives not kept: 4 waves per workgroup (the staging then is not amortised),
-// and software pipelining the QK^T of the next tile (or 32-key half tile) ahead of the
-// softmax (the extra score registers cost occupancy and it measured slower).
+// software pipelining the QK^T of the next tile (or 32-key half tile) ahead of the softmax
+// (the extra score registers cost occupancy and it measured slower), and a persistent form
+// (16 waves per CU streaming consecutive rows through two LDS buffers, the next row's K / V
+// DMA issued during the current row's key loop: 20% slower at N = 512, its 16 waves meeting
+// at a barrier every row).
 // The per-tile arithmetic (transposed score tile S^T = K Q'^T on 32x32x16 MFMA, bias added
 // by MFMA against an identity fragment, lazy rescale with threshold 8 ln 2, exp2 with the
 // folded FMA, v_dot2 row sums on the rounded probabilities, masked-key sentinel, all-masked
@@ -49,8 +52,8 @@ constexpr float RESCALE_THRESHOLD = 8.0f / LOG2E;
 #ifndef GNN_ROW_WAVES
 #define GNN_ROW_WAVES 8
 #endif
-#ifndef GNN_ROW_MINBLOCKS
-#define GNN_ROW_MINBLOCKS 2
+#ifndef GNN_ROW_WAVES_PER_SIMD  // occupancy the register allocation is held to (128 VGPRs at 4)
+#define GNN_ROW_WAVES_PER_SIMD 4
 #endif
 #ifndef GNN_ROW_SETPRIO
 #define GNN_ROW_SETPRIO 1
@@ -139,7 +142,7 @@ __device__ __forceinline__ typename TypeOps<T>::V4 tr_read4_r(const unsigned cha
 }
 
 template <typename T, bool HAS_BIAS>
-__global__ __launch_bounds__(NT, GNN_ROW_MINBLOCKS) void triattn_row_kernel(const gnn_triattn_args a) {
+__global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel(const gnn_triattn_args a) {
   typedef typename TypeOps<T>::V8 V8;
   typedef typename TypeOps<T>::V4 V4;
   extern __shared__ __align__(256) unsigned char smem_raw[];
@@ -175,7 +178,7 @@ __global__ __launch_bounds__(NT, GNN_ROW_MINBLOCKS) void triattn_row_kernel(cons
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
@@ -285,8 +288,12 @@ __global__ __launch_bounds__(NT, GNN_ROW_MINBLOCKS) void triattn_row_kernel(cons
     // The first tiles' LDS reads are the same for every query block; keeping the compiler
     // from hoisting them out of this loop keeps their registers free for the key loop.
     asm volatile("" : "+v"(koff[0]), "+v"(koff[1]), "+v"(tr_off));
+    // N as this block sees it, opaque to the compiler: otherwise the tail-mask compares of the
+    // first tile's bias load are hoisted out of the loop as live 64-bit lane masks
+    int Nq = N;
+    asm volatile("" : "+s"(Nq));
     const int myq = qblk * 32 + l32;
-    const bool qok = myq < N;
+    const bool qok = myq < Nq;
     V8 qf[2];
     {
       const T* qp = (const T*)a.q + b * a.q_stride[0] + s * a.q_stride[1] + h * a.q_stride[3] +
@@ -334,7 +341,7 @@ __global__ __launch_bounds__(NT, GNN_ROW_MINBLOCKS) void triattn_row_kernel(cons
     // mask, online softmax and O^T += V^T P^T for the scores of tile t
     auto softmax_pv = [&](f32x16 (&sc)[2], int t, uint64_t live) {
       if (live != ~0ull) {
-        const int nvalid = min(KT, N - t * KT);
+        const int nvalid = min(KT, Nq - t * KT);
         const uint64_t valid = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
@@ -407,25 +414,25 @@ __global__ __launch_bounds__(NT, GNN_ROW_MINBLOCKS) void triattn_row_kernel(cons
 #endif
     if (full) {
       // no masked key: tiles in order, liveness from N alone (no LDS reads in the loop)
-      if constexpr (HAS_BIAS) load_bias_row<T>(bb, brow, 0, N, g);
+      if constexpr (HAS_BIAS) load_bias_row<T>(bb, brow, 0, Nq, g);
       for (int t = 0; t < ntiles; ++t) {
         f32x16 sc[2];
         ROW_PRIO_HI();
         qk(sc, t);
         ROW_PRIO_LO();
-        if (HAS_BIAS && t + 1 < ntiles) load_bias_row<T>(bb, brow, (t + 1) * KT, N, g);
-        const int nvalid = N - t * KT;
+        if (HAS_BIAS && t + 1 < ntiles) load_bias_row<T>(bb, brow, (t + 1) * KT, Nq, g);
+        const int nvalid = Nq - t * KT;
         softmax_pv(sc, t, nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull));
       }
     } else {
-      if constexpr (HAS_BIAS) load_bias_row<T>(bb, brow, hdr.tile_list[0] * KT, N, g);
+      if constexpr (HAS_BIAS) load_bias_row<T>(bb, brow, hdr.tile_list[0] * KT, Nq, g);
       for (int it = 0; it < nrun; ++it) {
         const int t = hdr.tile_list[it];
         f32x16 sc[2];
         ROW_PRIO_HI();
         qk(sc, t);
         ROW_PRIO_LO();
-        if (HAS_BIAS && it + 1 < nrun) load_bias_row<T>(bb, brow, hdr.tile_list[it + 1] * KT, N, g);
+        if (HAS_BIAS && it + 1 < nrun) load_bias_row<T>(bb, brow, hdr.tile_list[it + 1] * KT, Nq, g);
         softmax_pv(sc, t, hdr.tile_live[t]);
       }
     }
