@@ -23,6 +23,7 @@
 #include "gnn_internal.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace gnn {
 
@@ -448,7 +449,12 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_kernel(const gnn_trimul_ar
 // once per workgroup), gate items stage through a tile of their own, the z tile is
 // double-buffered and the LayerNorm is wave-local (the 8 threads of a pixel are lanes of
 // one wave and reduce with cross-lane shuffles: the same two-pass mean / variance), so a
-// tile costs one barrier.
+// tile costs one barrier. A wave's gate item covers one of the two 32-pixel sub-tiles of its
+// projection unit, so the unit visits that sub-tile first and the gate MFMAs reuse its z
+// fragments (3 LDS fragment reads per k-step for 5 MFMAs). Accumulators start at zero and
+// the biases join in the epilogue, as the reference's linear layers add them (after the
+// product); the gates fold theirs into the exp2 argument. A tile whose mask values are all
+// one skips the mask multiply.
 template <int CK>
 struct ProjFastLds {
   static constexpr int ZR = CK + 8;  // z and gate-weight row pitch (16-bit elements)
@@ -461,7 +467,8 @@ struct ProjFastLds {
   static constexpr size_t bgo = gbuf + (size_t)PW * 32 * EG * 2;   // [CK] fp32
   static constexpr size_t lnw = bgo + (size_t)CK * 4;              // gamma, beta [2][CK] fp32
   static constexpr size_t mk = lnw + 2 * (size_t)CK * 4;           // [2][PTP] fp32
-  static constexpr size_t total = mk + 2 * (size_t)PTP * 4;
+  static constexpr size_t mk1 = mk + 2 * (size_t)PTP * 4;          // [2] int: tile mask all ones
+  static constexpr size_t total = mk1 + 16;
 };
 
 template <typename T, int CK, int CHK>  // CHK: c_hidden at compile time, 0 = from the arguments
@@ -486,8 +493,10 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
   float* lnw = reinterpret_cast<float*>(smem_raw + LD::lnw);
   float* lnb = lnw + CK;
   float* mk = reinterpret_cast<float*>(smem_raw + LD::mk);
+  int* mk1 = reinterpret_cast<int*>(smem_raw + LD::mk1);
   const bool outgoing = a.outgoing != 0;
   const int64_t ntiles = (int64_t)a.B * N * ((N + PTP - 1) / PTP);
+  constexpr float NLOG2E = -1.4426950408889634f;
 
   // ---- per-workgroup constants
   {
@@ -497,7 +506,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
       store8(&wgo_s[r * ZR + k0], load8(wgo + r * CK + k0));
     }
     for (int c = tid; c < CK; c += PNT) {
-      bgo_s[c] = ld_or<T>(a.g_out_b, c, 0.f);
+      bgo_s[c] = ld_or<T>(a.g_out_b, c, 0.f) * NLOG2E;  // the exp2 argument's bias term
       lnw[c] = ld_or<T>(a.ln_in_w, c, 1.f);
       lnb[c] = ld_or<T>(a.ln_in_b, c, 0.f);
     }
@@ -554,7 +563,11 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
       }
       store8(&zs[(nb * PTP + xpl) * ZR + k], TypeOps<T>::from_f32(z));
     }
-    if (tid < PTP) mk[nb * PTP + tid] = mreg;
+    if (tid < PTP) {  // wave 0 (PTP = 64): the tile's mask values and whether all are one
+      mk[nb * PTP + tid] = mreg;
+      const bool all1 = __ballot(mreg != 1.f) == 0;
+      if (tid == 0) mk1[nb] = all1;
+    }
   };
 
   // ---- projections of one tile
@@ -568,26 +581,22 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
   const bool has_go = wave < NGI;
   const int uo = wave % (CK / 32), so = wave / (CK / 32);  // this wave's gate item
 
+  // the unit's sub-tiles in the order (so, 1 - so): the gate item's sub-tile first
+  const int s_first = has_go ? so : 0;
+
   auto compute = [&](const PTile& tl, int cb) {
     const T* z = zs + cb * PTP * ZR;
     const float* m = mk + cb * PTP;
+    const bool all1 = mk1[cb] != 0;
     // gate item: acc = [channel][pixel], row = channel 32uo + 8(r/4) + 4g + r%4, col = pixel
-    // 32so + l32. Its MFMAs go first; the epilogue comes after the unit's.
+    // 32so + l32 (zero-initialised; bias in the epilogue)
     f32x16 accgo;
-    if (has_go) {
 #pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bgo_s[32 * uo + 8 * rg + 4 * g]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) accgo[4 * rg + e] = b4[e];
-      }
-#pragma unroll
-      for (int k = 0; k < NKS; ++k) {
-        const V8 wf = load8(&wgo_s[(32 * uo + l32) * ZR + 16 * k + 8 * g]);
-        const V8 zf = load8(&z[(32 * so + l32) * ZR + 16 * k + 8 * g]);
-        Mma<T, PREC_NATIVE>::step(accgo, wf, zf);
-      }
-    }
+    for (int r = 0; r < 16; ++r) accgo[r] = 0.f;
+    const T* zrow0 = z + (32 * s_first + l32) * ZR + 8 * g;        // sub-tile s_first
+    const T* zrow1 = z + (32 * (1 - s_first) + l32) * ZR + 8 * g;  // the other one
+    const T* wgrow_s = wgo_s + (32 * uo + l32) * ZR + 8 * g;
+    bool go_done = !has_go;
     // gated projection units: acc = [pixel][channel], row = pixel 32s + 8(r/4) + 4g + r%4,
     // col = channel 32u + l32; staged as [channel][pixel] for 128-byte row stores
     for (int u = wave; u < npg; u += PW) {
@@ -601,35 +610,54 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
           wgf[k] = load8(wgrow + 16 * k);
         }
         bp = ld_or<T>(a.p_in_b, ch, 0.f);
-        bg = ld_or<T>(a.g_in_b, ch, 0.f);
+        bg = ld_or<T>(a.g_in_b, ch, 0.f) * NLOG2E;  // the exp2 argument's bias term
         wp_unit = u;
       }
       f32x16 accp[PSUB], accg[PSUB];
 #pragma unroll
-      for (int s = 0; s < PSUB; ++s) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          accp[s][r] = bp;
-          accg[s][r] = bg;
-        }
-#pragma unroll
-        for (int k = 0; k < NKS; ++k) {
-          const V8 zf = load8(&z[(32 * s + l32) * ZR + 16 * k + 8 * g]);
-          Mma<T, PREC_NATIVE>::step(accp[s], zf, wpf[k]);
-          Mma<T, PREC_NATIVE>::step(accg[s], zf, wgf[k]);
-        }
-      }
-#pragma unroll
       for (int s = 0; s < PSUB; ++s)
 #pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          accp[s][r] = 0.f;
+          accg[s][r] = 0.f;
+        }
+      auto kloop = [&](auto with_go) {
+#pragma unroll
+        for (int k = 0; k < NKS; ++k) {
+          const V8 z0 = load8(zrow0 + 16 * k);
+          const V8 z1 = load8(zrow1 + 16 * k);
+          Mma<T, PREC_NATIVE>::step(accp[0], z0, wpf[k]);
+          Mma<T, PREC_NATIVE>::step(accg[0], z0, wgf[k]);
+          if constexpr (decltype(with_go)::value) Mma<T, PREC_NATIVE>::step(accgo, load8(wgrow_s + 16 * k), z0);
+          Mma<T, PREC_NATIVE>::step(accp[1], z1, wpf[k]);
+          Mma<T, PREC_NATIVE>::step(accg[1], z1, wgf[k]);
+        }
+      };
+      if (!go_done) {
+        kloop(std::true_type{});
+        go_done = true;
+      } else {
+        kloop(std::false_type{});
+      }
+#pragma unroll
+      for (int s = 0; s < PSUB; ++s) {
+        const int sub = s == 0 ? s_first : 1 - s_first;
+#pragma unroll
         for (int rg = 0; rg < 4; ++rg) {
-          const int pt = 32 * s + 8 * rg + 4 * g;  // pixel within the tile
-          const f32x4 m4 = *reinterpret_cast<const f32x4*>(&m[pt]);
+          const int pt = 32 * sub + 8 * rg + 4 * g;  // pixel within the tile
           f32x4 v;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = accp[s][4 * rg + e] * sigmoid_acc(accg[s][4 * rg + e]) * m4[e];
+          for (int e = 0; e < 4; ++e)
+            v[e] = (accp[s][4 * rg + e] + bp) *
+                   __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(accg[s][4 * rg + e], NLOG2E, bg)));
+          if (!all1) {
+            const f32x4 m4 = *reinterpret_cast<const f32x4*>(&m[pt]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] *= m4[e];
+          }
           store4(&ebuf[l32 * ER + pt], TypeOps<T>::from_f32(v));
         }
+      }
       wave_lds_sync();
       // 16-byte stores, 8 lanes per 64-pixel channel row
 #pragma unroll
@@ -653,12 +681,18 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
       }
       wave_lds_sync();
     }
+    if (!go_done) {  // no projection unit this tile: the gate item on its own
+#pragma unroll
+      for (int k = 0; k < NKS; ++k) Mma<T, PREC_NATIVE>::step(accgo, load8(wgrow_s + 16 * k), load8(zrow0 + 16 * k));
+    }
     if (has_go) {
 #pragma unroll
       for (int rg = 0; rg < 4; ++rg) {
+        const f32x4 nb4 = *reinterpret_cast<const f32x4*>(&bgo_s[32 * uo + 8 * rg + 4 * g]);
         f32x4 v;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = sigmoid_acc(accgo[4 * rg + e]);
+        for (int e = 0; e < 4; ++e)
+          v[e] = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(accgo[4 * rg + e], NLOG2E, nb4[e])));
         store4(&gbuf[l32 * EG + 8 * rg + 4 * g], TypeOps<T>::from_f32(v));
       }
       wave_lds_sync();
@@ -1058,7 +1092,10 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
 // round_up(N, 32): the projection stage writes zeros into columns N .. NP-1 of a and b. Rows
 // past N are loaded from row N-1 (their outputs are never stored). The finished tile is
 // staged in LDS, 128 rows at a time, and written with 16-byte row stores. The larger tile
-// halves the L2 -> LDS bytes per flop, which bound the 128-row tile.
+// halves the L2 -> LDS bytes per flop, which bound the 128-row tile. At N = 512 the kernel
+// moves its a / b / o bytes at about 4.5 TB/s, near the 4.9 TB/s a device-to-device copy
+// reaches; measured without gain: a fifth stage (160 KB of LDS), and reading the next
+// stage's fragments into a second register set while the current stage multiplies.
 template <int BM>
 struct ContractDma {
   static constexpr int BN = 256, BK = 32;
