@@ -15,7 +15,10 @@ the same workload, which also serves as the parity gate before timing). ``cold_m
 each kernel again after a 512 MiB scratch write (inputs then come from HBM, not from the
 Infinity Cache that holds them in the warm loop); ``value`` is the warm figure.
 ``attention_backward`` times one gnn_triattn_bwd call (dq, dk, dv and the pair-bias
-gradient) on the same attention inputs, outside the step.
+gradient) on the same attention inputs, outside the step. ``trimul_backward`` times forward +
+backward of the outgoing trimul with gradients on x and every weight, on the HIP path and on
+autograd through the torch restatement (what the reference runs for gradients), outside the
+step.
 """
 
 import argparse
@@ -48,7 +51,7 @@ def parse():
                          "the 256 MB Infinity Cache (0 skips)")
     ap.add_argument("--only", choices=["attn", "trimul"], default=None,
                     help="profile helper: run only one op (the JSON line is then partial)")
-    ap.add_argument("--no-backward", action="store_true", help="skip the attention backward timing")
+    ap.add_argument("--no-backward", action="store_true", help="skip the backward timings")
     ap.add_argument("--copy-calib", action="store_true",
                     help="profile helper: run a plain 256 MiB device copy (known HBM bytes) and exit, "
                          "to scale FETCH_SIZE / WRITE_SIZE counter readings")
@@ -265,6 +268,41 @@ def main():
                     "mfma_frac": round(bwd_flops / (bwd_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                     "algorithmic_flops": bwd_flops, "dbias_splits": splits}
 
+    # ---- trimul backward (not part of the step): forward + backward of the public op with
+    # gradients on x and every weight, through the HIP path (_TrimulHip) and through autograd
+    # over the torch restatement of trimul_torch, which is what the reference runs for
+    # gradients (it has no native trimul backward)
+    tri_backward = None
+    if args.only in (None, "trimul") and not args.no_backward:
+        from geometric_nn_ops_torch.triangle import _trimul as TM
+
+        gout = rn(1, N, N, C).to(dev, dt)
+
+        def fwd_bwd(use_torch):
+            xg = xd.detach().requires_grad_()
+            wg = {kk: vv.detach().requires_grad_() for kk, vv in wd.items()}
+            if use_torch:
+                y = TM.trimul_torch(xg, "outgoing", md, eps=1e-5, **wg)
+            else:
+                y = TM.triangle_multiplicative_update(xg, "outgoing", md, eps=1e-5, **wg)
+            y.backward(gout)
+
+        tri_backward = {"direction": "outgoing",
+                        "reference_behaviour": "autograd through trimul_torch (no native backward)"}
+        for label, use_torch in (("hip_fwd_bwd_ms", False), ("torch_autograd_fwd_bwd_ms", True)):
+            for _ in range(2):
+                fwd_bwd(use_torch)
+            tev = []
+            for _ in range(5):
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                fwd_bwd(use_torch)
+                e1.record(stream)
+                tev.append((e0, e1))
+            torch.cuda.synchronize()
+            tri_backward[label] = round(sorted(e0.elapsed_time(e1) for e0, e1 in tev)[len(tev) // 2], 4)
+
     # ---- algorithmic FLOPs / bytes per launch
     M = N * N
     e = 2
@@ -337,6 +375,7 @@ def main():
                             "the reference does not travel to it",
         "wall_s_timed": round(wall, 4),
         "attention_backward": backward,
+        "trimul_backward": tri_backward,
     }
     if cpu is not None:
         cpu_tflops = step_flops / cpu["seconds_per_step"] / 1e12

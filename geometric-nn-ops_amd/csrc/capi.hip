@@ -147,6 +147,40 @@ int gnn_pair_bias_proj(const gnn_pair_bias_args* args, void* stream) {
   return hip_status((hipError_t)rc, "pair_bias_proj");
 }
 
+int64_t gnn_layernorm_partials(int64_t rows, int64_t K) { return layernorm_partials(rows, K); }
+
+int gnn_layernorm_rows(const gnn_layernorm_args* args, void* stream) {
+  if (!args) return set_error(GNN_ERR_ARG, "layernorm_rows: args is NULL");
+  const gnn_layernorm_args& a = *args;
+  if (!a.x || !a.out) return set_error(GNN_ERR_ARG, "layernorm_rows: x and out are required");
+  if (a.rows < 1 || a.K < 1) return set_error(GNN_ERR_ARG, "layernorm_rows: rows and K must be positive");
+  if (a.x_stride < a.K || a.out_stride < a.K || (a.dy && a.dy_stride < a.K))
+    return set_error(GNN_ERR_ARG, "layernorm_rows: a row stride is smaller than K");
+  if (a.dy && a.bias) return set_error(GNN_ERR_ARG, "layernorm_rows: bias is a forward-only argument");
+  int rc = layernorm_rows(a, (hipStream_t)stream);
+  if (rc < 0) return rc;
+  return hip_status((hipError_t)rc, "layernorm_rows");
+}
+
+int gnn_trimul_gate_bwd(const gnn_gate_bwd_args* args, void* stream) {
+  if (!args) return set_error(GNN_ERR_ARG, "trimul_gate_bwd: args is NULL");
+  const gnn_gate_bwd_args& a = *args;
+  if (!a.grad || !a.value || !a.gate_pre || !a.d_value || !a.d_gate_pre)
+    return set_error(GNN_ERR_ARG, "trimul_gate_bwd: grad, value, gate_pre, d_value and d_gate_pre are required");
+  if (a.rows < 1 || a.K < 1) return set_error(GNN_ERR_ARG, "trimul_gate_bwd: rows and K must be positive");
+  const int64_t st[5] = {a.grad_stride, a.value_stride, a.gate_stride, a.dv_stride, a.dg_stride};
+  const void* ptr[5] = {a.grad, a.value, a.gate_pre, a.d_value, a.d_gate_pre};
+  const int64_t esz = a.dtype == GNN_F32 ? 4 : 2;
+  for (int i = 0; i < 5; ++i) {
+    if (st[i] < a.K) return set_error(GNN_ERR_ARG, "trimul_gate_bwd: a row stride is smaller than K");
+    if ((st[i] * esz) % 16 != 0 || !aligned(ptr[i], 16))
+      return set_error(GNN_ERR_ARG, "trimul_gate_bwd: rows must be 16-byte aligned");
+  }
+  int rc = gate_bwd(a, (hipStream_t)stream);
+  if (rc < 0) return rc;
+  return hip_status((hipError_t)rc, "trimul_gate_bwd");
+}
+
 const char* gnn_last_error(void) { return g_last_error.c_str(); }
 
 const char* gnn_version(void) { return "0.1.0 gfx950"; }

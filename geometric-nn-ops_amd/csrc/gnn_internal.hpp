@@ -34,4 +34,9 @@ int trimul_out(const gnn_trimul_args& a, hipStream_t stream);
 
 int pair_bias_proj(const gnn_pair_bias_args& a, hipStream_t stream);
 
+// Backward helpers of the triangle multiplicative update.
+int64_t layernorm_partials(int64_t rows, int64_t K);
+int layernorm_rows(const gnn_layernorm_args& a, hipStream_t stream);
+int gate_bwd(const gnn_gate_bwd_args& a, hipStream_t stream);
+
 }  // namespace gnn

@@ -1,0 +1,242 @@
+// Element-wise and LayerNorm kernels of the triangle multiplicative update's backward, for
+// gfx950.
+//
+// The reference has no native trimul backward: a forward that needs gradients runs its
+// pure-torch trimul_torch under autograd (geometric_nn_ops_torch/triangle/_trimul.py:31-36,
+// math in triangle/_reference/trimul.py:57-97). This library differentiates that same math.
+// The plain matrix products of the backward (weight gradients, input gradients of the
+// linear layers, the contraction's two products per channel) go to the vendor GEMM; the
+// rest is here:
+//
+//   layernorm_rows   y = (x - mean) * rstd * w + b per row, or its backward
+//                      xh = (x - mean) * rstd,  g = dy * w,
+//                      dx = rstd * (g - mean(g) - xh * mean(g * xh)),
+//                    plus per-workgroup column sums of dy * xh (-> dw) and dy (-> db), so
+//                    the weight gradients need no atomics and sum in a fixed order.
+//   gate_bwd         the backward of  out = value * sigmoid(gate_pre) [* mask per row]:
+//                      d_value = grad * s * m,   d_gate_pre = grad * value * m * s * (1 - s).
+//                    Used for the output gate (value = p_out(LN(o)), no mask) and for the
+//                    gated input projection (value = p_in(z), mask = the pair mask).
+//
+// Layout: one 32-lane half-wave per row (K a multiple of 32, at most 512: each lane holds
+// K / 32 consecutive columns, reduced with xor shuffles inside the half-wave); 16 rows per
+// 256-thread workgroup in flight (two per half-wave, loads issued together), a grid of at most
+// 4096 workgroups striding over the rows. Every tensor is
+// read once and written once, so both kernels are bound by HBM bandwidth.
+#include <algorithm>
+
+#include "gnn_common.hpp"
+#include "gnn_internal.hpp"
+
+namespace gnn {
+
+namespace {
+
+constexpr int LN_THREADS = 256;                 // 8 half-waves: 8 rows at a time
+constexpr int LN_ROWS = LN_THREADS / 32;
+constexpr int LN_MAX_K = 512;
+constexpr int LN_UNROLL = 2;                    // rows per half-wave step
+constexpr int LN_MAX_GRID = 4096;               // partial rows of the weight gradients
+
+template <typename T>
+__device__ __forceinline__ float ld1(const void* p, int64_t i, float dflt) {
+  return p ? TypeOps<T>::to_f32(((const T*)p)[i]) : dflt;
+}
+
+__device__ __forceinline__ float half_wave_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < 32; m <<= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
+// KPL columns per lane (K = 32 * KPL), lane c of a half-wave owning columns KPL c .. KPL c + KPL-1.
+// A half-wave takes LN_UNROLL rows per step, their loads issued together.
+template <typename T, int KPL, bool BWD>
+__global__ __launch_bounds__(LN_THREADS) void layernorm_rows_kernel(const gnn_layernorm_args a) {
+  const int K = 32 * KPL;
+  const int tid = threadIdx.x, hw = tid >> 5, c = tid & 31;
+  const int k0 = c * KPL;
+  float w[KPL], bsum[KPL], wsum[KPL];
+#pragma unroll
+  for (int e = 0; e < KPL; ++e) {
+    w[e] = ld1<T>(a.weight, k0 + e, 1.f);
+    bsum[e] = 0.f;  // backward: column sums of dy
+    wsum[e] = 0.f;  // backward: column sums of dy * xh
+  }
+  const float inv_k = 1.0f / (float)K;
+  const int64_t step = (int64_t)gridDim.x * LN_ROWS * LN_UNROLL;
+  for (int64_t r0 = ((int64_t)blockIdx.x * LN_ROWS + hw) * LN_UNROLL; r0 < a.rows; r0 += step) {
+    float x[LN_UNROLL][KPL], dy[LN_UNROLL][KPL];
+#pragma unroll
+    for (int u = 0; u < LN_UNROLL; ++u) {
+      const int64_t r = min(r0 + u, a.rows - 1);  // a row past the end repeats the last (not stored)
+      const T* xr = (const T*)a.x + r * a.x_stride + k0;
+#pragma unroll
+      for (int e = 0; e < KPL; ++e) x[u][e] = TypeOps<T>::to_f32(xr[e]);
+      if constexpr (BWD) {
+        const T* dyr = (const T*)a.dy + r * a.dy_stride + k0;
+#pragma unroll
+        for (int e = 0; e < KPL; ++e) dy[u][e] = TypeOps<T>::to_f32(dyr[e]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < LN_UNROLL; ++u) {
+      const int64_t r = r0 + u;
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < KPL; ++e) s += x[u][e];
+      const float mean = half_wave_sum(s) * inv_k;
+      float q = 0.f;
+#pragma unroll
+      for (int e = 0; e < KPL; ++e) {
+        x[u][e] -= mean;
+        q += x[u][e] * x[u][e];
+      }
+      const float rstd = 1.0f / sqrtf(half_wave_sum(q) * inv_k + a.eps);
+      if (r >= a.rows) continue;  // uniform over the half-wave (after its shuffles)
+      T* orow = (T*)a.out + r * a.out_stride + k0;
+      if constexpr (!BWD) {
+#pragma unroll
+        for (int e = 0; e < KPL; ++e)
+          orow[e] = TypeOps<T>::from_f32(x[u][e] * rstd * w[e] + ld1<T>(a.bias, k0 + e, 0.f));
+      } else {
+        float g[KPL];
+        float sg = 0.f, sgx = 0.f;
+#pragma unroll
+        for (int e = 0; e < KPL; ++e) {
+          const float xh = x[u][e] * rstd;
+          bsum[e] += dy[u][e];
+          wsum[e] += dy[u][e] * xh;
+          g[e] = dy[u][e] * w[e];
+          sg += g[e];
+          sgx += g[e] * xh;
+          x[u][e] = xh;
+        }
+        const float mg = half_wave_sum(sg) * inv_k, mgx = half_wave_sum(sgx) * inv_k;
+#pragma unroll
+        for (int e = 0; e < KPL; ++e) orow[e] = TypeOps<T>::from_f32(rstd * (g[e] - mg - x[u][e] * mgx));
+      }
+    }
+  }
+  if constexpr (BWD) {
+    if (!a.partial) return;  // uniform over the workgroup
+    // the 8 half-waves' column sums meet in LDS, summed in half-wave order
+    __shared__ float red[LN_ROWS][2][LN_MAX_K];
+#pragma unroll
+    for (int e = 0; e < KPL; ++e) {
+      red[hw][0][k0 + e] = wsum[e];
+      red[hw][1][k0 + e] = bsum[e];
+    }
+    __syncthreads();
+    float* part = a.partial + (int64_t)blockIdx.x * 2 * K;
+    for (int i = tid; i < 2 * K; i += LN_THREADS) {
+      const int which = i / K, col = i % K;
+      float acc = 0.f;
+#pragma unroll
+      for (int h = 0; h < LN_ROWS; ++h) acc += red[h][which][col];
+      part[i] = acc;
+    }
+  }
+}
+
+template <typename T, bool BWD>
+int launch_ln(const gnn_layernorm_args& a, hipStream_t st) {
+  const int grid = (int)layernorm_partials(a.rows, a.K);
+  switch (a.K / 32) {
+#define GNN_LN_CASE(KPL)                                                                              \
+  case KPL:                                                                                           \
+    hipLaunchKernelGGL((layernorm_rows_kernel<T, KPL, BWD>), dim3(grid), dim3(LN_THREADS), 0, st, a); \
+    break;
+    GNN_LN_CASE(1)
+    GNN_LN_CASE(2)
+    GNN_LN_CASE(3)
+    GNN_LN_CASE(4)
+    GNN_LN_CASE(5)
+    GNN_LN_CASE(6)
+    GNN_LN_CASE(7)
+    GNN_LN_CASE(8)
+    GNN_LN_CASE(9)
+    GNN_LN_CASE(10)
+    GNN_LN_CASE(11)
+    GNN_LN_CASE(12)
+    GNN_LN_CASE(13)
+    GNN_LN_CASE(14)
+    GNN_LN_CASE(15)
+    GNN_LN_CASE(16)
+#undef GNN_LN_CASE
+    default:
+      return set_error(GNN_ERR_UNSUPPORTED, "layernorm_rows: K must be a multiple of 32, at most 512");
+  }
+  return (int)hipGetLastError();
+}
+
+// ---- gate backward: 8 consecutive elements per thread ----------------------------------
+constexpr int GB_THREADS = 256;
+
+template <typename T>
+__global__ __launch_bounds__(GB_THREADS) void gate_bwd_kernel(const gnn_gate_bwd_args a) {
+  typedef typename TypeOps<T>::V8 V8;
+  const int64_t kc = a.K / 8;  // 8-element chunks per row
+  const int64_t total = a.rows * kc;
+  for (int64_t i = (int64_t)blockIdx.x * GB_THREADS + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * GB_THREADS) {
+    const int64_t r = i / kc, k = (i % kc) * 8;
+    const f32x8 gr = TypeOps<T>::to_f32(load8((const T*)a.grad + r * a.grad_stride + k));
+    const f32x8 v = TypeOps<T>::to_f32(load8((const T*)a.value + r * a.value_stride + k));
+    const f32x8 gp = TypeOps<T>::to_f32(load8((const T*)a.gate_pre + r * a.gate_stride + k));
+    const float m = a.mask ? TypeOps<T>::to_f32(((const T*)a.mask)[r * a.mask_stride]) : 1.f;
+    f32x8 dv, dg;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      // sigmoid with the hardware exp2 and reciprocal, as the forward's gates
+      const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gp[e] * -1.4426950408889634f));
+      const float gm = gr[e] * m;
+      dv[e] = gm * s;
+      dg[e] = gm * v[e] * s * (1.0f - s);
+    }
+    store8((T*)a.d_value + r * a.dv_stride + k, TypeOps<T>::from_f32(dv));
+    store8((T*)a.d_gate_pre + r * a.dg_stride + k, TypeOps<T>::from_f32(dg));
+  }
+}
+
+template <typename T>
+int launch_gate(const gnn_gate_bwd_args& a, hipStream_t st) {
+  const int64_t chunks = a.rows * (a.K / 8);
+  const int64_t want = (chunks + GB_THREADS - 1) / GB_THREADS;
+  const int grid = (int)std::min<int64_t>(want, (int64_t)persistent_grid((const void*)gate_bwd_kernel<T>,
+                                                                         GB_THREADS, 0) * 4);
+  hipLaunchKernelGGL(gate_bwd_kernel<T>, dim3(grid < 1 ? 1 : grid), dim3(GB_THREADS), 0, st, a);
+  return (int)hipGetLastError();
+}
+
+}  // namespace
+
+int64_t layernorm_partials(int64_t rows, int64_t K) {
+  (void)K;
+  const int64_t want = (rows + LN_ROWS * LN_UNROLL - 1) / (LN_ROWS * LN_UNROLL);
+  return want < 1 ? 1 : (want > LN_MAX_GRID ? LN_MAX_GRID : want);
+}
+
+int layernorm_rows(const gnn_layernorm_args& a, hipStream_t st) {
+  if (a.K % 32 != 0 || a.K > LN_MAX_K)
+    return set_error(GNN_ERR_UNSUPPORTED, "layernorm_rows: K must be a multiple of 32, at most 512");
+  const bool bwd = a.dy != nullptr;
+  switch (a.dtype) {
+    case GNN_BF16: return bwd ? launch_ln<bf16, true>(a, st) : launch_ln<bf16, false>(a, st);
+    case GNN_F16: return bwd ? launch_ln<f16, true>(a, st) : launch_ln<f16, false>(a, st);
+    case GNN_F32: return bwd ? launch_ln<float, true>(a, st) : launch_ln<float, false>(a, st);
+  }
+  return set_error(GNN_ERR_ARG, "layernorm_rows: unknown dtype");
+}
+
+int gate_bwd(const gnn_gate_bwd_args& a, hipStream_t st) {
+  if (a.K % 8 != 0) return set_error(GNN_ERR_UNSUPPORTED, "gate_bwd: K must be a multiple of 8");
+  switch (a.dtype) {
+    case GNN_BF16: return launch_gate<bf16>(a, st);
+    case GNN_F16: return launch_gate<f16>(a, st);
+    case GNN_F32: return launch_gate<float>(a, st);
+  }
+  return set_error(GNN_ERR_ARG, "gate_bwd: unknown dtype");
+}
+
+}  // namespace gnn

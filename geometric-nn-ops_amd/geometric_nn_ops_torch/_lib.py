@@ -147,6 +147,48 @@ class PairBiasArgs(ctypes.Structure):
     ]
 
 
+class LayerNormArgs(ctypes.Structure):
+    """Mirror of ``gnn_layernorm_args``."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("dy", ctypes.c_void_p),
+        ("weight", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("partial", ctypes.c_void_p),
+        ("rows", ctypes.c_int64),
+        ("K", ctypes.c_int64),
+        ("x_stride", ctypes.c_int64),
+        ("dy_stride", ctypes.c_int64),
+        ("out_stride", ctypes.c_int64),
+        ("eps", ctypes.c_float),
+        ("dtype", ctypes.c_int32),
+    ]
+
+
+class GateBwdArgs(ctypes.Structure):
+    """Mirror of ``gnn_gate_bwd_args``."""
+
+    _fields_ = [
+        ("grad", ctypes.c_void_p),
+        ("value", ctypes.c_void_p),
+        ("gate_pre", ctypes.c_void_p),
+        ("mask", ctypes.c_void_p),
+        ("d_value", ctypes.c_void_p),
+        ("d_gate_pre", ctypes.c_void_p),
+        ("rows", ctypes.c_int64),
+        ("K", ctypes.c_int64),
+        ("grad_stride", ctypes.c_int64),
+        ("value_stride", ctypes.c_int64),
+        ("gate_stride", ctypes.c_int64),
+        ("mask_stride", ctypes.c_int64),
+        ("dv_stride", ctypes.c_int64),
+        ("dg_stride", ctypes.c_int64),
+        ("dtype", ctypes.c_int32),
+    ]
+
+
 # Every symbol include/gnn_triangle.h declares, with its ctypes signature.
 _SIGNATURES = {
     "gnn_triattn_fwd": (ctypes.c_int, [ctypes.POINTER(TriAttnArgs), ctypes.c_void_p]),
@@ -161,6 +203,9 @@ _SIGNATURES = {
     "gnn_trimul_contract": (ctypes.c_int, [ctypes.POINTER(TrimulArgs), ctypes.c_void_p]),
     "gnn_trimul_out": (ctypes.c_int, [ctypes.POINTER(TrimulArgs), ctypes.c_void_p]),
     "gnn_pair_bias_proj": (ctypes.c_int, [ctypes.POINTER(PairBiasArgs), ctypes.c_void_p]),
+    "gnn_layernorm_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int64]),
+    "gnn_layernorm_rows": (ctypes.c_int, [ctypes.POINTER(LayerNormArgs), ctypes.c_void_p]),
+    "gnn_trimul_gate_bwd": (ctypes.c_int, [ctypes.POINTER(GateBwdArgs), ctypes.c_void_p]),
     "gnn_last_error": (ctypes.c_char_p, []),
     "gnn_version": (ctypes.c_char_p, []),
 }

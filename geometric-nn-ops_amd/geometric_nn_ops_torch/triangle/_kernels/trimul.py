@@ -148,3 +148,169 @@ def trimul_hip(
     run_stage("gnn_trimul_fwd", args, x.device)
     del keep, workspace
     return out.reshape(x.shape)
+
+
+# ------------------------------------------------------------------------------ backward
+# The reference has no native trimul backward: with gradients it runs trimul_torch under
+# autograd (geometric_nn_ops_torch/triangle/_trimul.py:31-36; math in
+# triangle/_reference/trimul.py:57-97). trimul_bwd_hip differentiates the same math. The
+# LayerNorms (forward recompute and backward, with deterministic per-workgroup weight-gradient
+# partials) and the two sigmoid gates run on this library's kernels (gnn_layernorm_rows,
+# gnn_trimul_gate_bwd); the plain matrix products (the three input projections as one
+# [4 Ch + C, C] linear, p_out, the contraction's two products per channel, the weight
+# gradients) go to the vendor GEMM through torch. a, b and o come from the forward's workspace.
+
+def layernorm_rows_hip(x2d, weight=None, bias=None, eps=1e-5, *, dy=None, partials=False):
+    """Row LayerNorm of ``x2d`` ``[R, K]`` (columns contiguous): ``LN(x)`` when ``dy`` is
+    None, else ``dx`` and, with ``partials``, ``(dweight, dbias)`` in fp32 summed over the
+    kernel's per-workgroup partial rows."""
+    lib = _lib.load()
+    R, K = x2d.shape
+    out = torch.empty((R, K), device=x2d.device, dtype=x2d.dtype)
+    a = _lib.LayerNormArgs()
+    a.x, a.out = x2d.data_ptr(), out.data_ptr()
+    a.weight = None if weight is None else weight.data_ptr()
+    a.rows, a.K = R, K
+    a.x_stride, a.out_stride = x2d.stride(0), out.stride(0)
+    a.eps, a.dtype = float(eps), _lib.DTYPE_CODE[x2d.dtype]
+    part = None
+    if dy is None:
+        a.bias = None if bias is None else bias.data_ptr()
+    else:
+        a.dy, a.dy_stride = dy.data_ptr(), dy.stride(0)
+        if partials:
+            part = torch.empty((lib.gnn_layernorm_partials(R, K), 2, K), device=x2d.device,
+                               dtype=torch.float32)
+            a.partial = part.data_ptr()
+    with torch.cuda.device(x2d.device):
+        rc = lib.gnn_layernorm_rows(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(x2d.device)))
+    _lib.check(rc, "gnn_layernorm_rows")
+    if part is None:
+        return out
+    sums = part.sum(0)
+    return out, sums[0], sums[1]
+
+
+def gate_bwd_hip(grad, value, gate_pre, mask_rows=None, *, d_value=None, d_gate_pre=None):
+    """Backward of ``value * sigmoid(gate_pre) * mask_rows[:, None]`` for ``[R, K]`` row
+    views (columns contiguous); writes into ``d_value`` / ``d_gate_pre`` (allocated when
+    None) and returns them."""
+    lib = _lib.load()
+    R, K = grad.shape
+    if d_value is None:
+        d_value = torch.empty((R, K), device=grad.device, dtype=grad.dtype)
+    if d_gate_pre is None:
+        d_gate_pre = torch.empty((R, K), device=grad.device, dtype=grad.dtype)
+    a = _lib.GateBwdArgs()
+    a.grad, a.value, a.gate_pre = grad.data_ptr(), value.data_ptr(), gate_pre.data_ptr()
+    a.d_value, a.d_gate_pre = d_value.data_ptr(), d_gate_pre.data_ptr()
+    if mask_rows is not None:
+        a.mask, a.mask_stride = mask_rows.data_ptr(), mask_rows.stride(0)
+    a.rows, a.K = R, K
+    a.grad_stride, a.value_stride, a.gate_stride = grad.stride(0), value.stride(0), gate_pre.stride(0)
+    a.dv_stride, a.dg_stride = d_value.stride(0), d_gate_pre.stride(0)
+    a.dtype = _lib.DTYPE_CODE[grad.dtype]
+    with torch.cuda.device(grad.device):
+        rc = lib.gnn_trimul_gate_bwd(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(grad.device)))
+    _lib.check(rc, "gnn_trimul_gate_bwd")
+    return d_value, d_gate_pre
+
+
+def _wgrad(d, t, slices=64):
+    """``d^T t`` for ``[M, O]`` / ``[M, I]`` with M in the hundreds of thousands: the sum
+    over M split into batched slices (one GEMM each, summed in fp32 in slice order), since a
+    single product with an O x I output leaves most of the GPU idle."""
+    M = d.shape[0]
+    while slices > 1 and M % slices:
+        slices //= 2
+    ds = d.reshape(slices, M // slices, d.shape[1])
+    ts = t.reshape(slices, M // slices, t.shape[1])
+    return torch.bmm(ts.transpose(1, 2), ds).sum(0, dtype=torch.float32).t()
+
+
+def _operand(ws, off, B, Ch, N, NP, dtype):
+    """The contraction operand of the workspace as ``[B * Ch, N, N]`` (row = output index,
+    column = contraction index), contiguous."""
+    el = torch.tensor([], dtype=dtype).element_size()
+    n = B * Ch * N * NP
+    flat = ws[off:off + n * el].view(dtype)
+    if el == 2:  # k-blocked [B, Ch, NP / 32, N, 32]
+        t = flat.view(B * Ch, NP // 32, N, 32).permute(0, 2, 1, 3).reshape(B * Ch, N, NP)
+    else:  # row-major [B, Ch, N, NP]
+        t = flat.view(B * Ch, N, NP)
+    return t[..., :N].contiguous()
+
+
+def trimul_bwd_hip(x, direction, mask, eps, weights, workspace, offsets, dout):
+    """Gradients ``(dx, {weight name: grad or None})`` of the triangle multiplicative update
+    given the forward's ``workspace`` / ``offsets`` (a, b, g, o) and the output gradient."""
+    outgoing = is_outgoing(direction)
+    N, C = x.shape[-2], x.shape[-1]
+    lead = x.shape[:-3]
+    B = math.prod(lead)
+    M = B * N * N
+    dt = x.dtype
+    dev = x.device
+    w = {k: (None if v is None else v.to(device=dev, dtype=dt)) for k, v in weights.items()}
+    Ch = w["p_in_weight"].shape[0] // 2
+    NP = (N + 31) // 32 * 32
+
+    def zeros_or(t, n):
+        return t if t is not None else torch.zeros(n, device=dev, dtype=dt)
+
+    xk = _aligned(x.reshape(M, C))
+    dout2 = _aligned(dout.reshape(M, C).to(dt))
+    z = layernorm_rows_hip(xk, w["norm_in_weight"], w["norm_in_bias"], eps)
+    # the three projections of z as one linear: [p_in (2 Ch); g_in (2 Ch); g_out (C)]
+    wcat = torch.cat([w["p_in_weight"], w["g_in_weight"], w["g_out_weight"]], 0)
+    bcat = torch.cat([zeros_or(w["p_in_bias"], 2 * Ch), zeros_or(w["g_in_bias"], 2 * Ch),
+                      zeros_or(w["g_out_bias"], C)])
+    lin = torch.nn.functional.linear(z, wcat, bcat)  # [M, 4 Ch + C]
+    p, gpre, gopre = lin[:, :2 * Ch], lin[:, 2 * Ch:4 * Ch], lin[:, 4 * Ch:]
+    # output stage: out = p_out(LN_out(o)) * sigmoid(gopre)
+    o_cm = workspace[offsets[3]:offsets[3] + B * Ch * N * NP * x.element_size()].view(dt).view(B, Ch, N, NP)
+    o_pm = o_cm[..., :N].permute(0, 2, 3, 1).reshape(M, Ch).contiguous()
+    on = layernorm_rows_hip(o_pm, w["norm_out_weight"], w["norm_out_bias"], eps)
+    y = torch.nn.functional.linear(on, w["p_out_weight"], w["p_out_bias"])
+    dlin = torch.empty((M, 4 * Ch + C), device=dev, dtype=dt)
+    dy, _ = gate_bwd_hip(dout2, y, gopre, d_gate_pre=dlin[:, 4 * Ch:])
+    grads = {}
+    grads["p_out_weight"] = _wgrad(dy, on)
+    grads["p_out_bias"] = dy.sum(0, dtype=torch.float32)
+    don = dy @ w["p_out_weight"]
+    do_pm, dlnw, dlnb = layernorm_rows_hip(o_pm, w["norm_out_weight"], eps=eps, dy=don, partials=True)
+    grads["norm_out_weight"], grads["norm_out_bias"] = dlnw, dlnb
+    # contraction: o_c = A_c B_c^T per (batch, channel) plane in the workspace's operand layout
+    A = _operand(workspace, offsets[0], B, Ch, N, NP, dt)
+    Bm = _operand(workspace, offsets[1], B, Ch, N, NP, dt)
+    do_cm = do_pm.reshape(B, N, N, Ch).permute(0, 3, 1, 2).reshape(B * Ch, N, N).contiguous()
+    dA = torch.bmm(do_cm, Bm)                    # dA[i, k] = sum_j dO[i, j] B[j, k]
+    dBt = torch.bmm(A.transpose(1, 2), do_cm)    # dB[j, k] = sum_i dO[i, j] A[i, k], as [k, j]
+    # planes -> the pixel layout of a / b (plane [i, k] is pixel (i, k) outgoing, (k, i) incoming)
+    dab = torch.empty((B, N, N, 2 * Ch), device=dev, dtype=dt)
+    dA4, dBt4 = dA.view(B, Ch, N, N), dBt.view(B, Ch, N, N)
+    if outgoing:
+        dab[..., :Ch] = dA4.permute(0, 2, 3, 1)
+        dab[..., Ch:] = dBt4.permute(0, 3, 2, 1)
+    else:
+        dab[..., :Ch] = dA4.permute(0, 3, 2, 1)
+        dab[..., Ch:] = dBt4.permute(0, 2, 3, 1)
+    dab = dab.view(M, 2 * Ch)
+    m_rows = None
+    if mask is not None:
+        m_rows = mask.to(device=dev, dtype=dt).expand(*x.shape[:-1]).reshape(M).contiguous()
+    gate_bwd_hip(dab, p, gpre, m_rows, d_value=dlin[:, :2 * Ch], d_gate_pre=dlin[:, 2 * Ch:4 * Ch])
+    dwcat = _wgrad(dlin, z)
+    dbcat = dlin.sum(0, dtype=torch.float32)
+    grads["p_in_weight"], grads["g_in_weight"], grads["g_out_weight"] = (
+        dwcat[:2 * Ch], dwcat[2 * Ch:4 * Ch], dwcat[4 * Ch:])
+    grads["p_in_bias"], grads["g_in_bias"], grads["g_out_bias"] = (
+        dbcat[:2 * Ch], dbcat[2 * Ch:4 * Ch], dbcat[4 * Ch:])
+    dz = dlin @ wcat
+    dx, dlnw, dlnb = layernorm_rows_hip(xk, w["norm_in_weight"], eps=eps, dy=dz, partials=True)
+    grads["norm_in_weight"], grads["norm_in_bias"] = dlnw, dlnb
+    out = {}
+    for key in _WEIGHT_KEYS:
+        src = weights.get(key)
+        out[key] = None if src is None else grads[key].to(src.dtype).reshape(src.shape)
+    return dx.reshape(x.shape), out

@@ -30,6 +30,10 @@
  *   gnn_triattn_bwd   -> EvoformerAttention.backward (triangle_attention.py:1278-1442)
  *   gnn_pair_bias_proj -> _project_pair_bias of attention_pair_bias
  *                        (geometric_nn_ops_torch/triangle/_reference/attention_pair_bias.py:17-22)
+ *   gnn_layernorm_rows, gnn_trimul_gate_bwd -> the LayerNorm and gate nodes of autograd
+ *                        through trimul_torch (triangle/_trimul.py:31-36,
+ *                        triangle/_reference/trimul.py:57-97): the reference's trimul
+ *                        backward, which has no native kernel
  */
 #ifndef GNN_TRIANGLE_H
 #define GNN_TRIANGLE_H
@@ -233,6 +237,63 @@ typedef struct gnn_pair_bias_args {
  * pair-rep half of attention_pair_bias (triangle/_attention_pair_bias.py:11-98); the
  * attention itself runs on gnn_triattn_fwd with N_seq = the multiplicity. */
 int gnn_pair_bias_proj(const gnn_pair_bias_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------------
+ * Backward of the triangle multiplicative update. The reference has no native backward:
+ * with gradients it runs trimul_torch under autograd (geometric_nn_ops_torch/triangle/
+ * _trimul.py:31-36; math in triangle/_reference/trimul.py:57-97). The library's backward
+ * differentiates that math with these two kernels plus vendor GEMMs for the plain matrix
+ * products (geometric_nn_ops_torch/triangle/_kernels/trimul.py::trimul_bwd_hip).
+ *
+ * Row LayerNorm over the last K columns (F.layer_norm semantics: biased variance,
+ * 1/sqrt(var + eps)), forward or backward:
+ *   forward  (dy == NULL): out = (x - mean) * rstd * weight + bias
+ *   backward (dy != NULL): xh = (x - mean) * rstd, g = dy * weight,
+ *                          out = dx = rstd * (g - mean(g) - xh * mean(g * xh));
+ *            and, if `partial` is set, partial[w][0][k] / partial[w][1][k] = the sums of
+ *            dy * xh / dy over the rows workgroup w handled (w < gnn_layernorm_partials):
+ *            the weight / bias gradients are their sums over w.
+ * Every tensor in `dtype` except `partial` (fp32); rows addressed by row strides (elements),
+ * columns contiguous; K a multiple of 32 and at most 512.
+ */
+typedef struct gnn_layernorm_args {
+  const void* x;      /* [rows, K] */
+  const void* dy;     /* NULL = forward; else [rows, K], the gradient of the output */
+  const void* weight; /* [K] or NULL (ones) */
+  const void* bias;   /* [K] or NULL (zeros); forward only */
+  void* out;          /* [rows, K]: LN(x) (forward) or dx (backward) */
+  float* partial;     /* backward, optional: [gnn_layernorm_partials(rows, K)][2][K] */
+  int64_t rows, K;
+  int64_t x_stride, dy_stride, out_stride;
+  float eps;
+  int32_t dtype; /* enum gnn_dtype */
+} gnn_layernorm_args;
+
+/* Replaces the LayerNorm autograd nodes of the reference's trimul_torch backward (the
+ * F.layer_norm calls at triangle/_reference/trimul.py:85 and :94); no native counterpart. */
+int64_t gnn_layernorm_partials(int64_t rows, int64_t K);
+int gnn_layernorm_rows(const gnn_layernorm_args* args, void* stream);
+
+/* Backward of out = value * sigmoid(gate_pre) * mask (mask per row, NULL = 1):
+ *   d_value = grad * s * mask,  d_gate_pre = grad * value * mask * s * (1 - s),  s = sigmoid(gate_pre).
+ * [rows, K] tensors by row strides (columns contiguous, rows and bases 16-byte aligned),
+ * mask [rows] by mask_stride, all in `dtype`; K a multiple of 8. */
+typedef struct gnn_gate_bwd_args {
+  const void* grad;
+  const void* value;
+  const void* gate_pre;
+  const void* mask;
+  void* d_value;
+  void* d_gate_pre;
+  int64_t rows, K;
+  int64_t grad_stride, value_stride, gate_stride, mask_stride, dv_stride, dg_stride;
+  int32_t dtype; /* enum gnn_dtype */
+} gnn_gate_bwd_args;
+
+/* Replaces the sigmoid / multiply autograd nodes of the gated projections in the reference's
+ * trimul_torch backward (triangle/_reference/trimul.py:86-90 and :95-97: p * sigmoid(g) * mask
+ * and p_out(o) * sigmoid(g_out(z))); no native counterpart. */
+int gnn_trimul_gate_bwd(const gnn_gate_bwd_args* args, void* stream);
 
 /* Message for the last failing call on this thread ("" if none). */
 const char* gnn_last_error(void);

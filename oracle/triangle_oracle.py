@@ -13,6 +13,8 @@ Reference files followed (paths relative to AMDResearch/geometric-nn-ops):
                                         1/sqrt(var + eps)), called at _reference/trimul.py:85,94
   * triangle_attention_grad (dq, dk, dv, N_seq-summed dbias): the autograd of
     _reference/triangle_attention.py:11-44 written out
+  * trimul_grad / layer_norm_grad (dx and every weight gradient): the autograd of
+    _reference/trimul.py:57-97 written out (the reference itself has no other backward)
   * attention_pair_bias (pair-bias projection, multiplicity broadcast, key mask with a
     caller-given magnitude, gate from s, output projection)
                                         geometric_nn_ops_torch/triangle/_reference/attention_pair_bias.py:17-89
@@ -29,7 +31,9 @@ sizes, against triangle_attention with N_seq = the multiplicity (the shared-bias
 identity), and the reference's known answers (masked keys ignored, cached bias equal to the
 recomputed one, copies with equal inputs equal, a per-batch mask equal to its per-copy
 repetition); triangle_attention_grad against central finite differences of
-triangle_attention (every input, with bias and mask).
+triangle_attention (every input, with bias and mask); trimul_grad and layer_norm_grad against
+central finite differences of trimul / layer_norm (every input and weight, both directions,
+with a mask).
 """
 
 from __future__ import annotations
@@ -208,6 +212,80 @@ def trimul_grid(x, direction="outgoing", mask=None, rows=(0,), cols=(0,), *, eps
     zg = layer_norm(xg, w.get("norm_in_weight"), w.get("norm_in_bias"), eps, dtype=dtype)
     g = sigmoid(linear(zg, w["g_out_weight"], w.get("g_out_bias"), dtype=dtype))
     return linear(on, w["p_out_weight"], w.get("p_out_bias"), dtype=dtype) * g
+
+
+# ------------------------------------------------ trimul gradients (autograd of the reference's
+# trimul_torch, _reference/trimul.py:57-97, written out)
+def layer_norm_grad(x, dy, weight=None, eps=1e-5, *, dtype=np.float64):
+    """``(dx, dweight, dbias)`` of ``sum(layer_norm(x, weight, bias) * dy)`` over the last
+    axis; the weight / bias gradients are summed over every leading axis."""
+    x = np.asarray(x, dtype=dtype)
+    dy = np.asarray(dy, dtype=dtype)
+    mean = x.mean(axis=-1, keepdims=True)
+    rstd = 1.0 / np.sqrt(((x - mean) ** 2).mean(axis=-1, keepdims=True) + dtype(eps))
+    xh = (x - mean) * rstd
+    g = dy if weight is None else dy * np.asarray(weight, dtype=dtype)
+    dx = rstd * (g - g.mean(axis=-1, keepdims=True) - xh * (g * xh).mean(axis=-1, keepdims=True))
+    lead = tuple(range(x.ndim - 1))
+    return dx, (dy * xh).sum(axis=lead), dy.sum(axis=lead)
+
+
+def trimul_grad(x, direction="outgoing", mask=None, dout=None, *, eps=1e-5, dtype=np.float64, **w):
+    """Gradients of ``sum(trimul(x, ...) * dout)``: a dict with ``"x"`` and one entry per
+    weight keyword (None where the weight is None). Weight gradients are summed over the
+    pixels and every batch axis; the mask gets none (the reference's mask is data)."""
+    outgoing = is_outgoing(direction)
+    x = np.asarray(x, dtype=dtype)
+    dout = np.asarray(dout, dtype=dtype)
+    W = {k: (None if v is None else np.asarray(v, dtype=dtype)) for k, v in w.items()}
+    c_hidden = W["p_in_weight"].shape[0] // 2
+    lead = tuple(range(x.ndim - 1))
+
+    def lin(t, wk, bk):
+        return linear(t, W[wk], W.get(bk), dtype=dtype)
+
+    z = layer_norm(x, W.get("norm_in_weight"), W.get("norm_in_bias"), eps, dtype=dtype)
+    lp, lg, lgo = lin(z, "p_in_weight", "p_in_bias"), lin(z, "g_in_weight", "g_in_bias"), \
+        lin(z, "g_out_weight", "g_out_bias")
+    sg, sgo = sigmoid(lg), sigmoid(lgo)
+    m = np.ones(x.shape[:-1] + (1,), dtype) if mask is None else \
+        np.broadcast_to(np.asarray(mask, dtype=dtype), x.shape[:-1])[..., None]
+    ab = lp * sg * m
+    a, b = ab[..., :c_hidden], ab[..., c_hidden:]
+    o = combine(a, b, outgoing)
+    on = layer_norm(o, W.get("norm_out_weight"), W.get("norm_out_bias"), eps, dtype=dtype)
+    y = lin(on, "p_out_weight", "p_out_bias")
+    # out = y * sgo
+    dy = dout * sgo
+    dlgo = dout * y * sgo * (1 - sgo)
+    def outer(d, t):  # sum over every leading axis of d[..., o] t[..., i]
+        return d.reshape(-1, d.shape[-1]).T @ t.reshape(-1, t.shape[-1])
+
+    gr = {"p_out_weight": outer(dy, on), "p_out_bias": dy.sum(axis=lead)}
+    don = dy @ W["p_out_weight"]
+    do, gr["norm_out_weight"], gr["norm_out_bias"] = layer_norm_grad(o, don, W.get("norm_out_weight"), eps,
+                                                                     dtype=dtype)
+    if outgoing:  # o[i, j] = sum_k a[i, k] b[j, k]
+        da = np.einsum("...ijc,...jkc->...ikc", do, b)
+        db = np.einsum("...ijc,...ikc->...jkc", do, a)
+    else:  # o[i, j] = sum_k a[k, i] b[k, j]
+        da = np.einsum("...ijc,...kjc->...kic", do, b)
+        db = np.einsum("...ijc,...kic->...kjc", do, a)
+    dab = np.concatenate([da, db], axis=-1)
+    dlp = dab * sg * m
+    dlg = dab * lp * m * sg * (1 - sg)
+    for name, d in (("p_in", dlp), ("g_in", dlg), ("g_out", dlgo)):
+        gr[f"{name}_weight"] = outer(d, z)
+        gr[f"{name}_bias"] = d.sum(axis=lead)
+    dz = dlp @ W["p_in_weight"] + dlg @ W["g_in_weight"] + dlgo @ W["g_out_weight"]
+    dx, gr["norm_in_weight"], gr["norm_in_bias"] = layer_norm_grad(x, dz, W.get("norm_in_weight"), eps,
+                                                                   dtype=dtype)
+    out = {"x": dx}
+    for key in ("norm_in_weight", "norm_in_bias", "p_in_weight", "p_in_bias", "g_in_weight", "g_in_bias",
+                "norm_out_weight", "norm_out_bias", "p_out_weight", "p_out_bias", "g_out_weight",
+                "g_out_bias"):
+        out[key] = None if W.get(key) is None else gr[key]
+    return out
 
 
 # ------------------------------------------------------------------------- metrics

@@ -164,8 +164,9 @@ def test_unsupported_configs_use_the_torch_path(config):
 
 
 def test_kernel_dispatch_rule_for_gpu_tensors():
-    """The GPU rule, evaluated on a stand-in tensor that reports is_cuda: kernel unless a
-    backward could run or the channel counts are outside the kernels' tiling."""
+    """The GPU rule, evaluated on a stand-in tensor that reports is_cuda: kernels (forward,
+    and the HIP backward when gradients are needed) unless the mask requires grad or the
+    channel counts are outside the kernels' tiling."""
     class FakeCuda:
         is_cuda = True
         dtype = torch.bfloat16
@@ -177,10 +178,15 @@ def test_kernel_dispatch_rule_for_gpu_tensors():
 
     w = {"p_in_weight": torch.zeros(256, 128)}
     assert not _trimul._needs_torch_path(FakeCuda(), w.items())
+    assert not _trimul._needs_grad(FakeCuda(), w.items())
+    # gradients go to the HIP forward + backward, unless the mask itself requires grad
     w_req = {"p_in_weight": torch.zeros(256, 128, requires_grad=True)}
-    assert _trimul._needs_torch_path(FakeCuda(), w_req.items())
+    assert not _trimul._needs_torch_path(FakeCuda(), w_req.items())
+    assert _trimul._needs_grad(FakeCuda(), w_req.items())
+    assert _trimul._needs_torch_path(FakeCuda(), w_req.items(), torch.ones(8, 8, requires_grad=True))
     with torch.no_grad():
-        assert not _trimul._needs_torch_path(FakeCuda(), w_req.items())
+        assert not _trimul._needs_grad(FakeCuda(), w_req.items())
+        assert not _trimul._needs_torch_path(FakeCuda(), w_req.items(), torch.ones(8, 8, requires_grad=True))
     assert _trimul._needs_torch_path(FakeCuda(), {"p_in_weight": torch.zeros(96, 128)}.items())
 
 

@@ -50,6 +50,12 @@ def _c_layout():
       printf("gnn_trimul_args %zu\n", sizeof(gnn_trimul_args));
       printf("gnn_pair_bias_args %zu\n", sizeof(gnn_pair_bias_args));
       printf("gnn_triattn_bwd_args %zu\n", sizeof(gnn_triattn_bwd_args));
+      printf("gnn_layernorm_args %zu\n", sizeof(gnn_layernorm_args));
+      printf("gnn_gate_bwd_args %zu\n", sizeof(gnn_gate_bwd_args));
+      P(gnn_layernorm_args, partial) P(gnn_layernorm_args, rows) P(gnn_layernorm_args, out_stride)
+      P(gnn_layernorm_args, eps) P(gnn_layernorm_args, dtype)
+      P(gnn_gate_bwd_args, d_gate_pre) P(gnn_gate_bwd_args, rows) P(gnn_gate_bwd_args, mask_stride)
+      P(gnn_gate_bwd_args, dg_stride) P(gnn_gate_bwd_args, dtype)
       P(gnn_triattn_args, lse) P(gnn_triattn_args, D) P(gnn_triattn_args, bias_stride)
       P(gnn_triattn_args, mask_stride) P(gnn_triattn_args, scale) P(gnn_triattn_args, precision)
       P(gnn_trimul_args, mask_stride) P(gnn_trimul_args, workspace_bytes) P(gnn_trimul_args, Ch)
@@ -75,8 +81,11 @@ def test_ctypes_structs_match_c_layout(tmp_path):
     assert int(lines["gnn_trimul_args"]) == ctypes.sizeof(_lib.TrimulArgs)
     assert int(lines["gnn_pair_bias_args"]) == ctypes.sizeof(_lib.PairBiasArgs)
     assert int(lines["gnn_triattn_bwd_args"]) == ctypes.sizeof(_lib.TriAttnBwdArgs)
+    assert int(lines["gnn_layernorm_args"]) == ctypes.sizeof(_lib.LayerNormArgs)
+    assert int(lines["gnn_gate_bwd_args"]) == ctypes.sizeof(_lib.GateBwdArgs)
     classes = {"gnn_triattn_args": _lib.TriAttnArgs, "gnn_trimul_args": _lib.TrimulArgs,
-               "gnn_pair_bias_args": _lib.PairBiasArgs, "gnn_triattn_bwd_args": _lib.TriAttnBwdArgs}
+               "gnn_pair_bias_args": _lib.PairBiasArgs, "gnn_triattn_bwd_args": _lib.TriAttnBwdArgs,
+               "gnn_layernorm_args": _lib.LayerNormArgs, "gnn_gate_bwd_args": _lib.GateBwdArgs}
     for key, val in lines.items():
         if "." not in key:
             continue
@@ -183,3 +192,43 @@ def test_triattn_bwd_argument_errors():
     a.dtype = _lib.GNN_F32
     assert lib.gnn_triattn_bwd(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
     assert b"bf16 / fp16" in lib.gnn_last_error()
+
+
+def test_trimul_backward_helper_argument_errors():
+    lib = _lib.load()
+    assert lib.gnn_layernorm_rows(None, None) == _lib.GNN_ERR_ARG
+    a = _lib.LayerNormArgs()
+    assert lib.gnn_layernorm_rows(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    assert b"required" in lib.gnn_last_error()
+    a.x = a.out = 4096
+    a.rows, a.K, a.x_stride, a.out_stride = 4, 96, 96, 64
+    assert lib.gnn_layernorm_rows(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    assert b"stride" in lib.gnn_last_error()
+    a.out_stride = 96
+    a.dy, a.dy_stride, a.bias = 4096, 96, 4096
+    assert lib.gnn_layernorm_rows(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    assert b"forward-only" in lib.gnn_last_error()
+    a.bias = None
+    a.K = a.x_stride = a.out_stride = a.dy_stride = 48
+    assert lib.gnn_layernorm_rows(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
+    assert b"multiple of 32" in lib.gnn_last_error()
+    assert lib.gnn_layernorm_partials(1 << 20, 128) == 4096
+    assert lib.gnn_layernorm_partials(20, 128) == 2
+
+    assert lib.gnn_trimul_gate_bwd(None, None) == _lib.GNN_ERR_ARG
+    g = _lib.GateBwdArgs()
+    assert lib.gnn_trimul_gate_bwd(ctypes.byref(g), None) == _lib.GNN_ERR_ARG
+    assert b"required" in lib.gnn_last_error()
+    g.grad = g.value = g.gate_pre = g.d_value = g.d_gate_pre = 4096
+    g.rows, g.K = 4, 64
+    g.grad_stride = g.value_stride = g.gate_stride = g.dv_stride = g.dg_stride = 64
+    g.grad_stride = 60
+    assert lib.gnn_trimul_gate_bwd(ctypes.byref(g), None) == _lib.GNN_ERR_ARG
+    g.grad_stride, g.value = 64, 4098
+    assert lib.gnn_trimul_gate_bwd(ctypes.byref(g), None) == _lib.GNN_ERR_ARG
+    assert b"aligned" in lib.gnn_last_error()
+    g.value = 4096
+    g.K = 12
+    g.grad_stride = g.value_stride = g.gate_stride = g.dv_stride = g.dg_stride = 16
+    assert lib.gnn_trimul_gate_bwd(ctypes.byref(g), None) == _lib.GNN_ERR_UNSUPPORTED
+    assert b"multiple of 8" in lib.gnn_last_error()

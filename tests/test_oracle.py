@@ -465,3 +465,88 @@ def test_attention_grad_matches_finite_differences():
     # masked keys receive no k / v gradient at all
     dropped = ~mask[:, :, 0, 0, :]
     assert np.all(grads[1][dropped] == 0) and np.all(grads[2][dropped] == 0)
+
+
+# ------------------------------------------------------------- trimul gradients
+def _trimul_case(rng, B, N, C, Ch):
+    w = {
+        "norm_in_weight": 1 + 0.3 * rng.standard_normal(C), "norm_in_bias": 0.3 * rng.standard_normal(C),
+        "p_in_weight": rng.standard_normal((2 * Ch, C)) / np.sqrt(C), "p_in_bias": 0.3 * rng.standard_normal(2 * Ch),
+        "g_in_weight": rng.standard_normal((2 * Ch, C)) / np.sqrt(C), "g_in_bias": 0.3 * rng.standard_normal(2 * Ch),
+        "norm_out_weight": 1 + 0.3 * rng.standard_normal(Ch), "norm_out_bias": 0.3 * rng.standard_normal(Ch),
+        "p_out_weight": rng.standard_normal((C, Ch)) / np.sqrt(Ch), "p_out_bias": 0.3 * rng.standard_normal(C),
+        "g_out_weight": rng.standard_normal((C, C)) / np.sqrt(C), "g_out_bias": 0.3 * rng.standard_normal(C),
+    }
+    x = rng.standard_normal((B, N, N, C))
+    mask = (rng.random((B, N, N)) < 0.8).astype(np.float64)
+    dout = rng.standard_normal((B, N, N, C))
+    return x, mask, dout, w
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_trimul_grad_matches_finite_differences(direction):
+    """Central differences of the (loop-pinned) forward oracle: every entry of dx and of every
+    weight gradient, with a mask, at a size where the contraction, both LayerNorms and the
+    gates all matter (a transposed contraction index or a dropped gate term fails here)."""
+    rng = np.random.default_rng(23 if direction == "outgoing" else 29)
+    x, mask, dout, w = _trimul_case(rng, 2, 3, 4, 2)
+    grads = O.trimul_grad(x, direction, mask, dout, **w)
+
+    def loss(xx, ww):
+        return float(np.sum(O.trimul(xx, direction, mask, **ww) * dout))
+
+    h = 1e-6
+    params = {"x": x, **w}
+    for name, base in params.items():
+        num = np.zeros_like(base)
+        for idx in np.ndindex(base.shape):
+            plus, minus = base.copy(), base.copy()
+            plus[idx] += h
+            minus[idx] -= h
+            if name == "x":
+                num[idx] = (loss(plus, w) - loss(minus, w)) / (2 * h)
+            else:
+                num[idx] = (loss(x, {**w, name: plus}) - loss(x, {**w, name: minus})) / (2 * h)
+        np.testing.assert_allclose(grads[name], num, rtol=1e-5, atol=1e-7, err_msg=name)
+
+
+def test_trimul_grad_without_optional_weights():
+    """LayerNorm affines and projection biases omitted: their gradients are None and the rest
+    still match finite differences of the forward."""
+    rng = np.random.default_rng(31)
+    x, mask, dout, w = _trimul_case(rng, 1, 3, 4, 2)
+    w = {k: v for k, v in w.items() if k.endswith("weight") and not k.startswith("norm")}
+    grads = O.trimul_grad(x, "incoming", None, dout, **w)
+    assert grads["norm_in_weight"] is None and grads["p_out_bias"] is None
+    h = 1e-6
+    num = np.zeros_like(x)
+    for idx in np.ndindex(x.shape):
+        plus, minus = x.copy(), x.copy()
+        plus[idx] += h
+        minus[idx] -= h
+        num[idx] = (np.sum(O.trimul(plus, "incoming", None, **w) * dout)
+                    - np.sum(O.trimul(minus, "incoming", None, **w) * dout)) / (2 * h)
+    np.testing.assert_allclose(grads["x"], num, rtol=1e-5, atol=1e-7)
+
+
+def test_layer_norm_grad_matches_finite_differences():
+    rng = np.random.default_rng(37)
+    x = rng.standard_normal((3, 7))
+    wt = 1 + 0.3 * rng.standard_normal(7)
+    b = 0.3 * rng.standard_normal(7)
+    dy = rng.standard_normal((3, 7))
+    dx, dw, db = O.layer_norm_grad(x, dy, wt)
+    h = 1e-6
+    for name, base, g in (("x", x, dx), ("w", wt, dw), ("b", b, db)):
+        num = np.zeros_like(base)
+        for idx in np.ndindex(base.shape):
+            args = {"x": x, "w": wt, "b": b}
+            plus, minus = base.copy(), base.copy()
+            plus[idx] += h
+            minus[idx] -= h
+            num[idx] = (np.sum(O.layer_norm(**{**{"x": x, "weight": wt, "bias": b},
+                                                **{{"x": "x", "w": "weight", "b": "bias"}[name]: plus}}) * dy)
+                        - np.sum(O.layer_norm(**{**{"x": x, "weight": wt, "bias": b},
+                                                  **{{"x": "x", "w": "weight", "b": "bias"}[name]: minus}}) * dy)
+                        ) / (2 * h)
+        np.testing.assert_allclose(g, num, rtol=1e-6, atol=1e-8, err_msg=name)

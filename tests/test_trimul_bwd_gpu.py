@@ -1,0 +1,156 @@
+"""Triangle multiplicative update backward on the GPU: gnn_layernorm_rows and
+gnn_trimul_gate_bwd against the oracle's closed forms, and every gradient of the public op
+(through _TrimulHip: HIP forward + HIP backward) against oracle/trimul_grad, which
+tests/test_oracle.py pins to finite differences of the forward oracle.
+
+The reference has no native trimul backward (its gradients come from autograd through
+trimul_torch, triangle/_trimul.py:31-36), so there is no reference tolerance for gradients;
+they are held to the reference's forward tolerance table for the same dtype
+(testutil/metrics.py:96-102: bf16 cos >= 1 - 1e-4 and rel-fro <= 1.5e-2, fp32 ieee
+cos >= 1 - 1e-6 and rel-fro <= 1.5e-3), each gradient tensor on its own.
+"""
+
+import numpy as np
+import pytest
+import torch
+from unittest import mock
+
+from helpers import TRIMUL_TOL, Tolerance, assert_close_to_oracle, gen, np_weights, pair_input, randn, to_np, \
+    trimul_weights
+from oracle import triangle_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _k():
+    from geometric_nn_ops_torch.triangle._kernels import trimul as K
+    return K
+
+
+# ------------------------------------------------------------------ LayerNorm rows kernel
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("K", [32, 96, 128, 512])
+def test_layernorm_rows_forward_and_backward(dtype, K):
+    R = 301
+    g = gen(K)
+    # rows are views into a wider buffer: the row stride is not K
+    xb = randn((R, K + 32), g=g, scale=2.0) + 0.5
+    x = xb.to(DEV, dtype)[:, 16:16 + K]
+    dyb = randn((R, K + 64), g=g)
+    dy = dyb.to(DEV, dtype)[:, :K]
+    w = (1 + 0.3 * randn((K,), g=g)).to(DEV, dtype)
+    b = (0.3 * randn((K,), g=g)).to(DEV, dtype)
+    tol = TRIMUL_TOL[dtype, "ieee"]
+    y = _k().layernorm_rows_hip(x, w, b, 1e-5)
+    assert_close_to_oracle("ln", y, O.layer_norm(to_np(x), to_np(w), to_np(b)), tol)
+    dx, dw, db = _k().layernorm_rows_hip(x, w, eps=1e-5, dy=dy, partials=True)
+    want = O.layer_norm_grad(to_np(x), to_np(dy), to_np(w))
+    assert_close_to_oracle("dx", dx, want[0], tol)
+    assert_close_to_oracle("dw", dw, want[1], Tolerance(1 - 1e-6, 1e-4))  # fp32 sums of fp32 products
+    assert_close_to_oracle("db", db, want[2], Tolerance(1 - 1e-6, 1e-4))
+
+
+def test_layernorm_rows_partials_are_deterministic():
+    x = randn((5000, 128), seed=3).to(DEV, torch.bfloat16)
+    dy = randn((5000, 128), seed=4).to(DEV, torch.bfloat16)
+    first = _k().layernorm_rows_hip(x, None, eps=1e-5, dy=dy, partials=True)
+    for _ in range(3):
+        again = _k().layernorm_rows_hip(x, None, eps=1e-5, dy=dy, partials=True)
+        for a, b in zip(first, again):
+            assert torch.equal(a, b)
+
+
+# ------------------------------------------------------------------ gate backward kernel
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("masked", [False, True], ids=["nomask", "mask"])
+def test_gate_bwd(dtype, masked):
+    R, K = 333, 96
+    g = gen(7)
+    buf = randn((R, 3 * K + 32), g=g, scale=3.0).to(DEV, dtype)
+    grad, value, gate = buf[:, :K], buf[:, K + 8:2 * K + 8], buf[:, 2 * K + 16:3 * K + 16]
+    mask = (torch.rand(R, generator=g) < 0.7).to(DEV, dtype) if masked else None
+    out = torch.zeros((R, 2 * K + 16), device=DEV, dtype=dtype)
+    dv, dg = _k().gate_bwd_hip(grad, value, gate, mask, d_value=out[:, :K], d_gate_pre=out[:, K + 16:])
+    gr, v, gp = (to_np(t) for t in (grad, value, gate))
+    s = 1 / (1 + np.exp(-gp))
+    m = to_np(mask)[:, None] if masked else 1.0
+    tol = TRIMUL_TOL[dtype, "ieee"]
+    assert_close_to_oracle("d_value", dv, gr * s * m, tol)
+    assert_close_to_oracle("d_gate_pre", dg, gr * v * m * s * (1 - s), tol)
+    assert torch.count_nonzero(out[:, K:K + 16]) == 0  # the gap between the two outputs is untouched
+
+
+# ------------------------------------------------------------------ the op's gradients
+def _run(x, direction, mask, w, dout):
+    from geometric_nn_ops_torch.triangle import triangle_multiplicative_update
+
+    x = x.to(DEV).requires_grad_()
+    wd = {k: v.to(DEV).requires_grad_() for k, v in w.items()}
+    out = triangle_multiplicative_update(x, direction, None if mask is None else mask.to(DEV), **wd)
+    out.backward(dout.to(DEV, out.dtype))
+    return out, x.grad, {k: v.grad for k, v in wd.items()}
+
+
+def _check_grads(x, direction, mask, w, dout, dtype):
+    _, gx, gw = _run(x, direction, mask, w, dout)
+    want = O.trimul_grad(to_np(x), direction, None if mask is None else to_np(mask), to_np(dout),
+                         **np_weights(w))
+    tol = TRIMUL_TOL[dtype, "ieee"]
+    assert_close_to_oracle("dx", gx, want["x"], tol)
+    for key, grad in gw.items():
+        assert grad is not None, key
+        assert grad.dtype == dtype
+        assert_close_to_oracle(key, grad, want[key], tol)
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_trimul_grads_match_oracle(direction, dtype):
+    w = trimul_weights(64, 32, dtype, seed=41, biases=True, ln_random=True)
+    x, mask = pair_input(2, 24, 64, dtype, seed=42)
+    dout = randn((2, 24, 24, 64), seed=43).to(dtype)
+    _check_grads(x, direction, mask, w, dout, dtype)
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_trimul_grads_c128_ragged_n(direction):
+    """c_z = c_hidden = 128 (the fixed-width projection kernel) at an N that is not a multiple
+    of 32 (row padding of the a / b operands)."""
+    dtype = torch.bfloat16
+    w = trimul_weights(128, 128, dtype, seed=51, biases=True, ln_random=True)
+    x, mask = pair_input(1, 40, 128, dtype, seed=52)
+    dout = randn((1, 40, 40, 128), seed=53).to(dtype)
+    _check_grads(x, direction, mask, w, dout, dtype)
+
+
+def test_trimul_grads_batched_no_mask_no_biases():
+    dtype = torch.bfloat16
+    w = trimul_weights(64, 64, dtype, seed=61)  # LN affine present, projection biases absent
+    x, _ = pair_input((2, 2), 16, 64, dtype, seed=62)
+    dout = randn((2, 2, 16, 16, 64), seed=63).to(dtype)
+    _check_grads(x, "incoming", None, w, dout, dtype)
+
+
+def test_grad_calls_take_the_hip_backward():
+    from geometric_nn_ops_torch.triangle import _trimul
+
+    w = trimul_weights(32, 32, torch.bfloat16, seed=1)
+    x, mask = pair_input(1, 12, 32, torch.bfloat16, seed=3)
+    with mock.patch.object(_trimul, "trimul_torch", wraps=_trimul.trimul_torch) as ref:
+        out, gx, _ = _run(x, "outgoing", mask, w, torch.ones(1, 12, 12, 32))
+    assert not ref.called
+    assert out.grad_fn is not None and "TrimulHip" in type(out.grad_fn).__name__
+    assert gx is not None and torch.isfinite(gx).all()
+
+
+def test_mask_requiring_grad_takes_the_torch_path():
+    from geometric_nn_ops_torch.triangle import _trimul, triangle_multiplicative_update
+
+    w = {k: v.to(DEV) for k, v in trimul_weights(32, 32, torch.float32, seed=1).items()}
+    x, mask = pair_input(1, 12, 32, torch.float32, seed=3)
+    mask = mask.to(DEV).requires_grad_()
+    with mock.patch.object(_trimul, "trimul_torch", wraps=_trimul.trimul_torch) as ref:
+        out = triangle_multiplicative_update(x.to(DEV).requires_grad_(), "outgoing", mask, **w)
+        out.sum().backward()
+    assert ref.called and mask.grad is not None

@@ -301,18 +301,16 @@ def test_no_grad_modes_use_the_kernel(no_backward):
     assert kern.called and not ref.called
 
 
-@pytest.mark.parametrize("case", ["input_requires_grad", "weights_require_grad", "float64"])
+@pytest.mark.parametrize("case", ["float64", "c_hidden_48"])
 def test_unsupported_configs_use_the_torch_path(case):
+    """Configurations without kernels. (Calls that need gradients run the HIP forward and
+    backward: tests/test_trimul_bwd_gpu.py.)"""
     from geometric_nn_ops_torch.triangle import triangle_multiplicative_update
 
     dtype = torch.float64 if case == "float64" else torch.float32
-    w = {k: v.to(DEV) for k, v in trimul_weights(32, 32, dtype, seed=1).items()}
+    w = {k: v.to(DEV) for k, v in trimul_weights(32, 48 if case == "c_hidden_48" else 32, dtype, seed=1).items()}
     x, mask = pair_input(1, 12, 32, dtype, seed=3)
     x = x.to(DEV)
-    if case == "input_requires_grad":
-        x.requires_grad_()
-    if case == "weights_require_grad":
-        w = {k: v.requires_grad_() for k, v in w.items()}
     with dispatch_spy() as (ref, kern):
         triangle_multiplicative_update(x, "outgoing", mask.to(DEV), **w)
     assert ref.called and not kern.called
