@@ -22,6 +22,11 @@ int triattn_bwd(const gnn_triattn_bwd_args& a, hipStream_t stream);
 bool triattn_row_applicable(const gnn_triattn_args& a);
 int triattn_row_fwd(const gnn_triattn_args& a, hipStream_t stream);
 
+// Row-resident attention backward for dq (with Delta) and dk / dv (16-bit inputs, head dim 32,
+// bounded N_res); the pair-bias gradient stays with the tiled backward's dbias kernel.
+bool triattn_bwd_row_applicable(const gnn_triattn_bwd_args& a);
+int triattn_bwd_row_dq_dkdv(const gnn_triattn_bwd_args& a, hipStream_t stream);
+
 // Workspace layout shared by the three trimul stages (byte offsets, see the C header).
 struct TrimulLayout {
   size_t off_a, off_b, off_g, off_o, total;

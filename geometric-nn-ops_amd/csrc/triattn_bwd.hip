@@ -26,7 +26,14 @@
 //              N_seq rows with the row's operands staged in LDS and sum_s dS accumulating in
 //              fp32 registers; the bias tile is loaded once as the scores' initial value.
 // The bias is added to the scores in fp32 exactly as in the forward (bf16 values, fp32
-// sums), and the mask sentinel after it, so P matches the forward's normaliser.
+// sums), and the mask sentinel after it, so P matches the forward's normaliser. P of a
+// masked key is divided by N_res, as the reference's backward does
+// (triangle_attention.py:753-766, :1033-1038): in a row whose keys are all masked the
+// forward's lse holds the bare sentinel (its log(l) term is below the fp32 ulp there), so
+// exp(S - lse) is 1 for every key where softmax gives 1 / N_res; in any other row a masked
+// key's P is 0 either way. dq and dk / dv divide per masked key; bwd_dbias, which sees a
+// row's keys one tile at a time, per row (its lse at the sentinel): -log2(N_res) joins the
+// exp2 argument.
 // 16-bit inputs, head dim <= 32 (padded to a multiple of 8 by the host).
 #include "gnn_common.hpp"
 #include "gnn_internal.hpp"
@@ -143,12 +150,14 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dkdv_kernel(const gnn_triattn_bwd_
     }
   }
   // key-side mask term: the sentinel for masked keys, -inf for keys past N (p = 0)
-  float kbias = 0.f;
+  float kbias = 0.f, kmul = 1.f;
   if (!kok) {
     kbias = -INFINITY;
   } else if (a.mask && a.mask[b * a.mask_stride[0] + s * a.mask_stride[1] + (int64_t)key * a.mask_stride[2]] == 0) {
     kbias = a.mask_value;
+    kmul = 1.0f / (float)N;  // masked key: P / N_res
   }
+  const bool any_masked = __any(kmul != 1.f);
   V8 idf[2];
   identity_frags<T>(idf, l32, g);
   const T* bias_plane = HAS_BIAS ? (const T*)a.bias + b * a.bias_stride[0] + h * a.bias_stride[1] : nullptr;
@@ -213,7 +222,8 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dkdv_kernel(const gnn_triattn_bwd_
         for (int e = 0; e < 4; ++e) {
           const int i = 4 * rg + e;
           const float x = sc[i] + kbias;
-          const float pv = fast_exp2((x - l4[e]) * LOG2E_B);
+          float pv = fast_exp2((x - l4[e]) * LOG2E_B);
+          if (any_masked) pv *= kmul;
           p[i] = pv;
           ds[i] = pv * (dp[i] - d4[e]);
         }
@@ -297,7 +307,6 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dq_kernel(const gnn_triattn_bwd_ar
     delta = part + __shfl_xor(part, 32);
     if (qok && g == 0) a.delta[lrow + qi] = delta;
   }
-  const float nl = -lse * LOG2E_B;
   V8 idf[2];
   identity_frags<T>(idf, l32, g);
   const T* brow = HAS_BIAS ? (const T*)a.bias + b * a.bias_stride[0] + h * a.bias_stride[1] +
@@ -342,13 +351,16 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dq_kernel(const gnn_triattn_bwd_ar
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int kj = k0 + r0 + 8 * (i / 4) + 4 * g + (i % 4);
-        float x = sc[i];
+        float x = sc[i], pm = 1.f;
         if (kj >= N) {
           x = -INFINITY;
         } else if (a.mask && a.mask[b * a.mask_stride[0] + s * a.mask_stride[1] + (int64_t)kj * a.mask_stride[2]] == 0) {
           x += a.mask_value;
+          pm = 1.0f / (float)N;  // masked key: P / N_res
         }
-        const float pv = fast_exp2(__builtin_fmaf(x, LOG2E_B, nl));
+        // subtract first: in a row whose keys are all masked both x and lse sit near the
+        // sentinel, and only their difference is exact
+        const float pv = fast_exp2((x - lse) * LOG2E_B) * pm;
         ds[i] = pv * (dp[i] - delta);
       }
       // dQ += dS K: A = dS^T accumulator (lane = query, k = keys), B = K read transposed
@@ -387,6 +399,7 @@ struct DbLds {
   float lse[DB_T];
   float delta[DB_T];
   float kb[DB_T];
+  float pl2;  // -log2(N_res) when the row's keys are all masked, else 0
 };
 
 template <typename T>
@@ -459,6 +472,8 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
       sm.lse[sr] = plse;
       sm.delta[sr] = pdel;
       sm.kb[sr] = pkb;
+      // every query of the row shares its keys' mask: the tile's first query (< N) decides
+      if (sr == 0) sm.pl2 = (a.mask && plse <= 0.5f * a.mask_value) ? -__log2f((float)N) : 0.f;
     }
   };
 
@@ -493,13 +508,13 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
         Mma<T, PREC_NATIVE>::step(scv, qf[kk], lds_row8<T>(sm.k, kr, 2 * kk + g));
         Mma<T, PREC_NATIVE>::step(dp, dof[kk], lds_row8<T>(sm.v, kr, 2 * kk + g));
       }
-      const float kb = sm.kb[kr];
+      const float kb = sm.kb[kr], pl2 = sm.pl2;
 #pragma unroll
       for (int rg = 0; rg < 4; ++rg)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = 4 * rg + e;
-          const float pv = fast_exp2((scv[i] + kb - l4[rg][e]) * LOG2E_B);
+          const float pv = fast_exp2(__builtin_fmaf(scv[i] + kb - l4[rg][e], LOG2E_B, pl2));
           acc[sub][i] += pv * (dp[i] - d4[rg][e]);
         }
     }
@@ -536,7 +551,10 @@ int launch_bwd(const gnn_triattn_bwd_args& a, hipStream_t stream) {
   const int64_t nb128 = (a.N + 127) / 128;
   const dim3 grid((uint32_t)(nb128 * a.H * a.S * a.B));
   // dq first: it also writes Delta, which dk / dv and dbias read
-  if (a.bias) {
+  if (triattn_bwd_row_applicable(a)) {
+    const int rc = triattn_bwd_row_dq_dkdv(a, stream);
+    if (rc != 0) return rc;
+  } else if (a.bias) {
     hipLaunchKernelGGL((bwd_dq_kernel<T, true>), grid, dim3(BNT), 0, stream, a);
     hipLaunchKernelGGL((bwd_dkdv_kernel<T, true>), grid, dim3(BNT), 0, stream, a);
   } else {

@@ -25,10 +25,12 @@ def run(q, k, v, bias, mask, scale, dout):
     return o, [t.grad for t in leaves], None if b is None else b.grad
 
 
-def check_against_oracle(shape, dtype, *, with_bias=True, with_mask=True, seed=0, scale=None):
+def check_against_oracle(shape, dtype, *, with_bias=True, with_mask=True, seed=0, scale=None, dead_rows=()):
     B, S, N, H, D = shape
     t = attention_inputs(B, S, N, H, D, dtype, seed=seed, with_bias=with_bias, bias_scale=0.5, device=DEV)
     mask = key_mask(B, S, N, seed=seed + 1, frac_keep=0.75, device=DEV) if with_mask else None
+    for s in dead_rows:  # every key of N_seq row s masked
+        mask[:, s] = False
     dout = (torch.randn(B, S, N, H, D, generator=gen(seed + 2))).to(DEV, dtype)
     o, (dq, dk, dv), db = run(t["q"], t["k"], t["v"], t.get("bias"), mask, scale, dout)
     want = O.triangle_attention_grad(to_np(t["q"]), to_np(t["k"]), to_np(t["v"]),
@@ -92,6 +94,20 @@ def test_ending_node_views():
     tol = TRIANGLE_ATTENTION_TOL[dtype, "ieee"]
     for name, got, ref in zip(("dq", "dk", "dv", "dbias"), (dq, dk, dv, db), want):
         assert_close_to_oracle(name, got, ref, tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16,
+                                   pytest.param(torch.float16, marks=pytest.mark.xfail(
+                                       strict=True, reason="fp16 mask_val too small to swamp the logits"))],
+                         ids=["bf16", "fp16"])
+@pytest.mark.parametrize("n", [64, 96], ids=["n64", "n96"])
+def test_fully_masked_rows(dtype, n):
+    """N_seq rows whose keys are all masked next to ordinary rows, as the reference's
+    test_fully_masked_row (tests/test_triangle_attention.py:535-562, fp16 a strict xfail
+    there too): the forward's lse of such a row is the bare sentinel, and P of a masked key
+    is divided by N_res (the reference's correction) to give softmax's uniform 1 / N_res.
+    n = 64 is one whole key tile, n = 96 a ragged one."""
+    check_against_oracle((1, 4, n, 2, 32), dtype, seed=61, dead_rows=(1, 3))
 
 
 def test_headline_rows_bf16():
