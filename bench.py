@@ -6,7 +6,11 @@ One step = the BASELINE.json headline workload at N_res = 512, bf16, B = 1:
   * the same with 'incoming' (mask: the last 64 residues padded on both axes).
 Every kernel is launched through the C ABI (libgnn_hip.so) with inputs, outputs and the
 trimul workspace already resident in HBM; per-kernel durations come from HIP events
-recorded on the launch stream inside the timed region.
+recorded on the launch stream around each launch, in a loop of their own; ``ms_per_step``
+and ``value`` come from ``--steps`` further steps launched back to back with events only
+around the whole loop. ``graph_ms_per_step`` times the same step captured once as a HIP graph
+and replayed ``--steps`` times (outputs checked bitwise against the eager ones): the entry
+points are capturable, and at this size replay gains nothing over eager launches.
 
 Prints ONE JSON line: value = algorithmic TFLOP/s of the whole step (dense attention
 FLOPs, softmax excluded; trimul 2 N^3 Ch + N^2 (10 C Ch + 2 C^2)), plus the roofline of
@@ -132,16 +136,19 @@ def main():
     def check(rc, what):
         _lib.check(rc, what)
 
+    def cur():  # the launch stream: the current one (a graph capture switches it)
+        return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
     kernels = []  # (name, callable)
     if args.only in (None, "attn"):
-        kernels.append(("triattn_fwd", lambda: check(lib.gnn_triattn_fwd(ctypes.byref(a), sh), "attn")))
+        kernels.append(("triattn_fwd", lambda: check(lib.gnn_triattn_fwd(ctypes.byref(a), cur()), "attn")))
     if args.only in (None, "trimul"):
         for direction in ("outgoing", "incoming"):
             targs = tri[direction][0]
             for stage in ("proj", "contract", "out"):
                 fn = getattr(lib, f"gnn_trimul_{stage}")
                 kernels.append((f"trimul_{stage}_{direction}",
-                                lambda fn=fn, targs=targs: check(fn(ctypes.byref(targs), sh), "trimul")))
+                                lambda fn=fn, targs=targs: check(fn(ctypes.byref(targs), cur()), "trimul")))
 
     # ---- parity gate + CPU baseline (numpy oracle, fp32, bounded sample)
     cpu = None
@@ -181,17 +188,15 @@ def main():
                "sample": f"numpy fp32 oracle: attention on {len(rows)} of {N} N_seq rows (time scaled "
                          f"x{N // len(rows)}), trimul full N={N} both directions"}
 
-    # ---- warmup, then exactly `steps` timed steps with per-kernel events
+    # ---- warmup, then `steps` steps with per-kernel events (each kernel's duration), then
+    # exactly `steps` timed steps launched eagerly and `steps` replays of the step captured
+    # as a HIP graph (the same launches; replays are checked bitwise against the eager
+    # outputs)
     for _ in range(args.warmup):
         for _, fn in kernels:
             fn()
     torch.cuda.synchronize()
     ev = {name: [] for name, _ in kernels}
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    t_start.record(stream)
     for _ in range(args.steps):
         for name, fn in kernels:
             e0 = torch.cuda.Event(enable_timing=True)
@@ -200,11 +205,45 @@ def main():
             fn()
             e1.record(stream)
             ev[name].append((e0, e1))
-    t_end.record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = t_start.elapsed_time(t_end) / args.steps
     kern_ms = {name: sum(e0.elapsed_time(e1) for e0, e1 in pairs) / len(pairs) for name, pairs in ev.items()}
+
+    def timed_steps(run_step):
+        t_start = torch.cuda.Event(enable_timing=True)
+        t_end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        t_start.record(stream)
+        for _ in range(args.steps):
+            run_step()
+        t_end.record(stream)
+        torch.cuda.synchronize()
+        return t_start.elapsed_time(t_end) / args.steps, time.perf_counter() - t0
+
+    def eager_step():
+        for _, fn in kernels:
+            fn()
+
+    outputs = ([od] if args.only in (None, "attn") else []) + \
+        ([tri[d][2] for d in ("outgoing", "incoming")] if args.only in (None, "trimul") else [])
+    eager_ms, wall_eager = timed_steps(eager_step)
+    want = [t.clone() for t in outputs]
+    graph_ms, graph_ok = None, None
+    try:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            eager_step()
+        for t in outputs:
+            t.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        graph_ok = all(torch.equal(t, w) for t, w in zip(outputs, want))
+        if graph_ok:
+            graph_ms, _ = timed_steps(graph.replay)
+            graph_ok = all(torch.equal(t, w) for t, w in zip(outputs, want))
+    except Exception as exc:  # pragma: no cover - reported, eager numbers stand
+        print(f"bench.py: HIP graph capture failed, eager timing used: {exc}", file=sys.stderr)
+    ms_step = eager_ms
 
     # ---- cold: each launch after a scratch write larger than L2 + Infinity Cache, so its
     # inputs come from HBM (at N=512 the warm inputs otherwise stay cache resident)
@@ -355,6 +394,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 5),
+        "graph_ms_per_step": round(graph_ms, 5) if graph_ms is not None else None,
+        "graph_replays_match_eager": graph_ok,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -373,7 +414,7 @@ def main():
         "cold_ms_per_step": round(sum(cold_ms.values()), 5) if cold_ms else None,
         "triton_reference": "unavailable: the reference's Triton kernels are not installed on the box and "
                             "the reference does not travel to it",
-        "wall_s_timed": round(wall, 4),
+        "wall_s_timed": round(wall_eager, 4),
         "attention_backward": backward,
         "trimul_backward": tri_backward,
     }
