@@ -659,24 +659,28 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
         }
       }
       wave_lds_sync();
-      // 16-byte stores, 8 lanes per 64-pixel channel row
+      // 16-byte stores, 8 lanes per 64-pixel channel row: lane = (channel row lane / 8 + 8 i,
+      // pixels 8 (lane % 8) ..). c_hidden is a multiple of 32, so the unit's 32 channels all
+      // belong to a or all to b, and store i is store 0 moved by 8 channel planes.
+      {
+        const int crow0 = lane >> 3, p0 = (lane & 7) * 8;
+        const bool in_a = 32 * u < Ch;
+        const int chh0 = 32 * u + crow0 - (in_a ? 0 : Ch);
+        T* drow = (in_a ? a_cm : b_cm) + ab_offset<T>((int64_t)tl.b * Ch + chh0, tl.row, tl.c0 + p0, N, NP);
+        const int64_t pstep = ab_offset<T>(8, 0, 0, N, NP);  // 8 channel planes
+        const bool full = tl.c0 + p0 + 8 <= N, tail = !full && tl.c0 + p0 < NP;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = lane + 64 * i;
-        const int crow = c / 8, p0 = (c % 8) * 8;
-        const int chg = 32 * u + crow;
-        T* dst = chg < Ch ? a_cm : b_cm;
-        const int chh = chg < Ch ? chg : chg - Ch;
-        T* drow = dst + ab_offset<T>((int64_t)tl.b * Ch + chh, tl.row, tl.c0 + p0, N, NP);
-        const V8 val = load8(&ebuf[crow * ER + p0]);
-        if (tl.c0 + p0 + 8 <= N) {
-          store8(drow, val);
-        } else if (tl.c0 + p0 < NP) {  // row tail: pixels N .. NP-1 are written as zeros
-          V8 v = val;
+        for (int i = 0; i < 4; ++i) {
+          const V8 val = load8(&ebuf[(crow0 + 8 * i) * ER + p0]);
+          if (full) {
+            store8(drow + i * pstep, val);
+          } else if (tail) {  // row tail: pixels N .. NP-1 are written as zeros
+            V8 v = val;
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (tl.c0 + p0 + e >= N) v[e] = TypeOps<T>::from_f32(0.f);
-          store8(drow, v);
+            for (int e = 0; e < 8; ++e)
+              if (tl.c0 + p0 + e >= N) v[e] = TypeOps<T>::from_f32(0.f);
+            store8(drow + i * pstep, v);
+          }
         }
       }
       wave_lds_sync();

@@ -110,6 +110,13 @@ def test_fully_masked_rows(dtype, n):
     check_against_oracle((1, 4, n, 2, 32), dtype, seed=61, dead_rows=(1, 3))
 
 
+@pytest.mark.parametrize("n", [1024, 1025], ids=["n1024_row_max", "n1025_tiled"])
+def test_row_kernel_limit(n):
+    """D = 32 at the row-resident backward's largest N_res (1024: K / V or Q' / dO of a row
+    fill 128 KB of LDS) and one past it (the tiled dq / dk-dv kernels take over)."""
+    check_against_oracle((1, 1, n, 2, 32), torch.bfloat16, seed=71)
+
+
 def test_headline_rows_bf16():
     """N_res = 512 (the headline width), 8 N_seq rows, pair bias and ragged masks."""
     check_against_oracle((1, 8, 512, 4, 32), torch.bfloat16, seed=41)
