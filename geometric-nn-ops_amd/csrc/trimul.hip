@@ -65,6 +65,24 @@ __host__ __device__ inline int64_t ab_offset(int64_t plane, int row, int k, int 
     return (plane * N + row) * NP + k;
 }
 
+// Sum over the 8 lanes 8k .. 8k + 7 (every lane gets it) with DPP lane moves instead of
+// LDS-routed shuffles: pairs (quad_perm 1,0,3,2), quads (2,3,0,1), then the two quads of the
+// half-row (row_half_mirror pairs lane i with 7 - i, which lies in the other quad).
+__device__ __forceinline__ float sum8_dpp(float x) {
+  auto mv = [](float v, int ctrl) {
+    int r;
+    switch (ctrl) {
+      case 0: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false); break;
+      case 1: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false); break;
+      default: r = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false); break;
+    }
+    return __int_as_float(r);
+  };
+  x += mv(x, 0);
+  x += mv(x, 1);
+  return x + mv(x, 2);
+}
+
 // Orders LDS accesses of the lanes of one wave (a wave executes its LDS operations in
 // order; this keeps the compiler from moving them across the exchange).
 __device__ __forceinline__ void wave_lds_sync() {
@@ -532,9 +550,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
 #pragma unroll
       for (int e = 0; e < 8; ++e) s += v[j][e];
     }
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 4);
+    s = sum8_dpp(s);
     const float mean = s * (1.0f / CK);
     float q = 0.f;
 #pragma unroll
@@ -544,10 +560,8 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
         const float d = v[j][e] - mean;
         q += d * d;
       }
-    q += __shfl_xor(q, 1);
-    q += __shfl_xor(q, 2);
-    q += __shfl_xor(q, 4);
-    const float rstd = 1.0f / sqrtf(q * (1.0f / CK) + a.eps);
+    q = sum8_dpp(q);
+    const float rstd = __builtin_amdgcn_rsqf(q * (1.0f / CK) + a.eps);  // as torch's rsqrt
 #pragma unroll
     for (int j = 0; j < XMF; ++j) {
       const int k = 8 * (xpart + 8 * j);
