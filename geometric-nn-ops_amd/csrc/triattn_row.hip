@@ -122,10 +122,24 @@ __device__ __forceinline__ float rowsum_add_r(const f16x8& v, float acc) {
   return acc;
 }
 
+// Maxima of scores, which are finite or -inf (never NaN): v_max3_f32 / v_max_f32 written
+// directly, because fmaxf's NaN rules make the compiler quiet each operand first (an extra
+// v_max_f32 x, x, x per operand in the reduction tree).
+__device__ __forceinline__ float max3_nn(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float max_nn(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 // max / sum over the lane pair (l, l ^ 32) with gfx950's v_permlane32_swap (no LDS trip)
 __device__ __forceinline__ float pair_max_swap(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max_nn(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float pair_sum_swap(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -355,13 +369,13 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
           }
         }
       }
-      float m0 = fmaxf(sc[0][0], sc[0][1]), m1 = fmaxf(sc[1][0], sc[1][1]);
+      float m0 = max3_nn(sc[0][0], sc[0][1], sc[0][2]), m1 = max3_nn(sc[1][0], sc[1][1], sc[1][2]);
 #pragma unroll
-      for (int i = 2; i < 16; ++i) {
-        m0 = fmaxf(m0, sc[0][i]);
-        m1 = fmaxf(m1, sc[1][i]);
+      for (int i = 3; i < 15; i += 2) {
+        m0 = max3_nn(m0, sc[0][i], sc[0][i + 1]);
+        m1 = max3_nn(m1, sc[1][i], sc[1][i + 1]);
       }
-      const float mh = fmaxf(m0, m1);
+      const float mh = max3_nn(m0, max_nn(sc[0][15], sc[1][15]), m1);
       const float mt = pair_max_swap(mh);
       if (__any(mt > m + RESCALE_THRESHOLD)) {
         const float mnew = fmaxf(m, mt);
