@@ -714,14 +714,15 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
         store4(&gbuf[l32 * EG + 8 * rg + 4 * g], TypeOps<T>::from_f32(v));
       }
       wave_lds_sync();
-      // 16-byte stores, 4 lanes per 32-channel pixel row segment
+      // 16-byte stores, 4 lanes per 32-channel pixel row segment; store 1 is store 0 moved
+      // by 16 pixels along the tile (a column step outgoing, a row step incoming)
+      {
+        const int px = lane >> 2, k0 = (lane & 3) * 8, pl = 32 * so + px;
+        T* dst = gout + proj_pix(tl, pl, N, outgoing) * CK + 32 * uo + k0;
+        const int64_t step16 = (outgoing ? 16 : 16 * (int64_t)N) * CK;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int c = lane + 64 * i;
-        const int px = c / 4, k0 = (c % 4) * 8;
-        const int pl = 32 * so + px;
-        if (tl.c0 + pl < N)
-          store8(gout + proj_pix(tl, pl, N, outgoing) * CK + 32 * uo + k0, load8(&gbuf[px * EG + k0]));
+        for (int i = 0; i < 2; ++i)
+          if (tl.c0 + pl + 16 * i < N) store8(dst + i * step16, load8(&gbuf[(px + 16 * i) * EG + k0]));
       }
     }
   };
@@ -1011,8 +1012,8 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
       const float2 v = red2[j * 32 + pp];
       var += f32x2{v.x, v.y};
     }
-    const float rs0 = 1.0f / sqrtf(var[0] * (1.0f / (float)Ch) + a.eps);
-    const float rs1 = 1.0f / sqrtf(var[1] * (1.0f / (float)Ch) + a.eps);
+    const float rs0 = __builtin_amdgcn_rsqf(var[0] * (1.0f / (float)Ch) + a.eps);  // as torch's rsqrt
+    const float rs1 = __builtin_amdgcn_rsqf(var[1] * (1.0f / (float)Ch) + a.eps);
     for (int k = k0; k < k0 + kc; k += 8) {
       f32x8 v0, v1;
 #pragma unroll
