@@ -43,10 +43,17 @@ __device__ __forceinline__ float ld1(const void* p, int64_t i, float dflt) {
   return p ? TypeOps<T>::to_f32(((const T*)p)[i]) : dflt;
 }
 
+// Sum over a half-wave (lanes 32h .. 32h + 31; every lane gets it) in VALU lane moves, no
+// LDS-routed shuffle: DPP pairs (quad_perm 1,0,3,2), quads (2,3,0,1), half-rows
+// (row_half_mirror) and rows (row_mirror) -- each mirror pairs a lane with one holding the
+// complementary partial sum -- then v_permlane16_swap joins the half-wave's two rows.
 __device__ __forceinline__ float half_wave_sum(float v) {
-#pragma unroll
-  for (int m = 1; m < 32; m <<= 1) v += __shfl_xor(v, m);
-  return v;
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // KPL columns per lane (K = 32 * KPL), lane c of a half-wave owning columns KPL c .. KPL c + KPL-1.
