@@ -35,7 +35,7 @@ namespace {
 constexpr int LN_THREADS = 256;                 // 8 half-waves: 8 rows at a time
 constexpr int LN_ROWS = LN_THREADS / 32;
 constexpr int LN_MAX_K = 512;
-constexpr int LN_UNROLL = 2;                    // rows per half-wave step
+constexpr int LN_UNROLL = 4;                    // rows per half-wave step
 constexpr int LN_MAX_GRID = 4096;               // partial rows of the weight gradients
 
 template <typename T>

@@ -213,7 +213,7 @@ def test_trimul_backward_helper_argument_errors():
     assert lib.gnn_layernorm_rows(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
     assert b"multiple of 32" in lib.gnn_last_error()
     assert lib.gnn_layernorm_partials(1 << 20, 128) == 4096
-    assert lib.gnn_layernorm_partials(20, 128) == 2
+    assert lib.gnn_layernorm_partials(40, 128) == 2
 
     assert lib.gnn_trimul_gate_bwd(None, None) == _lib.GNN_ERR_ARG
     g = _lib.GateBwdArgs()
