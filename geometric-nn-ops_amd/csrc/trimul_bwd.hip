@@ -63,14 +63,24 @@ __global__ __launch_bounds__(LN_THREADS) void layernorm_rows_kernel(const gnn_la
   const int K = 32 * KPL;
   const int tid = threadIdx.x, hw = tid >> 5, c = tid & 31;
   const int k0 = c * KPL;
-  float w[KPL], bsum[KPL], wsum[KPL];
+  float w[KPL], bv[KPL], bsum[KPL], wsum[KPL];
 #pragma unroll
   for (int e = 0; e < KPL; ++e) {
     w[e] = ld1<T>(a.weight, k0 + e, 1.f);
+    bv[e] = BWD ? 0.f : ld1<T>(a.bias, k0 + e, 0.f);
     bsum[e] = 0.f;  // backward: column sums of dy
     wsum[e] = 0.f;  // backward: column sums of dy * xh
   }
   const float inv_k = 1.0f / (float)K;
+  // K = 128 (four columns per lane) with rows aligned to four elements: one vector access
+  // per lane and row instead of four scalar ones
+  typedef typename TypeOps<T>::V4 TV4;
+  constexpr bool V4 = KPL == 4;
+  constexpr int64_t VB = sizeof(TV4);
+  auto al = [&](const void* p, int64_t stride) {
+    return (uintptr_t)p % VB == 0 && (stride * (int64_t)sizeof(T)) % VB == 0;
+  };
+  const bool vec = V4 && al(a.x, a.x_stride) && al(a.out, a.out_stride) && (!BWD || al(a.dy, a.dy_stride));
   const int64_t step = (int64_t)gridDim.x * LN_ROWS * LN_UNROLL;
   for (int64_t r0 = ((int64_t)blockIdx.x * LN_ROWS + hw) * LN_UNROLL; r0 < a.rows; r0 += step) {
     float x[LN_UNROLL][KPL], dy[LN_UNROLL][KPL];
@@ -78,12 +88,24 @@ __global__ __launch_bounds__(LN_THREADS) void layernorm_rows_kernel(const gnn_la
     for (int u = 0; u < LN_UNROLL; ++u) {
       const int64_t r = min(r0 + u, a.rows - 1);  // a row past the end repeats the last (not stored)
       const T* xr = (const T*)a.x + r * a.x_stride + k0;
+      if (V4 && vec) {
+        const f32x4 xv = TypeOps<T>::to_f32(*reinterpret_cast<const TV4*>(xr));
 #pragma unroll
-      for (int e = 0; e < KPL; ++e) x[u][e] = TypeOps<T>::to_f32(xr[e]);
+        for (int e = 0; e < KPL; ++e) x[u][e] = xv[e % 4];
+      } else {
+#pragma unroll
+        for (int e = 0; e < KPL; ++e) x[u][e] = TypeOps<T>::to_f32(xr[e]);
+      }
       if constexpr (BWD) {
         const T* dyr = (const T*)a.dy + r * a.dy_stride + k0;
+        if (V4 && vec) {
+          const f32x4 dv = TypeOps<T>::to_f32(*reinterpret_cast<const TV4*>(dyr));
 #pragma unroll
-        for (int e = 0; e < KPL; ++e) dy[u][e] = TypeOps<T>::to_f32(dyr[e]);
+          for (int e = 0; e < KPL; ++e) dy[u][e] = dv[e % 4];
+        } else {
+#pragma unroll
+          for (int e = 0; e < KPL; ++e) dy[u][e] = TypeOps<T>::to_f32(dyr[e]);
+        }
       }
     }
 #pragma unroll
@@ -103,9 +125,15 @@ __global__ __launch_bounds__(LN_THREADS) void layernorm_rows_kernel(const gnn_la
       if (r >= a.rows) continue;  // uniform over the half-wave (after its shuffles)
       T* orow = (T*)a.out + r * a.out_stride + k0;
       if constexpr (!BWD) {
+        float y[KPL];
 #pragma unroll
-        for (int e = 0; e < KPL; ++e)
-          orow[e] = TypeOps<T>::from_f32(x[u][e] * rstd * w[e] + ld1<T>(a.bias, k0 + e, 0.f));
+        for (int e = 0; e < KPL; ++e) y[e] = x[u][e] * rstd * w[e] + bv[e];
+        if (V4 && vec) {
+          *reinterpret_cast<TV4*>(orow) = TypeOps<T>::from_f32(f32x4{y[0], y[1 % KPL], y[2 % KPL], y[3 % KPL]});
+        } else {
+#pragma unroll
+          for (int e = 0; e < KPL; ++e) orow[e] = TypeOps<T>::from_f32(y[e]);
+        }
       } else {
         float g[KPL];
         float sg = 0.f, sgx = 0.f;
@@ -121,7 +149,13 @@ __global__ __launch_bounds__(LN_THREADS) void layernorm_rows_kernel(const gnn_la
         }
         const float mg = half_wave_sum(sg) * inv_k, mgx = half_wave_sum(sgx) * inv_k;
 #pragma unroll
-        for (int e = 0; e < KPL; ++e) orow[e] = TypeOps<T>::from_f32(rstd * (g[e] - mg - x[u][e] * mgx));
+        for (int e = 0; e < KPL; ++e) g[e] = rstd * (g[e] - mg - x[u][e] * mgx);
+        if (V4 && vec) {
+          *reinterpret_cast<TV4*>(orow) = TypeOps<T>::from_f32(f32x4{g[0], g[1 % KPL], g[2 % KPL], g[3 % KPL]});
+        } else {
+#pragma unroll
+          for (int e = 0; e < KPL; ++e) orow[e] = TypeOps<T>::from_f32(g[e]);
+        }
       }
     }
   }
