@@ -255,7 +255,7 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
                            : nullptr;
   V8 qf[R][DP / 16];
   f32x16 o[R][DP / 32];
-  float m[R], lsum[R];
+  float m[R], lsum[R], mx[R];  // mx: exact running maximum (m moves lazily)
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int s = min(s0 + r, (int)a.S - 1);
@@ -275,6 +275,7 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[r][cc][i] = 0.f;
     m[r] = -INFINITY;
+    mx[r] = -INFINITY;
     lsum[r] = 0.f;
   }
 
@@ -458,6 +459,7 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
       }
       const float mh = fmaxf(m0, m1);
       const float mt = fmaxf(mh, __int_as_float(__builtin_amdgcn_ds_bpermute(xlane, __float_as_int(mh))));
+      mx[r] = fmaxf(mx[r], mt);
       if (__any(mt > m[r] + RESCALE_THRESHOLD)) {
         const float mnew = fmaxf(m[r], mt);
         const float alpha = fast_exp2((m[r] - mnew) * LOG2E);  // 0 on the first tile (m = -inf)
@@ -548,8 +550,9 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
           store4(orow + d0, TypeOps<T>::from_f32(x));
         }
       }
-    if (a.lse && g == 0)  // natural-log lse of the logits
-      a.lse[(((int64_t)b * a.S + s) * H + h) * N + myq] = m[r] + __log2f(ltot) * (1.0f / LOG2E);
+    const int64_t ridx = (((int64_t)b * a.S + s) * H + h) * N + myq;
+    if (a.lse && g == 0) a.lse[ridx] = m[r] + __log2f(ltot) * (1.0f / LOG2E);  // natural-log lse
+    if (a.row_max && g == 0) a.row_max[ridx] = mx[r];
   }
 }
 

@@ -32,10 +32,19 @@
 // (16 waves per CU streaming consecutive rows through two LDS buffers, the next row's K / V
 // DMA issued during the current row's key loop: 20% slower at N = 512, its 16 waves meeting
 // at a barrier every row).
-// The per-tile arithmetic (transposed score tile S^T = K Q'^T on 32x32x16 MFMA, bias added
-// by MFMA against an identity fragment, lazy rescale with threshold 8 ln 2, exp2 with the
-// folded FMA, v_dot2 row sums on the rounded probabilities, masked-key sentinel, all-masked
-// rows reproducing mean(v)) is the tiled kernel's, so both paths give identical results.
+// Per tile: the transposed score tile S^T = K Q'^T on 32x32x16 MFMA, the pair bias added by
+// MFMA against an identity fragment, and, on tiles with a masked key or keys past N, the
+// per-key mask term (0 / mask_value / -inf from a per-row table in LDS) added by one more
+// MFMA per 32-key half (a rank-1 product: the term in column 0 of A times ones in row 0 of B),
+// so masking costs no per-score VALU work. The softmax is evaluated against a reference
+// maximum m taken from the row's first tile only: p = exp2((s - m) log2 e) may then exceed 1
+// on later tiles, which costs nothing in precision (bf16 / fp32 are relative) and removes the
+// per-tile maximum reduction. A query block whose row sum ends above 2^64 (so p or the
+// accumulators could have overflowed) is recomputed with the per-tile maximum and lazy
+// rescale (threshold 8 ln 2), the pass that also serves callers asking for the exact row
+// maximum. exp2 with the folded FMA, v_dot2 row sums on the rounded probabilities, and rows
+// whose keys are all masked reproducing mean(v) (the sentinel swamps the logits; subtract
+// first) are as in the tiled kernel, which gives the same results to rounding.
 #include "gnn_common.hpp"
 #include "gnn_internal.hpp"
 
@@ -81,11 +90,16 @@ struct RowHdr {
   int full;  // every key < N is live (no masked key): tiles run in order, liveness is arithmetic
 };
 constexpr int HDR_BYTES = (int)((sizeof(RowHdr) + 255) / 256 * 256);
+// per-key additive mask term of the row, one 16-bit value per key of every tile
+__host__ __device__ constexpr int mask_table_bytes(int ntiles) { return (ntiles * KT * 2 + 255) / 256 * 256; }
 
 size_t row_smem_bytes(int64_t N) {
-  const int64_t ntiles = (N + KT - 1) / KT;
-  return HDR_BYTES + 2 * (size_t)ntiles * TILE_BYTES;
+  const int ntiles = (int)((N + KT - 1) / KT);
+  return HDR_BYTES + mask_table_bytes(ntiles) + 2 * (size_t)ntiles * TILE_BYTES;
 }
+
+// query blocks whose row sum ends above this are recomputed with the per-tile maximum
+constexpr float FAST_LSUM_LIMIT = 18446744073709551616.0f;  // 2^64
 
 template <typename T> struct BiasFragR {
   typename TypeOps<T>::V8 f[2][2];  // f[sub][t] = bias[q][tile*64 + sub*32 + 16t + 8g + 0..7]
@@ -159,6 +173,7 @@ template <typename T, bool HAS_BIAS>
 __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel(const gnn_triattn_args a) {
   typedef typename TypeOps<T>::V8 V8;
   typedef typename TypeOps<T>::V4 V4;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   extern __shared__ __align__(256) unsigned char smem_raw[];
   RowHdr& hdr = *reinterpret_cast<RowHdr*>(smem_raw);
 
@@ -167,7 +182,8 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
   const int D = (int)a.D;
   const int S = (int)a.S;
   const int ntiles = (N + KT - 1) / KT;
-  unsigned char* ks = smem_raw + HDR_BYTES;
+  uint16_t* mbt = reinterpret_cast<uint16_t*>(smem_raw + HDR_BYTES);
+  unsigned char* ks = smem_raw + HDR_BYTES + mask_table_bytes(ntiles);
   unsigned char* vs = ks + ntiles * TILE_BYTES;
 
   // Logical order: heads fastest when all H bias planes of a batch fit one XCD's L2
@@ -248,8 +264,11 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
     }
   }
 
-  // ---- key liveness of the row (wave 0) and the tiles to run.
+  // ---- key liveness of the row, the tiles to run and the per-key mask term (wave 0):
+  // 0 for a kept key, mask_value for a masked one, -inf past N.
   if (wave == 0) {
+    const uint16_t mterm = __builtin_bit_cast(uint16_t, TypeOps<T>::from_f32(a.mask_value));
+    const uint16_t ninf = __builtin_bit_cast(uint16_t, TypeOps<T>::from_f32(-INFINITY));
     int n = 0;
     bool full = true;
     for (int t = 0; t < ntiles; ++t) {
@@ -257,6 +276,7 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
       const bool valid = key < N;
       bool live = valid;
       if (live && a.mask) live = a.mask[b * a.mask_stride[0] + s * a.mask_stride[1] + (int64_t)key * a.mask_stride[2]] != 0;
+      mbt[key] = !valid ? ninf : (live ? (uint16_t)0 : mterm);
       const uint64_t bits = __ballot(live);
       full &= bits == __ballot(valid);
       if (lane == 0) {
@@ -279,7 +299,6 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
   const int nrun = hdr.nrun;
   const bool dead = hdr.dead != 0;
   const bool full = hdr.full != 0;
-  const float mval = a.mask_value;
 
   // identity A-fragments for the bias MFMA (element e of lane group g in step t is key
   // 16t + 8g + e of the 32-key sub-tile; row l32 holds a 1 there iff l32 is that key)
@@ -288,6 +307,7 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int e = 0; e < 8; ++e) idf[t][e] = TypeOps<T>::from_f32(l32 == 16 * t + 8 * g + e ? 1.f : 0.f);
+  const uint32_t one_bits = __builtin_bit_cast(uint16_t, TypeOps<T>::from_f32(1.f));
 
   // per-lane LDS offsets: K fragment of k-step kk for key row l32 of a 32-key sub-tile
   // (the swizzle term (key / 4) % 4 only depends on l32), and the V^T transposed-read base.
@@ -297,6 +317,8 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
   const int tr_r = lane & 15;
   int tr_off = ((tr_r >> 2) * 32 + 16 * ((lane >> 4) & 1) + 4 * (tr_r & 3)) * 2 + 4 * g * ROW_BYTES;
 
+  // exact row maxima are only tracked for callers that ask for them (per-tile maximum pass)
+  const bool want_max = a.row_max != nullptr;
   const int nqb = (N + 31) / 32;
   for (int qblk = wave; qblk < nqb; qblk += NW) {
     // The first tiles' LDS reads are the same for every query block; keeping the compiler
@@ -327,13 +349,12 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
                                    (int64_t)(qok ? myq : 0) * a.bias_stride[2]
                              : nullptr;
     f32x16 o;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) o[i] = 0.f;
-    float m = -INFINITY, lsum = 0.f;
+    float m, lsum, mx;
     BiasFragR<T> bb;
 
-    // S^T (+ bias) of tile t into acc: acc[sub][i] is key t*64 + sub*32 + 8*(i/4) + 4g + i%4.
-    auto qk = [&](f32x16 (&acc)[2], int t) {
+    // S^T (+ bias, + key mask term on partial tiles) of tile t into acc: acc[sub][i] is key
+    // t*64 + sub*32 + 8*(i/4) + 4g + i%4.
+    auto qk = [&](f32x16 (&acc)[2], int t, bool partial) {
       const unsigned char* kt = ks + t * TILE_BYTES;
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
@@ -350,40 +371,46 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
 #pragma unroll
           for (int sub = 0; sub < 2; ++sub) Mma<T, PREC_NATIVE>::step(acc[sub], idf[t2], bb.f[sub][t2]);
       }
-    };
-
-    // mask, online softmax and O^T += V^T P^T for the scores of tile t
-    auto softmax_pv = [&](f32x16 (&sc)[2], int t, uint64_t live) {
-      if (live != ~0ull) {
-        const int nvalid = min(KT, Nq - t * KT);
-        const uint64_t valid = nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull);
+      if (partial) {
+        // A[key][0] = the key's mask term (lane group 0), B[0][q] = 1: adds the term to every
+        // query of the key row; all other products are 0 * 0 (or 0 * 1).
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
-          const uint32_t lb = ((uint32_t)(live >> (32 * sub)) >> (4 * g)) & 0x0F0F0F0Fu;
-          const uint32_t vb = ((uint32_t)(valid >> (32 * sub)) >> (4 * g)) & 0x0F0F0F0Fu;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int bit = 8 * (i / 4) + (i % 4);
-            const float x = ((lb >> bit) & 1u) ? sc[sub][i] : sc[sub][i] + mval;
-            sc[sub][i] = ((vb >> bit) & 1u) ? x : -INFINITY;
-          }
+          const uint32_t term = mbt[t * KT + sub * 32 + l32];
+          const u32x4 av = {g ? 0u : term, 0u, 0u, 0u};
+          const u32x4 bv = {one_bits, 0u, 0u, 0u};
+          Mma<T, PREC_NATIVE>::step(acc[sub], __builtin_bit_cast(V8, av), __builtin_bit_cast(V8, bv));
         }
       }
-      float m0 = max3_nn(sc[0][0], sc[0][1], sc[0][2]), m1 = max3_nn(sc[1][0], sc[1][1], sc[1][2]);
+    };
+
+    // online softmax and O^T += V^T P^T for the scores of tile t. `first`: the row's first
+    // tile sets the reference maximum; `per_tile`: every tile's maximum is taken and the
+    // accumulators rescaled when it grows past the threshold.
+    auto softmax_pv = [&](f32x16 (&sc)[2], int t, bool first, bool per_tile) {
+      if (first || per_tile) {
+        float m0 = max3_nn(sc[0][0], sc[0][1], sc[0][2]), m1 = max3_nn(sc[1][0], sc[1][1], sc[1][2]);
 #pragma unroll
-      for (int i = 3; i < 15; i += 2) {
-        m0 = max3_nn(m0, sc[0][i], sc[0][i + 1]);
-        m1 = max3_nn(m1, sc[1][i], sc[1][i + 1]);
-      }
-      const float mh = max3_nn(m0, max_nn(sc[0][15], sc[1][15]), m1);
-      const float mt = pair_max_swap(mh);
-      if (__any(mt > m + RESCALE_THRESHOLD)) {
-        const float mnew = fmaxf(m, mt);
-        const float alpha = fast_exp2((m - mnew) * LOG2E);  // 0 on the first tile (m = -inf)
-        m = mnew;
-        lsum *= alpha;
+        for (int i = 3; i < 15; i += 2) {
+          m0 = max3_nn(m0, sc[0][i], sc[0][i + 1]);
+          m1 = max3_nn(m1, sc[1][i], sc[1][i + 1]);
+        }
+        const float mh = max3_nn(m0, max_nn(sc[0][15], sc[1][15]), m1);
+        const float mt = pair_max_swap(mh);
+        if (first) {
+          m = mt;  // o and the row sum are still zero
+          mx = mt;
+        } else {
+          mx = max_nn(mx, mt);
+          if (__any(mt > m + RESCALE_THRESHOLD)) {
+            const float mnew = fmaxf(m, mt);
+            const float alpha = fast_exp2((m - mnew) * LOG2E);
+            m = mnew;
+            lsum *= alpha;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[i] *= alpha;
+            for (int i = 0; i < 16; ++i) o[i] *= alpha;
+          }
+        }
       }
       const float nm = -m * LOG2E;
       // per 32-key half: exponentiate, round to the MFMA type, accumulate the row sum and
@@ -426,30 +453,42 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
 #define ROW_PRIO_HI()
 #define ROW_PRIO_LO()
 #endif
-    if (full) {
-      // no masked key: tiles in order, liveness from N alone (no LDS reads in the loop)
-      if constexpr (HAS_BIAS) load_bias_row<T>(bb, brow, 0, Nq, g);
-      for (int t = 0; t < ntiles; ++t) {
-        f32x16 sc[2];
-        ROW_PRIO_HI();
-        qk(sc, t);
-        ROW_PRIO_LO();
-        if (HAS_BIAS && t + 1 < ntiles) load_bias_row<T>(bb, brow, (t + 1) * KT, Nq, g);
-        const int nvalid = Nq - t * KT;
-        softmax_pv(sc, t, nvalid >= 64 ? ~0ull : ((1ull << nvalid) - 1ull));
+    // every tile of the row, with the reference maximum from the first tile, or (per_tile)
+    // with each tile's maximum and lazy rescale
+    auto sweep = [&](bool per_tile) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[i] = 0.f;
+      lsum = 0.f;
+      m = -INFINITY;
+      mx = -INFINITY;
+      if (full) {
+        // no masked key: tiles in order; only the last one can hold keys past N
+        const bool tail = Nq % KT != 0;
+        if constexpr (HAS_BIAS) load_bias_row<T>(bb, brow, 0, Nq, g);
+        for (int t = 0; t < ntiles; ++t) {
+          f32x16 sc[2];
+          ROW_PRIO_HI();
+          qk(sc, t, tail && t == ntiles - 1);
+          ROW_PRIO_LO();
+          if (HAS_BIAS && t + 1 < ntiles) load_bias_row<T>(bb, brow, (t + 1) * KT, Nq, g);
+          softmax_pv(sc, t, t == 0, per_tile);
+        }
+      } else {
+        if constexpr (HAS_BIAS) load_bias_row<T>(bb, brow, hdr.tile_list[0] * KT, Nq, g);
+        for (int it = 0; it < nrun; ++it) {
+          const int t = hdr.tile_list[it];
+          f32x16 sc[2];
+          ROW_PRIO_HI();
+          qk(sc, t, hdr.tile_live[t] != ~0ull);
+          ROW_PRIO_LO();
+          if (HAS_BIAS && it + 1 < nrun) load_bias_row<T>(bb, brow, hdr.tile_list[it + 1] * KT, Nq, g);
+          softmax_pv(sc, t, it == 0, per_tile);
+        }
       }
-    } else {
-      if constexpr (HAS_BIAS) load_bias_row<T>(bb, brow, hdr.tile_list[0] * KT, Nq, g);
-      for (int it = 0; it < nrun; ++it) {
-        const int t = hdr.tile_list[it];
-        f32x16 sc[2];
-        ROW_PRIO_HI();
-        qk(sc, t);
-        ROW_PRIO_LO();
-        if (HAS_BIAS && it + 1 < nrun) load_bias_row<T>(bb, brow, hdr.tile_list[it + 1] * KT, Nq, g);
-        softmax_pv(sc, t, hdr.tile_live[t]);
-      }
-    }
+    };
+    // A block whose row sum exceeds FAST_LSUM_LIMIT anywhere (p or the accumulators may have
+    // overflowed) runs again with per-tile maxima; so do blocks whose exact maxima are asked for.
+    if (want_max || (sweep(false), __any(!(lsum <= FAST_LSUM_LIMIT)))) sweep(true);
 
     // ---- normalise and store. o[i] is O[myq][8*(i/4) + 4g + i%4].
     const float ltot = pair_sum_swap(lsum);
@@ -464,8 +503,9 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
           store4(orow + d0, TypeOps<T>::from_f32(x));
         }
       }
-      if (a.lse && g == 0)
-        a.lse[(((int64_t)b * a.S + s) * H + h) * N + myq] = m + __log2f(ltot) * (1.0f / LOG2E);
+      const int64_t ridx = (((int64_t)b * a.S + s) * H + h) * N + myq;
+      if (a.lse && g == 0) a.lse[ridx] = m + __log2f(ltot) * (1.0f / LOG2E);
+      if (want_max && g == 0) a.row_max[ridx] = mx;
     }
   }
 }

@@ -36,6 +36,7 @@ class TriAttnArgs(ctypes.Structure):
         ("bias", ctypes.c_void_p),
         ("mask", ctypes.c_void_p),
         ("lse", ctypes.c_void_p),
+        ("row_max", ctypes.c_void_p),
         ("B", ctypes.c_int64),
         ("S", ctypes.c_int64),
         ("N", ctypes.c_int64),

@@ -56,7 +56,7 @@ def _prepare_bias(bias: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
 
 
 def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=False, use_exp2=False,
-                           lse=None, mask_value=None):
+                           lse=None, mask_value=None, row_max=None):
     """Triangle attention forward on the canonical 5D layout.
 
     q/k/v ``[B, N_seq, N_res, H, D]`` (bf16, fp16 or fp32, on a HIP device); bias
@@ -64,7 +64,8 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
     ``None``. ``dynamic`` is accepted for API parity and has no effect (N is always a
     runtime argument); ``use_exp2`` likewise (the kernel always evaluates the softmax in
     base 2). ``lse``, if given, is a float32 ``[B, N_seq, H, N_res]`` tensor that receives
-    the natural-log log-sum-exp of each query's logits. ``mask_value`` overrides the logit
+    the natural-log log-sum-exp of each query's logits; ``row_max``, likewise shaped, receives
+    each query's largest logit (scaled q.k + bias + mask term). ``mask_value`` overrides the logit
     offset of masked keys (default: the dtype's sentinel rounded to the dtype, as the
     reference launcher applies it).
     """
@@ -106,6 +107,9 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
     if lse is not None:
         assert lse.shape == (B, S, H, N) and lse.dtype == torch.float32 and lse.is_contiguous()
         args.lse = lse.data_ptr()
+    if row_max is not None:
+        assert row_max.shape == (B, S, H, N) and row_max.dtype == torch.float32 and row_max.is_contiguous()
+        args.row_max = row_max.data_ptr()
     args.scale = float(scale)
     args.mask_value = rounded_mask_value(q.dtype) if mask_value is None else float(mask_value)
     args.dtype = _lib.DTYPE_CODE[q.dtype]

@@ -16,6 +16,7 @@ missing: a GPU call then raises.
 """
 
 import torch
+from torch.autograd.function import once_differentiable
 
 from .. import _ops
 from ._kernels import triangle_attention as _hip
@@ -36,7 +37,9 @@ def _needs_torch_path(q, k, v, bias) -> bool:
 
 class _TriangleAttentionHip(torch.autograd.Function):
     """HIP forward that keeps the log-sum-exp, HIP backward (reference
-    EvoformerAttention, triangle_attention.py:1091-1442)."""
+    EvoformerAttention, triangle_attention.py:1091-1442). The backward kernels record no
+    graph, so it is ``once_differentiable``: a second derivative raises instead of coming
+    back wrong."""
 
     @staticmethod
     def forward(ctx, q, k, v, bias, mask, scale):
@@ -49,6 +52,7 @@ class _TriangleAttentionHip(torch.autograd.Function):
         return o
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, do):
         q, k, v, bias, mask, o, lse = ctx.saved_tensors
         dq, dk, dv, dbias = _hip.triangle_attention_bwd_hip(q, k, v, o, do, lse, bias=bias, mask=mask,

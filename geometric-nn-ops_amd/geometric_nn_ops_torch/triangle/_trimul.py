@@ -1,24 +1,25 @@
-"""Public ``triangle_multiplicative_update`` (reference geometric_nn_ops_torch/triangle/_trimul.py).
+"""``triangle_multiplicative_update``: the public entry point, with the reference's signature
+(geometric_nn_ops_torch/triangle/_trimul.py:39-88 of AMDResearch/geometric-nn-ops).
 
-Two backends with the same math:
-  * the gfx950 HIP kernels in ``_kernels.trimul``: the forward, and a backward
-    (``trimul_bwd_hip``) the reference does not have;
-  * the pure-torch, autograd-differentiable path in ``_reference.trimul``.
+Where a call goes:
+  * a forward that no backward can follow (grad disabled, or nothing requires grad) on a HIP
+    tensor of a kernel dtype runs the gfx950 kernels through the ``gnn_amd::trimul_fwd``
+    operator;
+  * a call that needs gradients, on the same tensors, runs ``_TrimulHip``: the kernels'
+    forward, then this library's backward (the reference's own grad calls run autograd
+    through its torch code, _trimul.py:31-36);
+  * CPU tensors, other dtypes, channel counts outside the kernels' tiling (c_z or c_hidden
+    not a multiple of 32, or above 512) and a mask that itself requires grad run the
+    autograd-differentiable torch restatement in ``_reference.trimul``.
+The kernels are never silently replaced: without the HIP library a GPU call raises.
 
-Dispatch: the reference (_trimul.py:31-36) runs its torch path whenever a backward could
-run (grad enabled and x or a weight requires grad). Here such calls run the HIP forward
-under ``_TrimulHip``, whose backward is the HIP one, when the inputs are on a HIP device in
-a kernel dtype with supported channel counts and the mask does not require grad. The torch
-path runs for CPU tensors, other dtypes and channel counts the kernels do not tile (c_z or
-c_hidden not a multiple of 32, or above 512). Inference calls run the HIP kernels through
-the ``gnn_amd::trimul_fwd`` operator (``geometric_nn_ops_torch._ops``). A missing HIP
-library is an error on GPU tensors, never a silent fallback.
-
-``p_in_weight`` / ``g_in_weight`` are the concatenated ``[a; b]`` projections
-(``[2 * C_hidden, C_z]``).
+The input projections come stacked: rows ``[0, C_hidden)`` of ``p_in_weight`` and
+``g_in_weight`` produce the left operand ``a``, rows ``[C_hidden, 2 C_hidden)`` the right
+operand ``b``.
 """
 
 import torch
+from torch.autograd.function import once_differentiable
 
 from .. import _ops
 from ._kernels import trimul as _hip
@@ -45,7 +46,10 @@ def _needs_torch_path(x: torch.Tensor, weights, mask=None) -> bool:
 
 
 class _TrimulHip(torch.autograd.Function):
-    """HIP forward that keeps its workspace (a, b, g, o) for the HIP backward."""
+    """HIP forward whose workspace (the contraction operands a, b and its output o) stays on
+    the autograd graph for the HIP backward; the graph owns it, so a backward with
+    ``retain_graph=True`` can run again. The backward's kernels record no graph of their
+    own, hence ``once_differentiable``: asking for a second derivative raises."""
 
     @staticmethod
     def forward(ctx, x, direction, mask, eps, *ws):
@@ -60,12 +64,12 @@ class _TrimulHip(torch.autograd.Function):
         return out.reshape(x.shape)
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, dout):
         x, *ws = ctx.saved_tensors
         weights = dict(zip(_hip._WEIGHT_KEYS, ws))
         dx, dw = _hip.trimul_bwd_hip(x, ctx.direction, ctx.mask, ctx.eps, weights, ctx.workspace,
                                       ctx.offsets, dout)
-        ctx.workspace = None
         return (dx, None, None, None, *(dw[k] for k in _hip._WEIGHT_KEYS))
 
 
@@ -87,19 +91,16 @@ def triangle_multiplicative_update(
     g_out_bias: torch.Tensor | None = None,
     eps: float = 1e-5,
 ) -> torch.Tensor:
-    """Triangle multiplicative update over a pair representation.
+    """Gated triangle update of a pair tensor: every pixel (i, j) gathers the channel-wise
+    products of row i with row j ("outgoing") or of column i with column j ("incoming").
 
-    Args:
-        x: ``[*, N, N, C_z]`` pair representation.
-        direction: ``"outgoing"`` or ``"incoming"``.
-        mask: optional ``[*, N, N]`` pair mask (1 = keep), broadcastable over the leading dims.
-        *_weight / *_bias: LayerNorm / projection / gate parameters.
-        eps: LayerNorm epsilon.
-
-    Returns:
-        ``[*, N, N, C_z]`` updated pair representation.
-
-    fp32 products follow ``torch.backends.cuda.matmul.fp32_precision``.
+    ``x`` is ``[..., N, N, C_z]`` with any number of leading batch dims; ``mask`` (1 keeps a
+    pixel) is ``[..., N, N]`` or broadcasts to it. The LayerNorms take ``norm_in_*`` (size
+    C_z) and ``norm_out_*`` (size C_hidden); ``p_in_weight`` / ``g_in_weight`` are the
+    stacked ``[2 C_hidden, C_z]`` projections with their optional biases; ``p_out_weight`` is
+    ``[C_z, C_hidden]`` and ``g_out_weight`` ``[C_z, C_z]``. ``eps`` goes to both
+    LayerNorms. The result has the shape and dtype of ``x``. With fp32 inputs the matrix
+    products honour ``torch.backends.cuda.matmul.fp32_precision``.
     """
     weights = dict(
         norm_in_weight=norm_in_weight,

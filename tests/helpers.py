@@ -152,3 +152,28 @@ def apb_key_mask(batch, v, *, seed=0, frac_keep=0.9, dtype=torch.float32, device
     m = torch.rand(batch, v, generator=gen(seed)) < frac_keep
     m[:, 0] = True
     return m.to(dtype).to(device)
+
+
+def trimul_pixels(x, mask, w, direction, rows, cols):
+    """``oracle.trimul`` at pixels ``(rows[i], cols[j])`` of a grid too large to copy whole.
+
+    The pixels need only the pair-grid lines ``U = rows + cols`` of x (grid rows for
+    'outgoing', columns for 'incoming'), so ``oracle.trimul_grid`` runs on x restricted to
+    those lines with line indices into U. Its output gate is then taken from the restricted
+    tensor at the compacted (line, line) position instead of at pixel (rows[i], cols[j]);
+    the factor is replaced by the gate of the true pixel (both gates are sigmoids, > 0)."""
+    wn = {k: to_np(v) for k, v in w.items()}
+    lines = sorted(set(rows) | set(cols))
+    pos = {r: i for i, r in enumerate(lines)}
+    ri, ci = [pos[r] for r in rows], [pos[c] for c in cols]
+    if direction == "outgoing":
+        xs, ms = to_np(x[:, lines]), to_np(mask[:, lines])
+    else:
+        xs, ms = to_np(x[:, :, lines]), to_np(mask[:, :, lines])
+    got = O.trimul_grid(xs, direction, ms, ri, ci, **wn)
+
+    def gate(pix):
+        z = O.layer_norm(pix, wn["norm_in_weight"], wn["norm_in_bias"])
+        return O.sigmoid(O.linear(z, wn["g_out_weight"], wn.get("g_out_bias")))
+
+    return got / gate(xs[:, ri][:, :, ci]) * gate(to_np(x[:, rows][:, :, cols]))

@@ -56,7 +56,7 @@ def _c_layout():
       P(gnn_layernorm_args, eps) P(gnn_layernorm_args, dtype)
       P(gnn_gate_bwd_args, d_gate_pre) P(gnn_gate_bwd_args, rows) P(gnn_gate_bwd_args, mask_stride)
       P(gnn_gate_bwd_args, dg_stride) P(gnn_gate_bwd_args, dtype)
-      P(gnn_triattn_args, lse) P(gnn_triattn_args, D) P(gnn_triattn_args, bias_stride)
+      P(gnn_triattn_args, lse) P(gnn_triattn_args, row_max) P(gnn_triattn_args, D) P(gnn_triattn_args, bias_stride)
       P(gnn_triattn_args, mask_stride) P(gnn_triattn_args, scale) P(gnn_triattn_args, precision)
       P(gnn_trimul_args, mask_stride) P(gnn_trimul_args, workspace_bytes) P(gnn_trimul_args, Ch)
       P(gnn_trimul_args, eps) P(gnn_trimul_args, precision)

@@ -550,3 +550,78 @@ def test_layer_norm_grad_matches_finite_differences():
                                                   **{{"x": "x", "w": "weight", "b": "bias"}[name]: minus}}) * dy)
                         ) / (2 * h)
         np.testing.assert_allclose(g, num, rtol=1e-6, atol=1e-8, err_msg=name)
+
+
+# ---------------------------------------------------------------------------------- metrics
+def test_rel_fro_known_answers():
+    """``rel_fro(a, b) = ||a - b|| / ||b||`` with ``b`` the reference (testutil/metrics.py:40-47):
+    the denominator is the second argument, so (2b, b) gives 1 and (b, 2b) gives 1/2."""
+    b = RNG(0).standard_normal((4, 8))
+    assert O.rel_fro(b, b) == 0.0
+    assert O.rel_fro(2 * b, b) == pytest.approx(1.0, abs=1e-15)
+    assert O.rel_fro(b, 2 * b) == pytest.approx(0.5, abs=1e-15)
+    assert O.rel_fro(-b, b) == pytest.approx(2.0, abs=1e-15)
+    # a 3-4-5 triangle: ||(3, 4) - (0, 0)|| against a unit reference
+    assert O.rel_fro(np.array([3.0, 4.0, 1.0]), np.array([0.0, 0.0, 1.0])) == pytest.approx(5.0, abs=1e-15)
+    # shape-agnostic: the Frobenius norm of the flattened arrays
+    assert O.rel_fro(2 * b.reshape(32), b.reshape(32)) == pytest.approx(1.0, abs=1e-15)
+    # a zero reference is clamped, not divided by (the reference clamps at 1e-30)
+    assert O.rel_fro(np.zeros(3), np.zeros(3)) == 0.0
+    assert O.rel_fro(np.full(3, 1e-20), np.zeros(3)) > 1e9
+
+
+def test_cos_known_answers():
+    """Cosine of the flattened arrays; two zero arrays count as 1 and one zero side as 0
+    (testutil/metrics.py:26-37, tests/test_metrics.py:14-38)."""
+    b = RNG(1).standard_normal((4, 8))
+    zero = np.zeros((4, 8))
+    assert O.cos(zero, zero) == 1.0
+    assert O.cos(zero, np.ones((4, 8))) == 0.0
+    assert O.cos(np.ones((4, 8)), zero) == 0.0
+    assert O.cos(b, b) == pytest.approx(1.0, abs=1e-15)
+    assert O.cos(3 * b, b) == pytest.approx(1.0, abs=1e-15)
+    assert O.cos(-b, b) == pytest.approx(-1.0, abs=1e-15)
+    assert O.cos(np.array([1.0, 0.0]), np.array([0.0, 1.0])) == 0.0
+    assert O.cos(np.array([1.0, 1.0]), np.array([1.0, 0.0])) == pytest.approx(2 ** -0.5, abs=1e-15)
+    assert math.isnan(O.cos(np.array([np.nan, 1.0]), np.array([1.0, 1.0])))
+
+
+def test_assert_close_to_oracle_rejects_mismatches():
+    """The GPU parity gate (tests/helpers.py) fails on a scaled, sign-flipped, non-finite or
+    reshaped candidate and on a zero candidate against a non-zero oracle, and passes the exact
+    match and two zero tensors (tests/test_metrics.py:14-38)."""
+    from helpers import Tolerance, assert_close_to_oracle
+
+    tol = Tolerance(1.0 - 1e-4, 1e-2)
+    want = RNG(2).standard_normal((4, 8))
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))  # noqa: E731
+    assert assert_close_to_oracle("exact", t(want), want, tol) == (pytest.approx(1.0), 0.0)
+    assert assert_close_to_oracle("zeros", t(np.zeros((4, 8))), np.zeros((4, 8)), tol) == (1.0, 0.0)
+    bad = {
+        "scaled": 1.05 * want,  # cosine 1, rel-Fro 0.05
+        "negated": -want,
+        "zero": np.zeros_like(want),
+        "nan": np.where(np.arange(32).reshape(4, 8) == 5, np.nan, want),
+        "transposed": want.T,
+    }
+    for name, got in bad.items():
+        with pytest.raises(AssertionError):
+            assert_close_to_oracle(name, t(got), want, tol)
+    # the north star's 1e-2 cap tightens a looser table entry
+    with pytest.raises(AssertionError):
+        assert_close_to_oracle("capped", t(1.02 * want), want, Tolerance(1.0 - 1e-4, 5e-2), rel_fro_max=1e-2)
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_trimul_pixels_from_lines_is_the_full_oracle(direction):
+    """The large-N tests' pixel oracle (helpers.trimul_pixels: trimul_grid on the needed grid
+    lines with the output gate re-taken at the true pixel) equals the full oracle there."""
+    from helpers import pair_input, trimul_pixels, trimul_weights
+
+    N = 14
+    w = trimul_weights(32, 16, torch.float64, seed=5, biases=True, ln_random=True)
+    x, mask = pair_input(1, N, 32, torch.float64, seed=6)
+    full = O.trimul(x.numpy(), direction, mask.numpy(), **{k: v.numpy() for k, v in w.items()})
+    rows, cols = [1, N - 4, N - 1], [0, N - 3, N - 1]
+    got = trimul_pixels(x, mask, w, direction, rows, cols)
+    np.testing.assert_allclose(got, full[:, rows][:, :, cols], rtol=1e-12, atol=1e-12)

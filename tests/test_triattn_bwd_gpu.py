@@ -126,3 +126,28 @@ def test_fp32_and_wide_heads_keep_the_torch_gradient():
     """fp32 inputs and head dims above 32 are differentiated by the torch path."""
     for dtype, d in ((torch.float32, 32), (torch.bfloat16, 64)):
         check_against_oracle((1, 2, 40, 2, d), dtype, seed=51)
+
+
+def test_backward_twice_with_retained_graph_and_no_second_derivative():
+    """A retained graph runs the HIP backward again with the same result; a second derivative
+    is refused (the backward kernels record no graph)."""
+    from geometric_nn_ops_torch.triangle import triangle_attention
+
+    B, S, N, H, D = 1, 2, 40, 2, 32
+    t = attention_inputs(B, S, N, H, D, torch.bfloat16, seed=21, with_bias=True, device=DEV)
+    q, k, v, bias = (t[n].detach().requires_grad_() for n in ("q", "k", "v", "bias"))
+    mask = key_mask(B, S, N, seed=22, device=DEV)
+    o = triangle_attention(q, k, v, bias, mask)
+    fn = o.grad_fn  # the public op reshapes the Function's output: walk past the view node
+    while fn is not None and "TriangleAttentionHip" not in type(fn).__name__:
+        fn = fn.next_functions[0][0] if fn.next_functions else None
+    assert fn is not None
+    dout = torch.randn(B, S, N, H, D, generator=gen(23)).to(DEV, torch.bfloat16)
+    first = torch.autograd.grad(o, [q, bias], dout, retain_graph=True)
+    o.backward(dout)
+    assert torch.equal(q.grad, first[0]) and torch.equal(bias.grad, first[1])
+
+    o2 = triangle_attention(q, k, v, bias, mask)
+    (gq,) = torch.autograd.grad(o2.float().square().sum(), q, create_graph=True)
+    with pytest.raises(RuntimeError):
+        gq.float().sum().backward()

@@ -154,3 +154,37 @@ def test_mask_requiring_grad_takes_the_torch_path():
         out = triangle_multiplicative_update(x.to(DEV).requires_grad_(), "outgoing", mask, **w)
         out.sum().backward()
     assert ref.called and mask.grad is not None
+
+
+def test_backward_twice_with_retained_graph():
+    """The forward's workspace belongs to the graph: a second backward over a graph kept with
+    ``retain_graph=True`` gives the same gradients as the first."""
+    from geometric_nn_ops_torch.triangle import triangle_multiplicative_update
+
+    dtype = torch.bfloat16
+    w = {k: v.to(DEV).requires_grad_() for k, v in trimul_weights(64, 64, dtype, seed=71, biases=True).items()}
+    x, mask = pair_input(1, 20, 64, dtype, seed=72)
+    x = x.to(DEV).requires_grad_()
+    out = triangle_multiplicative_update(x, "incoming", mask.to(DEV), **w)
+    assert "TrimulHip" in type(out.grad_fn).__name__
+    dout = randn((1, 20, 20, 64), seed=73).to(DEV, dtype)
+    first = torch.autograd.grad(out, [x, w["p_in_weight"], w["norm_out_weight"]], dout, retain_graph=True)
+    out.backward(dout)
+    assert torch.equal(x.grad, first[0])
+    assert torch.equal(w["p_in_weight"].grad, first[1])
+    assert torch.equal(w["norm_out_weight"].grad, first[2])
+
+
+def test_second_derivative_raises():
+    """The HIP backward records no graph of its own, so a double backward is refused rather
+    than returning partial second-order gradients."""
+    from geometric_nn_ops_torch.triangle import triangle_multiplicative_update
+
+    dtype = torch.bfloat16
+    w = {k: v.to(DEV) for k, v in trimul_weights(32, 32, dtype, seed=74).items()}
+    x, _ = pair_input(1, 12, 32, dtype, seed=75)
+    x = x.to(DEV).requires_grad_()
+    out = triangle_multiplicative_update(x, "outgoing", None, **w)
+    (gx,) = torch.autograd.grad(out.float().square().sum(), x, create_graph=True)
+    with pytest.raises(RuntimeError):
+        gx.float().sum().backward()
