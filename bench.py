@@ -122,6 +122,7 @@ def main():
     a.bias_stride = _lib.I64x4(bd.stride(0), bd.stride(2), bd.stride(3), bd.stride(4))
     a.scale, a.mask_value = D**-0.5, rounded_mask_value(dt)
     a.dtype, a.precision = _lib.GNN_BF16, _lib.GNN_PREC_IEEE
+    attn_ws = TA.workspace_for(a, dev)  # noqa: F841 -- kept alive for every launch below
 
     wd = {kk: vv.to(dev) for kk, vv in w.items()}
     xd, md = x.to(dev), tmask.to(dev)

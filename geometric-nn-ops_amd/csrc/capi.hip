@@ -54,12 +54,17 @@ static int check_triattn(const gnn_triattn_args& a) {
       if (st[t][d] % 8 != 0)
         return set_error(GNN_ERR_ARG, "triangle_attention: q/k/v/o strides must be multiples of 8 elements");
   }
-  if (a.bias) {
+  if (a.bias && !triattn_row_applicable(a)) {
     if (a.bias_stride[3] != 1 || a.bias_stride[2] % 8 != 0 || !aligned(a.bias, 16))
       return set_error(GNN_ERR_ARG,
                        "triangle_attention: bias needs unit key stride, a query stride that is a multiple "
                        "of 8 and 16-byte alignment");
   }
+  const size_t need = triattn_row_applicable(a) ? triattn_row_workspace_bytes(a) : 0;
+  if (need && (!a.workspace || a.workspace_bytes < need || !aligned(a.workspace, 16)))
+    return set_error(GNN_ERR_WORKSPACE,
+                     "triangle_attention: workspace missing, smaller than gnn_triattn_workspace_bytes() or "
+                     "not 16-byte aligned");
   return GNN_OK;
 }
 
@@ -75,6 +80,11 @@ int gnn_triattn_fwd(const gnn_triattn_args* args, void* stream) {
   int rc = triattn_fwd(*args, (hipStream_t)stream);
   if (rc < 0) return rc;
   return hip_status((hipError_t)rc, "triangle_attention");
+}
+
+size_t gnn_triattn_workspace_bytes(const gnn_triattn_args* args) {
+  if (!args) return 0;
+  return triattn_row_applicable(*args) ? triattn_row_workspace_bytes(*args) : 0;
 }
 
 int gnn_triattn_bwd(const gnn_triattn_bwd_args* args, void* stream) {

@@ -20,6 +20,7 @@ int triattn_bwd(const gnn_triattn_bwd_args& a, hipStream_t stream);
 // Row-resident attention (16-bit inputs, head dim <= 32, bounded N_res): the whole row of
 // K and V staged in LDS, no barrier in the key loop.
 bool triattn_row_applicable(const gnn_triattn_args& a);
+size_t triattn_row_workspace_bytes(const gnn_triattn_args& a);
 int triattn_row_fwd(const gnn_triattn_args& a, hipStream_t stream);
 
 // Row-resident attention backward for dq (with Delta) and dk / dv (16-bit inputs, head dim 32,

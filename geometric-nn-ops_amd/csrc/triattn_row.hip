@@ -105,22 +105,55 @@ template <typename T> struct BiasFragR {
   typename TypeOps<T>::V8 f[2][2];  // f[sub][t] = bias[q][tile*64 + sub*32 + 16t + 8g + 0..7]
 };
 
+// The pair bias in fragment order. bias[b, h] is shared by every N_seq row, so a launch
+// reads it S times; in the caller's row-major layout one 16-byte fragment load per lane
+// touches 32 query rows (32 cache lines for 1 KB) and those loads are bound by the L1's
+// line rate. A pre-pass writes each (b, h, 32-query block, 64-key tile) as 4 KB in the
+// order the fragments are consumed: fragment f = 2 sub + t of lane l at byte
+// 1024 f + 16 l. Every fragment load is then one contiguous 1 KB range, and queries or keys
+// past N hold zeros (the identity MFMA multiplies every loaded value, so padding must be
+// finite).
+constexpr int BIAS_TILE_ELEMS = 2048;  // 4 KB of 16-bit values per (query block, key tile)
+
+int64_t bias_tile_count(int64_t B, int64_t H, int64_t N) {
+  const int64_t nqb = (N + 31) / 32, ntiles = (N + KT - 1) / KT;
+  return B * H * nqb * ntiles;
+}
+
 template <typename T>
-__device__ __forceinline__ void load_bias_row(BiasFragR<T>& bf, const T* brow, int kbase, int N, int g) {
-  if (kbase + KT <= N) {
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) bf.f[sub][t] = load8(brow + kbase + sub * 32 + 16 * t + 8 * g);
-    return;
-  }
+__device__ __forceinline__ void load_bias_tile(BiasFragR<T>& bf, const T* tile) {
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int key = kbase + sub * 32 + 16 * t + 8 * g;
-      bf.f[sub][t] = load8_bias_tail<T>(brow, key, N);
-    }
+    for (int t = 0; t < 2; ++t) bf.f[sub][t] = load8(tile + (2 * sub + t) * 512);
+}
+
+// One thread per 16-byte fragment chunk; chunk id
+// ((((b H + h) nqb + qblock) ntiles + tile) 4 + f) 64 + lane. Any bias strides.
+template <typename T>
+__global__ __launch_bounds__(256) void bias_tiles_kernel(const gnn_triattn_args a, T* tiles, int64_t nchunks) {
+  const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (id >= nchunks) return;
+  const int N = (int)a.N, H = (int)a.H;
+  const int nqb = (N + 31) / 32, ntiles = (N + KT - 1) / KT;
+  const int lane = (int)(id & 63), f = (int)((id >> 6) & 3);
+  int64_t rest = id >> 8;
+  const int t = (int)(rest % ntiles);
+  rest /= ntiles;
+  const int qb = (int)(rest % nqb);
+  rest /= nqb;
+  const int h = (int)(rest % H);
+  const int64_t b = rest / H;
+  const int q = qb * 32 + (lane & 31);
+  const int key0 = t * KT + (f >> 1) * 32 + 16 * (f & 1) + 8 * (lane >> 5);
+  const T* row = (const T*)a.bias + b * a.bias_stride[0] + h * a.bias_stride[1] + (int64_t)min(q, N - 1) * a.bias_stride[2];
+  typename TypeOps<T>::V8 v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int key = key0 + e;
+    v[e] = (q < N && key < N) ? row[(int64_t)key * a.bias_stride[3]] : TypeOps<T>::from_f32(0.f);
+  }
+  store8(tiles + id * 8, v);
 }
 
 __device__ __forceinline__ float rowsum_add_r(const bf16x8& v, float acc) {
@@ -324,12 +357,8 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
     // The first tiles' LDS reads are the same for every query block; keeping the compiler
     // from hoisting them out of this loop keeps their registers free for the key loop.
     asm volatile("" : "+v"(koff[0]), "+v"(koff[1]), "+v"(tr_off));
-    // N as this block sees it, opaque to the compiler: otherwise the tail-mask compares of the
-    // first tile's bias load are hoisted out of the loop as live 64-bit lane masks
-    int Nq = N;
-    asm volatile("" : "+s"(Nq));
     const int myq = qblk * 32 + l32;
-    const bool qok = myq < Nq;
+    const bool qok = myq < N;
     V8 qf[2];
     {
       const T* qp = (const T*)a.q + b * a.q_stride[0] + s * a.q_stride[1] + h * a.q_stride[3] +
@@ -345,9 +374,9 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
         }
       }
     }
-    const T* brow = HAS_BIAS ? (const T*)a.bias + b * a.bias_stride[0] + h * a.bias_stride[1] +
-                                   (int64_t)(qok ? myq : 0) * a.bias_stride[2]
-                             : nullptr;
+    // this block's bias tiles (fragment order, see bias_tiles_kernel) and this lane's chunk
+    const T* btile = HAS_BIAS ? (const T*)a.workspace + (((int64_t)b * H + h) * nqb + qblk) * ntiles * BIAS_TILE_ELEMS + lane * 8
+                              : nullptr;
     f32x16 o;
     float m, lsum, mx;
     BiasFragR<T> bb;
@@ -463,25 +492,25 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
       mx = -INFINITY;
       if (full) {
         // no masked key: tiles in order; only the last one can hold keys past N
-        const bool tail = Nq % KT != 0;
-        if constexpr (HAS_BIAS) load_bias_row<T>(bb, brow, 0, Nq, g);
+        const bool tail = N % KT != 0;
+        if constexpr (HAS_BIAS) load_bias_tile<T>(bb, btile);
         for (int t = 0; t < ntiles; ++t) {
           f32x16 sc[2];
           ROW_PRIO_HI();
           qk(sc, t, tail && t == ntiles - 1);
           ROW_PRIO_LO();
-          if (HAS_BIAS && t + 1 < ntiles) load_bias_row<T>(bb, brow, (t + 1) * KT, Nq, g);
+          if (HAS_BIAS && t + 1 < ntiles) load_bias_tile<T>(bb, btile + (t + 1) * BIAS_TILE_ELEMS);
           softmax_pv(sc, t, t == 0, per_tile);
         }
       } else {
-        if constexpr (HAS_BIAS) load_bias_row<T>(bb, brow, hdr.tile_list[0] * KT, Nq, g);
+        if constexpr (HAS_BIAS) load_bias_tile<T>(bb, btile + hdr.tile_list[0] * BIAS_TILE_ELEMS);
         for (int it = 0; it < nrun; ++it) {
           const int t = hdr.tile_list[it];
           f32x16 sc[2];
           ROW_PRIO_HI();
           qk(sc, t, hdr.tile_live[t] != ~0ull);
           ROW_PRIO_LO();
-          if (HAS_BIAS && it + 1 < nrun) load_bias_row<T>(bb, brow, hdr.tile_list[it + 1] * KT, Nq, g);
+          if (HAS_BIAS && it + 1 < nrun) load_bias_tile<T>(bb, btile + hdr.tile_list[it + 1] * BIAS_TILE_ELEMS);
           softmax_pv(sc, t, it == 0, per_tile);
         }
       }
@@ -512,6 +541,11 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
 
 template <typename T, bool HAS_BIAS>
 int launch_row(const gnn_triattn_args& a, hipStream_t stream) {
+  if (HAS_BIAS) {
+    const int64_t nchunks = bias_tile_count(a.B, a.H, a.N) * 256;
+    hipLaunchKernelGGL((bias_tiles_kernel<T>), dim3((uint32_t)((nchunks + 255) / 256)), dim3(256), 0, stream, a,
+                       (T*)a.workspace, nchunks);
+  }
   const size_t smem = row_smem_bytes(a.N);
   const void* fn = (const void*)triattn_row_kernel<T, HAS_BIAS>;
   if (smem > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
@@ -521,6 +555,10 @@ int launch_row(const gnn_triattn_args& a, hipStream_t stream) {
 }
 
 }  // namespace
+
+size_t triattn_row_workspace_bytes(const gnn_triattn_args& a) {
+  return a.bias ? (size_t)bias_tile_count(a.B, a.H, a.N) * BIAS_TILE_ELEMS * 2 : 0;
+}
 
 bool triattn_row_applicable(const gnn_triattn_args& a) {
   return (a.dtype == GNN_BF16 || a.dtype == GNN_F16) && a.D <= 32 && a.N <= GNN_ROW_MAX_N && a.N >= 1 &&

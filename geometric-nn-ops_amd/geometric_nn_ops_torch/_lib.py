@@ -52,6 +52,8 @@ class TriAttnArgs(ctypes.Structure):
         ("mask_value", ctypes.c_float),
         ("dtype", ctypes.c_int32),
         ("precision", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -193,6 +195,7 @@ class GateBwdArgs(ctypes.Structure):
 # Every symbol include/gnn_triangle.h declares, with its ctypes signature.
 _SIGNATURES = {
     "gnn_triattn_fwd": (ctypes.c_int, [ctypes.POINTER(TriAttnArgs), ctypes.c_void_p]),
+    "gnn_triattn_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(TriAttnArgs)]),
     "gnn_triattn_bwd": (ctypes.c_int, [ctypes.POINTER(TriAttnBwdArgs), ctypes.c_void_p]),
     "gnn_trimul_workspace_bytes": (
         ctypes.c_size_t,

@@ -18,6 +18,7 @@ from .._masking import rounded_mask_value
 
 MAX_HEAD_DIM = 128  # the kernel's largest head-dim tile
 MAX_N_RES = 32768
+ROW_MAX_N = 1024  # 16-bit inputs with D <= 32 up to this N_res run the row-resident kernel
 
 
 def supports(q: torch.Tensor) -> bool:
@@ -43,8 +44,10 @@ def _prepare(t: torch.Tensor) -> torch.Tensor:
 
 
 def _prepare_bias(bias: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-    """``[B, 1, H, N, N]`` bias in ``dtype`` with unit key stride, a query pitch that is a
-    multiple of 8 elements and a 16-byte aligned base (zero padding past N)."""
+    """``[B, 1, H, N, N]`` bias in ``dtype``. The 16-bit row kernel reads any strides (its
+    pre-pass rewrites the bias in fragment order); the tiled kernel needs unit key stride, a
+    query pitch that is a multiple of 8 elements and a 16-byte aligned base, so such views
+    are copied with the pitch padded (zeros past N)."""
     bias = bias.to(dtype)
     if bias.stride(-1) == 1 and bias.stride(-2) % 8 == 0 and bias.data_ptr() % 16 == 0:
         return bias
@@ -53,6 +56,17 @@ def _prepare_bias(bias: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     padded = torch.zeros((B, 1, H, N, pitch), device=bias.device, dtype=bias.dtype)
     padded[..., :N] = bias
     return padded[..., :N]
+
+
+def workspace_for(args, device) -> torch.Tensor | None:
+    """Sets ``args.workspace`` to a fresh scratch tensor of the size the library asks for
+    (``None`` when the call needs none); the caller keeps the tensor alive over the launch."""
+    nbytes = _lib.load().gnn_triattn_workspace_bytes(ctypes.byref(args))
+    if nbytes == 0:
+        return None
+    ws = torch.empty(nbytes, device=device, dtype=torch.uint8)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
+    return ws
 
 
 def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=False, use_exp2=False,
@@ -95,8 +109,9 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
     args.k_stride = _lib.I64x4(*kk.stride()[:4])
     args.v_stride = _lib.I64x4(*vk.stride()[:4])
     args.o_stride = _lib.I64x4(*o.stride()[:4])
+    row_kernel = q.dtype in (torch.bfloat16, torch.float16) and Dp <= 32 and N <= ROW_MAX_N
     if bias is not None:
-        bias = _prepare_bias(bias, q.dtype)
+        bias = bias.to(q.dtype) if row_kernel else _prepare_bias(bias, q.dtype)
         args.bias = bias.data_ptr()
         args.bias_stride = _lib.I64x4(bias.stride(0), bias.stride(2), bias.stride(3), bias.stride(4))
     if mask is not None:
@@ -116,9 +131,11 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
     precision = _precision.matmul_precision(fp32_operands=q.dtype == torch.float32)
     args.precision = _lib.PRECISION_CODE[precision]
 
+    ws = workspace_for(args, q.device)
     with torch.cuda.device(q.device):
         rc = lib.gnn_triattn_fwd(ctypes.byref(args), ctypes.c_void_p(_lib.stream_handle(q.device)))
     _lib.check(rc, "gnn_triattn_fwd")
+    del ws
     if Dp != D:
         o = o[..., :D].contiguous()
     return o

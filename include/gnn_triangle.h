@@ -85,16 +85,26 @@ typedef struct gnn_triattn_args {
   int64_t k_stride[4];
   int64_t v_stride[4];
   int64_t o_stride[4];
-  int64_t bias_stride[4]; /* b, h, i, j (j stride must be 1) */
+  int64_t bias_stride[4]; /* b, h, i, j (any strides for 16-bit inputs with D <= 32 and
+                             N <= 1024; otherwise j stride 1, i stride a multiple of 8) */
   int64_t mask_stride[3]; /* b, s, j */
   float scale;
   float mask_value;
   int32_t dtype;     /* enum gnn_dtype, shared by q, k, v, o, bias */
   int32_t precision; /* enum gnn_precision */
+  void* workspace;   /* caller scratch of gnn_triattn_workspace_bytes(args) bytes (NULL when 0) */
+  size_t workspace_bytes;
 } gnn_triattn_args;
 
 /* Replaces the forward launch of EvoformerAttention (triangle_attention.py:1091-1276). */
 int gnn_triattn_fwd(const gnn_triattn_args* args, void* stream);
+
+/* Bytes of device scratch gnn_triattn_fwd needs for these arguments (shapes, dtype, bias
+ * present): the pair bias rewritten in the order the 16-bit row-resident kernel reads it
+ * (B * H * ceil(N/32) * ceil(N/64) * 4 KB), 0 for calls that need none. No reference
+ * counterpart: the reference's launcher reads the bias in place (triangle_attention.py:
+ * 1231-1262). The scratch is only used during the call. */
+size_t gnn_triattn_workspace_bytes(const gnn_triattn_args* args);
 
 /* ---------------------------------------------------------------------------------
  * Triangle attention backward (bf16 / fp16, head dim <= 32).

@@ -119,6 +119,32 @@ def test_triattn_argument_errors():
         _lib.check(_lib.GNN_ERR_ARG, "gnn_triattn_fwd")
 
 
+def test_triattn_workspace():
+    """The 16-bit row path with a pair bias needs caller scratch for the bias in fragment
+    order (4 KB per 32-query x 64-key tile per (batch, head)); other calls need none, and a
+    missing or short workspace is refused before any launch."""
+    lib = _lib.load()
+    a = _lib.TriAttnArgs()
+    a.q = a.k = a.v = a.o = 4096
+    a.B, a.S, a.N, a.H, a.D = 2, 3, 100, 4, 32
+    for st in ("q_stride", "k_stride", "v_stride", "o_stride"):
+        setattr(a, st, _lib.I64x4(3 * 100 * 128, 100 * 128, 128, 32))
+    a.dtype = _lib.GNN_BF16
+    assert lib.gnn_triattn_workspace_bytes(ctypes.byref(a)) == 0  # no bias
+    a.bias = 8192
+    a.bias_stride = _lib.I64x4(4 * 100 * 100, 100 * 100, 1, 100)  # a transposed view is fine here
+    need = 2 * 4 * 4 * 2 * 4096  # B * H * ceil(100/32) * ceil(100/64) tiles of 4 KB
+    assert lib.gnn_triattn_workspace_bytes(ctypes.byref(a)) == need
+    assert lib.gnn_triattn_fwd(ctypes.byref(a), None) == _lib.GNN_ERR_WORKSPACE
+    a.workspace, a.workspace_bytes = 1 << 20, need - 1
+    assert lib.gnn_triattn_fwd(ctypes.byref(a), None) == _lib.GNN_ERR_WORKSPACE
+    assert b"workspace" in lib.gnn_last_error()
+    a.dtype = _lib.GNN_F32  # the tiled kernel reads the bias in place
+    assert lib.gnn_triattn_workspace_bytes(ctypes.byref(a)) == 0
+    assert lib.gnn_triattn_fwd(ctypes.byref(a), None) == _lib.GNN_ERR_ARG  # ... with unit key stride
+    assert b"unit key stride" in lib.gnn_last_error()
+
+
 def test_trimul_argument_errors_and_workspace():
     lib = _lib.load()
     off = (ctypes.c_size_t * 4)()
