@@ -70,6 +70,12 @@ constexpr float RESCALE_THRESHOLD = 8.0f / LOG2E;
 #ifndef GNN_ROW_MAX_N
 #define GNN_ROW_MAX_N 1024
 #endif
+#ifndef GNN_ROW_KPREFETCH  // next tile's K fragments read from LDS during the current softmax
+#define GNN_ROW_KPREFETCH 0   // measured slower: the extra live fragments spill at 128 VGPRs
+#endif
+#ifndef GNN_ROW_VPREFETCH  // a 32-key half's V^T fragments read before its exponentials
+#define GNN_ROW_VPREFETCH 0   // measured neutral
+#endif
 #ifndef GNN_ROW_HEADS_FIRST_BYTES
 #define GNN_ROW_HEADS_FIRST_BYTES (8 << 20)
 #endif
@@ -128,15 +134,18 @@ __device__ __forceinline__ void load_bias_tile(BiasFragR<T>& bf, const T* tile) 
     for (int t = 0; t < 2; ++t) bf.f[sub][t] = load8(tile + (2 * sub + t) * 512);
 }
 
-// One thread per 16-byte fragment chunk; chunk id
-// ((((b H + h) nqb + qblock) ntiles + tile) 4 + f) 64 + lane. Any bias strides.
+// One thread per 16-byte chunk of the caller's bias, taken in row-major order within each
+// 32 x 64 tile (8 consecutive threads read one 128-byte query row) and written to its slot in
+// fragment order: chunk c = key / 8 of query row r goes to fragment f = 2 (c / 4) + (c / 2) % 2,
+// lane r + 32 (c % 2). Tile id ((b H + h) nqb + query block) ntiles + key tile. Any strides;
+// 16-byte loads where the row chunk is unit-stride, aligned and inside N.
 template <typename T>
 __global__ __launch_bounds__(256) void bias_tiles_kernel(const gnn_triattn_args a, T* tiles, int64_t nchunks) {
   const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (id >= nchunks) return;
   const int N = (int)a.N, H = (int)a.H;
   const int nqb = (N + 31) / 32, ntiles = (N + KT - 1) / KT;
-  const int lane = (int)(id & 63), f = (int)((id >> 6) & 3);
+  const int i = (int)(id & 255), r = i >> 3, c = i & 7;
   int64_t rest = id >> 8;
   const int t = (int)(rest % ntiles);
   rest /= ntiles;
@@ -144,16 +153,21 @@ __global__ __launch_bounds__(256) void bias_tiles_kernel(const gnn_triattn_args 
   rest /= nqb;
   const int h = (int)(rest % H);
   const int64_t b = rest / H;
-  const int q = qb * 32 + (lane & 31);
-  const int key0 = t * KT + (f >> 1) * 32 + 16 * (f & 1) + 8 * (lane >> 5);
-  const T* row = (const T*)a.bias + b * a.bias_stride[0] + h * a.bias_stride[1] + (int64_t)min(q, N - 1) * a.bias_stride[2];
-  typename TypeOps<T>::V8 v;
+  const int q = qb * 32 + r, key0 = t * KT + 8 * c;
+  typename TypeOps<T>::V8 v = zero8<T>();
+  if (q < N) {
+    const T* p = (const T*)a.bias + b * a.bias_stride[0] + h * a.bias_stride[1] + (int64_t)q * a.bias_stride[2] +
+                 (int64_t)key0 * a.bias_stride[3];
+    if (a.bias_stride[3] == 1 && key0 + 8 <= N && ((uintptr_t)p & 15) == 0) {
+      v = load8(p);
+    } else {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int key = key0 + e;
-    v[e] = (q < N && key < N) ? row[(int64_t)key * a.bias_stride[3]] : TypeOps<T>::from_f32(0.f);
+      for (int e = 0; e < 8; ++e)
+        if (key0 + e < N) v[e] = p[(int64_t)e * a.bias_stride[3]];
+    }
   }
-  store8(tiles + id * 8, v);
+  const int f = 2 * (c >> 2) + ((c >> 1) & 1), lane = r + 32 * (c & 1);
+  store8(tiles + (((id >> 8) * 4 + f) * 64 + lane) * 8, v);
 }
 
 __device__ __forceinline__ float rowsum_add_r(const bf16x8& v, float acc) {
@@ -383,8 +397,19 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
 
     // S^T (+ bias, + key mask term on partial tiles) of tile t into acc: acc[sub][i] is key
     // t*64 + sub*32 + 8*(i/4) + 4g + i%4.
-    auto qk = [&](f32x16 (&acc)[2], int t, bool partial) {
+    // K fragments of tile t (k-step kk of 32-key half sub)
+    auto load_k = [&](V8 (&kf)[2][2], int t) {
       const unsigned char* kt = ks + t * TILE_BYTES;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) kf[kk][sub] = load8((const T*)(kt + sub * 32 * ROW_BYTES + koff[kk]));
+    };
+    V8 kf[2][2];
+    auto qk = [&](f32x16 (&acc)[2], int t, bool partial) {
+#if !GNN_ROW_KPREFETCH
+      load_k(kf, t);
+#endif
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
@@ -392,8 +417,7 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-          Mma<T, PREC_NATIVE>::step(acc[sub], load8((const T*)(kt + sub * 32 * ROW_BYTES + koff[kk])), qf[kk]);
+        for (int sub = 0; sub < 2; ++sub) Mma<T, PREC_NATIVE>::step(acc[sub], kf[kk][sub], qf[kk]);
       if constexpr (HAS_BIAS) {
 #pragma unroll
         for (int t2 = 0; t2 < 2; ++t2)
@@ -448,6 +472,21 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
       const unsigned char* vt = vs + t * TILE_BYTES;
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
+        V8 vf[2];
+        auto load_v = [&](int kk) {
+          const unsigned char* vb = vt + (sub * 32 + 16 * kk) * ROW_BYTES + tr_off;
+          const V4 lo = tr_read4_r<T>(vb);
+          const V4 hi = tr_read4_r<T>(vb + 8 * ROW_BYTES);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            vf[kk][e] = lo[e];
+            vf[kk][e + 4] = hi[e];
+          }
+        };
+        if (GNN_ROW_VPREFETCH) {
+          load_v(0);
+          load_v(1);
+        }
         if (!dead) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) sc[sub][i] = fast_exp2(__builtin_fmaf(sc[sub][i], LOG2E, nm));
@@ -461,16 +500,8 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
                      sc[sub][8 * kk + 4], sc[sub][8 * kk + 5], sc[sub][8 * kk + 6], sc[sub][8 * kk + 7]};
           const V8 pf = TypeOps<T>::from_f32(x);
           lsum = rowsum_add_r(pf, lsum);
-          const unsigned char* vb = vt + (sub * 32 + 16 * kk) * ROW_BYTES + tr_off;
-          const V4 lo = tr_read4_r<T>(vb);
-          const V4 hi = tr_read4_r<T>(vb + 8 * ROW_BYTES);
-          V8 vf;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            vf[e] = lo[e];
-            vf[e + 4] = hi[e];
-          }
-          Mma<T, PREC_NATIVE>::step(o, vf, pf);
+          if (!GNN_ROW_VPREFETCH) load_v(kk);
+          Mma<T, PREC_NATIVE>::step(o, vf[kk], pf);
         }
       }
     };
@@ -494,22 +525,26 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
         // no masked key: tiles in order; only the last one can hold keys past N
         const bool tail = N % KT != 0;
         if constexpr (HAS_BIAS) load_bias_tile<T>(bb, btile);
+        if (GNN_ROW_KPREFETCH) load_k(kf, 0);
         for (int t = 0; t < ntiles; ++t) {
           f32x16 sc[2];
           ROW_PRIO_HI();
           qk(sc, t, tail && t == ntiles - 1);
           ROW_PRIO_LO();
+          if (GNN_ROW_KPREFETCH && t + 1 < ntiles) load_k(kf, t + 1);  // in flight during the softmax
           if (HAS_BIAS && t + 1 < ntiles) load_bias_tile<T>(bb, btile + (t + 1) * BIAS_TILE_ELEMS);
           softmax_pv(sc, t, t == 0, per_tile);
         }
       } else {
         if constexpr (HAS_BIAS) load_bias_tile<T>(bb, btile + hdr.tile_list[0] * BIAS_TILE_ELEMS);
+        if (GNN_ROW_KPREFETCH) load_k(kf, hdr.tile_list[0]);
         for (int it = 0; it < nrun; ++it) {
           const int t = hdr.tile_list[it];
           f32x16 sc[2];
           ROW_PRIO_HI();
           qk(sc, t, hdr.tile_live[t] != ~0ull);
           ROW_PRIO_LO();
+          if (GNN_ROW_KPREFETCH && it + 1 < nrun) load_k(kf, hdr.tile_list[it + 1]);
           if (HAS_BIAS && it + 1 < nrun) load_bias_tile<T>(bb, btile + hdr.tile_list[it + 1] * BIAS_TILE_ELEMS);
           softmax_pv(sc, t, it == 0, per_tile);
         }
