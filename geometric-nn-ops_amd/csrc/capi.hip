@@ -36,7 +36,9 @@ static int hip_status(hipError_t e, const char* who) {
 
 static bool aligned(const void* p, size_t n) { return ((uintptr_t)p % n) == 0; }
 
-static int check_triattn(const gnn_triattn_args& a) {
+// caller_workspace: the caller provides the scratch (gnn_triattn_fwd); false for the entry
+// point whose scratch is the library's static array.
+static int check_triattn(const gnn_triattn_args& a, bool caller_workspace = true) {
   if (!a.q || !a.k || !a.v || !a.o)
     return set_error(GNN_ERR_ARG, "triangle_attention: q, k, v and o are required");
   if (a.B < 1 || a.S < 1 || a.N < 1 || a.H < 1 || a.D < 1)
@@ -61,7 +63,7 @@ static int check_triattn(const gnn_triattn_args& a) {
                        "of 8 and 16-byte alignment");
   }
   const size_t need = triattn_row_applicable(a) ? triattn_row_workspace_bytes(a) : 0;
-  if (need && (!a.workspace || a.workspace_bytes < need || !aligned(a.workspace, 16)))
+  if (caller_workspace && need && (!a.workspace || a.workspace_bytes < need || !aligned(a.workspace, 16)))
     return set_error(GNN_ERR_WORKSPACE,
                      "triangle_attention: workspace missing, smaller than gnn_triattn_workspace_bytes() or "
                      "not 16-byte aligned");
@@ -80,6 +82,14 @@ int gnn_triattn_fwd(const gnn_triattn_args* args, void* stream) {
   int rc = triattn_fwd(*args, (hipStream_t)stream);
   if (rc < 0) return rc;
   return hip_status((hipError_t)rc, "triangle_attention");
+}
+
+int gnn_triattn_fwd_noalloc(const gnn_triattn_args* args, void* stream) {
+  if (!args) return set_error(GNN_ERR_ARG, "triangle_attention: args is NULL");
+  if (int rc = check_triattn(*args, false)) return rc;
+  int rc = triattn_fwd_noalloc(*args, (hipStream_t)stream);
+  if (rc < 0) return rc;
+  return hip_status((hipError_t)rc, "triangle_attention (no-alloc)");
 }
 
 size_t gnn_triattn_workspace_bytes(const gnn_triattn_args* args) {

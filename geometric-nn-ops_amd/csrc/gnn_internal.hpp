@@ -21,6 +21,10 @@ int triattn_bwd(const gnn_triattn_bwd_args& a, hipStream_t stream);
 // K and V staged in LDS, no barrier in the key loop.
 bool triattn_row_applicable(const gnn_triattn_args& a);
 size_t triattn_row_workspace_bytes(const gnn_triattn_args& a);
+
+// The attention forward with its scratch in a static device array (no allocation anywhere).
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)16 << 20;
+int triattn_fwd_noalloc(const gnn_triattn_args& a, hipStream_t stream);
 int triattn_row_fwd(const gnn_triattn_args& a, hipStream_t stream);
 
 // Row-resident attention backward for dq (with Delta) and dk / dv (16-bit inputs, head dim 32,

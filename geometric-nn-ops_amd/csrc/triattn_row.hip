@@ -45,6 +45,8 @@
 // maximum. exp2 with the folded FMA, v_dot2 row sums on the rounded probabilities, and rows
 // whose keys are all masked reproducing mean(v) (the sentinel swamps the logits; subtract
 // first) are as in the tiled kernel, which gives the same results to rounding.
+#include <mutex>
+
 #include "gnn_common.hpp"
 #include "gnn_internal.hpp"
 
@@ -603,6 +605,47 @@ bool triattn_row_applicable(const gnn_triattn_args& a) {
 int triattn_row_fwd(const gnn_triattn_args& a, hipStream_t stream) {
   if (a.dtype == GNN_BF16) return a.bias ? launch_row<bf16, true>(a, stream) : launch_row<bf16, false>(a, stream);
   return a.bias ? launch_row<f16, true>(a, stream) : launch_row<f16, false>(a, stream);
+}
+
+// ---- allocation-free forward: the bias tiles go to a static device array of the library.
+// Each device that loads the library holds its own copy of `scratch` until the process ends.
+// In host code the array's name is not a device address: the address is taken once per
+// device with hipGetSymbolAddress (with that device current) and only that pointer is passed
+// to kernels. Calls on one device share the array, so calls that overlap on one device race;
+// the pre-pass rewrites every byte a call reads, so no state needs clearing between calls.
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[MAX_DEVICES];
+}  // namespace
+
+int triattn_fwd_noalloc(const gnn_triattn_args& a, hipStream_t stream) {
+  const size_t need = triattn_row_applicable(a) ? triattn_row_workspace_bytes(a) : 0;
+  if (need > NOALLOC_SCRATCH_BYTES)
+    return set_error(GNN_ERR_UNSUPPORTED,
+                     "triangle_attention (no-alloc): the pair bias in fragment order needs more than the 16 MiB "
+                     "static scratch (B * H * ceil(N/32) * ceil(N/64) * 4 KB); use gnn_triattn_fwd with a workspace");
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
+    return set_error(GNN_ERR_ARG, "triangle_attention (no-alloc): no current HIP device");
+  void* ptr;
+  {
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_ptr[dev]) {
+      void* p = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p)
+        return set_error(GNN_ERR_ARG, "triangle_attention (no-alloc): hipGetSymbolAddress(scratch) failed");
+      scratch_ptr[dev] = p;
+    }
+    ptr = scratch_ptr[dev];
+  }
+  gnn_triattn_args b = a;
+  b.workspace = ptr;
+  b.workspace_bytes = NOALLOC_SCRATCH_BYTES;
+  return triattn_fwd(b, stream);
 }
 
 }  // namespace gnn

@@ -196,6 +196,7 @@ class GateBwdArgs(ctypes.Structure):
 _SIGNATURES = {
     "gnn_triattn_fwd": (ctypes.c_int, [ctypes.POINTER(TriAttnArgs), ctypes.c_void_p]),
     "gnn_triattn_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(TriAttnArgs)]),
+    "gnn_triattn_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(TriAttnArgs), ctypes.c_void_p]),
     "gnn_triattn_bwd": (ctypes.c_int, [ctypes.POINTER(TriAttnBwdArgs), ctypes.c_void_p]),
     "gnn_trimul_workspace_bytes": (
         ctypes.c_size_t,

@@ -106,6 +106,16 @@ int gnn_triattn_fwd(const gnn_triattn_args* args, void* stream);
  * 1231-1262). The scratch is only used during the call. */
 size_t gnn_triattn_workspace_bytes(const gnn_triattn_args* args);
 
+/* gnn_triattn_fwd without any allocation by the caller or the library: the scratch that
+ * gnn_triattn_workspace_bytes() would ask for lives in a static 16 MiB device array of the
+ * library instead (args->workspace is ignored). No counterpart in the reference; it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid it). Calls needing more scratch than 16 MiB (B * H * ceil(N/32) *
+ * ceil(N/64) * 4 KB, e.g. B * H > 16 at N_res = 1024) return GNN_ERR_UNSUPPORTED. Every
+ * call on one device shares that device's array: calls that overlap on one device (other
+ * streams or threads) race. */
+int gnn_triattn_fwd_noalloc(const gnn_triattn_args* args, void* stream);
+
 /* ---------------------------------------------------------------------------------
  * Triangle attention backward (bf16 / fp16, head dim <= 32).
  * Given the forward's inputs, its output o, the upstream gradient dout and the forward's

@@ -145,6 +145,23 @@ def test_triattn_workspace():
     assert b"unit key stride" in lib.gnn_last_error()
 
 
+def test_triattn_noalloc_rejects_calls_beyond_its_static_scratch():
+    """The allocation-free entry point refuses, before touching the device, a call whose bias
+    tiles exceed its 16 MiB array (here B * H * ceil(N/32) * ceil(N/64) * 4 KB = 32 MiB)."""
+    lib = _lib.load()
+    a = _lib.TriAttnArgs()
+    a.q = a.k = a.v = a.o = 4096
+    a.B, a.S, a.N, a.H, a.D = 1, 1, 1024, 16, 32
+    for st in ("q_stride", "k_stride", "v_stride", "o_stride"):
+        setattr(a, st, _lib.I64x4(1024 * 1024 * 16 * 32, 1024 * 16 * 32, 16 * 32, 32))
+    a.bias = 8192
+    a.bias_stride = _lib.I64x4(16 * 1024 * 1024, 1024 * 1024, 1024, 1)
+    a.dtype = _lib.GNN_BF16
+    assert lib.gnn_triattn_workspace_bytes(ctypes.byref(a)) == 32 << 20
+    assert lib.gnn_triattn_fwd_noalloc(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
+    assert b"16 MiB" in lib.gnn_last_error()
+
+
 def test_trimul_argument_errors_and_workspace():
     lib = _lib.load()
     off = (ctypes.c_size_t * 4)()
