@@ -198,6 +198,15 @@ __device__ __forceinline__ float max_nn(float a, float b) {
   asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
   return r;
 }
+// The compiler places the wait states an MFMA result needs before a VALU instruction reads it
+// (12 for a 32x32x16 MFMA) only in front of instructions it generates, not in front of inline
+// assembly. max3_nn / max_nn read the score accumulators straight after the QK^T MFMAs, so
+// this fence comes first: tied to the accumulators (it is placed after the MFMAs that write
+// them), it supplies 16 wait states. Without it the maxima sometimes saw accumulators still
+// being written, and the results changed from call to call in their last bits.
+__device__ __forceinline__ void mfma_result_fence(f32x16& a, f32x16& b) {
+  asm volatile("s_nop 7\n\ts_nop 7" : "+v"(a), "+v"(b));
+}
 
 // max / sum over the lane pair (l, l ^ 32) with gfx950's v_permlane32_swap (no LDS trip)
 __device__ __forceinline__ float pair_max_swap(float x) {
@@ -444,6 +453,7 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
     // accumulators rescaled when it grows past the threshold.
     auto softmax_pv = [&](f32x16 (&sc)[2], int t, bool first, bool per_tile) {
       if (first || per_tile) {
+        mfma_result_fence(sc[0], sc[1]);
         float m0 = max3_nn(sc[0][0], sc[0][1], sc[0][2]), m1 = max3_nn(sc[1][0], sc[1][1], sc[1][2]);
 #pragma unroll
         for (int i = 3; i < 15; i += 2) {

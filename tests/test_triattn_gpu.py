@@ -363,3 +363,31 @@ def test_bias_pitch_padding_does_not_reach_valid_keys(dtype, n):
         want = triangle_attention(t["q"], t["k"], t["v"], t["bias"].contiguous(), mask)
     assert torch.isfinite(got).all()
     torch.testing.assert_close(got, want, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize(("n", "with_mask", "with_bias"),
+                         [(64, True, False), (200, False, False), (200, True, False), (200, True, True)],
+                         ids=["n64_mask", "n200", "n200_mask", "n200_mask_bias"])
+def test_repeated_calls_are_bit_identical(n, with_mask, with_bias):
+    """The forward is deterministic: calls on the same inputs, with other kernels run in
+    between (which shifts the timing of the attention waves), return the same bits. Covers
+    tiles that start from the key mask term (masked keys, keys past N) with and without the
+    pair bias."""
+    from geometric_nn_ops_torch.triangle import triangle_attention, triangle_multiplicative_update
+    from helpers import pair_input, trimul_weights
+
+    B, S, H, D = 1, 2, 4, 32
+    t = attention_inputs(B, S, n, H, D, torch.bfloat16, seed=3, device=DEV)
+    bias = t["bias"] if with_bias else None
+    mask = key_mask(B, S, n, seed=4, device=DEV) if with_mask else None
+    x, m = pair_input(1, 256, 128, torch.bfloat16, seed=2, device=DEV)
+    w = trimul_weights(128, 128, torch.bfloat16, seed=3, device=DEV)
+    outs = []
+    with torch.no_grad():
+        for _ in range(6):
+            for _ in range(2):
+                triangle_multiplicative_update(x, "outgoing", m, **w)
+            outs.append(triangle_attention(t["q"], t["k"], t["v"], bias, mask))
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0]), int((o != outs[0]).sum())
