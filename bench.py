@@ -326,12 +326,12 @@ def main():
     flops["triattn_fwd"] = attn_flops(1, N, N, H, D)
     nbytes["triattn_fwd"] = attn_bytes(1, N, N, H, D, e)
     for direction in ("outgoing", "incoming"):
-        flops[f"trimul_proj_{direction}"] = 2.0 * M * C * (4 * CH + C)
-        nbytes[f"trimul_proj_{direction}"] = e * M * C + e * M + 2 * e * M * CH + e * M * C
+        flops[f"trimul_proj_{direction}"] = 2.0 * M * C * (4 * CH + C)  # p_in, g_in, output gate
+        nbytes[f"trimul_proj_{direction}"] = e * M * C + e * M + 2 * e * M * CH + e * M * C  # x, mask -> a, b, g
         flops[f"trimul_contract_{direction}"] = 2.0 * N**3 * CH
         nbytes[f"trimul_contract_{direction}"] = 3.0 * e * M * CH
-        flops[f"trimul_out_{direction}"] = 2.0 * M * CH * C
-        nbytes[f"trimul_out_{direction}"] = e * M * CH + 2.0 * e * M * C
+        flops[f"trimul_out_{direction}"] = 2.0 * M * CH * C  # p_out
+        nbytes[f"trimul_out_{direction}"] = e * M * CH + 2.0 * e * M * C  # o, g -> out
     per_kernel, kern_mean = {}, {}
     for name, fn in kernels:
         med, mean, reps = window_ms(fn, stream)

@@ -4,6 +4,12 @@ cueq lays q / k / v out as ``(B, N, H, S, D)``; the public op takes ``(B, N, S, 
 head and sequence axes are swapped as strided views (the kernel reads them without copies)
 and the output is swapped back. bias ``(B, 1, H, S, S)`` and mask ``(B, N, 1, 1, S)`` are
 layout-compatible. The result is always rank 5, as cueq returns it.
+
+``return_aux=True`` also returns cueq's auxiliary tensors, ``(out, lse, max)``: the natural-log
+log-sum-exp and the maximum of each query's logits (scaled q.k + bias + masked-key term), fp32,
+shaped ``(B, N, H, S, 1)``. The reference's shim refuses them because its Triton kernel does
+not expose them (hipequivariance_ops_torch/cuequivariance_ops_torch/triangle_attention.py:34-38);
+the HIP forward writes both.
 """
 
 import torch
@@ -15,15 +21,49 @@ from geometric_nn_ops_torch.triangle import triangle_attention as _triangle_atte
 CUEQ_TRIATTN_FALLBACK_THRESHOLD = 16
 
 
+def _rank5(t):
+    return t if t is None or t.dim() >= 5 else t.reshape((1,) * (5 - t.dim()) + tuple(t.shape))
+
+
+def _aux(q, k, v, bias, mask, scale):
+    """(lse, max) ``[B, N, H, S]`` of the logits, for canonical ``[B, N, S, H, D]`` q / k / v."""
+    from geometric_nn_ops_torch.triangle._kernels import triangle_attention as hip
+    from geometric_nn_ops_torch.triangle._masking import masked_key_bias
+
+    B, Nseq, S, H, D = q.shape
+    if bias is not None:
+        bias = (bias.unsqueeze(-4) if bias.dim() == 4 else bias).broadcast_to(B, 1, H, S, S)
+    if mask is not None:
+        mask = mask.broadcast_to(B, Nseq, 1, 1, S)
+    if q.is_cuda and q.dtype in (torch.bfloat16, torch.float16, torch.float32) and hip.supports(q):
+        lse = torch.empty((B, Nseq, H, S), device=q.device, dtype=torch.float32)
+        mx = torch.empty_like(lse)
+        with torch.no_grad():
+            hip.triangle_attention_hip(q.detach(), k.detach(), v.detach(), None if bias is None else bias.detach(),
+                                       mask, scale, lse=lse, row_max=mx)
+        return lse, mx
+    # other tensors: the logits in fp32 (fp64 stays fp64), as the torch path computes them
+    ct = torch.float64 if q.dtype == torch.float64 else torch.float32
+    scale = D ** -0.5 if scale is None else scale
+    with torch.no_grad():
+        logits = (q.to(ct).transpose(-2, -3) * scale) @ k.to(ct).transpose(-2, -3).transpose(-1, -2)
+        if bias is not None:
+            logits = logits + bias.to(ct)
+        if mask is not None:
+            logits = logits + masked_key_bias(mask, q.dtype).to(ct)
+        return torch.logsumexp(logits, -1).float(), logits.amax(-1).float()
+
+
 def triangle_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bias: torch.Tensor,
                        mask: torch.Tensor | None = None, scale: float | None = None,
                        return_aux: bool = False):
-    if return_aux:
-        raise NotImplementedError(
-            "cuequivariance_ops_torch shim: triangle_attention(return_aux=True) is not supported")
     swap = lambda t: t.transpose(-2, -3)  # noqa: E731
-    out = swap(_triangle_attention(swap(q), swap(k), swap(v), bias,
-                                   None if mask is None else mask.bool(), scale))
-    if out.dim() < 5:
-        out = out.reshape((1,) * (5 - out.dim()) + tuple(out.shape))
-    return out
+    mask = None if mask is None else mask.bool()
+    out = _rank5(swap(_triangle_attention(swap(q), swap(k), swap(v), bias, mask, scale)))
+    if not return_aux:
+        return out
+    q5, k5, v5 = (_rank5(swap(t)) for t in (q, k, v))
+    bias5 = None if bias is None else (bias if bias.dim() >= 4 else _rank5(bias))
+    mask5 = None if mask is None else _rank5(mask)
+    lse, mx = _aux(q5, k5, v5, bias5, mask5, scale)
+    return out, lse.unsqueeze(-1), mx.unsqueeze(-1)

@@ -109,6 +109,38 @@ def triangle_attention(q, k, v, bias=None, mask=None, scale=None, *, dtype=np.fl
     return out
 
 
+def triangle_attention_lse_max(q, k, bias=None, mask=None, scale=None, *, mask_value=None,
+                               dtype=np.float64):
+    """Per-query natural-log log-sum-exp and maximum of triangle_attention's logits, each
+    ``[B, N_seq, H, N_res]``: the auxiliary outputs of cueq's triangle_attention(return_aux)
+    (the reference's shim refuses them, hipequivariance_ops_torch/cuequivariance_ops_torch/
+    triangle_attention.py:34-38). Masked keys get ``mask_value`` (default: the dtype's
+    sentinel, as in ``triangle_attention``)."""
+    q = np.asarray(q, dtype=dtype)
+    k = np.asarray(k, dtype=dtype)
+    B, S, N, H, D = q.shape
+    if scale is None:
+        scale = D ** -0.5
+    qs = np.transpose(q, (0, 1, 3, 2, 4)) * dtype(scale)
+    ks = np.transpose(k, (0, 1, 3, 2, 4))
+    logits = qs @ np.swapaxes(ks, -1, -2)  # [B, S, H, N, N]
+    if bias is not None:
+        bias = np.asarray(bias, dtype=dtype)
+        if bias.ndim == 4:
+            bias = bias[:, None]
+        logits = logits + np.broadcast_to(bias, (B, 1, H, N, N))
+    if mask is not None:
+        mask = np.broadcast_to(np.asarray(mask, dtype=bool), (B, S, 1, 1, N))
+        if mask_value is None:
+            name = "float64" if dtype == np.float64 else "float32"
+            logits = logits + masked_key_bias(mask, dtype, name)
+        else:
+            logits = logits + np.where(mask, 0.0, mask_value).astype(dtype)
+    mx = logits.max(-1)
+    lse = mx + np.log(np.exp(logits - mx[..., None]).sum(-1))
+    return lse, mx
+
+
 # ------------------------------------------------------------- trimul (_reference/trimul.py)
 def is_outgoing(direction: str) -> bool:
     if direction not in DIRECTIONS:

@@ -84,6 +84,50 @@ def test_attention_matches_loops():
                                want, rtol=1e-12, atol=1e-12)
 
 
+def _lse_max_loops(q, k, bias, mask, scale, mask_value):
+    """Per-query log-sum-exp and maximum of the logits, with explicit Python loops."""
+    B, S, N, H, D = q.shape
+    lse = np.zeros((B, S, H, N))
+    mx = np.zeros((B, S, H, N))
+    for b in range(B):
+        for s in range(S):
+            for h in range(H):
+                for i in range(N):
+                    row = []
+                    for j in range(N):
+                        x = sum(q[b, s, i, h, d] * scale * k[b, s, j, h, d] for d in range(D))
+                        x += bias[b, 0, h, i, j] if bias is not None else 0.0
+                        x += 0.0 if mask is None or mask[b, s, 0, 0, j] else mask_value
+                        row.append(x)
+                    mx[b, s, h, i] = max(row)
+                    lse[b, s, h, i] = math.log(sum(math.exp(x) for x in row))
+    return lse, mx
+
+
+def test_lse_max_match_loops():
+    """Known answers too: one live key -> both equal its logit; equal logits -> lse = max +
+    log(number of keys)."""
+    r = RNG(7)
+    B, S, N, H, D = 1, 2, 6, 2, 3
+    q, k = (r.standard_normal((B, S, N, H, D)) for _ in range(2))
+    bias = r.standard_normal((B, 1, H, N, N))
+    mask = r.random((B, S, 1, 1, N)) < 0.7
+    mask[..., 1] = True
+    lse, mx = O.triangle_attention_lse_max(q, k, bias, mask, 0.4, mask_value=-30.0)
+    want = _lse_max_loops(q, k, bias, mask, 0.4, -30.0)
+    np.testing.assert_allclose(lse, want[0], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(mx, want[1], rtol=1e-12, atol=1e-12)
+    assert not np.allclose(lse, mx)
+    one = np.zeros((1, 1, 1, 1, N), dtype=bool)
+    one[..., 2] = True
+    lse1, mx1 = O.triangle_attention_lse_max(q[:, :1], k[:, :1], bias, one)
+    logit = np.einsum("bihd,bhd->bhi", q[:, 0] * 3 ** -0.5, k[:, 0, 2]) + bias[:, 0, :, :, 2]
+    np.testing.assert_allclose(mx1[:, 0], logit, rtol=1e-12)
+    np.testing.assert_allclose(lse1[:, 0], logit, rtol=1e-12)
+    lse0, mx0 = O.triangle_attention_lse_max(np.zeros((1, 1, N, H, D)), k[:, :1])
+    np.testing.assert_allclose(lse0, mx0 + math.log(N), rtol=1e-12)
+
+
 def test_attention_transposes_are_not_symmetric():
     """Swapping q and k (a transposed product) must change the result."""
     r = RNG(1)

@@ -79,8 +79,35 @@ def test_triangle_attention_layout_and_rank():
     qb, kb, vb, bb, mb = _cueq_attention_inputs(batch=False)
     out4 = cueq.triangle_attention(qb, kb, vb, bb[0], mask=mb)
     assert out4.dim() == 5 and out4.shape[0] == 1
-    with pytest.raises(NotImplementedError, match="return_aux"):
-        cueq.triangle_attention(q, k, v, bias, return_aux=True)
+
+
+def _aux_oracle(q, k, bias, mask, scale):
+    """cueq-layout (lse, max) from oracle.triangle_attention_lse_max (canonical layout)."""
+    import numpy as np
+
+    from oracle import triangle_oracle as O
+
+    sw = lambda t: np.swapaxes(t.double().cpu().numpy(), -2, -3)  # noqa: E731
+    lse, mx = O.triangle_attention_lse_max(sw(q), sw(k), bias.double().cpu().numpy(),
+                                           None if mask is None else mask.cpu().numpy(), scale)
+    return lse[..., None], mx[..., None]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64], ids=["fp32", "fp64"])
+def test_triangle_attention_return_aux_cpu(dtype):
+    """(out, lse, max) with lse / max the log-sum-exp and maximum of each query's logits,
+    (B, N, H, S, 1) fp32, against the oracle; out is the plain call's output."""
+    import numpy as np
+
+    q, k, v, bias, mask = (t if t.dtype == torch.bool else t.to(dtype) for t in _cueq_attention_inputs())
+    out, lse, mx = cueq.triangle_attention(q, k, v, bias, mask=mask, scale=0.3, return_aux=True)
+    assert torch.equal(out, cueq.triangle_attention(q, k, v, bias, mask=mask, scale=0.3))
+    B, N, H, S, _ = q.shape
+    assert lse.shape == mx.shape == (B, N, H, S, 1) and lse.dtype == mx.dtype == torch.float32
+    want_lse, want_mx = _aux_oracle(q, k, bias, mask, 0.3)
+    np.testing.assert_allclose(lse.numpy(), want_lse, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(mx.numpy(), want_mx, rtol=1e-5, atol=1e-5)
+    assert (lse >= mx).all()
 
 
 def test_trimul_precision_policy():
@@ -125,6 +152,29 @@ def test_attention_pair_bias_argument_mapping():
         cueq.attention_pair_bias(t["s"], t["q"], t["k"], t["v"], t["z"], **{**kw, "num_heads": 3})
     cached, _ = cueq.attention_pair_bias(t["s"], t["q"], t["k"], t["v"], pz, **kw, is_cached_z_proj=True)
     assert torch.equal(cached, out)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32], ids=["bf16", "fp16", "fp32"])
+def test_triangle_attention_return_aux_gpu(dtype):
+    """The HIP forward's lse and exact row maximum (row kernel for 16-bit, tiled kernel for
+    fp32) against the fp64 oracle; the output equals the plain call's, also under autograd."""
+    from helpers import assert_close_to_oracle, Tolerance
+
+    q, k, v, bias, mask = _cueq_attention_inputs("cuda", dtype)
+    with torch.no_grad():
+        out, lse, mx = cueq.triangle_attention(q, k, v, bias, mask=mask, scale=0.3, return_aux=True)
+        assert torch.equal(out, cueq.triangle_attention(q, k, v, bias, mask=mask, scale=0.3))
+    want_lse, want_mx = _aux_oracle(q, k, bias, mask, 0.3)
+    tol = Tolerance(1 - 1e-5, 5e-3 if dtype != torch.float32 else 1e-5)
+    assert_close_to_oracle("lse", lse, want_lse, tol)
+    assert_close_to_oracle("max", mx, want_mx, tol)
+    if dtype != torch.float32:
+        qg = q.detach().requires_grad_()
+        out2, lse2, _ = cueq.triangle_attention(qg, k, v, bias, mask=mask, scale=0.3, return_aux=True)
+        assert torch.equal(out2.detach(), out) and torch.equal(lse2, lse)
+        out2.float().sum().backward()
+        assert qg.grad is not None and torch.isfinite(qg.grad).all()
 
 
 @pytest.mark.gpu
