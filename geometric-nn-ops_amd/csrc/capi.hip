@@ -201,6 +201,46 @@ int gnn_trimul_gate_bwd(const gnn_gate_bwd_args* args, void* stream) {
   return hip_status((hipError_t)rc, "trimul_gate_bwd");
 }
 
+int gnn_trimul_contract_bwd(const gnn_trimul_contract_bwd_args* args, void* stream) {
+  if (!args) return set_error(GNN_ERR_ARG, "trimul_contract_bwd: args is NULL");
+  const gnn_trimul_contract_bwd_args& a = *args;
+  if (!a.a || !a.b || !a.do_i || !a.do_j || !a.da || !a.db)
+    return set_error(GNN_ERR_ARG, "trimul_contract_bwd: a, b, do_i, do_j, da and db are required");
+  if (a.dtype != GNN_BF16 && a.dtype != GNN_F16)
+    return set_error(GNN_ERR_UNSUPPORTED, "trimul_contract_bwd: 16-bit dtypes only");
+  if (a.planes < 1 || a.N < 1) return set_error(GNN_ERR_ARG, "trimul_contract_bwd: planes and N must be positive");
+  const void* ptr[6] = {a.a, a.b, a.do_i, a.do_j, a.da, a.db};
+  for (const void* p : ptr)
+    if (!aligned(p, 16)) return set_error(GNN_ERR_ARG, "trimul_contract_bwd: pointers must be 16-byte aligned");
+  if (a.planes * ((a.N + 127) / 128) * ((a.N + 255) / 256) >= ((int64_t)1 << 31) || a.N >= ((int64_t)1 << 30))
+    return set_error(GNN_ERR_UNSUPPORTED, "trimul_contract_bwd: grid too large");
+  int rc = trimul_contract_bwd(a, (hipStream_t)stream);
+  if (rc < 0) return rc;
+  return hip_status((hipError_t)rc, "trimul_contract_bwd");
+}
+
+int gnn_trimul_relayout(const gnn_trimul_relayout_args* args, void* stream) {
+  if (!args) return set_error(GNN_ERR_ARG, "trimul_relayout: args is NULL");
+  const gnn_trimul_relayout_args& a = *args;
+  if (!a.src || !a.dst) return set_error(GNN_ERR_ARG, "trimul_relayout: src and dst are required");
+  if (a.dtype != GNN_BF16 && a.dtype != GNN_F16)
+    return set_error(GNN_ERR_UNSUPPORTED, "trimul_relayout: 16-bit dtypes only");
+  if (a.mode != GNN_RELAYOUT_PLANES_TO_PIXELS && a.mode != GNN_RELAYOUT_PIXELS_TO_BLOCKED)
+    return set_error(GNN_ERR_ARG, "trimul_relayout: unknown mode");
+  if (a.B < 1 || a.N < 1 || a.Ch < 1) return set_error(GNN_ERR_ARG, "trimul_relayout: B, N and Ch must be positive");
+  if (a.Ch % 8 || a.src_ld % 8 || a.dst_ld % 8 || a.src_c0 % 8 || a.dst_c0 % 8 || a.src_c0 < 0 || a.dst_c0 < 0)
+    return set_error(GNN_ERR_ARG, "trimul_relayout: Ch, row pitches and channel offsets must be multiples of 8");
+  if (!aligned(a.src, 16) || !aligned(a.dst, 16))
+    return set_error(GNN_ERR_ARG, "trimul_relayout: src and dst must be 16-byte aligned");
+  const int64_t N8 = (a.N + 7) / 8 * 8;
+  if (a.mode == GNN_RELAYOUT_PLANES_TO_PIXELS ? (a.src_ld < N8 || a.dst_c0 + a.Ch > a.dst_ld)
+                                              : (a.src_c0 + a.Ch > a.src_ld))
+    return set_error(GNN_ERR_ARG, "trimul_relayout: a row pitch is too small for its rows");
+  int rc = trimul_relayout(a, (hipStream_t)stream);
+  if (rc < 0) return rc;
+  return hip_status((hipError_t)rc, "trimul_relayout");
+}
+
 const char* gnn_last_error(void) { return g_last_error.c_str(); }
 
 const char* gnn_version(void) { return "0.1.0 gfx950"; }

@@ -193,6 +193,45 @@ class GateBwdArgs(ctypes.Structure):
 
 
 # Every symbol include/gnn_triangle.h declares, with its ctypes signature.
+class TrimulContractBwdArgs(ctypes.Structure):
+    """Mirror of ``gnn_trimul_contract_bwd_args``."""
+
+    _fields_ = [
+        ("a", ctypes.c_void_p),
+        ("b", ctypes.c_void_p),
+        ("do_i", ctypes.c_void_p),
+        ("do_j", ctypes.c_void_p),
+        ("da", ctypes.c_void_p),
+        ("db", ctypes.c_void_p),
+        ("planes", ctypes.c_int64),
+        ("N", ctypes.c_int64),
+        ("dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class TrimulRelayoutArgs(ctypes.Structure):
+    """Mirror of ``gnn_trimul_relayout_args``."""
+
+    _fields_ = [
+        ("src", ctypes.c_void_p),
+        ("dst", ctypes.c_void_p),
+        ("B", ctypes.c_int64),
+        ("N", ctypes.c_int64),
+        ("Ch", ctypes.c_int64),
+        ("src_ld", ctypes.c_int64),
+        ("dst_ld", ctypes.c_int64),
+        ("src_c0", ctypes.c_int64),
+        ("dst_c0", ctypes.c_int64),
+        ("mode", ctypes.c_int32),
+        ("transposed", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+RELAYOUT_PLANES_TO_PIXELS, RELAYOUT_PIXELS_TO_BLOCKED = 0, 1
+
 _SIGNATURES = {
     "gnn_triattn_fwd": (ctypes.c_int, [ctypes.POINTER(TriAttnArgs), ctypes.c_void_p]),
     "gnn_triattn_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(TriAttnArgs)]),
@@ -211,6 +250,8 @@ _SIGNATURES = {
     "gnn_layernorm_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int64]),
     "gnn_layernorm_rows": (ctypes.c_int, [ctypes.POINTER(LayerNormArgs), ctypes.c_void_p]),
     "gnn_trimul_gate_bwd": (ctypes.c_int, [ctypes.POINTER(GateBwdArgs), ctypes.c_void_p]),
+    "gnn_trimul_contract_bwd": (ctypes.c_int, [ctypes.POINTER(TrimulContractBwdArgs), ctypes.c_void_p]),
+    "gnn_trimul_relayout": (ctypes.c_int, [ctypes.POINTER(TrimulRelayoutArgs), ctypes.c_void_p]),
     "gnn_last_error": (ctypes.c_char_p, []),
     "gnn_version": (ctypes.c_char_p, []),
 }

@@ -156,9 +156,12 @@ def trimul_hip(
 # triangle/_reference/trimul.py:57-97). trimul_bwd_hip differentiates the same math. The
 # LayerNorms (forward recompute and backward, with deterministic per-workgroup weight-gradient
 # partials) and the two sigmoid gates run on this library's kernels (gnn_layernorm_rows,
-# gnn_trimul_gate_bwd); the plain matrix products (the three input projections as one
-# [4 Ch + C, C] linear, p_out, the contraction's two products per channel, the weight
-# gradients) go to the vendor GEMM through torch. a, b and o come from the forward's workspace.
+# gnn_trimul_gate_bwd), and for 16-bit types so do the contraction's two N^3 products per
+# channel (gnn_trimul_contract_bwd, reading a and b in place in the forward's workspace) and
+# the moves between pixel-major tensors and per-channel planes (gnn_trimul_relayout). The
+# other matrix products (the three input projections as one [4 Ch + C, C] linear, p_out, the
+# weight gradients, and fp32's contraction products) go to the vendor GEMM through torch.
+# a, b and o come from the forward's workspace.
 
 def layernorm_rows_hip(x2d, weight=None, bias=None, eps=1e-5, *, dy=None, partials=False):
     """Row LayerNorm of ``x2d`` ``[R, K]`` (columns contiguous): ``LN(x)`` when ``dy`` is
@@ -241,6 +244,46 @@ def _operand(ws, off, B, Ch, N, NP, dtype):
     return t[..., :N].contiguous()
 
 
+def relayout_hip(src, dst, mode, B, N, Ch, *, src_ld, dst_ld, src_c0=0, dst_c0=0, transposed=False):
+    """gnn_trimul_relayout (16-bit) between pixel-major rows and per-channel planes."""
+    lib = _lib.load()
+    a = _lib.TrimulRelayoutArgs()
+    a.src, a.dst = src.data_ptr(), dst.data_ptr()
+    a.B, a.N, a.Ch = B, N, Ch
+    a.src_ld, a.dst_ld, a.src_c0, a.dst_c0 = src_ld, dst_ld, src_c0, dst_c0
+    a.mode, a.transposed, a.dtype = mode, int(transposed), _lib.DTYPE_CODE[src.dtype]
+    with torch.cuda.device(src.device):
+        rc = lib.gnn_trimul_relayout(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(src.device)))
+    _lib.check(rc, "gnn_trimul_relayout")
+    return dst
+
+
+def contract_bwd_hip(workspace, offsets, do_pm, B, Ch, N):
+    """``(dA, dB)`` ``[B, Ch, N, NP]`` of the contraction o_c = A_c B_c^T for 16-bit types:
+    ``dA_c = dO_c B_c`` and ``dB_c = dO_c^T A_c``, with A and B read in place from the
+    forward's ``workspace`` and dO given pixel-major, ``do_pm`` ``[B N N, Ch]`` (plane c of
+    batch b: dO_c[i, j] = do_pm[(b, i, j), c])."""
+    lib = _lib.load()
+    dt, dev = do_pm.dtype, do_pm.device
+    NP = (N + 31) // 32 * 32
+    do_i = torch.empty((B, Ch, NP // 32, NP, 32), device=dev, dtype=dt)  # [i / 32][j][i % 32]
+    do_j = torch.empty_like(do_i)                                       # [j / 32][i][j % 32]
+    for t, transposed in ((do_i, False), (do_j, True)):
+        relayout_hip(do_pm, t, _lib.RELAYOUT_PIXELS_TO_BLOCKED, B, N, Ch, src_ld=do_pm.stride(0), dst_ld=32,
+                     transposed=transposed)
+    da = torch.empty((B, Ch, N, NP), device=dev, dtype=dt)
+    db = torch.empty_like(da)
+    a = _lib.TrimulContractBwdArgs()
+    a.a = workspace.data_ptr() + offsets[0]
+    a.b = workspace.data_ptr() + offsets[1]
+    a.do_i, a.do_j, a.da, a.db = do_i.data_ptr(), do_j.data_ptr(), da.data_ptr(), db.data_ptr()
+    a.planes, a.N, a.dtype = B * Ch, N, _lib.DTYPE_CODE[dt]
+    with torch.cuda.device(dev):
+        rc = lib.gnn_trimul_contract_bwd(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(dev)))
+    _lib.check(rc, "gnn_trimul_contract_bwd")
+    return da, db
+
+
 def trimul_bwd_hip(x, direction, mask, eps, weights, workspace, offsets, dout):
     """Gradients ``(dx, {weight name: grad or None})`` of the triangle multiplicative update
     given the forward's ``workspace`` / ``offsets`` (a, b, g, o) and the output gradient."""
@@ -269,7 +312,11 @@ def trimul_bwd_hip(x, direction, mask, eps, weights, workspace, offsets, dout):
     p, gpre, gopre = lin[:, :2 * Ch], lin[:, 2 * Ch:4 * Ch], lin[:, 4 * Ch:]
     # output stage: out = p_out(LN_out(o)) * sigmoid(gopre)
     o_cm = workspace[offsets[3]:offsets[3] + B * Ch * N * NP * x.element_size()].view(dt).view(B, Ch, N, NP)
-    o_pm = o_cm[..., :N].permute(0, 2, 3, 1).reshape(M, Ch).contiguous()
+    if x.element_size() == 2:
+        o_pm = relayout_hip(o_cm, torch.empty((M, Ch), device=dev, dtype=dt), _lib.RELAYOUT_PLANES_TO_PIXELS,
+                            B, N, Ch, src_ld=NP, dst_ld=Ch)
+    else:
+        o_pm = o_cm[..., :N].permute(0, 2, 3, 1).reshape(M, Ch).contiguous()
     on = layernorm_rows_hip(o_pm, w["norm_out_weight"], w["norm_out_bias"], eps)
     y = torch.nn.functional.linear(on, w["p_out_weight"], w["p_out_bias"])
     dlin = torch.empty((M, 4 * Ch + C), device=dev, dtype=dt)
@@ -280,22 +327,25 @@ def trimul_bwd_hip(x, direction, mask, eps, weights, workspace, offsets, dout):
     don = dy @ w["p_out_weight"]
     do_pm, dlnw, dlnb = layernorm_rows_hip(o_pm, w["norm_out_weight"], eps=eps, dy=don, partials=True)
     grads["norm_out_weight"], grads["norm_out_bias"] = dlnw, dlnb
-    # contraction: o_c = A_c B_c^T per (batch, channel) plane in the workspace's operand layout
-    A = _operand(workspace, offsets[0], B, Ch, N, NP, dt)
-    Bm = _operand(workspace, offsets[1], B, Ch, N, NP, dt)
-    do_cm = do_pm.reshape(B, N, N, Ch).permute(0, 3, 1, 2).reshape(B * Ch, N, N).contiguous()
-    dA = torch.bmm(do_cm, Bm)                    # dA[i, k] = sum_j dO[i, j] B[j, k]
-    dBt = torch.bmm(A.transpose(1, 2), do_cm)    # dB[j, k] = sum_i dO[i, j] A[i, k], as [k, j]
-    # planes -> the pixel layout of a / b (plane [i, k] is pixel (i, k) outgoing, (k, i) incoming)
-    dab = torch.empty((B, N, N, 2 * Ch), device=dev, dtype=dt)
-    dA4, dBt4 = dA.view(B, Ch, N, N), dBt.view(B, Ch, N, N)
-    if outgoing:
-        dab[..., :Ch] = dA4.permute(0, 2, 3, 1)
-        dab[..., Ch:] = dBt4.permute(0, 3, 2, 1)
-    else:
-        dab[..., :Ch] = dA4.permute(0, 3, 2, 1)
-        dab[..., Ch:] = dBt4.permute(0, 2, 3, 1)
-    dab = dab.view(M, 2 * Ch)
+    # contraction: o_c = A_c B_c^T per (batch, channel) plane; dO_c[i, j] is pixel (i, j).
+    # dA / dB planes go back to the pixel layout of a / b (plane [i, k] is pixel (i, k)
+    # outgoing, (k, i) incoming), into the two halves of dab.
+    dab = torch.empty((M, 2 * Ch), device=dev, dtype=dt)
+    if x.element_size() == 2:  # this library's kernels, reading A and B in the workspace
+        dA, dB = contract_bwd_hip(workspace, offsets, do_pm, B, Ch, N)
+        for t, c0 in ((dA, 0), (dB, Ch)):
+            relayout_hip(t, dab, _lib.RELAYOUT_PLANES_TO_PIXELS, B, N, Ch, src_ld=NP, dst_ld=2 * Ch, dst_c0=c0,
+                         transposed=not outgoing)
+    else:  # fp32: the vendor GEMM
+        A = _operand(workspace, offsets[0], B, Ch, N, NP, dt)
+        Bm = _operand(workspace, offsets[1], B, Ch, N, NP, dt)
+        do_cm = do_pm.view(B, N, N, Ch).permute(0, 3, 1, 2).reshape(B * Ch, N, N).contiguous()
+        dA4 = torch.bmm(do_cm, Bm).view(B, Ch, N, N)                                   # dO B
+        dB4 = torch.bmm(A.transpose(1, 2), do_cm).view(B, Ch, N, N).transpose(-1, -2)  # dO^T A
+        perm = (0, 2, 3, 1) if outgoing else (0, 3, 2, 1)
+        dab4 = dab.view(B, N, N, 2 * Ch)
+        dab4[..., :Ch] = dA4.permute(*perm)
+        dab4[..., Ch:] = dB4.permute(*perm)
     m_rows = None
     if mask is not None:
         m_rows = mask.to(device=dev, dtype=dt).expand(*x.shape[:-1]).reshape(M).contiguous()

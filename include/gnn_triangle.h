@@ -34,6 +34,9 @@
  *                        through trimul_torch (triangle/_trimul.py:31-36,
  *                        triangle/_reference/trimul.py:57-97): the reference's trimul
  *                        backward, which has no native kernel
+ *   gnn_trimul_contract_bwd, gnn_trimul_relayout -> the autograd products of the
+ *                        contraction's einsum (triangle/_reference/trimul.py:44-54) and the
+ *                        strided copies around them, in that same backward
  */
 #ifndef GNN_TRIANGLE_H
 #define GNN_TRIANGLE_H
@@ -315,6 +318,64 @@ typedef struct gnn_gate_bwd_args {
  * trimul_torch backward (triangle/_reference/trimul.py:86-90 and :95-97: p * sigmoid(g) * mask
  * and p_out(o) * sigmoid(g_out(z))); no native counterpart. */
 int gnn_trimul_gate_bwd(const gnn_gate_bwd_args* args, void* stream);
+
+/* The two N^3 products of the contraction's backward, per (batch, channel) plane p < planes
+ * (16-bit dtypes):
+ *   dA_p[i][k] = sum_j dO_p[i][j] B_p[j][k],   dB_p[j][k] = sum_i dO_p[i][j] A_p[i][k].
+ * A and B are the forward's workspace operands as gnn_trimul_fwd left them (k-blocked,
+ * [planes][NP / 32][N][32], NP = round_up(N, 32): element (i, k) at ((k / 32) N + i) 32 + k % 32
+ * of its plane). dO is given twice, column-blocked with its rows zero-padded to NP:
+ *   do_i = [planes][NP / 32][NP][32], element (i, j) at ((i / 32) NP + j) 32 + i % 32 (zero for j >= N),
+ *   do_j = [planes][NP / 32][NP][32], element (i, j) at ((j / 32) NP + i) 32 + j % 32 (zero for i >= N).
+ * da / db = [planes][N][NP] row-major (columns N .. NP-1 not written). All pointers 16-byte
+ * aligned, in `dtype`. */
+typedef struct gnn_trimul_contract_bwd_args {
+  const void* a;
+  const void* b;
+  const void* do_i;
+  const void* do_j;
+  void* da;
+  void* db;
+  int64_t planes; /* B * Ch */
+  int64_t N;
+  int32_t dtype;  /* GNN_BF16 or GNN_F16 */
+  int32_t reserved;
+} gnn_trimul_contract_bwd_args;
+
+/* Replaces the autograd products of the einsum in _combine_projections
+ * (triangle/_reference/trimul.py:44-54), which the reference differentiates with torch;
+ * no native counterpart. */
+int gnn_trimul_contract_bwd(const gnn_trimul_contract_bwd_args* args, void* stream);
+
+/* Relayouts between the pixel-major rows of the op ([B, N, N] pixels, channels contiguous) and
+ * per-channel planes, for 16-bit dtypes (B * Ch planes, channel c of batch b = plane b Ch + c):
+ *   GNN_RELAYOUT_PLANES_TO_PIXELS:  src = planes [B * Ch][N][src_ld] (row r, column s);
+ *       dst[pixel][dst_c0 + c] with pixel (r, s), or (s, r) when `transposed`; dst rows of
+ *       dst_ld elements. src_ld >= round_up(N, 8).
+ *   GNN_RELAYOUT_PIXELS_TO_BLOCKED: src[pixel (i, j)][src_c0 + c] (rows of src_ld elements) ->
+ *       dst = [B * Ch][NP / 32][NP][32], NP = round_up(N, 32): element (i, j) at
+ *       ((i / 32) NP + j) 32 + i % 32, or at ((j / 32) NP + i) 32 + j % 32 when `transposed`;
+ *       every element with i >= N or j >= N is written as zero (the dO operands of
+ *       gnn_trimul_contract_bwd: do_i untransposed, do_j transposed).
+ * Ch, the row pitches and channel offsets multiples of 8; pointers 16-byte aligned. */
+enum gnn_relayout_mode { GNN_RELAYOUT_PLANES_TO_PIXELS = 0, GNN_RELAYOUT_PIXELS_TO_BLOCKED = 1 };
+
+typedef struct gnn_trimul_relayout_args {
+  const void* src;
+  void* dst;
+  int64_t B, N, Ch;
+  int64_t src_ld, dst_ld;
+  int64_t src_c0, dst_c0;
+  int32_t mode;       /* enum gnn_relayout_mode */
+  int32_t transposed;
+  int32_t dtype;      /* GNN_BF16 or GNN_F16 */
+  int32_t reserved;
+} gnn_trimul_relayout_args;
+
+/* Replaces the strided copies (permute / contiguous) between the trimul backward's pixel-major
+ * tensors and the contraction's planes; no counterpart in the reference, whose backward is
+ * autograd through trimul_torch (triangle/_reference/trimul.py:57-97). */
+int gnn_trimul_relayout(const gnn_trimul_relayout_args* args, void* stream);
 
 /* Message for the last failing call on this thread ("" if none). */
 const char* gnn_last_error(void);

@@ -52,6 +52,9 @@ def _c_layout():
       printf("gnn_triattn_bwd_args %zu\n", sizeof(gnn_triattn_bwd_args));
       printf("gnn_layernorm_args %zu\n", sizeof(gnn_layernorm_args));
       printf("gnn_gate_bwd_args %zu\n", sizeof(gnn_gate_bwd_args));
+      printf("gnn_trimul_contract_bwd_args %zu\n", sizeof(gnn_trimul_contract_bwd_args));
+      P(gnn_trimul_contract_bwd_args, do_j) P(gnn_trimul_contract_bwd_args, db)
+      P(gnn_trimul_contract_bwd_args, planes) P(gnn_trimul_contract_bwd_args, N) P(gnn_trimul_contract_bwd_args, dtype)
       P(gnn_layernorm_args, partial) P(gnn_layernorm_args, rows) P(gnn_layernorm_args, out_stride)
       P(gnn_layernorm_args, eps) P(gnn_layernorm_args, dtype)
       P(gnn_gate_bwd_args, d_gate_pre) P(gnn_gate_bwd_args, rows) P(gnn_gate_bwd_args, mask_stride)
@@ -83,9 +86,11 @@ def test_ctypes_structs_match_c_layout(tmp_path):
     assert int(lines["gnn_triattn_bwd_args"]) == ctypes.sizeof(_lib.TriAttnBwdArgs)
     assert int(lines["gnn_layernorm_args"]) == ctypes.sizeof(_lib.LayerNormArgs)
     assert int(lines["gnn_gate_bwd_args"]) == ctypes.sizeof(_lib.GateBwdArgs)
+    assert int(lines["gnn_trimul_contract_bwd_args"]) == ctypes.sizeof(_lib.TrimulContractBwdArgs)
     classes = {"gnn_triattn_args": _lib.TriAttnArgs, "gnn_trimul_args": _lib.TrimulArgs,
                "gnn_pair_bias_args": _lib.PairBiasArgs, "gnn_triattn_bwd_args": _lib.TriAttnBwdArgs,
-               "gnn_layernorm_args": _lib.LayerNormArgs, "gnn_gate_bwd_args": _lib.GateBwdArgs}
+               "gnn_layernorm_args": _lib.LayerNormArgs, "gnn_gate_bwd_args": _lib.GateBwdArgs,
+               "gnn_trimul_contract_bwd_args": _lib.TrimulContractBwdArgs}
     for key, val in lines.items():
         if "." not in key:
             continue
@@ -275,3 +280,17 @@ def test_trimul_backward_helper_argument_errors():
     g.grad_stride = g.value_stride = g.gate_stride = g.dv_stride = g.dg_stride = 16
     assert lib.gnn_trimul_gate_bwd(ctypes.byref(g), None) == _lib.GNN_ERR_UNSUPPORTED
     assert b"multiple of 8" in lib.gnn_last_error()
+
+    assert lib.gnn_trimul_contract_bwd(None, None) == _lib.GNN_ERR_ARG
+    cb = _lib.TrimulContractBwdArgs()
+    assert lib.gnn_trimul_contract_bwd(ctypes.byref(cb), None) == _lib.GNN_ERR_ARG
+    assert b"required" in lib.gnn_last_error()
+    cb.a = cb.b = cb.do_i = cb.do_j = cb.da = cb.db = 4096
+    cb.planes, cb.N, cb.dtype = 4, 64, _lib.GNN_F32
+    assert lib.gnn_trimul_contract_bwd(ctypes.byref(cb), None) == _lib.GNN_ERR_UNSUPPORTED
+    assert b"16-bit" in lib.gnn_last_error()
+    cb.dtype, cb.N = _lib.GNN_BF16, 0
+    assert lib.gnn_trimul_contract_bwd(ctypes.byref(cb), None) == _lib.GNN_ERR_ARG
+    cb.N, cb.db = 64, 4104
+    assert lib.gnn_trimul_contract_bwd(ctypes.byref(cb), None) == _lib.GNN_ERR_ARG
+    assert b"aligned" in lib.gnn_last_error()

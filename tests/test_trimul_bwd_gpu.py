@@ -81,6 +81,70 @@ def test_gate_bwd(dtype, masked):
     assert torch.count_nonzero(out[:, K:K + 16]) == 0  # the gap between the two outputs is untouched
 
 
+# ------------------------------------------------------- contraction backward kernel
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("N", [1, 37, 64, 100, 300, 512, 700])
+def test_contract_bwd_kernel(dtype, N):
+    """gnn_trimul_contract_bwd against fp32 matmuls of the same 16-bit operands: dA = dO B and
+    dB = dO^T A per plane, A and B given k-blocked in a workspace as the forward leaves them
+    (128-row tiles below N = 512, 256-row tiles from 512 on; N not a multiple of 32 exercises
+    the zero-padded dO rows against the clamped operand rows)."""
+    from oracle.triangle_oracle import rel_fro
+
+    B, Ch = 1, 8
+    NP = (N + 31) // 32 * 32
+    g = gen(N)
+    A, Bm, dO = (randn((B, Ch, N, N), g=g).to(DEV, dtype) for _ in range(3))
+
+    def kblocked(t):  # [B, Ch, N, N] -> [B, Ch, NP / 32, N, 32], zero columns past N
+        z = torch.zeros((B, Ch, N, NP), device=DEV, dtype=dtype)
+        z[..., :N] = t
+        return z.view(B, Ch, N, NP // 32, 32).permute(0, 1, 3, 2, 4).contiguous()
+
+    nbytes = B * Ch * N * NP * 2
+    cm = (nbytes + 255) // 256 * 256
+    ws = torch.zeros(2 * cm, device=DEV, dtype=torch.uint8)
+    ws[:nbytes].view(dtype).copy_(kblocked(A).flatten())
+    ws[cm:cm + nbytes].view(dtype).copy_(kblocked(Bm).flatten())
+    do_pm = dO.permute(0, 2, 3, 1).reshape(B * N * N, Ch).contiguous()
+    da, db = _k().contract_bwd_hip(ws, (0, cm), do_pm, B, Ch, N)
+    want_a = dO.float() @ Bm.float()
+    want_b = dO.float().transpose(-1, -2) @ A.float()
+    bound = 4e-3 if dtype == torch.bfloat16 else 1e-3  # one rounding of the outputs
+    for got, want in ((da[..., :N], want_a), (db[..., :N], want_b)):
+        assert torch.isfinite(got).all()
+        assert rel_fro(got.double().cpu().numpy(), want.double().cpu().numpy()) < bound
+
+
+@pytest.mark.parametrize("N", [5, 40, 96, 130])
+def test_relayout_kernels(N):
+    """gnn_trimul_relayout against torch permutes, bit-exact: pixel rows -> i- and j-blocked
+    planes (zero outside N x N), and planes -> pixel rows (plain and transposed) into a
+    channel window of wider rows (the halves of dab)."""
+    from geometric_nn_ops_torch import _lib
+
+    K = _k()
+    B, Ch, dtype = 2, 24, torch.bfloat16
+    NP = (N + 31) // 32 * 32
+    pm = randn((B, N, N, Ch + 8), seed=N).to(DEV, dtype)  # 8 extra channels: src_c0 = 8
+    blocked = torch.full((B, Ch, NP // 32, NP, 32), float("nan"), device=DEV, dtype=dtype)
+    sq = torch.zeros((B, Ch, NP, NP), device=DEV, dtype=dtype)
+    sq[:, :, :N, :N] = pm[..., 8:].permute(0, 3, 1, 2)
+    for transposed, want in ((False, sq.view(B, Ch, NP // 32, 32, NP).transpose(-1, -2)),
+                             (True, sq.view(B, Ch, NP, NP // 32, 32).permute(0, 1, 3, 2, 4))):
+        K.relayout_hip(pm.view(-1, Ch + 8), blocked, _lib.RELAYOUT_PIXELS_TO_BLOCKED, B, N, Ch, src_ld=Ch + 8,
+                       dst_ld=32, src_c0=8, transposed=transposed)
+        assert torch.equal(blocked, want.contiguous())
+    planes = randn((B, Ch, N, NP), seed=N + 1).to(DEV, dtype)
+    for transposed in (False, True):
+        out = torch.full((B, N, N, 2 * Ch), float("nan"), device=DEV, dtype=dtype)
+        K.relayout_hip(planes, out, _lib.RELAYOUT_PLANES_TO_PIXELS, B, N, Ch, src_ld=NP, dst_ld=2 * Ch,
+                       dst_c0=Ch, transposed=transposed)
+        want = planes[..., :N].permute(0, 3, 2, 1) if transposed else planes[..., :N].permute(0, 2, 3, 1)
+        assert torch.equal(out[..., Ch:], want)
+        assert torch.isnan(out[..., :Ch]).all()  # the other channel window is untouched
+
+
 # ------------------------------------------------------------------ the op's gradients
 def _run(x, direction, mask, w, dout):
     from geometric_nn_ops_torch.triangle import triangle_multiplicative_update
