@@ -182,6 +182,8 @@ int gnn_layernorm_rows(const gnn_layernorm_args* args, void* stream) {
   return hip_status((hipError_t)rc, "layernorm_rows");
 }
 
+int64_t gnn_gate_bwd_partials(int64_t rows, int64_t K) { return gate_bwd_partials(rows, K); }
+
 int gnn_trimul_gate_bwd(const gnn_gate_bwd_args* args, void* stream) {
   if (!args) return set_error(GNN_ERR_ARG, "trimul_gate_bwd: args is NULL");
   const gnn_gate_bwd_args& a = *args;

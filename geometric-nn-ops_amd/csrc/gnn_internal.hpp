@@ -47,6 +47,7 @@ int pair_bias_proj(const gnn_pair_bias_args& a, hipStream_t stream);
 // Backward helpers of the triangle multiplicative update.
 int64_t layernorm_partials(int64_t rows, int64_t K);
 int layernorm_rows(const gnn_layernorm_args& a, hipStream_t stream);
+int64_t gate_bwd_partials(int64_t rows, int64_t K);
 int gate_bwd(const gnn_gate_bwd_args& a, hipStream_t stream);
 int trimul_contract_bwd(const gnn_trimul_contract_bwd_args& a, hipStream_t stream);
 int trimul_relayout(const gnn_trimul_relayout_args& a, hipStream_t stream);

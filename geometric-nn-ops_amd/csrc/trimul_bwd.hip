@@ -212,13 +212,18 @@ int launch_ln(const gnn_layernorm_args& a, hipStream_t st) {
 }
 
 // ---- gate backward: 8 consecutive elements per thread ----------------------------------
+// With partial sums (PART), K / 8 divides the block, so a thread keeps the same 8 columns over
+// its whole grid-stride walk: it sums the values it stores in registers, and the workgroup
+// adds up the threads of each column through LDS once at the end (a fixed order, no atomics).
 constexpr int GB_THREADS = 256;
+constexpr int GB_MAX_GRID = 1024;  // partial rows of the bias gradients
 
-template <typename T>
+template <typename T, bool PART>
 __global__ __launch_bounds__(GB_THREADS) void gate_bwd_kernel(const gnn_gate_bwd_args a) {
   typedef typename TypeOps<T>::V8 V8;
   const int64_t kc = a.K / 8;  // 8-element chunks per row
   const int64_t total = a.rows * kc;
+  f32x8 sdv = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, sdg = sdv;
   for (int64_t i = (int64_t)blockIdx.x * GB_THREADS + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * GB_THREADS) {
     const int64_t r = i / kc, k = (i % kc) * 8;
@@ -235,22 +240,56 @@ __global__ __launch_bounds__(GB_THREADS) void gate_bwd_kernel(const gnn_gate_bwd
       dv[e] = gm * s;
       dg[e] = gm * v[e] * s * (1.0f - s);
     }
-    store8((T*)a.d_value + r * a.dv_stride + k, TypeOps<T>::from_f32(dv));
-    store8((T*)a.d_gate_pre + r * a.dg_stride + k, TypeOps<T>::from_f32(dg));
+    const V8 dvr = TypeOps<T>::from_f32(dv), dgr = TypeOps<T>::from_f32(dg);
+    store8((T*)a.d_value + r * a.dv_stride + k, dvr);
+    store8((T*)a.d_gate_pre + r * a.dg_stride + k, dgr);
+    if constexpr (PART) {
+      sdv += TypeOps<T>::to_f32(dvr);
+      sdg += TypeOps<T>::to_f32(dgr);
+    }
+  }
+  if constexpr (PART) {
+    __shared__ float red[GB_THREADS][17];  // padded rows: the column walk below spreads over banks
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      red[tid][e] = sdv[e];
+      red[tid][8 + e] = sdg[e];
+    }
+    __syncthreads();
+    const int K = (int)a.K, nkc = (int)kc;
+    for (int c = tid; c < 2 * K; c += GB_THREADS) {
+      const int which = c / K, col = c % K;
+      float sum = 0.f;
+      for (int t = col / 8; t < GB_THREADS; t += nkc) sum += red[t][8 * which + col % 8];
+      a.partial[((int64_t)blockIdx.x * 2 + which) * K + col] = sum;
+    }
   }
 }
 
 template <typename T>
 int launch_gate(const gnn_gate_bwd_args& a, hipStream_t st) {
+  if (a.partial) {
+    const int64_t grid = gate_bwd_partials(a.rows, a.K);
+    if (grid < 1) return set_error(GNN_ERR_UNSUPPORTED, "gate_bwd: partial sums need K / 8 to divide 256");
+    hipLaunchKernelGGL((gate_bwd_kernel<T, true>), dim3((uint32_t)grid), dim3(GB_THREADS), 0, st, a);
+    return (int)hipGetLastError();
+  }
   const int64_t chunks = a.rows * (a.K / 8);
   const int64_t want = (chunks + GB_THREADS - 1) / GB_THREADS;
-  const int grid = (int)std::min<int64_t>(want, (int64_t)persistent_grid((const void*)gate_bwd_kernel<T>,
-                                                                         GB_THREADS, 0) * 4);
-  hipLaunchKernelGGL(gate_bwd_kernel<T>, dim3(grid < 1 ? 1 : grid), dim3(GB_THREADS), 0, st, a);
+  const int grid = (int)std::min<int64_t>(
+      want, (int64_t)persistent_grid((const void*)gate_bwd_kernel<T, false>, GB_THREADS, 0) * 4);
+  hipLaunchKernelGGL((gate_bwd_kernel<T, false>), dim3(grid < 1 ? 1 : grid), dim3(GB_THREADS), 0, st, a);
   return (int)hipGetLastError();
 }
 
 }  // namespace
+
+int64_t gate_bwd_partials(int64_t rows, int64_t K) {
+  if (K < 8 || K % 8 != 0 || GB_THREADS % (K / 8) != 0) return 0;
+  const int64_t want = (rows * (K / 8) + GB_THREADS - 1) / GB_THREADS;
+  return want < 1 ? 1 : (want > GB_MAX_GRID ? GB_MAX_GRID : want);
+}
 
 int64_t layernorm_partials(int64_t rows, int64_t K) {
   (void)K;

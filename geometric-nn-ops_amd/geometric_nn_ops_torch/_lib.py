@@ -180,6 +180,7 @@ class GateBwdArgs(ctypes.Structure):
         ("mask", ctypes.c_void_p),
         ("d_value", ctypes.c_void_p),
         ("d_gate_pre", ctypes.c_void_p),
+        ("partial", ctypes.c_void_p),
         ("rows", ctypes.c_int64),
         ("K", ctypes.c_int64),
         ("grad_stride", ctypes.c_int64),
@@ -249,6 +250,7 @@ _SIGNATURES = {
     "gnn_pair_bias_proj": (ctypes.c_int, [ctypes.POINTER(PairBiasArgs), ctypes.c_void_p]),
     "gnn_layernorm_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int64]),
     "gnn_layernorm_rows": (ctypes.c_int, [ctypes.POINTER(LayerNormArgs), ctypes.c_void_p]),
+    "gnn_gate_bwd_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int64]),
     "gnn_trimul_gate_bwd": (ctypes.c_int, [ctypes.POINTER(GateBwdArgs), ctypes.c_void_p]),
     "gnn_trimul_contract_bwd": (ctypes.c_int, [ctypes.POINTER(TrimulContractBwdArgs), ctypes.c_void_p]),
     "gnn_trimul_relayout": (ctypes.c_int, [ctypes.POINTER(TrimulRelayoutArgs), ctypes.c_void_p]),

@@ -194,17 +194,22 @@ def layernorm_rows_hip(x2d, weight=None, bias=None, eps=1e-5, *, dy=None, partia
     return out, sums[0], sums[1]
 
 
-def gate_bwd_hip(grad, value, gate_pre, mask_rows=None, *, d_value=None, d_gate_pre=None):
+def gate_bwd_hip(grad, value, gate_pre, mask_rows=None, *, d_value=None, d_gate_pre=None, sums=False):
     """Backward of ``value * sigmoid(gate_pre) * mask_rows[:, None]`` for ``[R, K]`` row
     views (columns contiguous); writes into ``d_value`` / ``d_gate_pre`` (allocated when
-    None) and returns them."""
+    None) and returns them, followed with ``sums`` by their fp32 column sums (the bias
+    gradients of the layers behind value and gate_pre), from the kernel's per-workgroup
+    partial rows where K allows it."""
     lib = _lib.load()
     R, K = grad.shape
     if d_value is None:
         d_value = torch.empty((R, K), device=grad.device, dtype=grad.dtype)
     if d_gate_pre is None:
         d_gate_pre = torch.empty((R, K), device=grad.device, dtype=grad.dtype)
+    nparts = lib.gnn_gate_bwd_partials(R, K) if sums else 0
+    part = torch.empty((nparts, 2, K), device=grad.device, dtype=torch.float32) if nparts else None
     a = _lib.GateBwdArgs()
+    a.partial = None if part is None else part.data_ptr()
     a.grad, a.value, a.gate_pre = grad.data_ptr(), value.data_ptr(), gate_pre.data_ptr()
     a.d_value, a.d_gate_pre = d_value.data_ptr(), d_gate_pre.data_ptr()
     if mask_rows is not None:
@@ -216,7 +221,12 @@ def gate_bwd_hip(grad, value, gate_pre, mask_rows=None, *, d_value=None, d_gate_
     with torch.cuda.device(grad.device):
         rc = lib.gnn_trimul_gate_bwd(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(grad.device)))
     _lib.check(rc, "gnn_trimul_gate_bwd")
-    return d_value, d_gate_pre
+    if not sums:
+        return d_value, d_gate_pre
+    if part is not None:
+        colsum = part.sum(0)
+        return d_value, d_gate_pre, colsum[0], colsum[1]
+    return (d_value, d_gate_pre, d_value.sum(0, dtype=torch.float32), d_gate_pre.sum(0, dtype=torch.float32))
 
 
 def _wgrad(d, t, slices=64):
@@ -320,10 +330,10 @@ def trimul_bwd_hip(x, direction, mask, eps, weights, workspace, offsets, dout):
     on = layernorm_rows_hip(o_pm, w["norm_out_weight"], w["norm_out_bias"], eps)
     y = torch.nn.functional.linear(on, w["p_out_weight"], w["p_out_bias"])
     dlin = torch.empty((M, 4 * Ch + C), device=dev, dtype=dt)
-    dy, _ = gate_bwd_hip(dout2, y, gopre, d_gate_pre=dlin[:, 4 * Ch:])
+    dy, _, db_pout, db_gout = gate_bwd_hip(dout2, y, gopre, d_gate_pre=dlin[:, 4 * Ch:], sums=True)
     grads = {}
     grads["p_out_weight"] = _wgrad(dy, on)
-    grads["p_out_bias"] = dy.sum(0, dtype=torch.float32)
+    grads["p_out_bias"] = db_pout
     don = dy @ w["p_out_weight"]
     do_pm, dlnw, dlnb = layernorm_rows_hip(o_pm, w["norm_out_weight"], eps=eps, dy=don, partials=True)
     grads["norm_out_weight"], grads["norm_out_bias"] = dlnw, dlnb
@@ -349,9 +359,10 @@ def trimul_bwd_hip(x, direction, mask, eps, weights, workspace, offsets, dout):
     m_rows = None
     if mask is not None:
         m_rows = mask.to(device=dev, dtype=dt).expand(*x.shape[:-1]).reshape(M).contiguous()
-    gate_bwd_hip(dab, p, gpre, m_rows, d_value=dlin[:, :2 * Ch], d_gate_pre=dlin[:, 2 * Ch:4 * Ch])
+    _, _, db_pin, db_gin = gate_bwd_hip(dab, p, gpre, m_rows, d_value=dlin[:, :2 * Ch],
+                                        d_gate_pre=dlin[:, 2 * Ch:4 * Ch], sums=True)
     dwcat = _wgrad(dlin, z)
-    dbcat = dlin.sum(0, dtype=torch.float32)
+    dbcat = torch.cat([db_pin, db_gin, db_gout])
     grads["p_in_weight"], grads["g_in_weight"], grads["g_out_weight"] = (
         dwcat[:2 * Ch], dwcat[2 * Ch:4 * Ch], dwcat[4 * Ch:])
     grads["p_in_bias"], grads["g_in_bias"], grads["g_out_bias"] = (

@@ -301,7 +301,12 @@ int gnn_layernorm_rows(const gnn_layernorm_args* args, void* stream);
 /* Backward of out = value * sigmoid(gate_pre) * mask (mask per row, NULL = 1):
  *   d_value = grad * s * mask,  d_gate_pre = grad * value * mask * s * (1 - s),  s = sigmoid(gate_pre).
  * [rows, K] tensors by row strides (columns contiguous, rows and bases 16-byte aligned),
- * mask [rows] by mask_stride, all in `dtype`; K a multiple of 8. */
+ * mask [rows] by mask_stride, all in `dtype`; K a multiple of 8.
+ * If `partial` is set, partial[w][0][k] / partial[w][1][k] receive the sums of the stored
+ * (rounded) d_value / d_gate_pre over the rows workgroup w handled, w < gnn_gate_bwd_partials
+ * (rows, K): the bias gradients of the two linear layers behind value and gate_pre are their
+ * sums over w. gnn_gate_bwd_partials returns 0 for the K it cannot split this way (K / 8
+ * must divide 256). */
 typedef struct gnn_gate_bwd_args {
   const void* grad;
   const void* value;
@@ -309,6 +314,7 @@ typedef struct gnn_gate_bwd_args {
   const void* mask;
   void* d_value;
   void* d_gate_pre;
+  float* partial; /* optional fp32 [gnn_gate_bwd_partials(rows, K)][2][K] */
   int64_t rows, K;
   int64_t grad_stride, value_stride, gate_stride, mask_stride, dv_stride, dg_stride;
   int32_t dtype; /* enum gnn_dtype */
@@ -317,6 +323,7 @@ typedef struct gnn_gate_bwd_args {
 /* Replaces the sigmoid / multiply autograd nodes of the gated projections in the reference's
  * trimul_torch backward (triangle/_reference/trimul.py:86-90 and :95-97: p * sigmoid(g) * mask
  * and p_out(o) * sigmoid(g_out(z))); no native counterpart. */
+int64_t gnn_gate_bwd_partials(int64_t rows, int64_t K);
 int gnn_trimul_gate_bwd(const gnn_gate_bwd_args* args, void* stream);
 
 /* The two N^3 products of the contraction's backward, per (batch, channel) plane p < planes

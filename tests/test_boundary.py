@@ -57,7 +57,7 @@ def _c_layout():
       P(gnn_trimul_contract_bwd_args, planes) P(gnn_trimul_contract_bwd_args, N) P(gnn_trimul_contract_bwd_args, dtype)
       P(gnn_layernorm_args, partial) P(gnn_layernorm_args, rows) P(gnn_layernorm_args, out_stride)
       P(gnn_layernorm_args, eps) P(gnn_layernorm_args, dtype)
-      P(gnn_gate_bwd_args, d_gate_pre) P(gnn_gate_bwd_args, rows) P(gnn_gate_bwd_args, mask_stride)
+      P(gnn_gate_bwd_args, d_gate_pre) P(gnn_gate_bwd_args, partial) P(gnn_gate_bwd_args, rows) P(gnn_gate_bwd_args, mask_stride)
       P(gnn_gate_bwd_args, dg_stride) P(gnn_gate_bwd_args, dtype)
       P(gnn_triattn_args, lse) P(gnn_triattn_args, row_max) P(gnn_triattn_args, D) P(gnn_triattn_args, bias_stride)
       P(gnn_triattn_args, mask_stride) P(gnn_triattn_args, scale) P(gnn_triattn_args, precision)
@@ -262,6 +262,9 @@ def test_trimul_backward_helper_argument_errors():
     assert b"multiple of 32" in lib.gnn_last_error()
     assert lib.gnn_layernorm_partials(1 << 20, 128) == 4096
     assert lib.gnn_layernorm_partials(40, 128) == 2
+    assert lib.gnn_gate_bwd_partials(1 << 20, 256) == 1024
+    assert lib.gnn_gate_bwd_partials(100, 128) == 7
+    assert lib.gnn_gate_bwd_partials(100, 96) == 0  # 12 chunks per row do not divide 256
 
     assert lib.gnn_trimul_gate_bwd(None, None) == _lib.GNN_ERR_ARG
     g = _lib.GateBwdArgs()

@@ -64,14 +64,23 @@ def test_layernorm_rows_partials_are_deterministic():
 # ------------------------------------------------------------------ gate backward kernel
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
 @pytest.mark.parametrize("masked", [False, True], ids=["nomask", "mask"])
-def test_gate_bwd(dtype, masked):
-    R, K = 333, 96
+@pytest.mark.parametrize("K", [96, 128])
+def test_gate_bwd(dtype, masked, K):
+    """Values against the oracle's formula, and the column sums (bias gradients): from the
+    kernel's per-workgroup partials at K = 128, from torch at K = 96 (12 chunks per row do
+    not divide the workgroup); both equal the sums of the stored outputs."""
+    R = 333 if K == 96 else 70000
     g = gen(7)
     buf = randn((R, 3 * K + 32), g=g, scale=3.0).to(DEV, dtype)
     grad, value, gate = buf[:, :K], buf[:, K + 8:2 * K + 8], buf[:, 2 * K + 16:3 * K + 16]
     mask = (torch.rand(R, generator=g) < 0.7).to(DEV, dtype) if masked else None
     out = torch.zeros((R, 2 * K + 16), device=DEV, dtype=dtype)
-    dv, dg = _k().gate_bwd_hip(grad, value, gate, mask, d_value=out[:, :K], d_gate_pre=out[:, K + 16:])
+    dv, dg, sdv, sdg = _k().gate_bwd_hip(grad, value, gate, mask, d_value=out[:, :K], d_gate_pre=out[:, K + 16:],
+                                         sums=True)
+    for got, t in ((sdv, dv), (sdg, dg)):
+        want = t.double().sum(0)
+        assert got.dtype == torch.float32
+        torch.testing.assert_close(got.double(), want, rtol=1e-5, atol=1e-3)
     gr, v, gp = (to_np(t) for t in (grad, value, gate))
     s = 1 / (1 + np.exp(-gp))
     m = to_np(mask)[:, None] if masked else 1.0
