@@ -177,9 +177,11 @@ def sigmoid(x):
 def combine(a, b, outgoing: bool) -> np.ndarray:
     """outgoing ``o[..., i, j, c] = sum_k a[..., i, k, c] b[..., j, k, c]``;
     incoming ``o[..., i, j, c] = sum_k a[..., k, i, c] b[..., k, j, c]``
-    (_reference/trimul.py:44-54), evaluated as one matmul per channel."""
-    am = np.moveaxis(a, -1, -3)  # [..., C, N, N]
-    bm = np.moveaxis(b, -1, -3)
+    (_reference/trimul.py:44-54), evaluated as one matmul per channel. The channel-major
+    copies are contiguous: numpy's matmul on the strided moveaxis views takes a non-BLAS
+    loop (about 100x slower at N = 256)."""
+    am = np.ascontiguousarray(np.moveaxis(a, -1, -3))  # [..., C, N, N]
+    bm = np.ascontiguousarray(np.moveaxis(b, -1, -3))
     if outgoing:
         o = am @ np.swapaxes(bm, -1, -2)
     else:

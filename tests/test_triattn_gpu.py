@@ -97,7 +97,8 @@ def test_public_op_accuracy_and_exp2(dtype):
     want = oracle_of(t, mask)
     for use_exp2 in (False, True):
         got = public(**dev(t), mask=mask.to(DEV), use_exp2=use_exp2)
-        assert_close_to_oracle("out", got, want, TRIANGLE_ATTENTION_TOL[dtype, "ieee"])
+        assert_close_to_oracle("out", got, want, TRIANGLE_ATTENTION_TOL[dtype, "ieee"],
+                               rel_fro_max=NORTH_STAR_REL_FRO if dtype != torch.float32 else None)
 
 
 def test_pairformer_shape():
@@ -326,7 +327,7 @@ def test_config_c2_n256():
 def test_headline_n512_rows():
     B, N, H, D = 1, 512, 4, 32
     t = attention_inputs(B, N, N, H, D, torch.bfloat16, seed=0, bias_scale=1.0)
-    rows = [0, 1, 127, 255, 300, 511]
+    rows = sorted(set(range(0, N, 8)) | {1, 127, 255, 300, 511})  # 69 of the 512 rows
     _rows_vs_oracle(t, None, rows, D**-0.5, TRIANGLE_ATTENTION_TOL[torch.bfloat16, "ieee"],
                     rel_fro_max=NORTH_STAR_REL_FRO)
 
@@ -337,7 +338,7 @@ def test_config_c4_n768_ragged():
     t = attention_inputs(B, N, N, H, D, torch.bfloat16, seed=0, bias_scale=2.0)
     lengths = torch.randint(384, 769, (N,), generator=gen(99))
     mask = (torch.arange(N)[None, :] < lengths[:, None]).reshape(B, N, 1, 1, N)
-    rows = [0, 5, int(lengths.argmin()), int(lengths.argmax()), 400, 767]
+    rows = sorted(set(range(0, N, 12)) | {5, int(lengths.argmin()), int(lengths.argmax()), 767})  # 67 rows
     _rows_vs_oracle(t, mask, rows, D**-0.5, TRIANGLE_ATTENTION_TOL[torch.bfloat16, "ieee"],
                     rel_fro_max=NORTH_STAR_REL_FRO)
 

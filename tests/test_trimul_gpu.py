@@ -105,7 +105,8 @@ def test_stages_against_oracle(direction, dtype):
     assert_close_to_oracle("b", b_cm.permute(*perm), st["b"], tol)
     assert_close_to_oracle("g", region(2, (B, N, N, C)), st["g"], tol)
     assert_close_to_oracle("o", o_cm.permute(0, 2, 3, 1), st["o"], tol)
-    assert_close_to_oracle("out", out, st["out"], tol)
+    assert_close_to_oracle("out", out, st["out"], tol,
+                           rel_fro_max=NORTH_STAR_REL_FRO if dtype != torch.float32 else None)
 
 
 @DIRECTIONS
@@ -141,7 +142,8 @@ def test_channel_widths(direction, channels):
     w = trimul_weights(channels, channels, torch.bfloat16, seed=17)
     x, mask = pair_input(1, 24, channels, torch.bfloat16, seed=18)
     assert_close_to_oracle("out", hip(x, direction, mask, w), oracle(x, direction, mask, w),
-                           Tolerance(1 - 1e-4, 2e-2))
+                           Tolerance(1 - 1e-4, 2e-2),
+                           rel_fro_max=NORTH_STAR_REL_FRO)
 
 
 @DIRECTIONS
@@ -152,7 +154,8 @@ def test_hidden_differs_from_channels(direction, c_z, c_hidden):
     w = trimul_weights(c_z, c_hidden, torch.bfloat16, seed=19)
     x, mask = pair_input(1, 24, c_z, torch.bfloat16, seed=20)
     assert_close_to_oracle("out", hip(x, direction, mask, w), oracle(x, direction, mask, w),
-                           Tolerance(1 - 1e-4, 2e-2))
+                           Tolerance(1 - 1e-4, 2e-2),
+                           rel_fro_max=NORTH_STAR_REL_FRO)
 
 
 @DIRECTIONS
@@ -161,7 +164,8 @@ def test_fixed_width_fp16(direction, channels):
     w = trimul_weights(channels, channels, torch.float16, seed=21, biases=True)
     x, mask = pair_input(1, 40, channels, torch.float16, seed=22)
     assert_close_to_oracle("out", hip(x, direction, mask, w), oracle(x, direction, mask, w),
-                           Tolerance(1 - 1e-4, 1e-2))
+                           Tolerance(1 - 1e-4, 1e-2),
+                           rel_fro_max=NORTH_STAR_REL_FRO)
 
 
 @DIRECTIONS
@@ -197,7 +201,8 @@ def test_layernorm_affine(direction, gamma):
     w["norm_out_bias"] = (torch.randn(C, generator=g) * 0.1).to(dt)
     x, mask = pair_input(1, N, C, dt, seed=20)
     assert_close_to_oracle("out", hip(x, direction, mask, w), oracle(x, direction, mask, w),
-                           Tolerance(1 - 1e-4, 2e-2))
+                           Tolerance(1 - 1e-4, 2e-2),
+                           rel_fro_max=NORTH_STAR_REL_FRO)
 
 
 def test_none_parameters():
