@@ -65,8 +65,9 @@ def parse():
     ap.add_argument("--cold-steps", type=int, default=3,
                     help="launches of each kernel timed cold, after a 512 MiB scratch write that evicts L2 and "
                          "the 256 MB Infinity Cache (0 skips)")
-    ap.add_argument("--only", choices=["attn", "trimul"], default=None,
-                    help="profile helper: run only one op (the JSON line is then partial)")
+    ap.add_argument("--only", choices=["attn", "trimul", "configs"], default=None,
+                    help="profile helper: run only one op, or only the other BASELINE configurations "
+                         "(the JSON line is then partial)")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward timings")
     ap.add_argument("--copy-calib", action="store_true",
                     help="profile helper: run a plain 256 MiB device copy (known HBM bytes) and exit, "
@@ -294,6 +295,9 @@ def main():
     attn = AttnCall(qd, kd, vd, bd)
     tri = {d: TrimulCall(xd, d, md, wd) for d in ("outgoing", "incoming")}
     stream = torch.cuda.current_stream(dev)
+    if args.only == "configs":  # profile helper: the other BASELINE configurations alone
+        print(json.dumps({"only": "configs", "configs": run_configs(dev, stream)}), flush=True)
+        return
 
     kernels = []  # (name, callable): one C-ABI entry point each
     if args.only in (None, "attn"):
@@ -676,6 +680,14 @@ def block(dev, stream, N, dtype, precision):
            "ops": {name: rates(fl[name], by[name], window_ms(fn, stream)[0], peak) for name, fn in ops}}
     res.update(rates(sum(fl.values()), sum(by.values()), window_ms(run_block, stream, warmup=3)[0], peak))
     res["parity"] = par
+    if dtype == torch.bfloat16:  # the three trimul kernels on their own (outgoing)
+        M, e2 = N * N, 2
+        sfl = {"proj": 2.0 * M * C * (4 * C + C), "contract": 2.0 * N**3 * C, "out": 2.0 * M * C * C}
+        sby = {"proj": e2 * M * C + 2 * e2 * M * C + e2 * M * C, "contract": 3.0 * e2 * M * C,
+               "out": e2 * M * C + 2.0 * e2 * M * C}
+        res["trimul_outgoing_kernels"] = {
+            name: rates(sfl[name], sby[name], window_ms(t_out.stage(name), stream)[0], peak)
+            for name in ("proj", "contract", "out")}
     return res
 
 

@@ -10,7 +10,9 @@
 // What changes is the schedule. At D = 32 one (b, s, h) row of K and V is N * 128 bytes
 // (64 KB at N = 512), so a workgroup stages the WHOLE row of K and V in LDS once and its
 // waves then sweep every key tile with no barrier at all:
-//   * one workgroup per (b, s, h); its NW waves take the row's 32-query blocks round robin;
+//   * one workgroup per (b, s, h); its NW waves take the row's 32-query blocks round robin
+//     (8 waves while two rows fit a CU's 160 KB of LDS, 16 once a row needs more than 80 KB,
+//     N > 576, so that a CU still runs 4 waves per SIMD);
 //   * K rows are 64 bytes with the four 16-byte chunks XOR-swizzled by (key / 4) % 4, so the
 //     32-lane fragment reads of QK^T hit 16 distinct bank groups; V keeps [key][d] rows for
 //     the ds_read_b64_tr_b16 V^T fragments of PV (a 64-byte pitch puts the four row windows
@@ -60,9 +62,6 @@ constexpr int TILE_BYTES = KT * ROW_BYTES;
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float RESCALE_THRESHOLD = 8.0f / LOG2E;
 
-#ifndef GNN_ROW_WAVES
-#define GNN_ROW_WAVES 8
-#endif
 #ifndef GNN_ROW_WAVES_PER_SIMD  // occupancy the register allocation is held to (128 VGPRs at 4)
 #define GNN_ROW_WAVES_PER_SIMD 4
 #endif
@@ -86,8 +85,8 @@ constexpr int64_t ROW_HEADS_FIRST_BYTES = GNN_ROW_HEADS_FIRST_BYTES;
 #define GNN_ROW_HEAD_PAIRS 1
 #endif
 constexpr bool ROW_HEAD_PAIRS = GNN_ROW_HEAD_PAIRS;
-constexpr int NW = GNN_ROW_WAVES;
-constexpr int NT = NW * 64;
+// waves of a workgroup: 8 while two workgroups fit the CU's LDS, else 16
+constexpr size_t ROW_TWO_PER_CU_BYTES = 80 * 1024;
 constexpr int ROW_MAX_TILES = (GNN_ROW_MAX_N + KT - 1) / KT;
 
 struct RowHdr {
@@ -227,8 +226,9 @@ __device__ __forceinline__ typename TypeOps<T>::V4 tr_read4_r(const unsigned cha
   return __builtin_bit_cast(typename TypeOps<T>::V4, v);
 }
 
-template <typename T, bool HAS_BIAS>
-__global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel(const gnn_triattn_args a) {
+template <typename T, bool HAS_BIAS, int NW>
+__global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel(const gnn_triattn_args a) {
+  constexpr int NT = NW * 64;
   typedef typename TypeOps<T>::V8 V8;
   typedef typename TypeOps<T>::V4 V4;
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -586,6 +586,15 @@ __global__ __launch_bounds__(NT, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel
   }
 }
 
+template <typename T, bool HAS_BIAS, int NW>
+int launch_row_nw(const gnn_triattn_args& a, hipStream_t stream, size_t smem) {
+  const void* fn = (const void*)triattn_row_kernel<T, HAS_BIAS, NW>;
+  if (smem > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  const int64_t nblk = a.B * a.S * a.H;
+  hipLaunchKernelGGL((triattn_row_kernel<T, HAS_BIAS, NW>), dim3((uint32_t)nblk), dim3(NW * 64), smem, stream, a);
+  return (int)hipGetLastError();
+}
+
 template <typename T, bool HAS_BIAS>
 int launch_row(const gnn_triattn_args& a, hipStream_t stream) {
   if (HAS_BIAS) {
@@ -594,11 +603,8 @@ int launch_row(const gnn_triattn_args& a, hipStream_t stream) {
                        (T*)a.workspace, nchunks);
   }
   const size_t smem = row_smem_bytes(a.N);
-  const void* fn = (const void*)triattn_row_kernel<T, HAS_BIAS>;
-  if (smem > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-  const int64_t nblk = a.B * a.S * a.H;
-  hipLaunchKernelGGL((triattn_row_kernel<T, HAS_BIAS>), dim3((uint32_t)nblk), dim3(NT), smem, stream, a);
-  return (int)hipGetLastError();
+  if (smem > ROW_TWO_PER_CU_BYTES) return launch_row_nw<T, HAS_BIAS, 16>(a, stream, smem);
+  return launch_row_nw<T, HAS_BIAS, 8>(a, stream, smem);
 }
 
 }  // namespace
