@@ -32,8 +32,10 @@
 //     and -inf for keys past N, on the VALU.
 //   * p = exp2(s * log2 e - m * log2 e): one FMA and one v_exp_f32 per score for 16-bit
 //     inputs; fp32 inputs and rows with no live key (m is then the -1e9 sentinel) use the
-//     exact (s - m) * log2 e. The row sum is taken on the rounded probabilities with
-//     v_dot2 (16-bit inputs), so the normaliser matches what the PV product consumes.
+//     exact (s - m) * log2 e. The row sum adds the fp32 probabilities before they are
+//     rounded for the PV product, as the reference's tl.sum(P_block, 1) does (v_add_f32
+//     issues alongside other waves' MFMAs; a v_dot2 on the rounded values holds the
+//     matrix pipe).
 //   * The running max only moves when a tile raises it by more than 8 ln 2, so most
 //     tiles skip the O / l rescale; p then stays below 2^8.
 //   * Key tiles whose keys are all masked are skipped when the row has at least one live
@@ -109,21 +111,10 @@ __device__ __forceinline__ typename TypeOps<T>::V4 tr_read4(const T* p) {
   return __builtin_bit_cast(typename TypeOps<T>::V4, v);
 }
 
-// Adds the 8 probabilities of a fragment (as rounded for the MFMA, so the normaliser
-// matches the numerator) to acc: two-element dot products with 1 for 16-bit types.
-__device__ __forceinline__ float rowsum_add(const bf16x8& v, float acc) {
-  const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
-#pragma unroll
-  for (int e = 0; e < 8; e += 2) acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{v[e], v[e + 1]}, one, acc, false);
-  return acc;
-}
-__device__ __forceinline__ float rowsum_add(const f16x8& v, float acc) {
-  const f16x2 one = {(f16)1.0f, (f16)1.0f};
-#pragma unroll
-  for (int e = 0; e < 8; e += 2) acc = __builtin_amdgcn_fdot2(f16x2{v[e], v[e + 1]}, one, acc, false);
-  return acc;
-}
-__device__ __forceinline__ float rowsum_add(const f32x8& v, float acc) {
+// acc + the 8 fp32 probabilities of fragment t of an accumulator (a pairwise tree)
+__device__ __forceinline__ float rowsum_add(const f32x16& p, int t, float acc) {
+  const f32x8 v = {p[8 * t + 0], p[8 * t + 1], p[8 * t + 2], p[8 * t + 3],
+                   p[8 * t + 4], p[8 * t + 5], p[8 * t + 6], p[8 * t + 7]};
   return acc + (((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7])));
 }
 
@@ -486,7 +477,7 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           pf[sub][kk] = frag_from_acc<T>(sc[sub], kk);
-          lsum[r] = rowsum_add(pf[sub][kk], lsum[r]);
+          lsum[r] = rowsum_add(sc[sub], kk, lsum[r]);
         }
       }
 

@@ -44,9 +44,11 @@
 // per-tile maximum reduction. A query block whose row sum ends above 2^64 (so p or the
 // accumulators could have overflowed) is recomputed with the per-tile maximum and lazy
 // rescale (threshold 8 ln 2), the pass that also serves callers asking for the exact row
-// maximum. exp2 with the folded FMA, v_dot2 row sums on the rounded probabilities, and rows
-// whose keys are all masked reproducing mean(v) (the sentinel swamps the logits; subtract
-// first) are as in the tiled kernel, which gives the same results to rounding.
+// maximum. exp2 with the folded FMA, row sums of the fp32 probabilities before they are
+// rounded for the PV product (as the reference's tl.sum(P_block, 1); v_add_f32, which issues
+// alongside other waves' MFMAs where v_dot2 would hold the matrix pipe), and rows whose keys
+// are all masked reproducing mean(v) (the sentinel swamps the logits; subtract first) are as
+// in the tiled kernel, which gives the same results to rounding.
 #include <mutex>
 
 #include "gnn_common.hpp"
@@ -171,17 +173,9 @@ __global__ __launch_bounds__(256) void bias_tiles_kernel(const gnn_triattn_args 
   store8(tiles + (((id >> 8) * 4 + f) * 64 + lane) * 8, v);
 }
 
-__device__ __forceinline__ float rowsum_add_r(const bf16x8& v, float acc) {
-  const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
-#pragma unroll
-  for (int e = 0; e < 8; e += 2) acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{v[e], v[e + 1]}, one, acc, false);
-  return acc;
-}
-__device__ __forceinline__ float rowsum_add_r(const f16x8& v, float acc) {
-  const f16x2 one = {(f16)1.0f, (f16)1.0f};
-#pragma unroll
-  for (int e = 0; e < 8; e += 2) acc = __builtin_amdgcn_fdot2(f16x2{v[e], v[e + 1]}, one, acc, false);
-  return acc;
+// acc + the sum of 8 fp32 probabilities (a pairwise tree, so the add chain per tile is short)
+__device__ __forceinline__ float rowsum_add_r(const f32x8& x, float acc) {
+  return acc + (((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7])));
 }
 
 // Maxima of scores, which are finite or -inf (never NaN): v_max3_f32 / v_max_f32 written
@@ -511,7 +505,7 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
           f32x8 x = {sc[sub][8 * kk + 0], sc[sub][8 * kk + 1], sc[sub][8 * kk + 2], sc[sub][8 * kk + 3],
                      sc[sub][8 * kk + 4], sc[sub][8 * kk + 5], sc[sub][8 * kk + 6], sc[sub][8 * kk + 7]};
           const V8 pf = TypeOps<T>::from_f32(x);
-          lsum = rowsum_add_r(pf, lsum);
+          lsum = rowsum_add_r(x, lsum);
           if (!GNN_ROW_VPREFETCH) load_v(kk);
           Mma<T, PREC_NATIVE>::step(o, vf[kk], pf);
         }
