@@ -167,6 +167,27 @@ int gnn_pair_bias_proj(const gnn_pair_bias_args* args, void* stream) {
   return hip_status((hipError_t)rc, "pair_bias_proj");
 }
 
+int gnn_apb_gate_out(const gnn_apb_gate_out_args* args, void* stream) {
+  if (!args) return set_error(GNN_ERR_ARG, "apb_gate_out: args is NULL");
+  const gnn_apb_gate_out_args& a = *args;
+  if (!a.s || !a.o || !a.g_w || !a.o_w || !a.out)
+    return set_error(GNN_ERR_ARG, "apb_gate_out: s, o, g_w, o_w and out are required");
+  if (a.M < 1 || a.Cs < 1 || a.D < 1 || a.Co < 1)
+    return set_error(GNN_ERR_ARG, "apb_gate_out: M, c_s, the attention width and c_out must be positive");
+  if (a.dtype != GNN_BF16 && a.dtype != GNN_F16 && a.dtype != GNN_F32)
+    return set_error(GNN_ERR_ARG, "apb_gate_out: unknown dtype");
+  const int64_t e = a.dtype == GNN_F32 ? 4 : 2;
+  const void* ptrs[] = {a.s, a.o, a.g_w, a.o_w, a.out};
+  for (const void* p : ptrs)
+    if (!aligned(p, 16)) return set_error(GNN_ERR_ARG, "apb_gate_out: tensors must be 16-byte aligned");
+  if ((a.s_ld * e) % 16 || (a.o_ld * e) % 16 || (a.out_ld * e) % 16 || a.s_ld < a.Cs || a.o_ld < a.D ||
+      a.out_ld < a.Co)
+    return set_error(GNN_ERR_ARG, "apb_gate_out: row pitches must cover the rows and be multiples of 16 bytes");
+  int rc = apb_gate_out(a, (hipStream_t)stream);
+  if (rc < 0) return rc;
+  return hip_status((hipError_t)rc, "apb_gate_out");
+}
+
 int64_t gnn_layernorm_partials(int64_t rows, int64_t K) { return layernorm_partials(rows, K); }
 
 int gnn_layernorm_rows(const gnn_layernorm_args* args, void* stream) {

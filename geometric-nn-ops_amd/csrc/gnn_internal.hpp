@@ -43,6 +43,7 @@ int trimul_contract(const gnn_trimul_args& a, hipStream_t stream);
 int trimul_out(const gnn_trimul_args& a, hipStream_t stream);
 
 int pair_bias_proj(const gnn_pair_bias_args& a, hipStream_t stream);
+int apb_gate_out(const gnn_apb_gate_out_args& a, hipStream_t stream);
 
 // Backward helpers of the triangle multiplicative update.
 int64_t layernorm_partials(int64_t rows, int64_t K);

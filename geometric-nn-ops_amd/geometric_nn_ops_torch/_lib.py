@@ -131,6 +131,29 @@ class TrimulArgs(ctypes.Structure):
     ]
 
 
+class ApbGateOutArgs(ctypes.Structure):
+    """Mirror of ``gnn_apb_gate_out_args``."""
+
+    _fields_ = [
+        ("s", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("g_w", ctypes.c_void_p),
+        ("g_b", ctypes.c_void_p),
+        ("o_w", ctypes.c_void_p),
+        ("o_b", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("M", ctypes.c_int64),
+        ("Cs", ctypes.c_int64),
+        ("D", ctypes.c_int64),
+        ("Co", ctypes.c_int64),
+        ("s_ld", ctypes.c_int64),
+        ("o_ld", ctypes.c_int64),
+        ("out_ld", ctypes.c_int64),
+        ("dtype", ctypes.c_int32),
+        ("precision", ctypes.c_int32),
+    ]
+
+
 class PairBiasArgs(ctypes.Structure):
     """Mirror of ``gnn_pair_bias_args``."""
 
@@ -248,6 +271,7 @@ _SIGNATURES = {
     "gnn_trimul_contract": (ctypes.c_int, [ctypes.POINTER(TrimulArgs), ctypes.c_void_p]),
     "gnn_trimul_out": (ctypes.c_int, [ctypes.POINTER(TrimulArgs), ctypes.c_void_p]),
     "gnn_pair_bias_proj": (ctypes.c_int, [ctypes.POINTER(PairBiasArgs), ctypes.c_void_p]),
+    "gnn_apb_gate_out": (ctypes.c_int, [ctypes.POINTER(ApbGateOutArgs), ctypes.c_void_p]),
     "gnn_layernorm_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int64]),
     "gnn_layernorm_rows": (ctypes.c_int, [ctypes.POINTER(LayerNormArgs), ctypes.c_void_p]),
     "gnn_gate_bwd_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int64]),

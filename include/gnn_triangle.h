@@ -30,6 +30,7 @@
  *   gnn_triattn_bwd   -> EvoformerAttention.backward (triangle_attention.py:1278-1442)
  *   gnn_pair_bias_proj -> _project_pair_bias of attention_pair_bias
  *                        (geometric_nn_ops_torch/triangle/_reference/attention_pair_bias.py:17-22)
+ *   gnn_apb_gate_out   -> its gate and output projection (attention_pair_bias.py:86-89)
  *   gnn_layernorm_rows, gnn_trimul_gate_bwd -> the LayerNorm and gate nodes of autograd
  *                        through trimul_torch (triangle/_trimul.py:31-36,
  *                        triangle/_reference/trimul.py:57-97): the reference's trimul
@@ -261,6 +262,33 @@ typedef struct gnn_pair_bias_args {
  * pair-rep half of attention_pair_bias (triangle/_attention_pair_bias.py:11-98); the
  * attention itself runs on gnn_triattn_fwd with N_seq = the multiplicity. */
 int gnn_pair_bias_proj(const gnn_pair_bias_args* args, void* stream);
+
+/* Gate and output projection of attention with pair bias, fused:
+ *   out = ( o * sigmoid(s g_w^T + g_b) ) o_w^T + o_b
+ * with each product rounded to the input dtype as the reference's F.linear, torch.sigmoid
+ * and multiply return it. s [M, Cs] (row pitch s_ld), o [M, D] (the attention output with
+ * heads merged, row pitch o_ld), g_w [D, Cs], o_w [Co, D] contiguous, g_b [D] / o_b [Co] or
+ * NULL, out [M, Co] (row pitch out_ld); one dtype for every tensor; fp32 products follow
+ * `precision` like the other fp32 kernels. Cs, D and Co multiples of 32, rows 16-byte
+ * aligned, and (Cs + D) small enough for the LDS tiles (up to 1024 + 1024 for 16-bit types,
+ * 512 + 512 for fp32). */
+typedef struct gnn_apb_gate_out_args {
+  const void* s;
+  const void* o;
+  const void* g_w;
+  const void* g_b;
+  const void* o_w;
+  const void* o_b;
+  void* out;
+  int64_t M, Cs, D, Co;
+  int64_t s_ld, o_ld, out_ld;
+  int32_t dtype;     /* enum gnn_dtype */
+  int32_t precision; /* enum gnn_precision */
+} gnn_apb_gate_out_args;
+
+/* Replaces the gate and output projection of attention_pair_bias_torch
+ * (geometric_nn_ops_torch/triangle/_reference/attention_pair_bias.py:86-89). */
+int gnn_apb_gate_out(const gnn_apb_gate_out_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------------
  * Backward of the triangle multiplicative update. The reference has no native backward:

@@ -51,15 +51,48 @@ def oracle(t, **kw):
 
 
 def test_uses_the_hip_kernels(monkeypatch):
-    """A forward-only GPU call goes through the pair-bias projection and attention kernels."""
+    """A forward-only GPU call goes through the pair-bias projection, attention and fused
+    gate / output projection kernels."""
     from geometric_nn_ops_torch.triangle._kernels import attention_pair_bias as K
 
     calls = []
-    real = K.pair_bias_projection_hip
-    monkeypatch.setattr(K, "pair_bias_projection_hip", lambda *a, **k: calls.append(1) or real(*a, **k))
+    for name in ("pair_bias_projection_hip", "gate_out_hip"):
+        real = getattr(K, name)
+        monkeypatch.setattr(K, name, lambda *a, _r=real, _n=name, **k: calls.append(_n) or _r(*a, **k))
     t = on_gpu(apb_inputs(1, 1, 4, 32, 32, 16, 16, seed=1), torch.bfloat16)
     out, _ = apb(**t)
-    assert calls and out.is_cuda and out.dtype == torch.bfloat16
+    assert calls == ["pair_bias_projection_hip", "gate_out_hip"] and out.is_cuda and out.dtype == torch.bfloat16
+
+
+@pytest.mark.parametrize(("dtype", "precision"),
+                         [(torch.float32, "ieee"), (torch.float32, "tf32"), (torch.bfloat16, "ieee"),
+                          (torch.float16, "ieee")], ids=["fp32_ieee", "fp32_tf32", "bf16", "fp16"])
+@pytest.mark.parametrize("biases", [True, False], ids=["biases", "no_biases"])
+def test_gate_out_kernel_matches_oracle(dtype, precision, biases):
+    """gnn_apb_gate_out on its own: c_s, attention width and c_out all different, a token
+    count that is not a multiple of the 32-token tile, s read through a padded row pitch
+    (the last 32 columns of a wider tensor), against the fp64 oracle of
+    (o * sigmoid(s Wg^T + bg)) Wo^T + bo (attention_pair_bias.py:86-89)."""
+    from geometric_nn_ops_torch.triangle._kernels import attention_pair_bias as K
+
+    M, Cs, D, Co = 77, 96, 64, 160
+    g = gen(31)
+    s_wide = torch.randn(M, Cs + 32, generator=g)
+    s = s_wide[:, 32:]
+    o = torch.randn(M, D, generator=g)
+    gw = torch.randn(D, Cs, generator=g) * Cs ** -0.5
+    ow = torch.randn(Co, D, generator=g) * D ** -0.5
+    gb = torch.randn(D, generator=g) * 0.3 if biases else None
+    ob = torch.randn(Co, generator=g) * 0.3 if biases else None
+    dev = lambda t: None if t is None else t.to(DEV, dtype)  # noqa: E731
+    with matmul_precision(precision):
+        got = K.gate_out_hip(dev(s_wide)[:, 32:], dev(o), dev(gw), dev(gb), dev(ow), dev(ob))
+    q = lambda t: None if t is None else to_np(t.to(dtype).double())  # noqa: E731
+    gate = O.sigmoid(O.linear(q(s), q(gw), q(gb)))
+    want = O.linear(q(o) * gate, q(ow), q(ob))
+    assert got.shape == (M, Co) and got.dtype == dtype
+    tol = {torch.bfloat16: 1e-2, torch.float16: 2e-3}.get(dtype, 2e-3 if precision == "tf32" else 1e-5)
+    assert O.rel_fro(to_np(got), want) <= tol
 
 
 @pytest.mark.parametrize(("dtype", "precision"),

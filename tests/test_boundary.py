@@ -53,6 +53,10 @@ def _c_layout():
       printf("gnn_layernorm_args %zu\n", sizeof(gnn_layernorm_args));
       printf("gnn_gate_bwd_args %zu\n", sizeof(gnn_gate_bwd_args));
       printf("gnn_trimul_contract_bwd_args %zu\n", sizeof(gnn_trimul_contract_bwd_args));
+      printf("gnn_apb_gate_out_args %zu\n", sizeof(gnn_apb_gate_out_args));
+      P(gnn_apb_gate_out_args, o_b) P(gnn_apb_gate_out_args, out) P(gnn_apb_gate_out_args, M)
+      P(gnn_apb_gate_out_args, Co) P(gnn_apb_gate_out_args, out_ld) P(gnn_apb_gate_out_args, dtype)
+      P(gnn_apb_gate_out_args, precision)
       P(gnn_trimul_contract_bwd_args, do_j) P(gnn_trimul_contract_bwd_args, db)
       P(gnn_trimul_contract_bwd_args, planes) P(gnn_trimul_contract_bwd_args, N) P(gnn_trimul_contract_bwd_args, dtype)
       P(gnn_layernorm_args, partial) P(gnn_layernorm_args, rows) P(gnn_layernorm_args, out_stride)
@@ -87,10 +91,12 @@ def test_ctypes_structs_match_c_layout(tmp_path):
     assert int(lines["gnn_layernorm_args"]) == ctypes.sizeof(_lib.LayerNormArgs)
     assert int(lines["gnn_gate_bwd_args"]) == ctypes.sizeof(_lib.GateBwdArgs)
     assert int(lines["gnn_trimul_contract_bwd_args"]) == ctypes.sizeof(_lib.TrimulContractBwdArgs)
+    assert int(lines["gnn_apb_gate_out_args"]) == ctypes.sizeof(_lib.ApbGateOutArgs)
     classes = {"gnn_triattn_args": _lib.TriAttnArgs, "gnn_trimul_args": _lib.TrimulArgs,
                "gnn_pair_bias_args": _lib.PairBiasArgs, "gnn_triattn_bwd_args": _lib.TriAttnBwdArgs,
                "gnn_layernorm_args": _lib.LayerNormArgs, "gnn_gate_bwd_args": _lib.GateBwdArgs,
-               "gnn_trimul_contract_bwd_args": _lib.TrimulContractBwdArgs}
+               "gnn_trimul_contract_bwd_args": _lib.TrimulContractBwdArgs,
+               "gnn_apb_gate_out_args": _lib.ApbGateOutArgs}
     for key, val in lines.items():
         if "." not in key:
             continue
@@ -297,3 +303,32 @@ def test_trimul_backward_helper_argument_errors():
     cb.N, cb.db = 64, 4104
     assert lib.gnn_trimul_contract_bwd(ctypes.byref(cb), None) == _lib.GNN_ERR_ARG
     assert b"aligned" in lib.gnn_last_error()
+
+
+def test_apb_gate_out_argument_errors():
+    """The fused gate / output projection refuses bad arguments before any launch."""
+    lib = _lib.load()
+    assert lib.gnn_apb_gate_out(None, None) == _lib.GNN_ERR_ARG
+    a = _lib.ApbGateOutArgs()
+    assert lib.gnn_apb_gate_out(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    assert b"required" in lib.gnn_last_error()
+    a.s = a.o = a.g_w = a.o_w = a.out = 4096
+    a.M, a.Cs, a.D, a.Co = 10, 64, 64, 64
+    a.s_ld = a.o_ld = a.out_ld = 64
+    a.dtype = _lib.GNN_BF16
+    a.Cs = a.s_ld = 48
+    assert lib.gnn_apb_gate_out(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
+    assert b"multiples of 32" in lib.gnn_last_error()
+    a.Cs, a.s_ld = 64, 60
+    assert lib.gnn_apb_gate_out(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    assert b"pitch" in lib.gnn_last_error()
+    a.s_ld = 64
+    a.s = 4098
+    assert lib.gnn_apb_gate_out(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    assert b"aligned" in lib.gnn_last_error()
+    a.s = 4096
+    a.Cs = a.D = a.s_ld = a.o_ld = 2048
+    assert lib.gnn_apb_gate_out(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
+    assert b"LDS" in lib.gnn_last_error()
+    a.dtype = 7
+    assert lib.gnn_apb_gate_out(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
