@@ -34,7 +34,11 @@
 // key's P is 0 either way. dq and dk / dv divide per masked key; bwd_dbias, which sees a
 // row's keys one tile at a time, per row (its lse at the sentinel): -log2(N_res) joins the
 // exp2 argument.
-// 16-bit inputs, head dim <= 32 (padded to a multiple of 8 by the host).
+// 16-bit inputs, head dim <= 128 (a multiple of 8, ensured by the host). Every kernel is
+// templated on DC, the number of 32-column chunks of the head dim (1, 2 or 4): the staged
+// tiles are DC swizzled [rows][32] tiles, the score and dP products sum over the chunks, and
+// dQ / dK / dV keep one 32 x 32 accumulator per chunk (columns past D are zeros on input and
+// not stored).
 #include "gnn_common.hpp"
 #include "gnn_internal.hpp"
 
@@ -110,17 +114,18 @@ __device__ __forceinline__ typename TypeOps<T>::V8 row8(const T* row, int d0, in
 
 // ------------------------------------------------------------------------- dK, dV
 // LDS: Q' tile and dO tile [64][32] (swizzled), lse and Delta of the tile's queries.
+template <int DC>
 struct DkdvLds {
-  unsigned char q[BT * ROWB];
-  unsigned char d[BT * ROWB];
+  unsigned char q[DC][BT * ROWB];
+  unsigned char d[DC][BT * ROWB];
   float lse[BT];
   float delta[BT];
 };
 
-template <typename T, bool HAS_BIAS>
-__global__ __launch_bounds__(BNT, 2) void bwd_dkdv_kernel(const gnn_triattn_bwd_args a) {
+template <typename T, bool HAS_BIAS, int DC>
+__global__ __launch_bounds__(BNT, DC > 2 ? 1 : 2) void bwd_dkdv_kernel(const gnn_triattn_bwd_args a) {
   typedef typename TypeOps<T>::V8 V8;
-  __shared__ __align__(16) DkdvLds sm;
+  __shared__ __align__(16) DkdvLds<DC> sm;
   const int N = (int)a.N, H = (int)a.H, D = (int)a.D;
   const int nkb = (N + 127) / 128;
   const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
@@ -139,15 +144,17 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dkdv_kernel(const gnn_triattn_bwd_
   const T* qp = (const T*)a.q + rowoff[0];
   const T* dop = (const T*)a.dout + rowoff[3];
   // this lane's key: K and V as B operands (lane = key, 8 consecutive d per lane group)
-  V8 kf[2], vf[2];
+  V8 kf[DC][2], vf[DC][2];
   {
     const T* kr = (const T*)a.k + rowoff[1] + (int64_t)(kok ? key : 0) * a.k_stride[2];
     const T* vr = (const T*)a.v + rowoff[2] + (int64_t)(kok ? key : 0) * a.v_stride[2];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      kf[kk] = row8(kr, 16 * kk + 8 * g, D, kok);
-      vf[kk] = row8(vr, 16 * kk + 8 * g, D, kok);
-    }
+    for (int dc = 0; dc < DC; ++dc)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        kf[dc][kk] = row8(kr, 32 * dc + 16 * kk + 8 * g, D, kok);
+        vf[dc][kk] = row8(vr, 32 * dc + 16 * kk + 8 * g, D, kok);
+      }
   }
   // key-side mask term: the sentinel for masked keys, -inf for keys past N (p = 0)
   float kbias = 0.f, kmul = 1.f;
@@ -164,9 +171,11 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dkdv_kernel(const gnn_triattn_bwd_
   const float* lse_row = a.lse + (((int64_t)b * a.S + s) * H + h) * N;
   const float* delta_row = a.delta + (((int64_t)b * a.S + s) * H + h) * N;
 
-  f32x16 dk, dv;
+  f32x16 dk[DC], dv[DC];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) dk[i] = dv[i] = 0.f;
+  for (int dc = 0; dc < DC; ++dc)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dk[dc][i] = dv[dc][i] = 0.f;
 
   const int ntq = (N + BT - 1) / BT;
   for (int tq = 0; tq < ntq; ++tq) {
@@ -177,10 +186,14 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dkdv_kernel(const gnn_triattn_bwd_
       const int r = tid >> 2, c = tid & 3;
       const int qi = q0 + r;
       const bool ok = qi < N;
-      V8 x = row8(qp + (int64_t)(ok ? qi : 0) * a.q_stride[2], 8 * c, D, ok);
-      const f32x8 xf = TypeOps<T>::to_f32(x) * a.scale;
-      *reinterpret_cast<V8*>(sm.q + swz(r, c)) = TypeOps<T>::from_f32(xf);
-      *reinterpret_cast<V8*>(sm.d + swz(r, c)) = row8(dop + (int64_t)(ok ? qi : 0) * a.do_stride[2], 8 * c, D, ok);
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) {
+        V8 x = row8(qp + (int64_t)(ok ? qi : 0) * a.q_stride[2], 32 * dc + 8 * c, D, ok);
+        const f32x8 xf = TypeOps<T>::to_f32(x) * a.scale;
+        *reinterpret_cast<V8*>(sm.q[dc] + swz(r, c)) = TypeOps<T>::from_f32(xf);
+        *reinterpret_cast<V8*>(sm.d[dc] + swz(r, c)) =
+            row8(dop + (int64_t)(ok ? qi : 0) * a.do_stride[2], 32 * dc + 8 * c, D, ok);
+      }
       if (tid < BT) {
         const int qq = q0 + tid;
         // absent queries: lse = +inf makes their P exactly 0 (their dO is 0 too)
@@ -197,10 +210,12 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dkdv_kernel(const gnn_triattn_bwd_
 #pragma unroll
       for (int i = 0; i < 16; ++i) sc[i] = dp[i] = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        Mma<T, PREC_NATIVE>::step(sc, lds_row8<T>(sm.q, r0 + l32, 2 * kk + g), kf[kk]);
-        Mma<T, PREC_NATIVE>::step(dp, lds_row8<T>(sm.d, r0 + l32, 2 * kk + g), vf[kk]);
-      }
+      for (int dc = 0; dc < DC; ++dc)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          Mma<T, PREC_NATIVE>::step(sc, lds_row8<T>(sm.q[dc], r0 + l32, 2 * kk + g), kf[dc][kk]);
+          Mma<T, PREC_NATIVE>::step(dp, lds_row8<T>(sm.d[dc], r0 + l32, 2 * kk + g), vf[dc][kk]);
+        }
       if constexpr (HAS_BIAS) {
         // A = bias rows (lane = query, 8 consecutive keys of the wave's 32), B = identity
         const int qi = q0 + r0 + l32;
@@ -231,38 +246,44 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dkdv_kernel(const gnn_triattn_bwd_
       // dV += P^T dO and dK += dS^T Q': A = the accumulators (lane = key, k = queries),
       // B = the staged tiles read transposed (k = queries, n = d)
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        Mma<T, PREC_NATIVE>::step(dv, acc_to_frag<T>(p, kk), tr_frag<T>(sm.d, r0, kk, lane));
-        Mma<T, PREC_NATIVE>::step(dk, acc_to_frag<T>(ds, kk), tr_frag<T>(sm.q, r0, kk, lane));
-      }
+      for (int dc = 0; dc < DC; ++dc)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          Mma<T, PREC_NATIVE>::step(dv[dc], acc_to_frag<T>(p, kk), tr_frag<T>(sm.d[dc], r0, kk, lane));
+          Mma<T, PREC_NATIVE>::step(dk[dc], acc_to_frag<T>(ds, kk), tr_frag<T>(sm.q[dc], r0, kk, lane));
+        }
     }
   }
-  // dk / dv[m = key][n = d]: lane = d (l32), rows = keys wave*32 + 8 (i / 4) + 4 g + i % 4
-  const int d = l32;
-  if (d < D) {
-    T* dkp = (T*)a.dk + b * a.dk_stride[0] + s * a.dk_stride[1] + h * a.dk_stride[3] + d;
-    T* dvp = (T*)a.dv + b * a.dv_stride[0] + s * a.dv_stride[1] + h * a.dv_stride[3] + d;
+  // dk / dv[m = key][n = d]: lane = d (32 dc + l32), rows = keys wave*32 + 8 (i / 4) + 4 g + i % 4
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int kj = kb * 128 + wave * 32 + 8 * (i / 4) + 4 * g + (i % 4);
-      if (kj < N) {
-        dkp[(int64_t)kj * a.dk_stride[2]] = TypeOps<T>::from_f32(dk[i]);
-        dvp[(int64_t)kj * a.dv_stride[2]] = TypeOps<T>::from_f32(dv[i]);
+  for (int dc = 0; dc < DC; ++dc) {
+    const int d = 32 * dc + l32;
+    if (d < D) {
+      T* dkp = (T*)a.dk + b * a.dk_stride[0] + s * a.dk_stride[1] + h * a.dk_stride[3] + d;
+      T* dvp = (T*)a.dv + b * a.dv_stride[0] + s * a.dv_stride[1] + h * a.dv_stride[3] + d;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kj = kb * 128 + wave * 32 + 8 * (i / 4) + 4 * g + (i % 4);
+        if (kj < N) {
+          dkp[(int64_t)kj * a.dk_stride[2]] = TypeOps<T>::from_f32(dk[dc][i]);
+          dvp[(int64_t)kj * a.dv_stride[2]] = TypeOps<T>::from_f32(dv[dc][i]);
+        }
       }
     }
   }
 }
 
 // ------------------------------------------------------------------------- dQ
+template <int DC>
 struct DqLds {
-  unsigned char k[BT * ROWB];
-  unsigned char v[BT * ROWB];
+  unsigned char k[DC][BT * ROWB];
+  unsigned char v[DC][BT * ROWB];
 };
 
-template <typename T, bool HAS_BIAS>
-__global__ __launch_bounds__(BNT, 2) void bwd_dq_kernel(const gnn_triattn_bwd_args a) {
+template <typename T, bool HAS_BIAS, int DC>
+__global__ __launch_bounds__(BNT, DC > 2 ? 1 : 2) void bwd_dq_kernel(const gnn_triattn_bwd_args a) {
   typedef typename TypeOps<T>::V8 V8;
-  __shared__ __align__(16) DqLds sm;
+  __shared__ __align__(16) DqLds<DC> sm;
   const int N = (int)a.N, H = (int)a.H, D = (int)a.D;
   const int nqb = (N + 127) / 128;
   const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
@@ -277,17 +298,20 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dq_kernel(const gnn_triattn_bwd_ar
   const T* kp = (const T*)a.k + b * a.k_stride[0] + s * a.k_stride[1] + h * a.k_stride[3];
   const T* vp = (const T*)a.v + b * a.v_stride[0] + s * a.v_stride[1] + h * a.v_stride[3];
   // this lane's query: Q' and dO as B operands (lane = query, 8 consecutive d)
-  V8 qf[2], dof[2];
+  V8 qf[DC][2], dof[DC][2];
   {
     const T* qr = (const T*)a.q + b * a.q_stride[0] + s * a.q_stride[1] + h * a.q_stride[3] +
                   (int64_t)(qok ? qi : 0) * a.q_stride[2];
     const T* dr = (const T*)a.dout + b * a.do_stride[0] + s * a.do_stride[1] + h * a.do_stride[3] +
                   (int64_t)(qok ? qi : 0) * a.do_stride[2];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      qf[kk] = TypeOps<T>::from_f32(TypeOps<T>::to_f32(row8(qr, 16 * kk + 8 * g, D, qok)) * a.scale);
-      dof[kk] = row8(dr, 16 * kk + 8 * g, D, qok);
-    }
+    for (int dc = 0; dc < DC; ++dc)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int d0 = 32 * dc + 16 * kk + 8 * g;
+        qf[dc][kk] = TypeOps<T>::from_f32(TypeOps<T>::to_f32(row8(qr, d0, D, qok)) * a.scale);
+        dof[dc][kk] = row8(dr, d0, D, qok);
+      }
   }
   const int64_t lrow = (((int64_t)b * a.S + s) * H + h) * N;
   const float lse = qok ? a.lse[lrow + qi] : INFINITY;  // absent queries: p = 0
@@ -298,12 +322,14 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dq_kernel(const gnn_triattn_bwd_ar
                     (int64_t)(qok ? qi : 0) * a.o_stride[2];
     float part = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const f32x8 x = TypeOps<T>::to_f32(row8(orow, 16 * kk + 8 * g, D, qok));
-      const f32x8 y = TypeOps<T>::to_f32(dof[kk]);
+    for (int dc = 0; dc < DC; ++dc)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) part = __builtin_fmaf(x[e], y[e], part);
-    }
+      for (int kk = 0; kk < 2; ++kk) {
+        const f32x8 x = TypeOps<T>::to_f32(row8(orow, 32 * dc + 16 * kk + 8 * g, D, qok));
+        const f32x8 y = TypeOps<T>::to_f32(dof[dc][kk]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) part = __builtin_fmaf(x[e], y[e], part);
+      }
     delta = part + __shfl_xor(part, 32);
     if (qok && g == 0) a.delta[lrow + qi] = delta;
   }
@@ -312,9 +338,11 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dq_kernel(const gnn_triattn_bwd_ar
   const T* brow = HAS_BIAS ? (const T*)a.bias + b * a.bias_stride[0] + h * a.bias_stride[1] +
                                  (int64_t)(qok ? qi : 0) * a.bias_stride[2]
                            : nullptr;
-  f32x16 dq;
+  f32x16 dq[DC];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) dq[i] = 0.f;
+  for (int dc = 0; dc < DC; ++dc)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dq[dc][i] = 0.f;
 
   const int ntk = (N + BT - 1) / BT;
   for (int tk = 0; tk < ntk; ++tk) {
@@ -324,8 +352,13 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dq_kernel(const gnn_triattn_bwd_ar
       const int r = tid >> 2, c = tid & 3;
       const int kj = k0 + r;
       const bool ok = kj < N;
-      *reinterpret_cast<V8*>(sm.k + swz(r, c)) = row8(kp + (int64_t)(ok ? kj : 0) * a.k_stride[2], 8 * c, D, ok);
-      *reinterpret_cast<V8*>(sm.v + swz(r, c)) = row8(vp + (int64_t)(ok ? kj : 0) * a.v_stride[2], 8 * c, D, ok);
+#pragma unroll
+      for (int dc = 0; dc < DC; ++dc) {
+        *reinterpret_cast<V8*>(sm.k[dc] + swz(r, c)) =
+            row8(kp + (int64_t)(ok ? kj : 0) * a.k_stride[2], 32 * dc + 8 * c, D, ok);
+        *reinterpret_cast<V8*>(sm.v[dc] + swz(r, c)) =
+            row8(vp + (int64_t)(ok ? kj : 0) * a.v_stride[2], 32 * dc + 8 * c, D, ok);
+      }
     }
     __syncthreads();
 #pragma unroll
@@ -336,10 +369,12 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dq_kernel(const gnn_triattn_bwd_ar
 #pragma unroll
       for (int i = 0; i < 16; ++i) sc[i] = dp[i] = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        Mma<T, PREC_NATIVE>::step(sc, lds_row8<T>(sm.k, r0 + l32, 2 * kk + g), qf[kk]);
-        Mma<T, PREC_NATIVE>::step(dp, lds_row8<T>(sm.v, r0 + l32, 2 * kk + g), dof[kk]);
-      }
+      for (int dc = 0; dc < DC; ++dc)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          Mma<T, PREC_NATIVE>::step(sc, lds_row8<T>(sm.k[dc], r0 + l32, 2 * kk + g), qf[dc][kk]);
+          Mma<T, PREC_NATIVE>::step(dp, lds_row8<T>(sm.v[dc], r0 + l32, 2 * kk + g), dof[dc][kk]);
+        }
       if constexpr (HAS_BIAS) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -365,18 +400,23 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dq_kernel(const gnn_triattn_bwd_ar
       }
       // dQ += dS K: A = dS^T accumulator (lane = query, k = keys), B = K read transposed
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-        Mma<T, PREC_NATIVE>::step(dq, acc_to_frag<T>(ds, kk), tr_frag<T>(sm.k, r0, kk, lane));
+      for (int dc = 0; dc < DC; ++dc)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+          Mma<T, PREC_NATIVE>::step(dq[dc], acc_to_frag<T>(ds, kk), tr_frag<T>(sm.k[dc], r0, kk, lane));
     }
   }
-  // dq[m = query][n = d]: lane = d, rows = queries wave*32 + 8 (i / 4) + 4 g + i % 4
-  const int d = l32;
-  if (d < D) {
-    T* dqp = (T*)a.dq + b * a.dq_stride[0] + s * a.dq_stride[1] + h * a.dq_stride[3] + d;
+  // dq[m = query][n = d]: lane = d (32 dc + l32), rows = queries wave*32 + 8 (i / 4) + 4 g + i % 4
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int qq = qb * 128 + wave * 32 + 8 * (i / 4) + 4 * g + (i % 4);
-      if (qq < N) dqp[(int64_t)qq * a.dq_stride[2]] = TypeOps<T>::from_f32(dq[i] * a.scale);
+  for (int dc = 0; dc < DC; ++dc) {
+    const int d = 32 * dc + l32;
+    if (d < D) {
+      T* dqp = (T*)a.dq + b * a.dq_stride[0] + s * a.dq_stride[1] + h * a.dq_stride[3] + d;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int qq = qb * 128 + wave * 32 + 8 * (i / 4) + 4 * g + (i % 4);
+        if (qq < N) dqp[(int64_t)qq * a.dq_stride[2]] = TypeOps<T>::from_f32(dq[dc][i] * a.scale);
+      }
     }
   }
 }
@@ -393,21 +433,23 @@ __global__ __launch_bounds__(BNT, 2) void bwd_dq_kernel(const gnn_triattn_bwd_ar
 // tile in LDS; 405 us) and a 128 x 64 tile with two workgroups per CU (384 us).
 constexpr int DB_T = 128;
 constexpr int DB_NT = 512;
-struct DbLds {
-  unsigned char q[DB_T * ROWB];
-  unsigned char d[DB_T * ROWB];
-  unsigned char k[DB_T * ROWB];
-  unsigned char v[DB_T * ROWB];
+template <int DC>
+struct DbLds {  // DC > 1 exceeds 64 KB: dynamic LDS
+  unsigned char q[DC][DB_T * ROWB];
+  unsigned char d[DC][DB_T * ROWB];
+  unsigned char k[DC][DB_T * ROWB];
+  unsigned char v[DC][DB_T * ROWB];
   float lse[DB_T];
   float delta[DB_T];
   float kb[DB_T];
   float pl2;  // -log2(N_res) when the row's keys are all masked, else 0
 };
 
-template <typename T>
+template <typename T, int DC>
 __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_bwd_args a) {
   typedef typename TypeOps<T>::V8 V8;
-  __shared__ __align__(16) DbLds sm;
+  extern __shared__ __align__(16) unsigned char db_smem[];
+  DbLds<DC>& sm = *reinterpret_cast<DbLds<DC>*>(db_smem);
   const int N = (int)a.N, H = (int)a.H, D = (int)a.D, S = (int)a.S;
   const int nt = (N + DB_T - 1) / DB_T;
   const int splits = a.dbias_splits > 1 ? a.dbias_splits : 1;
@@ -445,7 +487,7 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
 
   // staging: thread = (row r = tid / 4, chunk c = tid % 4) of each of the four tiles
   const int sr = tid >> 2, sc4 = tid & 3;
-  V8 pq, pd, pk, pv;
+  V8 pq[DC], pd[DC], pk[DC], pv[DC];
   float plse = 0.f, pdel = 0.f, pkb = 0.f;
   auto load_stage = [&](int s) {
     const int qi = q0 + sr, kj = k0 + sr;
@@ -454,10 +496,14 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
     const int64_t doo = (int64_t)b * a.do_stride[0] + (int64_t)s * a.do_stride[1] + (int64_t)h * a.do_stride[3];
     const int64_t ko = (int64_t)b * a.k_stride[0] + (int64_t)s * a.k_stride[1] + (int64_t)h * a.k_stride[3];
     const int64_t vo = (int64_t)b * a.v_stride[0] + (int64_t)s * a.v_stride[1] + (int64_t)h * a.v_stride[3];
-    pq = row8((const T*)a.q + qo + (int64_t)(qok ? qi : 0) * a.q_stride[2], 8 * sc4, D, qok);
-    pd = row8((const T*)a.dout + doo + (int64_t)(qok ? qi : 0) * a.do_stride[2], 8 * sc4, D, qok);
-    pk = row8((const T*)a.k + ko + (int64_t)(kok ? kj : 0) * a.k_stride[2], 8 * sc4, D, kok);
-    pv = row8((const T*)a.v + vo + (int64_t)(kok ? kj : 0) * a.v_stride[2], 8 * sc4, D, kok);
+#pragma unroll
+    for (int dc = 0; dc < DC; ++dc) {
+      const int c0 = 32 * dc + 8 * sc4;
+      pq[dc] = row8((const T*)a.q + qo + (int64_t)(qok ? qi : 0) * a.q_stride[2], c0, D, qok);
+      pd[dc] = row8((const T*)a.dout + doo + (int64_t)(qok ? qi : 0) * a.do_stride[2], c0, D, qok);
+      pk[dc] = row8((const T*)a.k + ko + (int64_t)(kok ? kj : 0) * a.k_stride[2], c0, D, kok);
+      pv[dc] = row8((const T*)a.v + vo + (int64_t)(kok ? kj : 0) * a.v_stride[2], c0, D, kok);
+    }
     if (sc4 == 0) {
       const int64_t lrow = (((int64_t)b * S + s) * H + h) * N;
       plse = qok ? a.lse[lrow + qi] : INFINITY;  // absent queries: p = 0
@@ -469,10 +515,13 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
     }
   };
   auto store_stage = [&]() {
-    *reinterpret_cast<V8*>(sm.q + swz(sr, sc4)) = TypeOps<T>::from_f32(TypeOps<T>::to_f32(pq) * a.scale);
-    *reinterpret_cast<V8*>(sm.d + swz(sr, sc4)) = pd;
-    *reinterpret_cast<V8*>(sm.k + swz(sr, sc4)) = pk;
-    *reinterpret_cast<V8*>(sm.v + swz(sr, sc4)) = pv;
+#pragma unroll
+    for (int dc = 0; dc < DC; ++dc) {
+      *reinterpret_cast<V8*>(sm.q[dc] + swz(sr, sc4)) = TypeOps<T>::from_f32(TypeOps<T>::to_f32(pq[dc]) * a.scale);
+      *reinterpret_cast<V8*>(sm.d[dc] + swz(sr, sc4)) = pd[dc];
+      *reinterpret_cast<V8*>(sm.k[dc] + swz(sr, sc4)) = pk[dc];
+      *reinterpret_cast<V8*>(sm.v[dc] + swz(sr, sc4)) = pv[dc];
+    }
     if (sc4 == 0) {
       sm.lse[sr] = plse;
       sm.delta[sr] = pdel;
@@ -490,12 +539,14 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
   for (int s = s_begin; s < s_end; ++s) {
     const bool has_next = s + 1 < s_end;
     if (has_next) load_stage(s + 1);
-    V8 qf[2], dof[2];
+    V8 qf[DC][2], dof[DC][2];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      qf[kk] = lds_row8<T>(sm.q, qw + l32, 2 * kk + g);
-      dof[kk] = lds_row8<T>(sm.d, qw + l32, 2 * kk + g);
-    }
+    for (int dc = 0; dc < DC; ++dc)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        qf[dc][kk] = lds_row8<T>(sm.q[dc], qw + l32, 2 * kk + g);
+        dof[dc][kk] = lds_row8<T>(sm.d[dc], qw + l32, 2 * kk + g);
+      }
     f32x4 l4[4], d4[4];
 #pragma unroll
     for (int rg = 0; rg < 4; ++rg) {
@@ -509,10 +560,12 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
 #pragma unroll
       for (int i = 0; i < 16; ++i) dp[i] = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        Mma<T, PREC_NATIVE>::step(scv, qf[kk], lds_row8<T>(sm.k, kr, 2 * kk + g));
-        Mma<T, PREC_NATIVE>::step(dp, dof[kk], lds_row8<T>(sm.v, kr, 2 * kk + g));
-      }
+      for (int dc = 0; dc < DC; ++dc)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          Mma<T, PREC_NATIVE>::step(scv, qf[dc][kk], lds_row8<T>(sm.k[dc], kr, 2 * kk + g));
+          Mma<T, PREC_NATIVE>::step(dp, dof[dc][kk], lds_row8<T>(sm.v[dc], kr, 2 * kk + g));
+        }
       const float kb = sm.kb[kr], pl2 = sm.pl2;
 #pragma unroll
       for (int rg = 0; rg < 4; ++rg)
@@ -551,25 +604,29 @@ __global__ __launch_bounds__(BNT) void bwd_dbias_reduce_kernel(const gnn_triattn
   }
 }
 
-template <typename T>
+template <typename T, int DC>
 int launch_bwd(const gnn_triattn_bwd_args& a, hipStream_t stream) {
   const int64_t nb128 = (a.N + 127) / 128;
   const dim3 grid((uint32_t)(nb128 * a.H * a.S * a.B));
   // dq first: it also writes Delta, which dk / dv and dbias read
-  if (triattn_bwd_row_applicable(a)) {
+  if (DC == 1 && triattn_bwd_row_applicable(a)) {
     const int rc = triattn_bwd_row_dq_dkdv(a, stream);
     if (rc != 0) return rc;
   } else if (a.bias) {
-    hipLaunchKernelGGL((bwd_dq_kernel<T, true>), grid, dim3(BNT), 0, stream, a);
-    hipLaunchKernelGGL((bwd_dkdv_kernel<T, true>), grid, dim3(BNT), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dq_kernel<T, true, DC>), grid, dim3(BNT), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<T, true, DC>), grid, dim3(BNT), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((bwd_dq_kernel<T, false>), grid, dim3(BNT), 0, stream, a);
-    hipLaunchKernelGGL((bwd_dkdv_kernel<T, false>), grid, dim3(BNT), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dq_kernel<T, false, DC>), grid, dim3(BNT), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<T, false, DC>), grid, dim3(BNT), 0, stream, a);
   }
   if (a.bias && a.dbias) {
     const int64_t nt = (a.N + DB_T - 1) / DB_T;
     const int splits = a.dbias_splits > 1 ? a.dbias_splits : 1;
-    hipLaunchKernelGGL(bwd_dbias_kernel<T>, dim3((uint32_t)(a.B * a.H * nt * nt * splits)), dim3(DB_NT), 0, stream, a);
+    const size_t smem = sizeof(DbLds<DC>);
+    const void* fn = (const void*)bwd_dbias_kernel<T, DC>;
+    if (smem > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    hipLaunchKernelGGL((bwd_dbias_kernel<T, DC>), dim3((uint32_t)(a.B * a.H * nt * nt * splits)), dim3(DB_NT), smem,
+                       stream, a);
     if (splits > 1) {
       const int64_t n = a.B * a.H * a.N * a.N;
       const int64_t blocks = std::min<int64_t>((n + BNT - 1) / BNT, 4096);
@@ -586,13 +643,16 @@ int triattn_bwd(const gnn_triattn_bwd_args& a, hipStream_t stream) {
     return set_error(GNN_ERR_ARG, "triangle_attention backward: dbias_splits > 1 needs dbias_ws");
   if (a.bias && a.dbias && (a.dbias_splits > a.S || a.dbias_splits > 64))
     return set_error(GNN_ERR_ARG, "triangle_attention backward: dbias_splits must be at most N_seq and 64");
-  if (a.D > 32)
-    return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention backward: head dim > 32 is not supported");
+  if (a.D > 128 || a.D % 8 != 0)
+    return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention backward: head dim must be a multiple of 8 and at most 128");
   if (a.B * a.S * a.H * ((a.N + 127) / 128) >= ((int64_t)1 << 31))
     return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention backward: grid too large");
+  const int dc = a.D <= 32 ? 1 : a.D <= 64 ? 2 : 4;  // 32-column chunks of the head dim
   switch (a.dtype) {
-    case GNN_BF16: return launch_bwd<bf16>(a, stream);
-    case GNN_F16: return launch_bwd<f16>(a, stream);
+    case GNN_BF16: return dc == 1 ? launch_bwd<bf16, 1>(a, stream) : dc == 2 ? launch_bwd<bf16, 2>(a, stream)
+                                                                             : launch_bwd<bf16, 4>(a, stream);
+    case GNN_F16: return dc == 1 ? launch_bwd<f16, 1>(a, stream) : dc == 2 ? launch_bwd<f16, 2>(a, stream)
+                                                                           : launch_bwd<f16, 4>(a, stream);
   }
   return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention backward: bf16 / fp16 only");
 }

@@ -142,9 +142,9 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
 
 
 def backward_supported(q: torch.Tensor) -> bool:
-    """Whether the HIP backward covers these inputs: 16-bit, head dim <= 32 and a multiple of 8."""
+    """Whether the HIP backward covers these inputs: 16-bit, head dim <= 128 and a multiple of 8."""
     d = q.shape[-1]
-    return q.dtype in (torch.bfloat16, torch.float16) and d <= 32 and d % 8 == 0
+    return q.dtype in (torch.bfloat16, torch.float16) and d <= 128 and d % 8 == 0
 
 
 def dbias_splits(B: int, S: int, N: int, H: int) -> int:

@@ -122,10 +122,32 @@ def test_headline_rows_bf16():
     check_against_oracle((1, 8, 512, 4, 32), torch.bfloat16, seed=41)
 
 
-def test_fp32_and_wide_heads_keep_the_torch_gradient():
-    """fp32 inputs and head dims above 32 are differentiated by the torch path."""
-    for dtype, d in ((torch.float32, 32), (torch.bfloat16, 64)):
-        check_against_oracle((1, 2, 40, 2, d), dtype, seed=51)
+def test_fp32_keeps_the_torch_gradient(monkeypatch):
+    """fp32 inputs are differentiated by the torch path (no HIP backward call)."""
+    from geometric_nn_ops_torch.triangle._kernels import triangle_attention as K
+
+    calls = []
+    real = K.triangle_attention_bwd_hip
+    monkeypatch.setattr(K, "triangle_attention_bwd_hip", lambda *a, **kw: calls.append(1) or real(*a, **kw))
+    check_against_oracle((1, 2, 40, 2, 32), torch.float32, seed=51)
+    assert calls == []
+
+
+@DTYPES
+@pytest.mark.parametrize("shape", [(1, 2, 40, 2, 64), (1, 3, 100, 2, 48), (1, 2, 130, 2, 128), (2, 2, 72, 1, 96)],
+                         ids=["n40_d64", "n100_d48", "n130_d128", "b2_n72_d96"])
+def test_wide_heads(shape, dtype, monkeypatch):
+    """Head dims above 32 (the reference's atom_d48 case, tests/test_triangle_attention.py:
+    46-51, among them) take the HIP backward: the tiled kernels in 32-column chunks of the
+    head dim (D = 48 and 64 in two, 96 and 128 in four, the columns past D zero), against
+    the oracle's gradients with bias and mask."""
+    from geometric_nn_ops_torch.triangle._kernels import triangle_attention as K
+
+    calls = []
+    real = K.triangle_attention_bwd_hip
+    monkeypatch.setattr(K, "triangle_attention_bwd_hip", lambda *a, **kw: calls.append(1) or real(*a, **kw))
+    check_against_oracle(shape, dtype, seed=53)
+    assert calls == [1]
 
 
 def test_backward_twice_with_retained_graph_and_no_second_derivative():
