@@ -79,6 +79,9 @@ constexpr float RESCALE_THRESHOLD = 8.0f / LOG2E;
 #ifndef GNN_ROW_VPREFETCH  // a 32-key half's V^T fragments read before its exponentials
 #define GNN_ROW_VPREFETCH 0   // measured neutral
 #endif
+#ifndef GNN_ROW_QPREFETCH  // 1: a wave's first q requested with the K / V staging, and (no-bias
+#define GNN_ROW_QPREFETCH 1   // kernel) the next block's q during the current sweep; 2: that also
+#endif                        // with bias (spills at 128 VGPRs); 0: each q loaded where it is used
 #ifndef GNN_ROW_HEADS_FIRST_BYTES
 #define GNN_ROW_HEADS_FIRST_BYTES (8 << 20)
 #endif
@@ -223,6 +226,7 @@ __device__ __forceinline__ typename TypeOps<T>::V4 tr_read4_r(const unsigned cha
 template <typename T, bool HAS_BIAS, int NW>
 __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel(const gnn_triattn_args a) {
   constexpr int NT = NW * 64;
+  constexpr bool QPF_SWEEP = GNN_ROW_QPREFETCH && (GNN_ROW_QPREFETCH == 2 || !HAS_BIAS);
   typedef typename TypeOps<T>::V8 V8;
   typedef typename TypeOps<T>::V4 V4;
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -264,6 +268,20 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
+  // q of query block qb for this lane, unconditionally loaded (row clamped to N - 1, columns
+  // past D read from column 0 and zeroed when used)
+  const int nqb = (N + 31) / 32;
+  const T* qrow = (const T*)a.q + b * a.q_stride[0] + s * a.q_stride[1] + h * a.q_stride[3];
+  auto load_q = [&](typename TypeOps<T>::V8 (&qr)[2], int qb) {
+    const T* qp = qrow + (int64_t)min(qb * 32 + l32, N - 1) * a.q_stride[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int d0 = 16 * t + 8 * g;
+      qr[t] = load8(qp + (d0 < D ? d0 : 0));
+    }
+  };
+  typename TypeOps<T>::V8 qraw[2];
+
   const int64_t ksn = a.k_stride[2], vsn = a.v_stride[2];
   const T* kp = (const T*)a.k + b * a.k_stride[0] + s * a.k_stride[1] + h * a.k_stride[3];
   const T* vp = (const T*)a.v + b * a.v_stride[0] + s * a.v_stride[1] + h * a.v_stride[3];
@@ -285,6 +303,8 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
       __builtin_amdgcn_global_load_lds((const void*)(vp + (int64_t)r * vsn + 8 * lch),
                                        (__attribute__((address_space(3))) void*)(vs + q * 1024), 16, 0, 0);
     }
+    // the wave's first query block's q, behind its staging so that it lands with it
+    if (GNN_ROW_QPREFETCH && wave < nqb) load_q(qraw, wave);
   } else {
     // D < 32: through registers, so that columns D .. 31 are zero. Chunk c = key c / 4,
     // columns 8 (c % 4) .. + 7; rows past N are zero.
@@ -314,6 +334,7 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
         }
       }
     }
+    if (GNN_ROW_QPREFETCH && wave < nqb) load_q(qraw, wave);
   }
 
   // ---- key liveness of the row, the tiles to run and the per-key mask term (wave 0):
@@ -371,7 +392,6 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
 
   // exact row maxima are only tracked for callers that ask for them (per-tile maximum pass)
   const bool want_max = a.row_max != nullptr;
-  const int nqb = (N + 31) / 32;
   for (int qblk = wave; qblk < nqb; qblk += NW) {
     // The first tiles' LDS reads are the same for every query block; keeping the compiler
     // from hoisting them out of this loop keeps their registers free for the key loop.
@@ -379,7 +399,17 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
     const int myq = qblk * 32 + l32;
     const bool qok = myq < N;
     V8 qf[2];
-    {
+    if (GNN_ROW_QPREFETCH) {
+      // later blocks: requested during the previous block's sweep (no-bias kernel, which has
+      // the registers to spare) or here
+      if (!QPF_SWEEP && qblk != wave) load_q(qraw, qblk);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int d0 = 16 * t + 8 * g;
+        f32x8 x = TypeOps<T>::to_f32(qraw[t]);
+        qf[t] = (qok && d0 < D) ? TypeOps<T>::from_f32(x * a.scale) : zero8<T>();
+      }
+    } else {
       const T* qp = (const T*)a.q + b * a.q_stride[0] + s * a.q_stride[1] + h * a.q_stride[3] +
                     (int64_t)(qok ? myq : 0) * a.q_stride[2];
 #pragma unroll
@@ -399,6 +429,13 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
     f32x16 o;
     float m, lsum, mx;
     BiasFragR<T> bb;
+    // the next block's q, requested after this block's first bias tile (so that waiting for
+    // that tile does not wait for it) and in flight during the sweep
+    bool qnext_sent = false;
+    auto prefetch_q = [&]() {
+      if (GNN_ROW_QPREFETCH && QPF_SWEEP && !qnext_sent && qblk + NW < nqb) load_q(qraw, qblk + NW);
+      qnext_sent = true;
+    };
 
     // S^T (+ bias, + key mask term on partial tiles) of tile t into acc: acc[sub][i] is key
     // t*64 + sub*32 + 8*(i/4) + 4g + i%4.
@@ -531,6 +568,7 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
         // no masked key: tiles in order; only the last one can hold keys past N
         const bool tail = N % KT != 0;
         if constexpr (HAS_BIAS) load_bias_tile<T>(bb, btile);
+        prefetch_q();
         if (GNN_ROW_KPREFETCH) load_k(kf, 0);
         for (int t = 0; t < ntiles; ++t) {
           f32x16 sc[2];
@@ -543,6 +581,7 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
         }
       } else {
         if constexpr (HAS_BIAS) load_bias_tile<T>(bb, btile + hdr.tile_list[0] * BIAS_TILE_ELEMS);
+        prefetch_q();
         if (GNN_ROW_KPREFETCH) load_k(kf, hdr.tile_list[0]);
         for (int it = 0; it < nrun; ++it) {
           const int t = hdr.tile_list[it];
