@@ -30,6 +30,8 @@ that of the dominant kernel, its bound chosen by arithmetic intensity against th
   * ``cold_ms``: every kernel again after a 512 MiB scratch write (inputs then come from HBM,
     not from the Infinity Cache that holds them in the warm loop);
   * ``graph_ms_per_step``: the step captured once as a HIP graph and replayed;
+  * ``hbm_reference``: a 1 GiB device copy (read + write) and fill timed the same way, the
+    streaming rate these boxes reach; HBM-bound kernels also report ``frac_of_copy``;
   * ``attention_backward`` / ``trimul_backward``: the gradient paths, outside the step.
 """
 
@@ -383,6 +385,22 @@ def main():
     except Exception as exc:  # pragma: no cover - reported, eager numbers stand
         print(f"bench.py: HIP graph capture failed, eager timing used: {exc}", file=sys.stderr)
 
+    # ---- what plain streaming reaches on this device: a 1 GiB device copy (read + write) and
+    # a 1 GiB fill, each timed as the kernels are; the memory-bound kernels' GB/s compare to these
+    hbm_ref = None
+    if args.only is None:
+        csrc = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
+        cdst = torch.empty_like(csrc)
+        copy_ms, _, _ = window_ms(lambda: cdst.copy_(csrc), stream)
+        fill_ms, _, _ = window_ms(lambda: cdst.fill_(1), stream)
+        hbm_ref = {"copy_gbs": round(2 * csrc.numel() / (copy_ms * 1e-3) / 1e9, 1),
+                   "fill_gbs": round(cdst.numel() / (fill_ms * 1e-3) / 1e9, 1),
+                   "copy_frac_of_peak": round(2 * csrc.numel() / (copy_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        for r in per_kernel.values():
+            if r["bound"] == "hbm":
+                r["frac_of_copy"] = round(r["gbs"] / hbm_ref["copy_gbs"], 4)
+        del csrc, cdst
+
     # ---- cold: each launch after a scratch write larger than L2 + Infinity Cache
     cold_ms = {}
     if args.cold_steps > 0:
@@ -525,6 +543,7 @@ def main():
         "graph_ms_per_step": round(graph_ms, 5) if graph_ms is not None else None,
         "graph_replays_match_eager": graph_ok,
         "kernels": per_kernel,
+        "hbm_reference": hbm_ref,
         "parity": gate,
         "cold_ms": cold_ms,
         "cold_ms_per_step": round(sum(cold_ms.values()), 5) if cold_ms else None,
