@@ -333,5 +333,19 @@ def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+def call(fn_name: str, args, device: torch.device) -> None:
+    """``fn_name(&args, stream)`` on ``device``'s current stream, with ``device`` current for
+    the call (the current device is switched only when it differs: the guard costs host time
+    on every launch), raising on a non-zero status."""
+    fn = getattr(load(), fn_name)
+    idx = device.index
+    if idx is None or idx == torch.cuda.current_device():
+        rc = fn(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream))
+    else:
+        with torch.cuda.device(idx):
+            rc = fn(ctypes.byref(args), ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream))
+    check(rc, fn_name)
+
+
 def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()

@@ -9,17 +9,28 @@ operators are forward-only, like the reference's Triton kernels).
 
 Registration follows the boundary the reference's callers bind
 (geometric_nn_ops_torch/triangle/_triattn.py:96, _trimul.py:87).
+
+The operator dispatch costs about 10 us of host time per call, so a plain eager call on real
+tensors (``eager_ok``) runs the same implementation function directly (``*_impl``); under
+torch.compile, FakeTensor or any dispatch mode the callers go through the operator.
 """
 
 from typing import Optional
 
 import torch
 
-__all__ = ["triangle_attention_fwd", "trimul_fwd", "attention_pair_bias_fwd"]
+__all__ = ["triangle_attention_fwd", "trimul_fwd", "attention_pair_bias_fwd", "eager_ok"]
 
 
-@torch.library.custom_op("gnn_amd::triangle_attention_fwd", mutates_args=())
-def triangle_attention_fwd(
+def eager_ok(*tensors) -> bool:
+    """True for an eager call whose tensor arguments are plain tensors (or None) with no
+    tracing or dispatch mode active: the operator's implementation may then run directly."""
+    if torch.compiler.is_compiling() or torch._C._len_torch_dispatch_stack() > 0:
+        return False
+    return all(t is None or type(t) is torch.Tensor for t in tensors)
+
+
+def triangle_attention_fwd_impl(
     q: torch.Tensor,
     k: torch.Tensor,
     v: torch.Tensor,
@@ -35,13 +46,16 @@ def triangle_attention_fwd(
     return triangle_attention_hip(q, k, v, bias=bias, mask=mask, scale=scale)
 
 
+triangle_attention_fwd = torch.library.custom_op("gnn_amd::triangle_attention_fwd", triangle_attention_fwd_impl,
+                                                 mutates_args=())
+
+
 @triangle_attention_fwd.register_fake
 def _triangle_attention_fwd_fake(q, k, v, bias, mask, scale):
     return q.new_empty(q.shape)
 
 
-@torch.library.custom_op("gnn_amd::trimul_fwd", mutates_args=())
-def trimul_fwd(
+def trimul_fwd_impl(
     x: torch.Tensor,
     direction: str,
     mask: Optional[torch.Tensor],
@@ -73,13 +87,15 @@ def trimul_fwd(
     )
 
 
+trimul_fwd = torch.library.custom_op("gnn_amd::trimul_fwd", trimul_fwd_impl, mutates_args=())
+
+
 @trimul_fwd.register_fake
 def _trimul_fwd_fake(x, direction, mask, *weights_and_eps):
     return x.new_empty(x.shape)
 
 
-@torch.library.custom_op("gnn_amd::attention_pair_bias_fwd", mutates_args=())
-def attention_pair_bias_fwd(
+def attention_pair_bias_fwd_impl(
     s: torch.Tensor,
     q: torch.Tensor,
     k: torch.Tensor,
@@ -110,6 +126,10 @@ def attention_pair_bias_fwd(
     if z_is_projected:
         return out, z.new_empty((0,))
     return out, pz.contiguous()
+
+
+attention_pair_bias_fwd = torch.library.custom_op("gnn_amd::attention_pair_bias_fwd", attention_pair_bias_fwd_impl,
+                                                  mutates_args=())
 
 
 @attention_pair_bias_fwd.register_fake

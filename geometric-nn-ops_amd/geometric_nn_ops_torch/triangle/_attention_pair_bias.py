@@ -92,7 +92,9 @@ def attention_pair_bias(
             proj_o_bias=proj_o_bias, mask=mask, scale=scale, inf=inf, eps=eps,
             z_is_projected=z_is_projected, return_z_proj=return_z_proj,
         )
-    out, pz = _ops.attention_pair_bias_fwd(
+    fwd = _ops.attention_pair_bias_fwd_impl if _ops.eager_ok(s, q, k, v, z, mask, *weights) else \
+        _ops.attention_pair_bias_fwd
+    out, pz = fwd(
         s, q, k, v, z, proj_g_weight, proj_o_weight, proj_z_weight, ln_z_weight, proj_g_bias,
         proj_o_bias, mask, scale, inf, eps, z_is_projected,
     )

@@ -39,7 +39,6 @@ def projection_supported(z: torch.Tensor, heads: int) -> bool:
 def pair_bias_projection_hip(z, ln_z_weight, proj_z_weight, eps=1e-5):
     """``z [B, U, V, Zc]`` -> ``[B, H, U, V]`` in z's dtype. The result is a view with a
     row pitch rounded up to 8 elements (what the attention kernel reads without a copy)."""
-    lib = _lib.load()
     B, U, V, Zc = z.shape
     H = proj_z_weight.shape[0]
     z = z.contiguous()
@@ -54,9 +53,7 @@ def pair_bias_projection_hip(z, ln_z_weight, proj_z_weight, eps=1e-5):
     a.out_stride = _lib.I64x3(buf.stride(0), buf.stride(1), buf.stride(2))
     a.eps = float(eps)
     a.dtype = _lib.DTYPE_CODE[z.dtype]
-    with torch.cuda.device(z.device):
-        rc = lib.gnn_pair_bias_proj(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(z.device)))
-    _lib.check(rc, "gnn_pair_bias_proj")
+    _lib.call("gnn_pair_bias_proj", a, z.device)
     return buf[..., :V]
 
 
@@ -81,7 +78,6 @@ def gate_out_supported(s, o_width, proj_g_weight, proj_o_weight) -> bool:
 def gate_out_hip(s, o, proj_g_weight, proj_g_bias, proj_o_weight, proj_o_bias):
     """``(o * sigmoid(s W_g^T + b_g)) W_o^T + b_o`` for ``s [..., Cs]``, ``o [..., D]`` in one
     kernel; returns ``[..., Co]`` in s's dtype."""
-    lib = _lib.load()
     dt = s.dtype
     lead = s.shape[:-1]
     cs, d, co = s.shape[-1], o.shape[-1], proj_o_weight.shape[0]
@@ -103,9 +99,7 @@ def gate_out_hip(s, o, proj_g_weight, proj_g_bias, proj_o_weight, proj_o_bias):
     a.s_ld, a.o_ld, a.out_ld = s2.stride(0), o2.stride(0), out.stride(0)
     a.dtype = _lib.DTYPE_CODE[dt]
     a.precision = _lib.PRECISION_CODE[_precision.matmul_precision(fp32_operands=dt == torch.float32)]
-    with torch.cuda.device(s.device):
-        rc = lib.gnn_apb_gate_out(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(s.device)))
-    _lib.check(rc, "gnn_apb_gate_out")
+    _lib.call("gnn_apb_gate_out", a, s.device)
     return out.reshape(*lead, co)
 
 

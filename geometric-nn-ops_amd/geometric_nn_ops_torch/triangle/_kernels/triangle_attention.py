@@ -26,8 +26,10 @@ def supports(q: torch.Tensor) -> bool:
     return q.shape[-1] <= MAX_HEAD_DIM and q.shape[-3] <= MAX_N_RES
 
 
-def _vectorizable(t: torch.Tensor, dims) -> bool:
-    return t.data_ptr() % 16 == 0 and t.stride(-1) == 1 and all(t.stride(d) % 8 == 0 for d in dims)
+def _vectorizable(t: torch.Tensor) -> bool:
+    """Unit stride on the last dim, the other strides multiples of 8 elements, 16-byte base."""
+    st = t.stride()
+    return t.data_ptr() % 16 == 0 and st[-1] == 1 and all(x % 8 == 0 for x in st[:-1])
 
 
 def _prepare(t: torch.Tensor) -> torch.Tensor:
@@ -36,9 +38,9 @@ def _prepare(t: torch.Tensor) -> torch.Tensor:
     d = t.shape[-1]
     if d % 8:
         t = torch.nn.functional.pad(t, (0, 8 - d % 8))
-    if not _vectorizable(t, range(t.dim() - 1)):
+    if not _vectorizable(t):
         t = t.contiguous()
-        if not _vectorizable(t, range(t.dim() - 1)):
+        if not _vectorizable(t):
             t = t.clone()
     return t
 
@@ -84,7 +86,6 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
     reference launcher applies it).
     """
     del dynamic, use_exp2
-    lib = _lib.load()
     if q.dtype not in _lib.DTYPE_CODE:
         raise TypeError(f"triangle_attention_hip: unsupported dtype {q.dtype}")
     dim_q, dim_k, dim_v = q.shape[-1], k.shape[-1], v.shape[-1]
@@ -132,9 +133,7 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
     args.precision = _lib.PRECISION_CODE[precision]
 
     ws = workspace_for(args, q.device)
-    with torch.cuda.device(q.device):
-        rc = lib.gnn_triattn_fwd(ctypes.byref(args), ctypes.c_void_p(_lib.stream_handle(q.device)))
-    _lib.check(rc, "gnn_triattn_fwd")
+    _lib.call("gnn_triattn_fwd", args, q.device)
     del ws
     if Dp != D:
         o = o[..., :D].contiguous()
@@ -160,7 +159,6 @@ def triangle_attention_bwd_hip(q, k, v, o, dout, lse, bias=None, mask=None, scal
     ``[B, 1, H, N, N]`` fp32 (``None`` without a bias or when ``need_dbias`` is false).
     Replaces EvoformerAttention.backward (triangle_attention.py:1278-1442); ``lse`` is the
     forward's ``[B, N_seq, H, N]`` natural-log log-sum-exp."""
-    lib = _lib.load()
     B, S, N, H, D = q.shape
     if scale is None:
         scale = D**-0.5
@@ -203,7 +201,5 @@ def triangle_attention_bwd_hip(q, k, v, o, dout, lse, bias=None, mask=None, scal
     a.mask_value = rounded_mask_value(q.dtype) if mask_value is None else float(mask_value)
     a.dtype = _lib.DTYPE_CODE[q.dtype]
     a.precision = _lib.GNN_PREC_IEEE
-    with torch.cuda.device(q.device):
-        rc = lib.gnn_triattn_bwd(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(q.device)))
-    _lib.check(rc, "gnn_triattn_bwd")
+    _lib.call("gnn_triattn_bwd", a, q.device)
     return dq, dk, dv, dbias

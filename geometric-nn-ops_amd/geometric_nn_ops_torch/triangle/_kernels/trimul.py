@@ -38,13 +38,21 @@ def supports(x: torch.Tensor, p_in_weight: torch.Tensor) -> bool:
 
 
 def _expect(name, t, shape):
-    if t is not None and tuple(t.shape) != tuple(shape):
+    if t is not None and t.shape != shape:
         raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
 
 
 def _aligned(t: torch.Tensor) -> torch.Tensor:
     t = t.contiguous()
     return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _kernel_ready(t: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
+    """``t`` on ``like``'s device and dtype, contiguous and 16-byte aligned (as is, when it
+    already is: the usual case for parameters, and the checks are cheaper than the copies)."""
+    if t.dtype == like.dtype and t.device == like.device and t.is_contiguous() and t.data_ptr() % 16 == 0:
+        return t
+    return _aligned(t.to(device=like.device, dtype=like.dtype))
 
 
 def build_args(x, direction, mask, eps, weights):
@@ -87,7 +95,7 @@ def build_args(x, direction, mask, eps, weights):
         w = weights.get(key)
         if w is None:
             continue
-        w = _aligned(w.to(device=x.device, dtype=x.dtype))
+        w = _kernel_ready(w, x)
         keep.append(w)
         setattr(args, _ARG_FIELD[key], w.data_ptr())
     dtype = _lib.DTYPE_CODE[x.dtype]
@@ -106,10 +114,7 @@ def build_args(x, direction, mask, eps, weights):
 
 
 def run_stage(fn_name: str, args, device) -> None:
-    lib = _lib.load()
-    with torch.cuda.device(device):
-        rc = getattr(lib, fn_name)(ctypes.byref(args), ctypes.c_void_p(_lib.stream_handle(device)))
-    _lib.check(rc, fn_name)
+    _lib.call(fn_name, args, device)
 
 
 def trimul_hip(
@@ -185,9 +190,7 @@ def layernorm_rows_hip(x2d, weight=None, bias=None, eps=1e-5, *, dy=None, partia
             part = torch.empty((lib.gnn_layernorm_partials(R, K), 2, K), device=x2d.device,
                                dtype=torch.float32)
             a.partial = part.data_ptr()
-    with torch.cuda.device(x2d.device):
-        rc = lib.gnn_layernorm_rows(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(x2d.device)))
-    _lib.check(rc, "gnn_layernorm_rows")
+    _lib.call("gnn_layernorm_rows", a, x2d.device)
     if part is None:
         return out
     sums = part.sum(0)
@@ -218,9 +221,7 @@ def gate_bwd_hip(grad, value, gate_pre, mask_rows=None, *, d_value=None, d_gate_
     a.grad_stride, a.value_stride, a.gate_stride = grad.stride(0), value.stride(0), gate_pre.stride(0)
     a.dv_stride, a.dg_stride = d_value.stride(0), d_gate_pre.stride(0)
     a.dtype = _lib.DTYPE_CODE[grad.dtype]
-    with torch.cuda.device(grad.device):
-        rc = lib.gnn_trimul_gate_bwd(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(grad.device)))
-    _lib.check(rc, "gnn_trimul_gate_bwd")
+    _lib.call("gnn_trimul_gate_bwd", a, grad.device)
     if not sums:
         return d_value, d_gate_pre
     if part is not None:
@@ -244,7 +245,7 @@ def _wgrad(d, t, slices=64):
 def _operand(ws, off, B, Ch, N, NP, dtype):
     """The contraction operand of the workspace as ``[B * Ch, N, N]`` (row = output index,
     column = contraction index), contiguous."""
-    el = torch.tensor([], dtype=dtype).element_size()
+    el = torch.empty((), dtype=dtype).element_size()
     n = B * Ch * N * NP
     flat = ws[off:off + n * el].view(dtype)
     if el == 2:  # k-blocked [B, Ch, NP / 32, N, 32]
@@ -256,15 +257,12 @@ def _operand(ws, off, B, Ch, N, NP, dtype):
 
 def relayout_hip(src, dst, mode, B, N, Ch, *, src_ld, dst_ld, src_c0=0, dst_c0=0, transposed=False):
     """gnn_trimul_relayout (16-bit) between pixel-major rows and per-channel planes."""
-    lib = _lib.load()
     a = _lib.TrimulRelayoutArgs()
     a.src, a.dst = src.data_ptr(), dst.data_ptr()
     a.B, a.N, a.Ch = B, N, Ch
     a.src_ld, a.dst_ld, a.src_c0, a.dst_c0 = src_ld, dst_ld, src_c0, dst_c0
     a.mode, a.transposed, a.dtype = mode, int(transposed), _lib.DTYPE_CODE[src.dtype]
-    with torch.cuda.device(src.device):
-        rc = lib.gnn_trimul_relayout(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(src.device)))
-    _lib.check(rc, "gnn_trimul_relayout")
+    _lib.call("gnn_trimul_relayout", a, src.device)
     return dst
 
 
@@ -273,7 +271,6 @@ def contract_bwd_hip(workspace, offsets, do_pm, B, Ch, N):
     ``dA_c = dO_c B_c`` and ``dB_c = dO_c^T A_c``, with A and B read in place from the
     forward's ``workspace`` and dO given pixel-major, ``do_pm`` ``[B N N, Ch]`` (plane c of
     batch b: dO_c[i, j] = do_pm[(b, i, j), c])."""
-    lib = _lib.load()
     dt, dev = do_pm.dtype, do_pm.device
     NP = (N + 31) // 32 * 32
     do_i = torch.empty((B, Ch, NP // 32, NP, 32), device=dev, dtype=dt)  # [i / 32][j][i % 32]
@@ -288,9 +285,7 @@ def contract_bwd_hip(workspace, offsets, do_pm, B, Ch, N):
     a.b = workspace.data_ptr() + offsets[1]
     a.do_i, a.do_j, a.da, a.db = do_i.data_ptr(), do_j.data_ptr(), da.data_ptr(), db.data_ptr()
     a.planes, a.N, a.dtype = B * Ch, N, _lib.DTYPE_CODE[dt]
-    with torch.cuda.device(dev):
-        rc = lib.gnn_trimul_contract_bwd(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(dev)))
-    _lib.check(rc, "gnn_trimul_contract_bwd")
+    _lib.call("gnn_trimul_contract_bwd", a, dev)
     return da, db
 
 

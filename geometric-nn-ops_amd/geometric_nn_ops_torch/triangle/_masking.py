@@ -4,6 +4,8 @@ Same sentinel values and spelling as the reference (geometric_nn_ops_torch/trian
 _masking.py:13-42): kept keys get exactly +0.0 and masked keys -mask_val(dtype).
 """
 
+import functools
+
 import torch
 
 
@@ -33,8 +35,10 @@ def masked_key_bias(mask: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return mask_val(dtype) * (mask.to(torch.float32) - 1)
 
 
+@functools.lru_cache(maxsize=None)
 def rounded_mask_value(dtype: torch.dtype) -> float:
     """The masked-key bias after the cast to the compute dtype, as the Triton launcher
-    applies it (triangle_attention.py:1470: ``masked_key_bias(mask, q.dtype).to(q.dtype)``)."""
+    applies it (triangle_attention.py:1470: ``masked_key_bias(mask, q.dtype).to(q.dtype)``).
+    One value per dtype, computed once (it is on every call's path)."""
     sentinel = torch.tensor(-mask_val(dtype), dtype=torch.float32)
     return float(sentinel.to(dtype).to(torch.float32))

@@ -125,7 +125,8 @@ def triangle_attention(
         return o.to(orig_dtype).reshape(orig_shape)
 
     compute_dtype = orig_dtype if orig_dtype in _KERNEL_DTYPES else torch.float32
-    o = _ops.triangle_attention_fwd(
+    fwd = _ops.triangle_attention_fwd_impl if _ops.eager_ok(q, k, v, bias, mask) else _ops.triangle_attention_fwd
+    o = fwd(
         q.to(compute_dtype),
         k.to(compute_dtype),
         v.to(compute_dtype),

@@ -120,4 +120,5 @@ def triangle_multiplicative_update(
         return trimul_torch(x, direction, mask, eps=eps, **weights)
     if _needs_grad(x, weights.items()):
         return _TrimulHip.apply(x, direction, mask, eps, *(weights[k] for k in _hip._WEIGHT_KEYS))
-    return _ops.trimul_fwd(x, direction, mask, eps=eps, **weights)
+    fwd = _ops.trimul_fwd_impl if _ops.eager_ok(x, mask, *weights.values()) else _ops.trimul_fwd
+    return fwd(x, direction, mask, eps=eps, **weights)
