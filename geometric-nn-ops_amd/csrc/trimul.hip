@@ -298,7 +298,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_kernel(const gnn_trimul_ar
   const int npg = 2 * Ch / 32, ngo = C / 32;
   T* __restrict__ a_cm = (T*)((unsigned char*)a.workspace + off_a);
   T* __restrict__ b_cm = (T*)((unsigned char*)a.workspace + off_b);
-  T* __restrict__ gout = (T*)((unsigned char*)a.workspace + off_g);
+  T* __restrict__ gout = (T*)(a.gate ? (unsigned char*)a.gate : (unsigned char*)a.workspace + off_g);
   const T* __restrict__ wp = (const T*)a.p_in_w;
   const T* __restrict__ wg = (const T*)a.g_in_w;
   const T* __restrict__ wgo = (const T*)a.g_out_w;
@@ -588,7 +588,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
   const int npg = 2 * Ch / 32;
   T* __restrict__ a_cm = (T*)((unsigned char*)a.workspace + off_a);
   T* __restrict__ b_cm = (T*)((unsigned char*)a.workspace + off_b);
-  T* __restrict__ gout = (T*)((unsigned char*)a.workspace + off_g);
+  T* __restrict__ gout = (T*)(a.gate ? (unsigned char*)a.gate : (unsigned char*)a.workspace + off_g);
   V8 wpf[NKS], wgf[NKS];
   float bp = 0.f, bg = 0.f;
   int wp_unit = -1;
@@ -936,7 +936,8 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
 
   const T* __restrict__ ocm = (const T*)((const unsigned char*)a.workspace + off_o);
   const int64_t blk = (((int64_t)b * N + p) * N + q0) * C;
-  const T* __restrict__ gblk = (const T*)((const unsigned char*)a.workspace + off_g) + blk;
+  const T* __restrict__ gblk =
+      (const T*)(a.gate ? (const unsigned char*)a.gate : (const unsigned char*)a.workspace + off_g) + blk;
   T* __restrict__ oblk = (T*)a.out + blk;
 
   V8 gr[OCH];
@@ -1382,10 +1383,10 @@ int check_args(const gnn_trimul_args& a, const char* who) {
     return set_error(GNN_ERR_UNSUPPORTED, "trimul: c_z and c_hidden above 512 are not supported");
   if (a.dtype != GNN_BF16 && a.dtype != GNN_F16 && a.dtype != GNN_F32)
     return set_error(GNN_ERR_ARG, "trimul: unknown dtype");
-  const void* vec[] = {a.x, a.out, a.p_in_w, a.g_in_w, a.p_out_w, a.g_out_w, a.workspace};
+  const void* vec[] = {a.x, a.out, a.p_in_w, a.g_in_w, a.p_out_w, a.g_out_w, a.workspace, a.gate};
   for (const void* ptr : vec)
     if (((uintptr_t)ptr) % 16 != 0)
-      return set_error(GNN_ERR_ARG, "trimul: x, out, weights and workspace must be 16-byte aligned");
+      return set_error(GNN_ERR_ARG, "trimul: x, out, weights, workspace and gate must be 16-byte aligned");
   const size_t e = a.dtype == GNN_F32 ? 4 : 2;
   if (e == 4 && (a.C > 256 || a.Ch > 256))
     return set_error(GNN_ERR_UNSUPPORTED, "trimul: fp32 c_z and c_hidden above 256 are not supported");
@@ -1396,8 +1397,10 @@ int check_args(const gnn_trimul_args& a, const char* who) {
   if (a.B * a.N * ((a.N + PTO - 1) / PTO) >= ((int64_t)1 << 31))
     return set_error(GNN_ERR_UNSUPPORTED, "trimul: grid too large");
   const TrimulLayout L = trimul_layout(a.B, a.N, a.C, a.Ch, a.dtype);
-  if (!a.workspace || a.workspace_bytes < L.total)
-    return set_error(GNN_ERR_WORKSPACE, "trimul: workspace missing or smaller than gnn_trimul_workspace_bytes()");
+  // with a separate gate buffer the workspace holds a, b and o only (the gate region is last)
+  if (!a.workspace || a.workspace_bytes < (a.gate ? L.off_g : L.total))
+    return set_error(GNN_ERR_WORKSPACE, "trimul: workspace missing or smaller than gnn_trimul_workspace_bytes() "
+                                        "(its gate offset when args.gate is set)");
   return GNN_OK;
 }
 
@@ -1411,8 +1414,8 @@ TrimulLayout trimul_layout(int64_t B, int64_t N, int64_t C, int64_t Ch, int32_t 
   TrimulLayout L;
   L.off_a = 0;
   L.off_b = cm;
-  L.off_g = 2 * cm;
-  L.off_o = 2 * cm + pm;
+  L.off_o = 2 * cm;
+  L.off_g = 3 * cm;  // last, so that a caller with its own gate buffer can stop the workspace there
   L.total = 3 * cm + pm;
   return L;
 }

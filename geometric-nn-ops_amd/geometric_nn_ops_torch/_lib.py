@@ -128,6 +128,7 @@ class TrimulArgs(ctypes.Structure):
         ("outgoing", ctypes.c_int32),
         ("dtype", ctypes.c_int32),
         ("precision", ctypes.c_int32),
+        ("gate", ctypes.c_void_p),
     ]
 
 

@@ -55,8 +55,10 @@ def _kernel_ready(t: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
     return _aligned(t.to(device=like.device, dtype=like.dtype))
 
 
-def build_args(x, direction, mask, eps, weights):
-    """Validated, kernel-ready tensors and the filled ``gnn_trimul_args``.
+def build_args(x, direction, mask, eps, weights, separate_gate=False):
+    """Validated, kernel-ready tensors and the filled ``gnn_trimul_args``. With
+    ``separate_gate`` the output gate gets a buffer of its own (in the keepalive list) and the
+    workspace holds only a, b and o, which is what a backward needs.
 
     Returns (args, keepalive, out, workspace, offsets)."""
     outgoing = is_outgoing(direction)
@@ -102,6 +104,11 @@ def build_args(x, direction, mask, eps, weights):
     offsets = (ctypes.c_size_t * 4)()
     lib = _lib.load()
     nbytes = lib.gnn_trimul_workspace_bytes(B, N, C, Ch, dtype, offsets)
+    if separate_gate:  # the gate region is the workspace's last: stop before it
+        nbytes = offsets[2]
+        gate = torch.empty((B, N, N, C), device=x.device, dtype=x.dtype)
+        keep.append(gate)
+        args.gate = gate.data_ptr()
     workspace = torch.empty(nbytes, device=x.device, dtype=torch.uint8)
     args.workspace, args.workspace_bytes = workspace.data_ptr(), nbytes
     args.B, args.N, args.C, args.Ch = B, N, C, Ch

@@ -48,13 +48,15 @@ def _needs_torch_path(x: torch.Tensor, weights, mask=None) -> bool:
 class _TrimulHip(torch.autograd.Function):
     """HIP forward whose workspace (the contraction operands a, b and its output o) stays on
     the autograd graph for the HIP backward; the graph owns it, so a backward with
-    ``retain_graph=True`` can run again. The backward's kernels record no graph of their
-    own, hence ``once_differentiable``: asking for a second derivative raises."""
+    ``retain_graph=True`` can run again. The output gate, which the backward recomputes,
+    gets a buffer of its own that is released after the forward. The backward's kernels
+    record no graph of their own, hence ``once_differentiable``: asking for a second
+    derivative raises."""
 
     @staticmethod
     def forward(ctx, x, direction, mask, eps, *ws):
         weights = dict(zip(_hip._WEIGHT_KEYS, ws))
-        args, keep, out, workspace, offsets = _hip.build_args(x, direction, mask, eps, weights)
+        args, keep, out, workspace, offsets = _hip.build_args(x, direction, mask, eps, weights, separate_gate=True)
         _hip.run_stage("gnn_trimul_fwd", args, x.device)
         del keep
         ctx.direction, ctx.eps, ctx.offsets = direction, eps, offsets

@@ -206,6 +206,12 @@ typedef struct gnn_trimul_args {
   int32_t outgoing;  /* 1 = "outgoing", 0 = "incoming" */
   int32_t dtype;     /* enum gnn_dtype */
   int32_t precision; /* enum gnn_precision */
+  /* Optional buffer for the output gate g ([B, N, N, C], input dtype, 16-byte aligned),
+   * written by the projection stage and read by the output stage. NULL: the gate region of
+   * the workspace. When set, the workspace needs only off[2] bytes (the gate region is laid
+   * out last), so a caller keeping a, b and o for a backward can release g after the
+   * forward. No reference counterpart. */
+  void* gate;
 } gnn_trimul_args;
 
 /* Workspace size in bytes for one call (a, b, the output gate and o, each in the
@@ -214,7 +220,8 @@ typedef struct gnn_trimul_args {
  *             bf16 / fp16: k-blocked [B, Ch, NP/32, N, 32], columns N .. NP-1 zero;
  *             fp32: row-major [B, Ch, N, NP]
  *   off[1] b  the same for b
- *   off[2] g  pixel-major   [B, N, N, C]    sigmoid(z Wg_out^T + bg_out)
+ *   off[2] g  pixel-major   [B, N, N, C]    sigmoid(z Wg_out^T + bg_out); the last region
+ *             (unused when gnn_trimul_args.gate is set)
  *   off[3] o  channel-major [B, Ch, N, NP]  the contraction output
  * where NP = N rounded up to a multiple of 32 (the row pitch; columns >= N of o unused).
  * No reference counterpart: the reference allocates its intermediates through torch

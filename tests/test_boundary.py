@@ -66,7 +66,7 @@ def _c_layout():
       P(gnn_triattn_args, lse) P(gnn_triattn_args, row_max) P(gnn_triattn_args, D) P(gnn_triattn_args, bias_stride)
       P(gnn_triattn_args, mask_stride) P(gnn_triattn_args, scale) P(gnn_triattn_args, precision)
       P(gnn_trimul_args, mask_stride) P(gnn_trimul_args, workspace_bytes) P(gnn_trimul_args, Ch)
-      P(gnn_trimul_args, eps) P(gnn_trimul_args, precision)
+      P(gnn_trimul_args, eps) P(gnn_trimul_args, precision) P(gnn_trimul_args, gate)
       P(gnn_pair_bias_args, out) P(gnn_pair_bias_args, H) P(gnn_pair_bias_args, out_stride)
       P(gnn_pair_bias_args, eps) P(gnn_pair_bias_args, dtype)
       P(gnn_triattn_bwd_args, delta) P(gnn_triattn_bwd_args, dbias_splits) P(gnn_triattn_bwd_args, D) P(gnn_triattn_bwd_args, dv_stride)
@@ -178,8 +178,9 @@ def test_trimul_argument_errors_and_workspace():
     off = (ctypes.c_size_t * 4)()
     n = lib.gnn_trimul_workspace_bytes(1, 512, 128, 128, _lib.GNN_BF16, off)
     plane = 128 * 512 * 512 * 2
-    assert off[0] == 0 and off[1] == plane and off[2] == 2 * plane
-    assert off[3] == 2 * plane + 512 * 512 * 128 * 2 and n == off[3] + plane
+    # a, b, o, then the gate region last (a caller with its own gate buffer stops at off[2])
+    assert off[0] == 0 and off[1] == plane and off[3] == 2 * plane
+    assert off[2] == 3 * plane and n == off[2] + 512 * 512 * 128 * 2
     assert lib.gnn_trimul_workspace_bytes(1, 100, 32, 32, _lib.GNN_F32, None) % 256 == 0
     a = _lib.TrimulArgs()
     assert lib.gnn_trimul_fwd(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
@@ -192,6 +193,15 @@ def test_trimul_argument_errors_and_workspace():
     a.workspace = 4096
     a.workspace_bytes = 10
     assert lib.gnn_trimul_contract(ctypes.byref(a), None) == _lib.GNN_ERR_WORKSPACE
+    # with its own gate buffer the workspace may stop at the gate offset, not before it
+    off = (ctypes.c_size_t * 4)()
+    lib.gnn_trimul_workspace_bytes(1, 8, 32, 32, _lib.GNN_BF16, off)
+    a.gate = 8192
+    a.workspace_bytes = off[2] - 1
+    assert lib.gnn_trimul_contract(ctypes.byref(a), None) == _lib.GNN_ERR_WORKSPACE
+    a.gate = 8200
+    assert lib.gnn_trimul_contract(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    assert b"16-byte aligned" in lib.gnn_last_error()
     with pytest.raises(RuntimeError, match="workspace"):
         _lib.check(_lib.GNN_ERR_WORKSPACE, "gnn_trimul_contract")
 

@@ -261,3 +261,51 @@ def test_second_derivative_raises():
     (gx,) = torch.autograd.grad(out.float().square().sum(), x, create_graph=True)
     with pytest.raises(RuntimeError):
         gx.float().sum().backward()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_separate_gate_buffer(dtype):
+    """gnn_trimul_args.gate: the output gate in a buffer of its own gives the same output bit
+    for bit, and the workspace then stops at the gate offset (a, b and o only), which is all
+    the autograd forward keeps for the backward."""
+    from geometric_nn_ops_torch.triangle import _trimul
+
+    K = _k()
+    w = {k: v.to(DEV) for k, v in trimul_weights(64, 64, dtype, seed=81, biases=True).items()}
+    x, mask = pair_input(1, 40, 64, dtype, seed=82)
+    x, mask = x.to(DEV), mask.to(DEV)
+    with torch.no_grad():
+        outs, wss = [], []
+        for sep in (False, True):
+            args, keep, out, ws, off = K.build_args(x, "incoming", mask, 1e-5, w, separate_gate=sep)
+            K.run_stage("gnn_trimul_fwd", args, x.device)
+            torch.cuda.synchronize()
+            outs.append(out)
+            wss.append((ws, off, keep))
+    assert torch.equal(outs[0], outs[1])
+    (ws0, off0, _), (ws1, off1, keep1) = wss
+    assert ws1.numel() == off1[2] < ws0.numel()
+    el = x.element_size()
+    N, Ch, NP = 40, 64, 64
+    assert torch.equal(ws0[:off0[3]], ws1[:off1[3]])  # a and b (zero-padded to NP, fully written)
+
+    def o_valid(ws, off):  # o is [B, Ch, N, NP]; columns >= N are not written
+        return ws[off[3]:off[3] + Ch * N * NP * el].view(dtype).view(Ch, N, NP)[..., :N]
+
+    assert torch.equal(o_valid(ws0, off0), o_valid(ws1, off1))
+    gate = keep1[-1]
+    assert torch.equal(ws0[off0[2]:off0[2] + gate.numel() * el].view(dtype).view(gate.shape), gate)
+    # the autograd forward keeps the a / b / o workspace only
+    captured = {}
+    real = _trimul._TrimulHip.forward
+
+    def spy(ctx, *args):
+        o = real(ctx, *args)
+        captured["ws"], captured["off"] = ctx.workspace, ctx.offsets
+        return o
+
+    xg = x.clone().requires_grad_()
+    with mock.patch.object(_trimul._TrimulHip, "forward", staticmethod(spy)):
+        out = _trimul.triangle_multiplicative_update(xg, "incoming", mask, **w)
+    assert torch.equal(out.detach(), outs[0])
+    assert captured["ws"].numel() == captured["off"][2]
