@@ -49,6 +49,7 @@
 // alongside other waves' MFMAs where v_dot2 would hold the matrix pipe), and rows whose keys
 // are all masked reproducing mean(v) (the sentinel swamps the logits; subtract first) are as
 // in the tiled kernel, which gives the same results to rounding.
+#include <algorithm>
 #include <mutex>
 
 #include "gnn_common.hpp"
@@ -82,6 +83,9 @@ constexpr float RESCALE_THRESHOLD = 8.0f / LOG2E;
 #ifndef GNN_ROW_QPREFETCH  // 1: a wave's first q requested with the K / V staging, and (no-bias
 #define GNN_ROW_QPREFETCH 1   // kernel) the next block's q during the current sweep; 2: that also
 #endif                        // with bias (spills at 128 VGPRs); 0: each q loaded where it is used
+#ifndef GNN_ROW_STAGGER  // the first workgroups run half a row (the other halves run last)
+#define GNN_ROW_STAGGER 1
+#endif
 #ifndef GNN_ROW_HEADS_FIRST_BYTES
 #define GNN_ROW_HEADS_FIRST_BYTES (8 << 20)
 #endif
@@ -245,7 +249,17 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
   // Logical order: heads fastest when all H bias planes of a batch fit one XCD's L2
   // together (the XCD then reads whole 4-head key rows of K and V), rows fastest otherwise
   // (an XCD then keeps a single bias plane).
-  const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
+  // Workgroups [0, nsplit) run the first half of their row's query blocks and workgroups
+  // [nrows, nrows + nsplit) the second half of the same rows, so that the first workgroups
+  // end half a row early and the two workgroups of a CU stage their rows at different times.
+  const uint32_t nrows = (uint32_t)(a.B * a.S * a.H);
+  uint32_t bid = blockIdx.x;
+  int qhalf = 0;  // 0: every query block, 1: the first half, 2: the second half
+  if (gridDim.x > nrows) {
+    if (bid < gridDim.x - nrows) qhalf = 1;
+    else if (bid >= nrows) { bid -= nrows; qhalf = 2; }
+  }
+  const uint32_t w = xcd_remap(bid, nrows);
   int s, h;
   if (ROW_HEAD_PAIRS && H % 2 == 0) {
     // head pairs fastest: the two heads of a pair share the 128-byte lines of K and V rows
@@ -271,6 +285,8 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
   // q of query block qb for this lane, unconditionally loaded (row clamped to N - 1, columns
   // past D read from column 0 and zeroed when used)
   const int nqb = (N + 31) / 32;
+  const int qlo = qhalf == 2 ? nqb / 2 : 0, qhi = qhalf == 1 ? nqb / 2 : nqb;
+  const int q0 = qlo + wave;  // this wave's first query block
   const T* qrow = (const T*)a.q + b * a.q_stride[0] + s * a.q_stride[1] + h * a.q_stride[3];
   auto load_q = [&](typename TypeOps<T>::V8 (&qr)[2], int qb) {
     const T* qp = qrow + (int64_t)min(qb * 32 + l32, N - 1) * a.q_stride[2];
@@ -304,7 +320,7 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
                                        (__attribute__((address_space(3))) void*)(vs + q * 1024), 16, 0, 0);
     }
     // the wave's first query block's q, behind its staging so that it lands with it
-    if (GNN_ROW_QPREFETCH && wave < nqb) load_q(qraw, wave);
+    if (GNN_ROW_QPREFETCH && q0 < qhi) load_q(qraw, q0);
   } else {
     // D < 32: through registers, so that columns D .. 31 are zero. Chunk c = key c / 4,
     // columns 8 (c % 4) .. + 7; rows past N are zero.
@@ -334,7 +350,7 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
         }
       }
     }
-    if (GNN_ROW_QPREFETCH && wave < nqb) load_q(qraw, wave);
+    if (GNN_ROW_QPREFETCH && q0 < qhi) load_q(qraw, q0);
   }
 
   // ---- key liveness of the row, the tiles to run and the per-key mask term (wave 0):
@@ -392,7 +408,7 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
 
   // exact row maxima are only tracked for callers that ask for them (per-tile maximum pass)
   const bool want_max = a.row_max != nullptr;
-  for (int qblk = wave; qblk < nqb; qblk += NW) {
+  for (int qblk = q0; qblk < qhi; qblk += NW) {
     // The first tiles' LDS reads are the same for every query block; keeping the compiler
     // from hoisting them out of this loop keeps their registers free for the key loop.
     asm volatile("" : "+v"(koff[0]), "+v"(koff[1]), "+v"(tr_off));
@@ -402,7 +418,7 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
     if (GNN_ROW_QPREFETCH) {
       // later blocks: requested during the previous block's sweep (no-bias kernel, which has
       // the registers to spare) or here
-      if (!QPF_SWEEP && qblk != wave) load_q(qraw, qblk);
+      if (!QPF_SWEEP && qblk != q0) load_q(qraw, qblk);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int d0 = 16 * t + 8 * g;
@@ -433,7 +449,7 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
     // that tile does not wait for it) and in flight during the sweep
     bool qnext_sent = false;
     auto prefetch_q = [&]() {
-      if (GNN_ROW_QPREFETCH && QPF_SWEEP && !qnext_sent && qblk + NW < nqb) load_q(qraw, qblk + NW);
+      if (GNN_ROW_QPREFETCH && QPF_SWEEP && !qnext_sent && qblk + NW < qhi) load_q(qraw, qblk + NW);
       qnext_sent = true;
     };
 
@@ -624,7 +640,17 @@ int launch_row_nw(const gnn_triattn_args& a, hipStream_t stream, size_t smem) {
   const void* fn = (const void*)triattn_row_kernel<T, HAS_BIAS, NW>;
   if (smem > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   const int64_t nblk = a.B * a.S * a.H;
-  hipLaunchKernelGGL((triattn_row_kernel<T, HAS_BIAS, NW>), dim3((uint32_t)nblk), dim3(NW * 64), smem, stream, a);
+  // split rows (first halves first, second halves last): as many as one workgroup per CU,
+  // when two workgroups share a CU and a row has at least two query blocks per wave
+  int64_t nsplit = 0;
+  if (GNN_ROW_STAGGER && NW == 8 && (a.N + 31) / 32 >= 2 * NW) {
+    int dev = 0, ncu = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+      nsplit = std::min<int64_t>(ncu, nblk);
+  }
+  hipLaunchKernelGGL((triattn_row_kernel<T, HAS_BIAS, NW>), dim3((uint32_t)(nblk + nsplit)), dim3(NW * 64), smem,
+                     stream, a);
   return (int)hipGetLastError();
 }
 

@@ -332,6 +332,30 @@ def test_headline_n512_rows():
                     rel_fro_max=NORTH_STAR_REL_FRO)
 
 
+@pytest.mark.parametrize("n", [512, 520, 576], ids=["n512", "n520_odd_blocks", "n576"])
+def test_split_rows_cover_every_query_block(n):
+    """At 481 <= N_res <= 576 the row kernel runs some rows as two half-row workgroups (the
+    first halves launched first, the second halves last, so the two workgroups of a CU stage
+    their rows at different times); with few rows every row is split. Every query of every
+    row must still be written once, lse included, also with an odd number of 32-query blocks
+    (N = 520: 17)."""
+    B, S, H, D = 1, 3, 2, 32
+    t = attention_inputs(B, S, n, H, D, torch.bfloat16, seed=31, bias_scale=1.0)
+    mask = key_mask(B, S, n, seed=32)
+    lse = torch.full((B, S, H, n), float("nan"), device=DEV)
+    got = hip_attn(**dev(t), mask=mask.to(DEV), lse=lse)
+    assert_close_to_oracle("out", got, oracle_of(t, mask), TRIANGLE_ATTENTION_TOL[torch.bfloat16, "ieee"],
+                           rel_fro_max=NORTH_STAR_REL_FRO)
+    q, k = to_np(t["q"]), to_np(t["k"])
+    qs = q.astype(np.float32) * np.float32(D**-0.5)  # q * scale rounded to bf16, as the kernel
+    qs = torch.from_numpy(qs).to(torch.bfloat16).double().numpy()
+    logits = np.einsum("bsihd,bsjhd->bshij", qs, k) + to_np(t["bias"]) + O.masked_key_bias(
+        mask.numpy(), np.float64, "bfloat16")
+    mx = logits.max(-1)
+    want = mx + np.log(np.exp(logits - mx[..., None]).sum(-1))
+    np.testing.assert_allclose(lse.cpu().numpy(), want, rtol=1e-3, atol=2e-2)
+
+
 def test_config_c4_n768_ragged():
     """bf16 N=768, bias 2*N(0,1), each row keeps a random prefix of length in [384, 768]."""
     B, N, H, D = 1, 768, 4, 32
