@@ -473,6 +473,13 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_kernel(const gnn_trimul_ar
 // the biases join in the epilogue, as the reference's linear layers add them (after the
 // product); the gates fold theirs into the exp2 argument. A tile whose mask values are all
 // one skips the mask multiply.
+// Column swizzle of the epilogue staging tiles: rows 16 .. 31 swap their 16-column halves,
+// so that rows r and r + 16 (the same banks with a pitch of 8 mod 16 elements) do not collide.
+#ifndef GNN_PROJ_EBSW
+#define GNN_PROJ_EBSW 1
+#endif
+__device__ __forceinline__ int EBSW(int row) { return GNN_PROJ_EBSW ? (row & 16) : 0; }
+
 template <int CK>
 struct ProjFastLds {
   static constexpr int ZR = CK + 8;  // z and gate-weight row pitch (16-bit elements)
@@ -669,7 +676,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] *= m4[e];
           }
-          store4(&ebuf[l32 * ER + pt], TypeOps<T>::from_f32(v));
+          store4(&ebuf[l32 * ER + (pt ^ EBSW(l32))], TypeOps<T>::from_f32(v));
         }
       }
       wave_lds_sync();
@@ -685,7 +692,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
         const bool full = tl.c0 + p0 + 8 <= N, tail = !full && tl.c0 + p0 < NP;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const V8 val = load8(&ebuf[(crow0 + 8 * i) * ER + p0]);
+          const V8 val = load8(&ebuf[(crow0 + 8 * i) * ER + (p0 ^ EBSW(crow0 + 8 * i))]);
           if (full) {
             store8(drow + i * pstep, val);
           } else if (tail) {  // row tail: pixels N .. NP-1 are written as zeros
@@ -711,7 +718,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           v[e] = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(accgo[4 * rg + e], NLOG2E, nb4[e])));
-        store4(&gbuf[l32 * EG + 8 * rg + 4 * g], TypeOps<T>::from_f32(v));
+        store4(&gbuf[l32 * EG + ((8 * rg + 4 * g) ^ EBSW(l32))], TypeOps<T>::from_f32(v));
       }
       wave_lds_sync();
       // 16-byte stores, 4 lanes per 32-channel pixel row segment; store 1 is store 0 moved
@@ -722,7 +729,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
         const int64_t step16 = (outgoing ? 16 : 16 * (int64_t)N) * CK;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-          if (tl.c0 + pl + 16 * i < N) store8(dst + i * step16, load8(&gbuf[(px + 16 * i) * EG + k0]));
+          if (tl.c0 + pl + 16 * i < N) store8(dst + i * step16, load8(&gbuf[(px + 16 * i) * EG + (k0 ^ EBSW(px + 16 * i))]));
       }
     }
   };
