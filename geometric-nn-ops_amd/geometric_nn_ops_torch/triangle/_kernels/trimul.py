@@ -246,7 +246,7 @@ def _wgrad(d, t, slices=64):
         slices //= 2
     ds = d.reshape(slices, M // slices, d.shape[1])
     ts = t.reshape(slices, M // slices, t.shape[1])
-    return torch.bmm(ts.transpose(1, 2), ds).sum(0, dtype=torch.float32).t()
+    return torch.bmm(ds.transpose(1, 2), ts).sum(0, dtype=torch.float32)  # [O, I], contiguous
 
 
 def _operand(ws, off, B, Ch, N, NP, dtype):
@@ -372,8 +372,18 @@ def trimul_bwd_hip(x, direction, mask, eps, weights, workspace, offsets, dout):
     dz = dlin @ wcat
     dx, dlnw, dlnb = layernorm_rows_hip(xk, w["norm_in_weight"], eps=eps, dy=dz, partials=True)
     grads["norm_in_weight"], grads["norm_in_bias"] = dlnw, dlnb
-    out = {}
+    # every parameter gradient is fp32 here: one concatenation and one conversion per
+    # parameter dtype instead of a small conversion launch per parameter
+    out = dict.fromkeys(_WEIGHT_KEYS)
+    by_dtype = {}
     for key in _WEIGHT_KEYS:
-        src = weights.get(key)
-        out[key] = None if src is None else grads[key].to(src.dtype).reshape(src.shape)
+        if weights.get(key) is not None:
+            by_dtype.setdefault(weights[key].dtype, []).append(key)
+    for pdt, keys in by_dtype.items():
+        flat = torch.cat([grads[k].reshape(-1) for k in keys]).to(pdt)
+        off = 0
+        for k in keys:
+            n = weights[k].numel()
+            out[k] = flat[off:off + n].view(weights[k].shape)
+            off += n
     return dx.reshape(x.shape), out
