@@ -472,24 +472,31 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
   // q0 + qw + 8 (i / 4) + 4 g + i % 4, key k0 + kw + 32 sub + l32
   f32x16 binit[2], acc[2];
   {
+    // indices clamped into the plane (elements past N are never stored), so the 32 loads
+    // issue back to back instead of one at a time behind a branch each
     const T* plane = (const T*)a.bias + b * a.bias_stride[0] + h * a.bias_stride[1];
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
-      const int kj = k0 + kw + 32 * sub + l32;
+      const int kj = min(k0 + kw + 32 * sub + l32, N - 1);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int qq = q0 + qw + 8 * (i / 4) + 4 * g + (i % 4);
-        binit[sub][i] = (qq < N && kj < N) ? TypeOps<T>::to_f32(plane[(int64_t)qq * a.bias_stride[2] + kj]) : 0.f;
+        const int qq = min(q0 + qw + 8 * (i / 4) + 4 * g + (i % 4), N - 1);
+        binit[sub][i] = TypeOps<T>::to_f32(plane[(int64_t)qq * a.bias_stride[2] + kj]);
         acc[sub][i] = 0.f;
       }
     }
   }
 
-  // staging: thread = (row r = tid / 4, chunk c = tid % 4) of each of the four tiles
+  // staging: thread = (row r = tid / 4, chunk c = tid % 4) of each of the four tiles. PF
+  // register sets hold the next PF N_seq rows, so each row's loads have PF rows of compute to
+  // arrive (two for D <= 32; wider heads have no registers to spare); the loads past the range
+  // repeat its last row (in bounds, never used).
+  constexpr int PF = 1;
   const int sr = tid >> 2, sc4 = tid & 3;
-  V8 pq[DC], pd[DC], pk[DC], pv[DC];
-  float plse = 0.f, pdel = 0.f, pkb = 0.f;
-  auto load_stage = [&](int s) {
+  V8 pq[PF][DC], pd[PF][DC], pk[PF][DC], pv[PF][DC];
+  float plse[PF], pdel[PF];
+  int pmk[PF];  // the key's raw mask byte (1 without a mask), compared only when staged
+  auto load_stage = [&](int set, int s) {
     const int qi = q0 + sr, kj = k0 + sr;
     const bool qok = qi < N, kok = kj < N;
     const int64_t qo = (int64_t)b * a.q_stride[0] + (int64_t)s * a.q_stride[1] + (int64_t)h * a.q_stride[3];
@@ -499,46 +506,41 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
 #pragma unroll
     for (int dc = 0; dc < DC; ++dc) {
       const int c0 = 32 * dc + 8 * sc4;
-      pq[dc] = row8((const T*)a.q + qo + (int64_t)(qok ? qi : 0) * a.q_stride[2], c0, D, qok);
-      pd[dc] = row8((const T*)a.dout + doo + (int64_t)(qok ? qi : 0) * a.do_stride[2], c0, D, qok);
-      pk[dc] = row8((const T*)a.k + ko + (int64_t)(kok ? kj : 0) * a.k_stride[2], c0, D, kok);
-      pv[dc] = row8((const T*)a.v + vo + (int64_t)(kok ? kj : 0) * a.v_stride[2], c0, D, kok);
+      pq[set][dc] = row8((const T*)a.q + qo + (int64_t)(qok ? qi : 0) * a.q_stride[2], c0, D, qok);
+      pd[set][dc] = row8((const T*)a.dout + doo + (int64_t)(qok ? qi : 0) * a.do_stride[2], c0, D, qok);
+      pk[set][dc] = row8((const T*)a.k + ko + (int64_t)(kok ? kj : 0) * a.k_stride[2], c0, D, kok);
+      pv[set][dc] = row8((const T*)a.v + vo + (int64_t)(kok ? kj : 0) * a.v_stride[2], c0, D, kok);
     }
     if (sc4 == 0) {
       const int64_t lrow = (((int64_t)b * S + s) * H + h) * N;
-      plse = qok ? a.lse[lrow + qi] : INFINITY;  // absent queries: p = 0
-      pdel = qok ? a.delta[lrow + qi] : 0.f;
-      pkb = !kok ? -INFINITY
-                 : ((a.mask && a.mask[b * a.mask_stride[0] + s * a.mask_stride[1] + (int64_t)kj * a.mask_stride[2]] == 0)
-                        ? a.mask_value
-                        : 0.f);
+      plse[set] = qok ? a.lse[lrow + qi] : INFINITY;  // absent queries: p = 0
+      pdel[set] = qok ? a.delta[lrow + qi] : 0.f;
+      pmk[set] = (a.mask && kok) ? (int)a.mask[b * a.mask_stride[0] + s * a.mask_stride[1] + (int64_t)kj * a.mask_stride[2]] : 1;
     }
   };
-  auto store_stage = [&]() {
+  auto store_stage = [&](int set) {
+    // the staged values are first touched here, so the wait for their loads stays here (the
+    // scaling of q would otherwise be scheduled at the top of the row's compute)
+#pragma unroll
+    for (int dc = 0; dc < DC; ++dc) asm volatile("" : "+v"(pq[set][dc]), "+v"(pd[set][dc]), "+v"(pk[set][dc]), "+v"(pv[set][dc]));
 #pragma unroll
     for (int dc = 0; dc < DC; ++dc) {
-      *reinterpret_cast<V8*>(sm.q[dc] + swz(sr, sc4)) = TypeOps<T>::from_f32(TypeOps<T>::to_f32(pq[dc]) * a.scale);
-      *reinterpret_cast<V8*>(sm.d[dc] + swz(sr, sc4)) = pd[dc];
-      *reinterpret_cast<V8*>(sm.k[dc] + swz(sr, sc4)) = pk[dc];
-      *reinterpret_cast<V8*>(sm.v[dc] + swz(sr, sc4)) = pv[dc];
+      *reinterpret_cast<V8*>(sm.q[dc] + swz(sr, sc4)) = TypeOps<T>::from_f32(TypeOps<T>::to_f32(pq[set][dc]) * a.scale);
+      *reinterpret_cast<V8*>(sm.d[dc] + swz(sr, sc4)) = pd[set][dc];
+      *reinterpret_cast<V8*>(sm.k[dc] + swz(sr, sc4)) = pk[set][dc];
+      *reinterpret_cast<V8*>(sm.v[dc] + swz(sr, sc4)) = pv[set][dc];
     }
     if (sc4 == 0) {
-      sm.lse[sr] = plse;
-      sm.delta[sr] = pdel;
-      sm.kb[sr] = pkb;
+      asm volatile("" : "+v"(plse[set]), "+v"(pdel[set]), "+v"(pmk[set]));
+      sm.lse[sr] = plse[set];
+      sm.delta[sr] = pdel[set];
+      sm.kb[sr] = k0 + sr >= N ? -INFINITY : pmk[set] == 0 ? a.mask_value : 0.f;
       // every query of the row shares its keys' mask: the tile's first query (< N) decides
-      if (sr == 0) sm.pl2 = (a.mask && plse <= 0.5f * a.mask_value) ? -__log2f((float)N) : 0.f;
+      if (sr == 0) sm.pl2 = (a.mask && plse[set] <= 0.5f * a.mask_value) ? -__log2f((float)N) : 0.f;
     }
   };
-
-  if (s_begin < s_end) {
-    load_stage(s_begin);
-    store_stage();
-  }
-  __syncthreads();
-  for (int s = s_begin; s < s_end; ++s) {
-    const bool has_next = s + 1 < s_end;
-    if (has_next) load_stage(s + 1);
+  // one N_seq row of the tile from LDS: sum_s dS += P (dP - Delta)
+  auto compute_row = [&]() {
     V8 qf[DC][2], dof[DC][2];
 #pragma unroll
     for (int dc = 0; dc < DC; ++dc)
@@ -576,11 +578,214 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
           acc[sub][i] += pv * (dp[i] - d4[rg][e]);
         }
     }
+  };
+
+  if (s_begin < s_end) {
+    const int last = s_end - 1;
+    load_stage(0, s_begin);
+    store_stage(0);
+#pragma unroll
+    for (int j = 0; j < PF; ++j) load_stage(j, min(s_begin + 1 + j, last));
     __syncthreads();
-    if (has_next) store_stage();
-    __syncthreads();
+    // whole groups of PF rows, with no branch between a set's loads and its use (the wait
+    // before staging a set then leaves the other set's loads in flight)
+    int s = s_begin;
+    for (; s + PF <= s_end; s += PF) {
+#pragma unroll
+      for (int ph = 0; ph < PF; ++ph) {
+        compute_row();
+        __syncthreads();
+        store_stage(ph);  // row s + ph + 1
+        __syncthreads();
+        load_stage(ph, min(s + ph + 1 + PF, last));
+      }
+    }
+    if (s < s_end) compute_row();  // PF = 2 and an odd number of rows: the last one is in LDS
   }
   // [B, H, N, N] fp32: the final gradient, or this split's slice of the workspace
+  float* out = (splits > 1 ? a.dbias_ws + (int64_t)split * a.B * H * N * N : a.dbias) + ((int64_t)b * H + h) * N * N;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    const int kj = k0 + kw + 32 * sub + l32;
+    if (kj >= N) continue;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int qq = q0 + qw + 8 * (i / 4) + 4 * g + (i % 4);
+      if (qq < N) out[(int64_t)qq * N + kj] = acc[sub][i];
+    }
+  }
+}
+
+// The D = 32 (16-bit) form of bwd_dbias_kernel: the four tiles of each N_seq row arrive by
+// global_load_lds (no staging registers) into a ring of DBD_NS stages, so the loads of the
+// next DBD_NS - 1 rows are in flight while a row is computed, with one barrier per row. q is
+// staged raw and scaled (Q' = T(q * scale), the same rounding) as its fragments are read. lse
+// and Delta ride in the same ring (dword DMA); the key-mask bytes of 64 rows at a time are
+// staged once per 64 rows.
+constexpr int DBD_NS = 3;
+constexpr int DBD_MROWS = 64;
+struct DbdStage {
+  unsigned char q[DB_T * ROWB];
+  unsigned char d[DB_T * ROWB];
+  unsigned char k[DB_T * ROWB];
+  unsigned char v[DB_T * ROWB];
+  float lse[DB_T];
+  float delta[DB_T];
+};
+struct DbdLds {
+  DbdStage st[DBD_NS];
+  unsigned char mask[DBD_MROWS][DB_T];
+};
+
+template <typename T>
+__global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_dma_kernel(const gnn_triattn_bwd_args a) {
+  typedef typename TypeOps<T>::V8 V8;
+  extern __shared__ __align__(16) unsigned char db_smem[];
+  DbdLds& sm = *reinterpret_cast<DbdLds*>(db_smem);
+  const int N = (int)a.N, H = (int)a.H, S = (int)a.S;
+  const int nt = (N + DB_T - 1) / DB_T;
+  const int splits = a.dbias_splits > 1 ? a.dbias_splits : 1;
+  const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
+  const int kt = w % nt;
+  const int qt = (w / nt) % nt;
+  const int split = (w / (nt * nt)) % splits;
+  const int64_t bh = w / ((uint32_t)splits * nt * nt);
+  const int h = (int)(bh % H), b = (int)(bh / H);
+  const int per = (S + splits - 1) / splits;
+  const int s_begin = split * per, s_end = min(S, s_begin + per);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
+  const int qw = 32 * (wave & 3), kw = 64 * (wave >> 2);
+  const int q0 = qt * DB_T, k0 = kt * DB_T;
+
+  f32x16 binit[2], acc[2];
+  {
+    // indices clamped into the plane (elements past N are never stored), so the 32 loads
+    // issue back to back instead of one at a time behind a branch each
+    const T* plane = (const T*)a.bias + b * a.bias_stride[0] + h * a.bias_stride[1];
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int kj = min(k0 + kw + 32 * sub + l32, N - 1);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int qq = min(q0 + qw + 8 * (i / 4) + 4 * g + (i % 4), N - 1);
+        binit[sub][i] = TypeOps<T>::to_f32(plane[(int64_t)qq * a.bias_stride[2] + kj]);
+        acc[sub][i] = 0.f;
+      }
+    }
+  }
+
+  // DMA work of a wave per row: tile wave / 2 (q, dO, k, v), its 16-row groups 4 (wave % 2) ..
+  // 4 (wave % 2) + 3 (lane l: row l / 4 of the group, physical chunk l % 4 = logical chunk
+  // (l % 4) ^ ((l / 16) % 4), the tiles' XOR swizzle), and one 64-float piece of lse / Delta
+  // (waves 4..7 write the same bytes as waves 0..3). Rows past N repeat row N - 1: finite
+  // values whose results are never stored.
+  const int tile = wave >> 1, grp0 = 4 * (wave & 1);
+  const int lrow = lane >> 2, ch = (lane & 3) ^ ((lane >> 4) & 3);
+  const T* tsrc = tile == 0 ? (const T*)a.q + b * a.q_stride[0] + h * a.q_stride[3]
+                : tile == 1 ? (const T*)a.dout + b * a.do_stride[0] + h * a.do_stride[3]
+                : tile == 2 ? (const T*)a.k + b * a.k_stride[0] + h * a.k_stride[3]
+                            : (const T*)a.v + b * a.v_stride[0] + h * a.v_stride[3];
+  const int64_t trs = tile == 0 ? a.q_stride[2] : tile == 1 ? a.do_stride[2] : tile == 2 ? a.k_stride[2] : a.v_stride[2];
+  const int64_t tss = tile == 0 ? a.q_stride[1] : tile == 1 ? a.do_stride[1] : tile == 2 ? a.k_stride[1] : a.v_stride[1];
+  const int trow0 = tile < 2 ? q0 : k0;
+  const int tbyte = tile * (DB_T * ROWB);  // offset of the tile within a stage
+  const int piece = wave & 3;
+  const float* ssrc = (piece < 2 ? a.lse : a.delta) + ((int64_t)b * S * H + h) * N + min(q0 + 64 * (piece & 1) + lane, N - 1);
+  const int sbyte = 4 * DB_T * ROWB + (piece >> 1) * (DB_T * 4) + (piece & 1) * 256;
+  auto issue = [&](int s, int stage) {
+    unsigned char* base = reinterpret_cast<unsigned char*>(&sm.st[stage]);
+    const T* src = tsrc + (int64_t)s * tss;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int grp = grp0 + j;
+      const int r = min(trow0 + 16 * grp + lrow, N - 1);
+      __builtin_amdgcn_global_load_lds((const void*)(src + (int64_t)r * trs + 8 * ch),
+                                       (__attribute__((address_space(3))) void*)(base + tbyte + grp * 1024), 16, 0, 0);
+    }
+    __builtin_amdgcn_global_load_lds((const void*)(ssrc + (int64_t)s * H * N),
+                                     (__attribute__((address_space(3))) void*)(base + sbyte), 4, 0, 0);
+  };
+  // the key-mask bytes of rows s0 .. s0 + 63 (clamped to the range) of the tile's keys
+  auto stage_mask = [&](int s0) {
+    const int kk = tid & (DB_T - 1), r0 = tid >> 7;
+    const unsigned char* mrow = a.mask + b * a.mask_stride[0] + (int64_t)min(k0 + kk, N - 1) * a.mask_stride[2];
+    unsigned char mv[DBD_MROWS / 4];
+#pragma unroll
+    for (int j = 0; j < DBD_MROWS / 4; ++j)
+      mv[j] = mrow[(int64_t)min(s0 + r0 + 4 * j, s_end - 1) * a.mask_stride[1]];
+#pragma unroll
+    for (int j = 0; j < DBD_MROWS / 4; ++j) sm.mask[r0 + 4 * j][kk] = mv[j];
+  };
+
+  const float scale = a.scale;
+  const bool has_mask = a.mask != nullptr;
+  const float pl2_masked = -__log2f((float)N);
+  auto compute_row = [&](int stage, int mrow) {
+    const DbdStage& st = sm.st[stage];
+    V8 qf[2], dof[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      qf[kk] = TypeOps<T>::from_f32(TypeOps<T>::to_f32(lds_row8<T>(st.q, qw + l32, 2 * kk + g)) * scale);
+      dof[kk] = lds_row8<T>(st.d, qw + l32, 2 * kk + g);
+    }
+    f32x4 l4[4], d4[4];
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      l4[rg] = *reinterpret_cast<const f32x4*>(&st.lse[qw + 8 * rg + 4 * g]);
+      d4[rg] = *reinterpret_cast<const f32x4*>(&st.delta[qw + 8 * rg + 4 * g]);
+    }
+    // every query of the row shares its keys' mask: the tile's first query decides
+    const float pl2 = (has_mask && st.lse[0] <= 0.5f * a.mask_value) ? pl2_masked : 0.f;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int kr = kw + 32 * sub + l32;
+      f32x16 scv = binit[sub], dp;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dp[i] = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        Mma<T, PREC_NATIVE>::step(scv, qf[kk], lds_row8<T>(st.k, kr, 2 * kk + g));
+        Mma<T, PREC_NATIVE>::step(dp, dof[kk], lds_row8<T>(st.v, kr, 2 * kk + g));
+      }
+      const float kb = (has_mask && sm.mask[mrow][kr] == 0) ? a.mask_value : 0.f;
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * rg + e;
+          const float pv = fast_exp2(__builtin_fmaf(scv[i] + kb - l4[rg][e], LOG2E_B, pl2));
+          acc[sub][i] += pv * (dp[i] - d4[rg][e]);
+        }
+    }
+  };
+
+  if (s_begin < s_end) {
+    const int last = s_end - 1;
+    // rows s_begin .. s_begin + NS - 2 in flight before the loop; row s's stage is
+    // (s - s_begin) % NS, and the row NS - 1 ahead goes into the stage computed last
+#pragma unroll
+    for (int j = 0; j < DBD_NS - 1; ++j) issue(min(s_begin + j, last), j);
+    int stage = 0;
+    for (int s = s_begin; s < s_end; ++s) {
+      const int rr = s - s_begin;
+      if (has_mask && rr % DBD_MROWS == 0) {
+        __syncthreads();  // every wave is done with the previous 64 rows' mask bytes
+        stage_mask(s);
+      }
+      // this wave's DMA of row s has landed once only the younger row's five remain (the
+      // DMA per wave and row: four tile groups and one lse / Delta piece); after the barrier
+      // every wave's has, and every wave is done with row s - 1's stage. (__syncthreads would
+      // wait for every load in flight.)
+      static_assert(DBD_NS == 3, "the wait below counts one younger row");
+      asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      int nstage = stage + DBD_NS - 1;
+      nstage -= nstage >= DBD_NS ? DBD_NS : 0;
+      issue(min(s + DBD_NS - 1, last), nstage);
+      compute_row(stage, rr % DBD_MROWS);
+      stage = stage + 1 == DBD_NS ? 0 : stage + 1;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA outlives the workgroup
+  }
   float* out = (splits > 1 ? a.dbias_ws + (int64_t)split * a.B * H * N * N : a.dbias) + ((int64_t)b * H + h) * N * N;
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub) {
@@ -604,6 +809,20 @@ __global__ __launch_bounds__(BNT) void bwd_dbias_reduce_kernel(const gnn_triattn
   }
 }
 
+// the DMA form of the dbias kernel moves 16-byte pieces of the q / dO / k / v rows: D = 32
+// and every row start 16-byte aligned
+bool dbias_dma_ok(const gnn_triattn_bwd_args& a) {
+  if (a.D != 32) return false;
+  const void* ptrs[4] = {a.q, a.dout, a.k, a.v};
+  const int64_t* strides[4] = {a.q_stride, a.do_stride, a.k_stride, a.v_stride};
+  for (int t = 0; t < 4; ++t) {
+    if (reinterpret_cast<uintptr_t>(ptrs[t]) % 16 != 0) return false;
+    for (int d = 0; d < 4; ++d)
+      if (strides[t][d] % 8 != 0) return false;
+  }
+  return true;
+}
+
 template <typename T, int DC>
 int launch_bwd(const gnn_triattn_bwd_args& a, hipStream_t stream) {
   const int64_t nb128 = (a.N + 127) / 128;
@@ -622,11 +841,18 @@ int launch_bwd(const gnn_triattn_bwd_args& a, hipStream_t stream) {
   if (a.bias && a.dbias) {
     const int64_t nt = (a.N + DB_T - 1) / DB_T;
     const int splits = a.dbias_splits > 1 ? a.dbias_splits : 1;
-    const size_t smem = sizeof(DbLds<DC>);
-    const void* fn = (const void*)bwd_dbias_kernel<T, DC>;
-    if (smem > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-    hipLaunchKernelGGL((bwd_dbias_kernel<T, DC>), dim3((uint32_t)(a.B * a.H * nt * nt * splits)), dim3(DB_NT), smem,
-                       stream, a);
+    const dim3 dgrid((uint32_t)(a.B * a.H * nt * nt * splits));
+    if (DC == 1 && dbias_dma_ok(a)) {
+      const size_t smem = sizeof(DbdLds);
+      (void)hipFuncSetAttribute((const void*)bwd_dbias_dma_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)smem);
+      hipLaunchKernelGGL((bwd_dbias_dma_kernel<T>), dgrid, dim3(DB_NT), smem, stream, a);
+    } else {
+      const size_t smem = sizeof(DbLds<DC>);
+      const void* fn = (const void*)bwd_dbias_kernel<T, DC>;
+      if (smem > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      hipLaunchKernelGGL((bwd_dbias_kernel<T, DC>), dgrid, dim3(DB_NT), smem, stream, a);
+    }
     if (splits > 1) {
       const int64_t n = a.B * a.H * a.N * a.N;
       const int64_t blocks = std::min<int64_t>((n + BNT - 1) / BNT, 4096);

@@ -117,6 +117,17 @@ def test_row_kernel_limit(n):
     check_against_oracle((1, 1, n, 2, 32), torch.bfloat16, seed=71)
 
 
+@pytest.mark.parametrize("splits", [1, 3], ids=["one_range", "three_ranges"])
+def test_dbias_long_row_ranges(splits, monkeypatch):
+    """The pair-bias gradient with N_seq ranges longer than 64 rows (the D = 32 kernel stages
+    the key-mask bytes 64 rows at a time) and ranges of uneven length, fully masked rows on
+    both sides of the 64-row boundary, ragged keys (N = 72)."""
+    from geometric_nn_ops_torch.triangle._kernels import triangle_attention as K
+
+    monkeypatch.setattr(K, "dbias_splits", lambda *a: splits)
+    check_against_oracle((1, 131, 72, 2, 32), torch.bfloat16, seed=83, dead_rows=(5, 64, 70))
+
+
 def test_headline_rows_bf16():
     """N_res = 512 (the headline width), 8 N_seq rows, pair bias and ragged masks."""
     check_against_oracle((1, 8, 512, 4, 32), torch.bfloat16, seed=41)
