@@ -624,6 +624,7 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
 // staged once per 64 rows.
 constexpr int DBD_NS = 3;
 constexpr int DBD_MROWS = 64;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 struct DbdStage {
   unsigned char q[DB_T * ROWB];
   unsigned char d[DB_T * ROWB];
@@ -637,7 +638,7 @@ struct DbdLds {
   unsigned char mask[DBD_MROWS][DB_T];
 };
 
-template <typename T>
+template <typename T, bool MASK>
 __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_dma_kernel(const gnn_triattn_bwd_args a) {
   typedef typename TypeOps<T>::V8 V8;
   extern __shared__ __align__(16) unsigned char db_smem[];
@@ -718,34 +719,39 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_dma_kernel(const gnn_triat
   };
 
   const float scale = a.scale;
-  const bool has_mask = a.mask != nullptr;
+  constexpr bool has_mask = MASK;
   const float pl2_masked = -__log2f((float)N);
   auto compute_row = [&](int stage, int mrow) {
     const DbdStage& st = sm.st[stage];
-    V8 qf[2], dof[2];
+    // dO fragments negated (a sign flip, exact) and the dP accumulator started at Delta: the
+    // MFMA yields Delta - dP, so dS = P (dP - Delta) needs no subtraction per element
+    V8 qf[2], ndof[2];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       qf[kk] = TypeOps<T>::from_f32(TypeOps<T>::to_f32(lds_row8<T>(st.q, qw + l32, 2 * kk + g)) * scale);
-      dof[kk] = lds_row8<T>(st.d, qw + l32, 2 * kk + g);
+      u32x4 u = __builtin_bit_cast(u32x4, lds_row8<T>(st.d, qw + l32, 2 * kk + g));
+      u ^= 0x80008000u;
+      ndof[kk] = __builtin_bit_cast(V8, u);
     }
-    f32x4 l4[4], d4[4];
+    f32x4 l4[4];
+    f32x16 dinit;
 #pragma unroll
     for (int rg = 0; rg < 4; ++rg) {
       l4[rg] = *reinterpret_cast<const f32x4*>(&st.lse[qw + 8 * rg + 4 * g]);
-      d4[rg] = *reinterpret_cast<const f32x4*>(&st.delta[qw + 8 * rg + 4 * g]);
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(&st.delta[qw + 8 * rg + 4 * g]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dinit[4 * rg + e] = d4[e];
     }
     // every query of the row shares its keys' mask: the tile's first query decides
     const float pl2 = (has_mask && st.lse[0] <= 0.5f * a.mask_value) ? pl2_masked : 0.f;
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
       const int kr = kw + 32 * sub + l32;
-      f32x16 scv = binit[sub], dp;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) dp[i] = 0.f;
+      f32x16 scv = binit[sub], ndp = dinit;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         Mma<T, PREC_NATIVE>::step(scv, qf[kk], lds_row8<T>(st.k, kr, 2 * kk + g));
-        Mma<T, PREC_NATIVE>::step(dp, dof[kk], lds_row8<T>(st.v, kr, 2 * kk + g));
+        Mma<T, PREC_NATIVE>::step(ndp, ndof[kk], lds_row8<T>(st.v, kr, 2 * kk + g));
       }
       const float kb = (has_mask && sm.mask[mrow][kr] == 0) ? a.mask_value : 0.f;
 #pragma unroll
@@ -753,8 +759,10 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_dma_kernel(const gnn_triat
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = 4 * rg + e;
-          const float pv = fast_exp2(__builtin_fmaf(scv[i] + kb - l4[rg][e], LOG2E_B, pl2));
-          acc[sub][i] += pv * (dp[i] - d4[rg][e]);
+          // the logit minus lse first (in a fully masked row both sit near the sentinel)
+          const float x = has_mask ? scv[i] + kb - l4[rg][e] : scv[i] - l4[rg][e];
+          const float pv = fast_exp2(has_mask ? __builtin_fmaf(x, LOG2E_B, pl2) : x * LOG2E_B);
+          acc[sub][i] -= pv * ndp[i];
         }
     }
   };
@@ -844,9 +852,15 @@ int launch_bwd(const gnn_triattn_bwd_args& a, hipStream_t stream) {
     const dim3 dgrid((uint32_t)(a.B * a.H * nt * nt * splits));
     if (DC == 1 && dbias_dma_ok(a)) {
       const size_t smem = sizeof(DbdLds);
-      (void)hipFuncSetAttribute((const void*)bwd_dbias_dma_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)smem);
-      hipLaunchKernelGGL((bwd_dbias_dma_kernel<T>), dgrid, dim3(DB_NT), smem, stream, a);
+      if (a.mask) {
+        (void)hipFuncSetAttribute((const void*)bwd_dbias_dma_kernel<T, true>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        hipLaunchKernelGGL((bwd_dbias_dma_kernel<T, true>), dgrid, dim3(DB_NT), smem, stream, a);
+      } else {
+        (void)hipFuncSetAttribute((const void*)bwd_dbias_dma_kernel<T, false>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        hipLaunchKernelGGL((bwd_dbias_dma_kernel<T, false>), dgrid, dim3(DB_NT), smem, stream, a);
+      }
     } else {
       const size_t smem = sizeof(DbLds<DC>);
       const void* fn = (const void*)bwd_dbias_kernel<T, DC>;
