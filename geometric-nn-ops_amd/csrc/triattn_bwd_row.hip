@@ -209,6 +209,11 @@ __global__ __launch_bounds__(RNT, 4) void bwd_dq_row_kernel(const gnn_triattn_bw
     }
     const float lse = qok ? a.lse[lrow + qi] : INFINITY;  // absent queries: p = 0
     const float pl2 = dead_row_log2(a, lse);
+    // Unless a query of the wave sits in a fully masked row, P = exp2(S log2 e - lse log2 e)
+    // takes one fma per element (lse is this lane's query's, constant along the accumulator);
+    // a fully masked row keeps S - lse formed first (both sit near the sentinel).
+    const bool dead = __any(pl2 != 0.f);
+    const float nl2 = -lse * LOG2E_R;
     const T* brow = HAS_BIAS ? (const T*)a.bias + b * a.bias_stride[0] + h * a.bias_stride[1] +
                                    (int64_t)(qok ? qi : 0) * a.bias_stride[2]
                              : nullptr;
@@ -246,9 +251,19 @@ __global__ __launch_bounds__(RNT, 4) void bwd_dq_row_kernel(const gnn_triattn_bw
       // P = exp(S - lse), subtracting first: in a row whose keys are all masked both sit
       // near the sentinel, and only their difference is exact
       f32x16 ds;
-      if (plain) {
+      if (plain && !dead) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) ds[i] = fast_exp2(__builtin_fmaf(sc[i] - lse, LOG2E_R, pl2)) * (dp[i] - delta);
+        for (int i = 0; i < 16; ++i) ds[i] = fast_exp2(__builtin_fmaf(sc[i], LOG2E_R, nl2)) * (dp[i] - delta);
+      } else if (!dead) {
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const f32x4 k4 = *reinterpret_cast<const f32x4*>(&hdr.kterm[32 * st + 8 * rg + 4 * g]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int i = 4 * rg + e;
+            ds[i] = fast_exp2(__builtin_fmaf(sc[i] + k4[e], LOG2E_R, nl2)) * (dp[i] - delta);
+          }
+        }
       } else {
 #pragma unroll
         for (int rg = 0; rg < 4; ++rg) {
