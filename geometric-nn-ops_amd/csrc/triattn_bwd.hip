@@ -50,6 +50,7 @@ constexpr float LOG2E_B = 1.4426950408889634f;
 constexpr int BT = 64;      // queries per LDS tile (dkdv) / keys per LDS tile (dq)
 constexpr int BNT = 256;    // threads per workgroup (4 waves)
 constexpr int ROWB = 64;    // bytes per staged row (32 x 16-bit)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // byte offset of (row r, 16-byte chunk c) in a [rows][32] 16-bit tile whose chunks are
 // XOR-swizzled by (r / 4) % 4: row-major fragment reads of 32 consecutive rows and the
@@ -541,32 +542,36 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
   };
   // one N_seq row of the tile from LDS: sum_s dS += P (dP - Delta)
   auto compute_row = [&]() {
-    V8 qf[DC][2], dof[DC][2];
+    // dO fragments negated and the dP accumulator started at Delta: the MFMA yields Delta - dP
+    V8 qf[DC][2], ndof[DC][2];
 #pragma unroll
     for (int dc = 0; dc < DC; ++dc)
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         qf[dc][kk] = lds_row8<T>(sm.q[dc], qw + l32, 2 * kk + g);
-        dof[dc][kk] = lds_row8<T>(sm.d[dc], qw + l32, 2 * kk + g);
+        u32x4 u = __builtin_bit_cast(u32x4, lds_row8<T>(sm.d[dc], qw + l32, 2 * kk + g));
+        u ^= 0x80008000u;
+        ndof[dc][kk] = __builtin_bit_cast(V8, u);
       }
-    f32x4 l4[4], d4[4];
+    f32x4 l4[4];
+    f32x16 dinit;
 #pragma unroll
     for (int rg = 0; rg < 4; ++rg) {
       l4[rg] = *reinterpret_cast<const f32x4*>(&sm.lse[qw + 8 * rg + 4 * g]);
-      d4[rg] = *reinterpret_cast<const f32x4*>(&sm.delta[qw + 8 * rg + 4 * g]);
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(&sm.delta[qw + 8 * rg + 4 * g]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dinit[4 * rg + e] = d4[e];
     }
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
       const int kr = kw + 32 * sub + l32;
-      f32x16 scv = binit[sub], dp;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) dp[i] = 0.f;
+      f32x16 scv = binit[sub], ndp = dinit;
 #pragma unroll
       for (int dc = 0; dc < DC; ++dc)
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           Mma<T, PREC_NATIVE>::step(scv, qf[dc][kk], lds_row8<T>(sm.k[dc], kr, 2 * kk + g));
-          Mma<T, PREC_NATIVE>::step(dp, dof[dc][kk], lds_row8<T>(sm.v[dc], kr, 2 * kk + g));
+          Mma<T, PREC_NATIVE>::step(ndp, ndof[dc][kk], lds_row8<T>(sm.v[dc], kr, 2 * kk + g));
         }
       const float kb = sm.kb[kr], pl2 = sm.pl2;
 #pragma unroll
@@ -575,7 +580,7 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
         for (int e = 0; e < 4; ++e) {
           const int i = 4 * rg + e;
           const float pv = fast_exp2(__builtin_fmaf(scv[i] + kb - l4[rg][e], LOG2E_B, pl2));
-          acc[sub][i] += pv * (dp[i] - d4[rg][e]);
+          acc[sub][i] -= pv * ndp[i];
         }
     }
   };
@@ -624,7 +629,6 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
 // staged once per 64 rows.
 constexpr int DBD_NS = 3;
 constexpr int DBD_MROWS = 64;
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 struct DbdStage {
   unsigned char q[DB_T * ROWB];
   unsigned char d[DB_T * ROWB];
