@@ -146,11 +146,25 @@ def backward_supported(q: torch.Tensor) -> bool:
     return q.dtype in (torch.bfloat16, torch.float16) and d <= 128 and d % 8 == 0
 
 
+_CUS = 256  # MI355X compute units; the pair-bias kernel's LDS ring holds one workgroup each
+_ROW_S = 1.5e-6  # one N_seq row of a 128 x 128 tile (measured at D = 32)
+_PLANE_BPS = 5.0e12  # a partial plane is written once and read once by the ordered reduction
+
+
 def dbias_splits(B: int, S: int, N: int, H: int) -> int:
-    """N_seq ranges for the pair-bias gradient: enough 128 x 128 tiles x ranges for about
-    two workgroups per compute unit of an MI355X (256 CUs), at most N_seq and 64."""
+    """N_seq ranges for the pair-bias gradient (at most N_seq and 64), minimising a cost
+    model: the rounds of (128 x 128 tile, range) workgroups over the compute units times the
+    rows per range, plus the fp32 partial plane that each range writes and the ordered
+    reduction reads back."""
     tiles = B * H * ((N + 127) // 128) ** 2
-    return max(1, min(S, 64, -(-512 // tiles)))
+    plane = B * H * N * N * 4
+    best, best_cost = 1, None
+    for s in range(1, min(S, 64) + 1):
+        rounds = -(-tiles * s // _CUS)
+        cost = rounds * -(-S // s) * _ROW_S + (2 * s * plane / _PLANE_BPS if s > 1 else 0.0)
+        if best_cost is None or cost < best_cost:
+            best, best_cost = s, cost
+    return best
 
 
 def triangle_attention_bwd_hip(q, k, v, o, dout, lse, bias=None, mask=None, scale=None, mask_value=None,

@@ -262,3 +262,19 @@ def test_attention_pair_bias_operator_fake():
         out, pz = torch.ops.gnn_amd.attention_pair_bias_fwd(s, q, q, q, z, w, w, torch.empty(4, 24, dtype=s.dtype),
                                                              None, None, None, None, None, None, 1e-5, False)
         assert out.shape == (6, 16, 32) and pz.shape == (2, 4, 16, 16)
+
+
+def test_dbias_splits_follow_the_measured_optimum():
+    """The pair-bias gradient's N_seq range count: within [1, min(N_seq, 64)], and at the
+    shapes timed on an MI355X (fwd + bwd, bf16, D = 32, B = 1, H = 4) a count that measured
+    at least as fast as the alternatives: N = 256: 16 ranges (0.305-0.312 ms; 32: 0.320-0.322);
+    N = 384: 7 (0.508-0.568; 15: 0.539-0.561); N = 512: 4 (1.024; 8: 1.021-1.045);
+    N = 768: 7 (3.117-3.160; 16: 3.151-3.167; 32: 3.25-3.30; 64: 3.45)."""
+    from geometric_nn_ops_torch.triangle._kernels.triangle_attention import dbias_splits
+
+    assert dbias_splits(1, 256, 256, 4) == 16
+    assert dbias_splits(1, 384, 384, 4) == 7
+    assert dbias_splits(1, 512, 512, 4) == 4
+    assert dbias_splits(1, 768, 768, 4) == 7
+    for B, S, N, H in ((1, 1, 32, 1), (1, 3, 72, 2), (2, 100, 300, 8), (1, 2048, 2048, 4), (4, 64, 64, 16)):
+        assert 1 <= dbias_splits(B, S, N, H) <= min(S, 64)
