@@ -258,7 +258,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the hot path shards over (b, s) rows and channels without collectives, see DESIGN.md",
+              "the hot path would shard over (b, s) rows and channels without collectives",
               file=sys.stderr)
         sys.exit(2)
 
