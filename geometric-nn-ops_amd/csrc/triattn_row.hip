@@ -41,14 +41,15 @@
 // so masking costs no per-score VALU work. The softmax is evaluated against a reference
 // maximum m taken from the row's first tile only: p = exp2((s - m) log2 e) may then exceed 1
 // on later tiles, which costs nothing in precision (bf16 / fp32 are relative) and removes the
-// per-tile maximum reduction. A query block whose row sum ends above 2^64 (so p or the
-// accumulators could have overflowed) is recomputed with the per-tile maximum and lazy
-// rescale (threshold 8 ln 2), the pass that also serves callers asking for the exact row
-// maximum. exp2 with the folded FMA, row sums of the fp32 probabilities before they are
-// rounded for the PV product (as the reference's tl.sum(P_block, 1); v_add_f32, which issues
-// alongside other waves' MFMAs where v_dot2 would hold the matrix pipe), and rows whose keys
-// are all masked reproducing mean(v) (the sentinel swamps the logits; subtract first) are as
-// in the tiled kernel, which gives the same results to rounding.
+// per-tile maximum reduction. A query block whose row sum ends above what the type holds
+// (2^64 for bf16, 65504 for fp16: p or the accumulators could have overflowed) is
+// recomputed with the per-tile maximum and lazy rescale (threshold 8 ln 2); callers asking
+// for the exact row maximum have every tile's maximum reduced on the same fast sweep. exp2
+// with the folded FMA, row sums of the fp32 probabilities before they are rounded for the PV
+// product (as the reference's tl.sum(P_block, 1); v_add_f32, which issues alongside other
+// waves' MFMAs where v_dot2 would hold the matrix pipe), and rows whose keys are all masked
+// reproducing mean(v) (the sentinel swamps the logits; subtract first) are as in the tiled
+// kernel, which gives the same results to rounding.
 #include <algorithm>
 #include <mutex>
 
@@ -114,8 +115,13 @@ size_t row_smem_bytes(int64_t N) {
   return HDR_BYTES + mask_table_bytes(ntiles) + 2 * (size_t)ntiles * TILE_BYTES;
 }
 
-// query blocks whose row sum ends above this are recomputed with the per-tile maximum
-constexpr float FAST_LSUM_LIMIT = 18446744073709551616.0f;  // 2^64
+// Query blocks whose row sum ends above this are recomputed with the per-tile maximum. A
+// lane's row sum bounds every probability it rounded for the PV product, so the limit is what
+// the MFMA type and the fp32 accumulators hold: fp16 rounds p above 65504 to inf (a logit
+// ln 65504 = 11.1 above the first tile's maximum already does), bf16 keeps 2^64 finite with
+// room for the products with v.
+template <typename T> struct FastLimit { static constexpr float value = 18446744073709551616.0f; };  // 2^64
+template <> struct FastLimit<f16> { static constexpr float value = 65504.0f; };
 
 template <typename T> struct BiasFragR {
   typename TypeOps<T>::V8 f[2][2];  // f[sub][t] = bias[q][tile*64 + sub*32 + 16t + 8g + 0..7]
@@ -406,7 +412,7 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
   const int tr_r = lane & 15;
   int tr_off = ((tr_r >> 2) * 32 + 16 * ((lane >> 4) & 1) + 4 * (tr_r & 3)) * 2 + 4 * g * ROW_BYTES;
 
-  // exact row maxima are only tracked for callers that ask for them (per-tile maximum pass)
+  // exact row maxima are only tracked for callers that ask for them
   const bool want_max = a.row_max != nullptr;
   for (int qblk = q0; qblk < qhi; qblk += NW) {
     // The first tiles' LDS reads are the same for every query block; keeping the compiler
@@ -497,9 +503,10 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
 
     // online softmax and O^T += V^T P^T for the scores of tile t. `first`: the row's first
     // tile sets the reference maximum; `per_tile`: every tile's maximum is taken and the
-    // accumulators rescaled when it grows past the threshold.
+    // accumulators rescaled when it grows past the threshold; otherwise, with `want_max`, each
+    // tile's maximum only updates the exact row maximum (the reference maximum stays).
     auto softmax_pv = [&](f32x16 (&sc)[2], int t, bool first, bool per_tile) {
-      if (first || per_tile) {
+      if (first || per_tile || want_max) {
         mfma_result_fence(sc[0], sc[1]);
         float m0 = max3_nn(sc[0][0], sc[0][1], sc[0][2]), m1 = max3_nn(sc[1][0], sc[1][1], sc[1][2]);
 #pragma unroll
@@ -514,7 +521,7 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
           mx = mt;
         } else {
           mx = max_nn(mx, mt);
-          if (__any(mt > m + RESCALE_THRESHOLD)) {
+          if (per_tile && __any(mt > m + RESCALE_THRESHOLD)) {
             const float mnew = fmaxf(m, mt);
             const float alpha = fast_exp2((m - mnew) * LOG2E);
             m = mnew;
@@ -611,9 +618,10 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
         }
       }
     };
-    // A block whose row sum exceeds FAST_LSUM_LIMIT anywhere (p or the accumulators may have
-    // overflowed) runs again with per-tile maxima; so do blocks whose exact maxima are asked for.
-    if (want_max || (sweep(false), __any(!(lsum <= FAST_LSUM_LIMIT)))) sweep(true);
+    // A block whose row sum exceeds FastLimit anywhere (p or the accumulators may have
+    // overflowed) runs again with per-tile maxima.
+    sweep(false);
+    if (__any(!(lsum <= FastLimit<T>::value))) sweep(true);
 
     // ---- normalise and store. o[i] is O[myq][8*(i/4) + 4g + i%4].
     const float ltot = pair_sum_swap(lsum);

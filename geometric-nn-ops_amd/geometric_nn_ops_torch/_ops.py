@@ -22,12 +22,17 @@ import torch
 __all__ = ["triangle_attention_fwd", "trimul_fwd", "attention_pair_bias_fwd", "eager_ok"]
 
 
+_PLAIN_TYPES = (torch.Tensor, torch.nn.Parameter)  # Parameter disables __torch_function__
+
+
 def eager_ok(*tensors) -> bool:
-    """True for an eager call whose tensor arguments are plain tensors (or None) with no
-    tracing or dispatch mode active: the operator's implementation may then run directly."""
+    """True for an eager call whose tensor arguments are plain tensors or module parameters
+    (or None) with no tracing or dispatch mode active: the operator's implementation may then
+    run directly. Tensor subclasses that override ``__torch_function__`` go through the
+    operator."""
     if torch.compiler.is_compiling() or torch._C._len_torch_dispatch_stack() > 0:
         return False
-    return all(t is None or type(t) is torch.Tensor for t in tensors)
+    return all(t is None or type(t) in _PLAIN_TYPES for t in tensors)
 
 
 def triangle_attention_fwd_impl(

@@ -66,7 +66,13 @@ GATE_OUT_MAX_32 = 1024
 GATE_OUT_MAX_WORK = 1 << 21
 
 
-def gate_out_supported(s, o_width, proj_g_weight, proj_o_weight) -> bool:
+def gate_out_supported(s, o, proj_g_weight, proj_o_weight) -> bool:
+    """Whether the fused kernel covers ``(o * sigmoid(s W_g^T + b_g)) W_o^T + b_o``. It takes
+    one token of s per token of o, so s must not broadcast against o (torch's ``o * g`` would
+    accept ``[1, U, Cs]`` against ``[BM, U, D]``); such calls keep the F.linear path."""
+    if tuple(s.shape[:-1]) != tuple(o.shape[:-1]):
+        return False
+    o_width = o.shape[-1]
     cs, co = s.shape[-1], proj_o_weight.shape[0]
     cap = GATE_OUT_MAX_32 if s.dtype == torch.float32 else GATE_OUT_MAX_16
     tokens = s.numel() // max(cs, 1)
@@ -138,7 +144,7 @@ def attention_pair_bias_hip(s, q, k, v, z, *, proj_g_weight, proj_o_weight, proj
     o = triangle_attention_hip(canon(q, U), canon(k, V), canon(v, V), bias=pz.unsqueeze(1), mask=keep,
                                scale=scale, mask_value=mask_value)
     o = o.reshape(BM, U, H * DH).to(s.dtype)
-    if gate_out_supported(s, H * DH, proj_g_weight, proj_o_weight):
+    if gate_out_supported(s, o, proj_g_weight, proj_o_weight):
         return gate_out_hip(s, o, proj_g_weight, proj_g_bias, proj_o_weight, proj_o_bias), pz
     g = torch.sigmoid(F.linear(s, proj_g_weight, proj_g_bias))
     out = F.linear(o * g, proj_o_weight, proj_o_bias)

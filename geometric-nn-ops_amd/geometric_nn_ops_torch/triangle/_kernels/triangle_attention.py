@@ -18,7 +18,6 @@ from .._masking import rounded_mask_value
 
 MAX_HEAD_DIM = 128  # the kernel's largest head-dim tile
 MAX_N_RES = 32768
-ROW_MAX_N = 1024  # 16-bit inputs with D <= 32 up to this N_res run the row-resident kernel
 
 
 def supports(q: torch.Tensor) -> bool:
@@ -58,6 +57,26 @@ def _prepare_bias(bias: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     padded = torch.zeros((B, 1, H, N, pitch), device=bias.device, dtype=bias.dtype)
     padded[..., :N] = bias
     return padded[..., :N]
+
+
+def _set_bias(args, bias: torch.Tensor) -> None:
+    args.bias = bias.data_ptr()
+    args.bias_stride = _lib.I64x4(bias.stride(0), bias.stride(2), bias.stride(3), bias.stride(4))
+
+
+def bias_for_kernel(args, bias: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Points ``args`` (shapes and dtype already set) at the ``[B, 1, H, N, N]`` pair bias in
+    ``dtype`` and returns the tensor the kernel will read (the caller keeps it alive). The
+    library asks for fragment-order scratch exactly when its row-resident kernel runs, and
+    that kernel's pre-pass reads any strides; otherwise the bias is given the unit key stride
+    and aligned pitch the tiled kernel needs. Asking the library keeps this decision in one
+    place (``triattn_row_applicable`` in the C sources)."""
+    bias = bias.to(dtype)
+    _set_bias(args, bias)
+    if _lib.load().gnn_triattn_workspace_bytes(ctypes.byref(args)) == 0:
+        bias = _prepare_bias(bias, dtype)
+        _set_bias(args, bias)
+    return bias
 
 
 def workspace_for(args, device) -> torch.Tensor | None:
@@ -110,11 +129,9 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
     args.k_stride = _lib.I64x4(*kk.stride()[:4])
     args.v_stride = _lib.I64x4(*vk.stride()[:4])
     args.o_stride = _lib.I64x4(*o.stride()[:4])
-    row_kernel = q.dtype in (torch.bfloat16, torch.float16) and Dp <= 32 and N <= ROW_MAX_N
+    args.dtype = _lib.DTYPE_CODE[q.dtype]
     if bias is not None:
-        bias = bias.to(q.dtype) if row_kernel else _prepare_bias(bias, q.dtype)
-        args.bias = bias.data_ptr()
-        args.bias_stride = _lib.I64x4(bias.stride(0), bias.stride(2), bias.stride(3), bias.stride(4))
+        bias = bias_for_kernel(args, bias, q.dtype)
     if mask is not None:
         if mask.dtype != torch.bool:
             raise ValueError(f"mask must be bool (keep=True/mask=False), got {mask.dtype}")
@@ -128,7 +145,6 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
         args.row_max = row_max.data_ptr()
     args.scale = float(scale)
     args.mask_value = rounded_mask_value(q.dtype) if mask_value is None else float(mask_value)
-    args.dtype = _lib.DTYPE_CODE[q.dtype]
     precision = _precision.matmul_precision(fp32_operands=q.dtype == torch.float32)
     args.precision = _lib.PRECISION_CODE[precision]
 

@@ -208,6 +208,36 @@ def test_operators_have_fake_implementations():
         assert out.shape == x.shape and out.dtype == x.dtype
 
 
+def test_fused_gate_needs_one_s_token_per_o_token():
+    """The fused gate / output projection takes its token count from s; an s that would only
+    broadcast against o (torch's o * g accepts it) keeps the F.linear path."""
+    from geometric_nn_ops_torch.triangle._kernels import attention_pair_bias as K
+
+    o, gw, ow = torch.empty(3, 40, 64), torch.empty(64, 96), torch.empty(32, 64)
+    assert K.gate_out_supported(torch.empty(3, 40, 96), o, gw, ow)
+    assert not K.gate_out_supported(torch.empty(1, 40, 96), o, gw, ow)
+    assert not K.gate_out_supported(torch.empty(40, 96), o, gw, ow)
+
+
+def test_eager_fast_path_accepts_module_parameters():
+    """Module weights are nn.Parameter: a plain eager call with them still runs the operator's
+    implementation directly; tensor subclasses and dispatch modes go through the operator."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from geometric_nn_ops_torch import _ops
+
+    t = torch.ones(3)
+    lin = torch.nn.Linear(4, 4)
+    assert _ops.eager_ok(t, None, lin.weight, lin.bias)
+
+    class Sub(torch.Tensor):
+        pass
+
+    assert not _ops.eager_ok(t, t.as_subclass(Sub))
+    with FakeTensorMode():
+        assert not _ops.eager_ok(torch.empty(3))
+
+
 
 # ---------------------------------------------------------------- attention with pair bias
 def test_attention_pair_bias_signature_matches_the_reference():

@@ -61,3 +61,39 @@ def test_compile_fullgraph_matches_eager():
         compiled = torch.compile(block, fullgraph=True, backend="aot_eager")(q, k, v, bias, amask, x, tmask)
     for e, c in zip(eager, compiled):
         assert torch.equal(e, c)
+
+
+def test_hip_graph_replays_match_eager():
+    """The entry points are capturable: attention (with its bias pre-pass) and both trimul
+    directions captured once as a HIP graph and replayed several times, with eager work and
+    synchronisations between the replays; every replay equals the eager result bit for bit.
+    (The library records no memset nodes: its scratch is rewritten in full by each call.)"""
+    from geometric_nn_ops_torch.triangle import triangle_attention, triangle_multiplicative_update
+
+    q, k, v, bias, amask = _attn_args()
+    x, tmask, w = _trimul_args()
+
+    def block():
+        return (triangle_attention(q, k, v, bias, amask),
+                triangle_multiplicative_update(x, "outgoing", tmask, **w),
+                triangle_multiplicative_update(x, "incoming", tmask, **w))
+
+    with torch.no_grad():
+        eager = block()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # warm the allocator and the library off the capture
+            block()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            captured = block()
+        for replay in range(4):
+            for t in captured:
+                t.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            for got, want in zip(captured, eager):
+                assert torch.equal(got, want), replay
+            block()  # eager work between the replays
+            torch.cuda.synchronize()

@@ -178,6 +178,38 @@ def test_triangle_attention_return_aux_gpu(dtype):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("jump", [0.0, 25.0], ids=["plain", "hot_later_keys"])
+def test_return_aux_is_one_forward(dtype, jump):
+    """return_aux=True on the HIP path is a single forward that writes o, lse and the exact
+    row maximum; o is bit-identical to the plain call. With keys in later 64-key tiles whose
+    logits lie `jump` above the first tile's (the row kernel measures its probabilities
+    against the first tile's maximum), lse and max still match the oracle."""
+    from geometric_nn_ops_torch.triangle._kernels import triangle_attention as hip
+    from helpers import Tolerance, assert_close_to_oracle
+
+    g = torch.Generator().manual_seed(5)
+    B, N, H, S, D = 1, 2, 4, 200, 32
+    q, k, v = (torch.randn(B, N, H, S, D, generator=g) for _ in range(3))
+    bias = 0.5 * torch.randn(1, 1, H, S, S, generator=g)
+    bias[..., [140, 190]] += jump
+    mask = torch.rand(B, N, 1, 1, S, generator=g) < 0.8
+    mask[..., 0] = True
+    q, k, v, bias, mask = (t.to("cuda", dtype) if t.is_floating_point() else t.to("cuda")
+                           for t in (q, k, v, bias, mask))
+    with torch.no_grad():
+        plain = cueq.triangle_attention(q, k, v, bias, mask=mask)
+        with mock.patch.object(hip, "triangle_attention_hip", wraps=hip.triangle_attention_hip) as spy:
+            out, lse, mx = cueq.triangle_attention(q, k, v, bias, mask=mask, return_aux=True)
+    assert spy.call_count == 1
+    assert torch.equal(out, plain) and torch.isfinite(out).all()
+    want_lse, want_mx = _aux_oracle(q, k, bias, mask, D**-0.5)
+    tol = Tolerance(1 - 1e-5, 5e-3)
+    assert_close_to_oracle("lse", lse, want_lse, tol)
+    assert_close_to_oracle("max", mx, want_mx, tol)
+
+
+@pytest.mark.gpu
 def test_shim_runs_the_hip_kernels_exactly():
     q, k, v, bias, mask = _cueq_attention_inputs("cuda", torch.bfloat16)
     swap = lambda t: t.transpose(-2, -3)  # noqa: E731

@@ -151,6 +151,45 @@ def test_uniform_logits(dtype):
     torch.testing.assert_close(out.double(), expected, rtol=0, atol=ulp)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("jump", [20.0, 60.0])
+@pytest.mark.parametrize(("with_bias", "with_mask"), [(False, False), (True, False), (True, True)],
+                         ids=["plain", "bias", "bias_mask"])
+@pytest.mark.parametrize("D", [32, 64], ids=["row_kernel", "tiled_kernel"])
+def test_large_logit_in_a_later_tile(dtype, jump, with_bias, with_mask, D):
+    """Keys in later 64-key tiles whose logits lie `jump` above everything in the first tile.
+    The row kernel's fast path measures probabilities against the first tile's maximum, so
+    they exceed 1 there: an fp16 probability above 65504 would round to inf (jump 20 already
+    gives e^20 = 4.9e8), a bf16 row sum above 2^64 needs the recompute with per-tile maxima
+    (jump 60). Outputs must stay finite and match the oracle, with and without bias / mask."""
+    B, S, N, H = 1, 3, 200, 2
+    t = attention_inputs(B, S, N, H, D, dtype, seed=31, with_bias=with_bias, bias_scale=1.0)
+    hot = [130, 199]  # tile 2 and the partial last tile
+    if with_bias:
+        b = t["bias"].float()
+        b[..., :, hot] += jump
+        t["bias"] = b.to(dtype)
+    else:
+        # q > 0 everywhere; k of the hot keys constant, so q . k * D^-1/2 ~ 0.8 sqrt(D) kappa
+        q = t["q"].float().abs()
+        t["q"] = q.to(dtype)
+        kappa = jump / (0.8 * D**0.5)
+        k = t["k"].float()
+        k[:, :, hot] = kappa
+        t["k"] = k.to(dtype)
+    mask = None
+    if with_mask:
+        mask = key_mask(B, S, N, seed=7)
+        mask[:, 0, ..., hot] = True   # row 0 keeps both hot keys
+        mask[:, 1, ..., hot] = False  # row 1 masks both
+        mask[:, 2, ..., 130] = True   # row 2 keeps one
+        mask[:, 2, ..., 199] = False
+    want = oracle_of(t, mask, D**-0.5)
+    got = hip_attn(**dev(t), mask=None if mask is None else mask.to(DEV), scale=D**-0.5)
+    assert torch.isfinite(got).all()
+    assert_close_to_oracle("out", got, want, TRIANGLE_ATTENTION_TOL[dtype, "ieee"], rel_fro_max=NORTH_STAR_REL_FRO)
+
+
 def test_mask_none_equals_all_keep():
     B, S, N, H, D = 1, 2, 32, 4, 32
     t = dev(attention_inputs(B, S, N, H, D, torch.bfloat16, seed=13))

@@ -306,6 +306,25 @@ def test_no_grad_modes_use_the_kernel(no_backward):
     assert kern.called and not ref.called
 
 
+def test_module_parameters_take_the_direct_implementation():
+    """Weights held as nn.Parameter (what a module passes) run the operator's implementation
+    directly in eager mode, not through the torch.library dispatch, with the same result."""
+    from geometric_nn_ops_torch import _ops
+    from geometric_nn_ops_torch.triangle import triangle_multiplicative_update
+
+    w = {k: v.to(DEV) for k, v in trimul_weights(32, 32, torch.bfloat16, seed=1).items()}
+    params = {k: torch.nn.Parameter(v) for k, v in w.items()}
+    x, mask = pair_input(1, 12, 32, torch.bfloat16, seed=3)
+    x, mask = x.to(DEV), mask.to(DEV)
+    with torch.no_grad():
+        want = triangle_multiplicative_update(x, "outgoing", mask, **w)
+        with mock.patch.object(_ops, "trimul_fwd", side_effect=AssertionError("dispatched")), \
+                mock.patch.object(_ops, "trimul_fwd_impl", wraps=_ops.trimul_fwd_impl) as impl:
+            got = triangle_multiplicative_update(x, "outgoing", mask, **params)
+    assert impl.called
+    torch.testing.assert_close(got, want, rtol=0, atol=0)
+
+
 @pytest.mark.parametrize("case", ["float64", "c_hidden_48"])
 def test_unsupported_configs_use_the_torch_path(case):
     """Configurations without kernels. (Calls that need gradients run the HIP forward and
