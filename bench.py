@@ -37,6 +37,7 @@ that of the dominant kernel, its bound chosen by arithmetic intensity against th
 
 import argparse
 import ctypes
+import gc
 import json
 import os
 import pathlib
@@ -71,6 +72,13 @@ def parse():
                     help="profile helper: run only one op, or only the other BASELINE configurations "
                          "(the JSON line is then partial)")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward timings")
+    ap.add_argument("--trace-steps", action="store_true",
+                    help="a spin_kernel marker launch before and after the timed eager steps and the timed graph "
+                         "replays, which --summarize-trace uses to pick them out of a kernel trace")
+    ap.add_argument("--summarize-trace", default=None, metavar="KERNEL_TRACE_CSV",
+                    help="print per-kernel durations and launch gaps of a rocprofv3 kernel trace and exit")
+    ap.add_argument("--sweep", action=argparse.BooleanOptionalAction, default=True,
+                    help="the trimul size sweep and peak-memory table of the public ops")
     ap.add_argument("--copy-calib", action="store_true",
                     help="profile helper: run a plain 256 MiB device copy (known HBM bytes) and exit, "
                          "to scale FETCH_SIZE / WRITE_SIZE counter readings")
@@ -78,6 +86,54 @@ def parse():
 
 
 # --------------------------------------------------------------------------------- timing
+def region_marker():
+    """One ``spin_kernel`` launch (torch.cuda._sleep), which a kernel trace shows by name:
+    ``--trace-steps`` puts one before and one after the timed steps, and
+    ``--summarize-trace`` reports the launches between each such pair."""
+    import torch
+
+    torch.cuda._sleep(1000)
+
+
+def summarize_trace(path, steps=None):
+    """Markdown tables of a rocprofv3 kernel-trace CSV: for each region between two
+    ``spin_kernel`` markers (the whole trace when there are none), per kernel the number of
+    launches and their mean / median duration, then the idle gaps between consecutive
+    launches and, given ``steps``, the span and kernel time per step."""
+    import csv
+
+    rows = []
+    with open(path, newline="") as fh:
+        for r in csv.DictReader(fh):
+            name = r["Kernel_Name"]
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]),
+                         "spin_kernel" if "::spin_kernel(" in name else
+                         name.replace("(anonymous namespace)", "anon").split("(")[0]))
+    rows.sort()
+    marks = [i for i, r in enumerate(rows) if r[2] == "spin_kernel"]
+    regions = [rows[marks[i] + 1:marks[i + 1]] for i in range(0, len(marks) - 1, 2)] if len(marks) >= 2 else [rows]
+    out = []
+    for ri, reg in enumerate(regions):
+        per = {}
+        for t0, t1, name in reg:
+            per.setdefault(name, []).append((t1 - t0) / 1e3)
+        busy = sum(sum(v) for v in per.values())
+        out += [f"### region {ri + 1}", "", "| kernel | launches | mean us | median us | share of busy time |",
+                "|---|---|---|---|---|"]
+        for name, ds in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+            out.append(f"| `{name}` | {len(ds)} | {sum(ds) / len(ds):.2f} | {statistics.median(ds):.2f} | "
+                       f"{sum(ds) / busy:.3f} |")
+        gaps = [(reg[i + 1][0] - reg[i][1]) / 1e3 for i in range(len(reg) - 1)]
+        span = (reg[-1][1] - reg[0][0]) / 1e3
+        out += ["", f"launches: {len(reg)}; busy {busy:.1f} us of a {span:.1f} us span; gap between launches: "
+                    f"mean {sum(gaps) / max(len(gaps), 1):.2f} us, median {statistics.median(gaps) if gaps else 0:.2f} us, "
+                    f"max {max(gaps) if gaps else 0:.2f} us"]
+        if steps:
+            out.append(f"per step ({steps} steps): span {span / steps:.1f} us, kernel time {busy / steps:.1f} us")
+        out.append("")
+    return "\n".join(out)
+
+
 def window_ms(fn, stream, window=100.0, warmup=10, min_reps=10, max_reps=5000):
     """(median, mean, reps) of event-pair durations of ``fn`` on ``stream``, repeated until
     the durations add up to ``window`` ms (at least ``min_reps``), after ``warmup`` calls."""
@@ -204,17 +260,14 @@ class AttnCall:
         a.B, a.S, a.N, a.H, a.D = B, S, N, H, D
         for name, t in (("q_stride", q), ("k_stride", k), ("v_stride", v), ("o_stride", self.o)):
             setattr(a, name, _lib.I64x4(*t.stride()[:4]))
-        if bias is not None:
-            if not (q.dtype in (torch.bfloat16, torch.float16) and D <= 32 and N <= TA.ROW_MAX_N):
-                bias = TA._prepare_bias(bias, q.dtype)  # the tiled kernel needs unit key stride
-            a.bias = bias.data_ptr()
-            a.bias_stride = _lib.I64x4(bias.stride(0), bias.stride(2), bias.stride(3), bias.stride(4))
         if mask is not None:
             a.mask = mask.data_ptr()
             a.mask_stride = _lib.I64x3(mask.stride(0), mask.stride(1), mask.stride(4))
         a.scale, a.mask_value = D**-0.5, rounded_mask_value(q.dtype)
         a.dtype = _lib.DTYPE_CODE[q.dtype]
         a.precision = _lib.PRECISION_CODE["bf16x3" if precision == "tf32" else "ieee"]
+        if bias is not None:
+            bias = TA.bias_for_kernel(a, bias, q.dtype)  # the layout the library's kernel reads
         self.ws = TA.workspace_for(a, q.device)
         self.args = a
         self.keep = (q, k, v, bias, mask)
@@ -256,6 +309,9 @@ class TrimulCall:
 # ------------------------------------------------------------------------------ main
 def main():
     args = parse()
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace, args.steps))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "the hot path would shard over (b, s) rows and channels without collectives",
@@ -353,21 +409,53 @@ def main():
     for _ in range(args.warmup):
         eager_step()
 
-    def timed_steps(run_step):
+    def timed_steps(run_step, trace=False):
         t_start = torch.cuda.Event(enable_timing=True)
         t_end = torch.cuda.Event(enable_timing=True)
+        if trace:
+            region_marker()
         torch.cuda.synchronize()
+        gc.disable()  # no collector pause inside the timed launches
         t0 = time.perf_counter()
         t_start.record(stream)
         for _ in range(args.steps):
             run_step()
         t_end.record(stream)
         torch.cuda.synchronize()
-        return t_start.elapsed_time(t_end) / args.steps, time.perf_counter() - t0
+        wall = time.perf_counter() - t0
+        gc.enable()
+        if trace:
+            region_marker()
+            torch.cuda.synchronize()
+        return t_start.elapsed_time(t_end) / args.steps, wall
 
     outputs = ([attn.o] if args.only in (None, "attn") else []) + \
         ([tri[d].out for d in ("outgoing", "incoming")] if args.only in (None, "trimul") else [])
-    ms_step, wall_eager = timed_steps(eager_step)
+    ms_step, wall_eager = timed_steps(eager_step, trace=args.trace_steps)
+
+    # ---- in-step durations: the same number of steps again with an event pair around every
+    # entry point, so each one runs in the cache state the step leaves it in (the step's other
+    # kernels evict its inputs from the 256 MB Infinity Cache, which the warm windows above
+    # keep them in); the sum of the per-entry-point means is checked against ms_per_step
+    in_ev = {name: [] for name, _ in kernels}
+    torch.cuda.synchronize()
+    gc.disable()
+    for _ in range(args.steps):
+        for name, fn in kernels:
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            in_ev[name].append((e0, e1))
+    torch.cuda.synchronize()
+    gc.enable()
+    in_step = {}
+    for name, pairs in in_ev.items():
+        ts = [e0.elapsed_time(e1) for e0, e1 in pairs]
+        in_step[name] = {"mean_ms": round(sum(ts) / len(ts), 5), "median_ms": round(statistics.median(ts), 5),
+                         "warm_mean_ms": round(kern_mean[name], 5)}
+    in_step_sum = sum(r["mean_ms"] for r in in_step.values())
     want_out = [t.clone() for t in outputs]
     graph_ms, graph_ok = None, None
     try:
@@ -380,7 +468,7 @@ def main():
         torch.cuda.synchronize()
         graph_ok = all(torch.equal(t, ww) for t, ww in zip(outputs, want_out))
         if graph_ok:
-            graph_ms, _ = timed_steps(graph.replay)
+            graph_ms, _ = timed_steps(graph.replay, trace=args.trace_steps)
             graph_ok = all(torch.equal(t, ww) for t, ww in zip(outputs, want_out))
     except Exception as exc:  # pragma: no cover - reported, eager numbers stand
         print(f"bench.py: HIP graph capture failed, eager timing used: {exc}", file=sys.stderr)
@@ -432,6 +520,12 @@ def main():
         public = {"triangle_attention_ms": round(pa[0], 5), "c_abi_triattn_fwd_ms": per_kernel["triattn_fwd"]["ms"],
                   "triangle_multiplicative_update_outgoing_ms": round(pt[0], 5),
                   "c_abi_trimul_fwd_outgoing_ms": round(capi_trimul[0], 5)}
+
+    # ---- the public ops: the reference harness's trimul size sweep, the attention ops, and
+    # peak memory per call
+    sweep = None
+    if args.sweep and args.only is None:
+        sweep = public_sweep(dev, stream)
 
     # ---- the other BASELINE configurations
     configs = None
@@ -498,9 +592,12 @@ def main():
         for label, use_torch in (("hip_fwd_bwd_ms", False), ("torch_autograd_fwd_bwd_ms", True)):
             tri_backward[label] = round(window_ms(lambda: fwd_bwd(use_torch), stream, warmup=2, min_reps=5)[0], 4)
 
-    # ---- roofline of the dominant kernel (its average launch time over the window)
-    dominant = max(kern_mean, key=kern_mean.get)
-    dk = rates(flops[dominant], nbytes[dominant], kern_mean[dominant])
+    # ---- roofline of the dominant kernel: its average launch time inside the step (the warm
+    # window's average beside it)
+    step_mean = {name: r["mean_ms"] for name, r in in_step.items()}
+    dominant = max(step_mean, key=step_mean.get)
+    dk = rates(flops[dominant], nbytes[dominant], step_mean[dominant])
+    dk_warm = rates(flops[dominant], nbytes[dominant], kern_mean[dominant])
     traffic = None
     if TRAFFIC_FILE.exists():
         try:
@@ -515,8 +612,14 @@ def main():
                 "unit": "GB/s", "frac": dk["hbm_frac"], "traffic": traffic}
     roof.update({"algorithmic_flops_per_launch": flops[dominant], "algorithmic_bytes_per_launch": nbytes[dominant],
                  "ai_flop_per_byte": dk["ai_flop_per_byte"], "ridge_flop_per_byte": round(RIDGE, 1),
-                 "avg_launch_ms": round(kern_mean[dominant], 5), "mfma_frac": dk["mfma_frac"],
-                 "hbm_frac": dk["hbm_frac"]})
+                 "avg_launch_ms": round(step_mean[dominant], 5), "timing": "mean of its launches in the timed steps",
+                 "mfma_frac": dk["mfma_frac"], "hbm_frac": dk["hbm_frac"],
+                 "warm": {"avg_launch_ms": round(kern_mean[dominant], 5), "achieved": dk_warm[
+                     "tflops" if dk["bound"] == "mfma" else "gbs"], "mfma_frac": dk_warm["mfma_frac"],
+                     "hbm_frac": dk_warm["hbm_frac"]}})
+    for name, r in in_step.items():
+        rr = rates(flops[name], nbytes[name], r["mean_ms"])
+        r.update({"tflops": rr["tflops"], "gbs": rr["gbs"], "mfma_frac": rr["mfma_frac"], "hbm_frac": rr["hbm_frac"]})
 
     step_flops = sum(flops[name] for name, _ in kernels)
     value = step_flops / (ms_step * 1e-3) / 1e12
@@ -542,6 +645,8 @@ def main():
         "mfma_frac_step": round(value / PEAK_BF16_TFLOPS, 4),
         "graph_ms_per_step": round(graph_ms, 5) if graph_ms is not None else None,
         "graph_replays_match_eager": graph_ok,
+        "in_step": {"kernels": in_step, "sum_of_means_ms": round(in_step_sum, 5),
+                    "sum_over_ms_per_step": round(in_step_sum / ms_step, 4)},
         "kernels": per_kernel,
         "hbm_reference": hbm_ref,
         "parity": gate,
@@ -549,6 +654,7 @@ def main():
         "cold_ms_per_step": round(sum(cold_ms.values()), 5) if cold_ms else None,
         "public_api_ms": public,
         "configs": configs,
+        "public_sweep": sweep,
         "triton_reference": "unavailable: the reference's Triton kernels are not installed on the box and "
                             "the reference does not travel to it",
         "wall_s_timed": round(wall_eager, 4),
@@ -560,6 +666,101 @@ def main():
     else:
         line["cpu_baseline"] = cpu_baseline(q, k, v, bias, x, tmask, w, step_flops)
     print(json.dumps(line), flush=True)
+
+
+# ---------------------------------------------------------- public ops: sweep and memory
+GIB = float(1 << 30)
+
+
+def peak_gib(fn):
+    """Peak allocated and reserved GiB over one call of ``fn`` (the reference harness's
+    peak_memory_gib, benchmarks/_bench_common.py:74-92: vendor-BLAS workspaces and the
+    allocator's cache released first, so the figure does not depend on run order)."""
+    import torch
+
+    torch.cuda.synchronize()
+    clear = getattr(torch._C, "_cuda_clearCublasWorkspaces", None)
+    if clear is not None:
+        clear()
+    torch.cuda.empty_cache()
+    torch.cuda.reset_peak_memory_stats()
+    fn()
+    torch.cuda.synchronize()
+    return {"allocated_gib": round(torch.cuda.max_memory_allocated() / GIB, 4),
+            "reserved_gib": round(torch.cuda.max_memory_reserved() / GIB, 4)}
+
+
+def public_sweep(dev, stream):
+    """The reference harness's trimul micro-benchmark through the public op
+    (benchmarks/bench_trimul_micro.py:55-98 at its sizes 256 / 384 / 512 / 768, :115), both
+    directions, bf16, c_z = 128: ``fwd_train_ms`` (x and the weights require grad, so the
+    forward saves what the backward needs), ``fwd_infer_ms`` (inference_mode) and ``bwd_ms``
+    (autograd.grad over x and every weight, retain_graph), each the median of a >= 100 ms
+    window; with the peak memory of one inference forward and of one forward + backward. The
+    same columns for triangle_attention at the headline shape and attention_pair_bias at the
+    AF3 pairformer size (its backward runs the torch path: the reference has no other)."""
+    import torch
+
+    from geometric_nn_ops_torch.triangle import (attention_pair_bias, triangle_attention,
+                                                 triangle_multiplicative_update)
+
+    def columns(fwd, grad_inputs):
+        def fwd_infer():
+            with torch.inference_mode():
+                return fwd()
+
+        out = fwd()
+        gout = torch.randn_like(out)
+
+        def bwd():
+            torch.autograd.grad([out], grad_inputs, grad_outputs=[gout], retain_graph=True)
+
+        def fwd_bwd():
+            y = fwd()
+            torch.autograd.grad([y], grad_inputs, grad_outputs=[gout])
+
+        row = {"fwd_train_ms": round(window_ms(fwd, stream, warmup=3, min_reps=5)[0], 5),
+               "fwd_infer_ms": round(window_ms(fwd_infer, stream, warmup=3, min_reps=5)[0], 5),
+               "bwd_ms": round(window_ms(bwd, stream, warmup=3, min_reps=5)[0], 5)}
+        del out
+        row["peak_fwd_infer"] = peak_gib(fwd_infer)
+        row["peak_fwd_bwd"] = peak_gib(fwd_bwd)
+        return row
+
+    res = {"trimul": {}}
+    C = 128
+    for N in (256, 384, 512, 768):
+        gen = Gen()
+        x = gen.randn(1, N, N, C, dtype=torch.bfloat16).to(dev).requires_grad_()
+        w = {kk: vv.to(dev).requires_grad_() for kk, vv in
+             trimul_weights(gen, C, C, torch.bfloat16, ln_random=True).items()}
+        live = torch.arange(N, device=dev) < N - N // 8
+        mask = (live[:, None] & live[None, :]).to(torch.bfloat16)[None]
+        for direction in ("outgoing", "incoming"):
+            res["trimul"][f"n{N}_{direction}"] = columns(
+                lambda: triangle_multiplicative_update(x, direction, mask, **w), [x, *w.values()])
+        del x, w
+
+    gen = Gen()
+    N, H, D = 512, 4, 32
+    q, k, v = (gen.randn(1, N, N, H, D, dtype=torch.bfloat16).to(dev).requires_grad_() for _ in range(3))
+    bias = gen.randn(1, 1, H, N, N, dtype=torch.bfloat16).to(dev).requires_grad_()
+    res["triangle_attention_n512"] = columns(lambda: triangle_attention(q, k, v, bias), [q, k, v, bias])
+    del q, k, v, bias
+
+    gen = Gen()
+    B, H, U, DH, Zc, Cs = 1, 16, 384, 24, 128, 384
+    s = gen.randn(B, U, Cs, dtype=torch.bfloat16).to(dev).requires_grad_()
+    q, k, v = (gen.randn(B, H, U, DH, dtype=torch.bfloat16).to(dev).requires_grad_() for _ in range(3))
+    z = gen.randn(B, U, U, Zc, dtype=torch.bfloat16).to(dev).requires_grad_()
+    wts = {"proj_g_weight": gen.randn(Cs, Cs, scale=Cs**-0.5), "proj_o_weight": gen.randn(Cs, Cs, scale=Cs**-0.5),
+           "proj_z_weight": gen.randn(H, Zc, scale=Zc**-0.5), "ln_z_weight": 1.0 + gen.randn(Zc, scale=0.1)}
+    wts = {kk: vv.to(dev, torch.bfloat16).requires_grad_() for kk, vv in wts.items()}
+    mask = (torch.arange(U, device=dev) < U - 40).to(torch.bfloat16)[None]
+    res["attention_pair_bias_af3_384"] = columns(
+        lambda: attention_pair_bias(s, q, k, v, z, mask=mask, **wts)[0], [s, q, k, v, z, *wts.values()])
+    res["attention_pair_bias_af3_384"]["shape"] = "B=1, tokens=384, H=16, DH=24, c_s=384, c_z=128, 40 keys masked"
+    return res
 
 
 # ------------------------------------------------------------------- other configurations
