@@ -95,6 +95,14 @@ template <typename T>
 __device__ __forceinline__ void store8(T* p, const typename TypeOps<T>::V8& v) {
   *reinterpret_cast<typename TypeOps<T>::V8*>(p) = v;
 }
+// load8 through a global-address-space pointer: a global_load counts only in vmcnt, where a
+// flat_load (what the compiler emits when it cannot prove a pointer global) counts in lgkmcnt
+// too, so that every later wait for an LDS read would also wait for it.
+template <typename T>
+__device__ __forceinline__ typename TypeOps<T>::V8 load8_global(const T* p) {
+  typedef typename TypeOps<T>::V8 V8;
+  return *(const __attribute__((address_space(1))) V8*)(p);
+}
 template <typename T>
 __device__ __forceinline__ typename TypeOps<T>::V4 load4(const T* p) {
   return *reinterpret_cast<const typename TypeOps<T>::V4*>(p);

@@ -147,7 +147,7 @@ __device__ __forceinline__ void load_bias_tile(BiasFragR<T>& bf, const T* tile) 
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-    for (int t = 0; t < 2; ++t) bf.f[sub][t] = load8(tile + (2 * sub + t) * 512);
+    for (int t = 0; t < 2; ++t) bf.f[sub][t] = load8_global(tile + (2 * sub + t) * 512);
 }
 
 // One thread per 16-byte chunk of the caller's bias, taken in row-major order within each

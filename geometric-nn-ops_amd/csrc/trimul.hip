@@ -174,16 +174,31 @@ __device__ __forceinline__ int64_t proj_pix(const PTile& tl, int pl, int N, bool
   const int qq = outgoing ? cpos : tl.row;
   return ((int64_t)tl.b * N + pp) * N + qq;
 }
+
+// The mask value of local pixel pl, requested as raw bits and converted only where the
+// tile is normalised (ProjMask::value). A use of a load's result right behind it makes the
+// compiler wait for every load in flight (vmcnt is an in-order counter), so converting the
+// mask where it is loaded would also wait for the next tile's x, which is requested just
+// before it and meant to arrive during the current tile's work. Pixels past N read pixel
+// N - 1 (in bounds) and count as 1.
 template <typename T>
-__device__ __forceinline__ float proj_mask(const gnn_trimul_args& a, const PTile& tl, int pl, int N,
-                                           bool outgoing) {
-  if (!a.mask || tl.c0 + pl >= N) return 1.f;
-  const int cpos = tl.c0 + pl;
-  const int pp = outgoing ? tl.row : cpos;
-  const int qq = outgoing ? cpos : tl.row;
-  return TypeOps<T>::to_f32(
-      ((const T*)a.mask)[tl.b * a.mask_stride[0] + pp * a.mask_stride[1] + qq * a.mask_stride[2]]);
-}
+struct ProjMask {
+  typedef typename std::conditional<sizeof(T) == 2, uint16_t, uint32_t>::type Bits;
+  Bits bits = 0;
+  bool use = false;  // the caller gave a mask and the pixel is inside the grid
+  __device__ __forceinline__ void request(const gnn_trimul_args& a, const PTile& tl, int pl, int N, bool outgoing) {
+    use = a.mask != nullptr && tl.c0 + pl < N;
+    if (a.mask) {  // uniform
+      const int cpos = min(tl.c0 + pl, N - 1);
+      const int pp = outgoing ? tl.row : cpos;
+      const int qq = outgoing ? cpos : tl.row;
+      bits = ((const Bits*)a.mask)[tl.b * a.mask_stride[0] + pp * a.mask_stride[1] + qq * a.mask_stride[2]];
+    }
+  }
+  __device__ __forceinline__ float value() const {
+    return use ? TypeOps<T>::to_f32(__builtin_bit_cast(T, bits)) : 1.f;
+  }
+};
 
 // Chunks of x per thread that the tile load must hold: ceil(C / 64), rounded up to 2, 4, 8.
 __host__ __device__ inline int proj_xm(int64_t C) { return C <= 128 ? 2 : C <= 256 ? 4 : 8; }
@@ -218,7 +233,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_kernel(const gnn_trimul_ar
   // ---- tile load + LayerNorm, thread = (pixel xpl, part xpart) holding chunks xpart + 8j
   const int xpl = tid >> 3, xpart = tid & 7, cpp = C / 8;
   V8 xr[XM];
-  float mreg = 1.f;
+  ProjMask<T> mreg;
   auto load_x = [&](const Tile& tl) {
     const bool in = tl.c0 + xpl < N;
     const T* src = (const T*)a.x + (in ? pix_index(tl, xpl) * C : 0);
@@ -228,7 +243,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_kernel(const gnn_trimul_ar
       xr[j] = zero8<T>();
       if (in && ci < cpp) xr[j] = load8(src + 8 * ci);
     }
-    if (tid < PTP) mreg = proj_mask<T>(a, tl, tid, N, outgoing);
+    mreg.request(a, tl, tid & (PTP - 1), N, outgoing);  // used by the threads tid < PTP
   };
   auto ln_partial = [&]() {
     float s = 0.f, n = 0.f;
@@ -290,7 +305,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_kernel(const gnn_trimul_ar
         store8(&zs[xpl * ZR + 8 * ci], TypeOps<T>::from_f32(v));
       }
     }
-    if (tid < PTP) mk[tid] = mreg;
+    if (tid < PTP) mk[tid] = mreg.value();
   };
 
   // ---- projections of one tile
@@ -539,16 +554,16 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
 
   // ---- tile load + wave-local LayerNorm: thread = (pixel xpl, part xpart), chunks xpart + 8j
   const int xpl = tid >> 3, xpart = tid & 7;
-  V8 xr[XMF];
-  float mreg = 1.f;
-  auto load_x = [&](const PTile& tl) {
-    const bool in = tl.c0 + xpl < N;
-    const T* src = (const T*)a.x + (in ? proj_pix(tl, xpl, N, outgoing) * CK : 0);
+  // Pixels past N load pixel N - 1 (finite values; their z only reaches their own outputs,
+  // which are stored as zeros or not at all), so the loads need no select and never wait
+  // for the previous tile's loads into the same registers.
+  auto load_x = [&](V8 (&xr)[XMF], ProjMask<T>& mreg, const PTile& tl) {
+    const T* src = (const T*)a.x + proj_pix(tl, min(xpl, N - 1 - tl.c0), N, outgoing) * CK;
 #pragma unroll
-    for (int j = 0; j < XMF; ++j) xr[j] = in ? load8(src + 8 * (xpart + 8 * j)) : zero8<T>();
-    if (tid < PTP) mreg = proj_mask<T>(a, tl, tid, N, outgoing);
+    for (int j = 0; j < XMF; ++j) xr[j] = load8(src + 8 * (xpart + 8 * j));
+    mreg.request(a, tl, tid & (PTP - 1), N, outgoing);  // used by the threads tid < PTP
   };
-  auto ln_store = [&](int nb) {
+  auto ln_store = [&](const V8 (&xr)[XMF], const ProjMask<T>& mreg, int nb) {
     f32x8 v[XMF];
     float s = 0.f;
 #pragma unroll
@@ -585,8 +600,9 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
       store8(&zs[(nb * PTP + xpl) * ZR + k], TypeOps<T>::from_f32(z));
     }
     if (tid < PTP) {  // wave 0 (PTP = 64): the tile's mask values and whether all are one
-      mk[nb * PTP + tid] = mreg;
-      const bool all1 = __ballot(mreg != 1.f) == 0;
+      const float mv = mreg.value();
+      mk[nb * PTP + tid] = mv;
+      const bool all1 = __ballot(mv != 1.f) == 0;
       if (tid == 0) mk1[nb] = all1;
     }
   };
@@ -604,6 +620,43 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
 
   // the unit's sub-tiles in the order (so, 1 - so): the gate item's sub-tile first
   const int s_first = has_go ? so : 0;
+
+  // global stores of a staged projection unit / gate item (16-byte stores from the wave's
+  // staging tile)
+  auto store_unit = [&](const PTile& tl, int u) {
+    // 8 lanes per 64-pixel channel row: lane = (channel row lane / 8 + 8 i, pixels
+    // 8 (lane % 8) ..). c_hidden is a multiple of 32, so the unit's 32 channels all belong to
+    // a or all to b, and store i is store 0 moved by 8 channel planes.
+    const int crow0 = lane >> 3, p0 = (lane & 7) * 8;
+    const bool in_a = 32 * u < Ch;
+    const int chh0 = 32 * u + crow0 - (in_a ? 0 : Ch);
+    T* drow = (in_a ? a_cm : b_cm) + ab_offset<T>((int64_t)tl.b * Ch + chh0, tl.row, tl.c0 + p0, N, NP);
+    const int64_t pstep = ab_offset<T>(8, 0, 0, N, NP);  // 8 channel planes
+    const bool full = tl.c0 + p0 + 8 <= N, tail = !full && tl.c0 + p0 < NP;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const V8 val = load8(&ebuf[(crow0 + 8 * i) * ER + (p0 ^ EBSW(crow0 + 8 * i))]);
+      if (full) {
+        store8(drow + i * pstep, val);
+      } else if (tail) {  // row tail: pixels N .. NP-1 are written as zeros
+        V8 v = val;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (tl.c0 + p0 + e >= N) v[e] = TypeOps<T>::from_f32(0.f);
+        store8(drow + i * pstep, v);
+      }
+    }
+  };
+  auto store_gate = [&](const PTile& tl) {
+    // 4 lanes per 32-channel pixel row segment; store 1 is store 0 moved by 16 pixels along
+    // the tile (a column step outgoing, a row step incoming)
+    const int px = lane >> 2, k0 = (lane & 3) * 8, pl = 32 * so + px;
+    T* dst = gout + proj_pix(tl, pl, N, outgoing) * CK + 32 * uo + k0;
+    const int64_t step16 = (outgoing ? 16 : 16 * (int64_t)N) * CK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      if (tl.c0 + pl + 16 * i < N) store8(dst + i * step16, load8(&gbuf[(px + 16 * i) * EG + (k0 ^ EBSW(px + 16 * i))]));
+  };
 
   auto compute = [&](const PTile& tl, int cb) {
     const T* z = zs + cb * PTP * ZR;
@@ -680,30 +733,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
         }
       }
       wave_lds_sync();
-      // 16-byte stores, 8 lanes per 64-pixel channel row: lane = (channel row lane / 8 + 8 i,
-      // pixels 8 (lane % 8) ..). c_hidden is a multiple of 32, so the unit's 32 channels all
-      // belong to a or all to b, and store i is store 0 moved by 8 channel planes.
-      {
-        const int crow0 = lane >> 3, p0 = (lane & 7) * 8;
-        const bool in_a = 32 * u < Ch;
-        const int chh0 = 32 * u + crow0 - (in_a ? 0 : Ch);
-        T* drow = (in_a ? a_cm : b_cm) + ab_offset<T>((int64_t)tl.b * Ch + chh0, tl.row, tl.c0 + p0, N, NP);
-        const int64_t pstep = ab_offset<T>(8, 0, 0, N, NP);  // 8 channel planes
-        const bool full = tl.c0 + p0 + 8 <= N, tail = !full && tl.c0 + p0 < NP;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const V8 val = load8(&ebuf[(crow0 + 8 * i) * ER + (p0 ^ EBSW(crow0 + 8 * i))]);
-          if (full) {
-            store8(drow + i * pstep, val);
-          } else if (tail) {  // row tail: pixels N .. NP-1 are written as zeros
-            V8 v = val;
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-              if (tl.c0 + p0 + e >= N) v[e] = TypeOps<T>::from_f32(0.f);
-            store8(drow + i * pstep, v);
-          }
-        }
-      }
+      store_unit(tl, u);
       wave_lds_sync();
     }
     if (!go_done) {  // no projection unit this tile: the gate item on its own
@@ -721,40 +751,332 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
         store4(&gbuf[l32 * EG + ((8 * rg + 4 * g) ^ EBSW(l32))], TypeOps<T>::from_f32(v));
       }
       wave_lds_sync();
-      // 16-byte stores, 4 lanes per 32-channel pixel row segment; store 1 is store 0 moved
-      // by 16 pixels along the tile (a column step outgoing, a row step incoming)
-      {
-        const int px = lane >> 2, k0 = (lane & 3) * 8, pl = 32 * so + px;
-        T* dst = gout + proj_pix(tl, pl, N, outgoing) * CK + 32 * uo + k0;
-        const int64_t step16 = (outgoing ? 16 : 16 * (int64_t)N) * CK;
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-          if (tl.c0 + pl + 16 * i < N) store8(dst + i * step16, load8(&gbuf[(px + 16 * i) * EG + (k0 ^ EBSW(px + 16 * i))]));
-      }
+      store_gate(tl);
     }
   };
 
   int64_t t = blockIdx.x;
   if (t >= ntiles) return;  // uniform over the workgroup
+  V8 xr[XMF];
+  ProjMask<T> mreg;
   PTile cur = proj_tile(t, N, outgoing);
-  load_x(cur);
+  load_x(xr, mreg, cur);
   __syncthreads();  // LN parameters and gate weights in LDS
-  ln_store(0);
+  ln_store(xr, mreg, 0);
   __syncthreads();
   int cb = 0;
   for (; t < ntiles; t += gridDim.x) {
     const int64_t tn = t + gridDim.x;
     const bool has_next = tn < ntiles;  // uniform over the workgroup
-    PTile nxt = cur;
-    if (has_next) {
-      nxt = proj_tile(tn, N, outgoing);
-      load_x(nxt);
-    }
+    // the next tile's x (the current one's again after the last tile: unconditional, so the
+    // compiler sees no path on which these loads are still in flight at the next iteration)
+    const PTile nxt = has_next ? proj_tile(tn, N, outgoing) : cur;
+    load_x(xr, mreg, nxt);
     compute(cur, cb);
-    if (has_next) ln_store(cb ^ 1);
+    ln_store(xr, mreg, cb ^ 1);  // after the last tile into the free buffer: nobody reads it
     __syncthreads();  // tile cb consumed by every wave, tile cb ^ 1 complete
     cb ^= 1;
     cur = nxt;
+  }
+}
+
+// ---- stage 1, ping-pong variant: 16-bit types with C = c_hidden = 128 ---------------------
+// The fixed-width kernel above runs every wave of its workgroup through the same sequence
+// (MFMAs, then the sigmoid epilogue, then the next tile's LayerNorm) between two barriers, so
+// the two waves that share a SIMD (w and w + 4) are always in the same phase and the matrix
+// pipe idles while the vector ALU works and the other way round. Here the workgroup is two
+// groups of four waves, A = waves 0-3 (one per SIMD) and B = waves 4-7, run half a tile
+// apart: in one barrier interval A runs the MFMAs of tile t while B runs the epilogue of tile
+// t - 1 and a half of the LayerNorm of tile t + 1, and in the next interval the roles swap.
+// Wave w owns projection unit w (32 channels of [a; b] with their g_in gate, weights in
+// registers for the whole launch) and gate item w (32 output-gate channels, 32(w % 4)..,
+// over the 32-pixel half w / 4 of the tile). Each group normalises the 32 pixels of its own
+// half (8 lanes per pixel, wave-local sums), so z of a tile is complete after the two
+// epilogue intervals that precede its first MFMA interval. Intervals (s = 0 .. 2 nt, with a
+// barrier after each; tiles t = 0 .. nt - 1 are this workgroup's):
+//   s = 2t:     A: MFMAs of t (z buffer t % 2), x of t + 1 requested (its half).
+//               B: epilogue of t - 1, LayerNorm of t + 1 (its half) into z buffer (t + 1) % 2.
+//   s = 2t + 1: A: epilogue of t, LayerNorm of t + 1 (its half).
+//               B: MFMAs of t, x of t + 2 requested (its half).
+// The mask values of a tile (read by the epilogues) are kept in three LDS slots, because B
+// reads tile t's while writing tile t + 2's.
+struct ProjPPLds {
+  static constexpr int CK = 128;
+  static constexpr int ZR = CK + 8;  // z and gate-weight row pitch (16-bit elements)
+  static constexpr int ER = 72;      // unit staging [32 channels][64 pixels + 8]
+  static constexpr int EG = 40;      // gate staging [32 pixels][32 channels + 8]
+  static constexpr size_t zs = 0;                                  // [2][PTP][ZR]
+  static constexpr size_t wgo = zs + 2 * (size_t)PTP * ZR * 2;     // [CK][ZR]
+  static constexpr size_t ebuf = wgo + (size_t)CK * ZR * 2;        // [PW][32][ER]
+  static constexpr size_t gbuf = ebuf + (size_t)PW * 32 * ER * 2;  // [PW][32][EG]
+  static constexpr size_t bgo = gbuf + (size_t)PW * 32 * EG * 2;   // [CK] fp32
+  static constexpr size_t lnw = bgo + (size_t)CK * 4;              // gamma, beta [2][CK] fp32
+  static constexpr size_t mk = lnw + 2 * (size_t)CK * 4;           // [3][PTP] fp32
+  static constexpr size_t mk1 = mk + 3 * (size_t)PTP * 4;          // [3][2] int: half all ones
+  static constexpr size_t total = mk1 + 32;
+};
+
+template <typename T>
+__global__ __launch_bounds__(PNT, 1) void trimul_proj_pp_kernel(const gnn_trimul_args a, int64_t NP,
+                                                                size_t off_a, size_t off_b, size_t off_g) {
+  static_assert(sizeof(T) == 2, "ping-pong projection: 16-bit types");
+  typedef typename TypeOps<T>::V8 V8;
+  typedef ProjPPLds LD;
+  constexpr int CK = LD::CK, Ch = CK;
+  constexpr int ZR = LD::ZR, ER = LD::ER, EG = LD::EG;
+  constexpr int NKS = CK / 16;  // k-steps
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int N = (int)a.N;
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2;  // 0: group A, 1: group B
+  T* zs = reinterpret_cast<T*>(smem_raw + LD::zs);
+  T* wgo_s = reinterpret_cast<T*>(smem_raw + LD::wgo);
+  T* ebuf = reinterpret_cast<T*>(smem_raw + LD::ebuf) + wave * 32 * ER;
+  T* gbuf = reinterpret_cast<T*>(smem_raw + LD::gbuf) + wave * 32 * EG;
+  float* bgo_s = reinterpret_cast<float*>(smem_raw + LD::bgo);
+  float* lnw = reinterpret_cast<float*>(smem_raw + LD::lnw);
+  float* lnb = lnw + CK;
+  float* mk = reinterpret_cast<float*>(smem_raw + LD::mk);
+  int* mk1 = reinterpret_cast<int*>(smem_raw + LD::mk1);
+  const bool outgoing = a.outgoing != 0;
+  const int64_t ntiles = (int64_t)a.B * N * ((N + PTP - 1) / PTP);
+  if ((int64_t)blockIdx.x >= ntiles) return;  // uniform over the workgroup
+  const int nt = (int)((ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x);  // this workgroup's tiles
+  constexpr float NLOG2E = -1.4426950408889634f;
+  auto tile_of = [&](int k) { return proj_tile((int64_t)blockIdx.x + (int64_t)k * gridDim.x, N, outgoing); };
+
+  // ---- per-workgroup constants
+  {
+    const T* wgo = (const T*)a.g_out_w;
+    for (int c = tid; c < CK * CK / 8; c += PNT) {
+      const int r = c / (CK / 8), k0 = (c % (CK / 8)) * 8;
+      store8(&wgo_s[r * ZR + k0], load8(wgo + r * CK + k0));
+    }
+    for (int c = tid; c < CK; c += PNT) {
+      bgo_s[c] = ld_or<T>(a.g_out_b, c, 0.f) * NLOG2E;  // the exp2 argument's bias term
+      lnw[c] = ld_or<T>(a.ln_in_w, c, 1.f);
+      lnb[c] = ld_or<T>(a.ln_in_b, c, 0.f);
+    }
+  }
+
+  // ---- the group's half of a tile: thread (pixel xpl, part xpart), chunks xpart + 8j
+  const int gt = tid & 255;
+  const int xpl = 32 * grp + (gt >> 3), xpart = gt & 7;
+  V8 xr[2];
+  ProjMask<T> mreg;
+  auto load_x = [&](const PTile& tl) {  // pixels past N load pixel N - 1, as in the kernel above
+    const T* src = (const T*)a.x + proj_pix(tl, min(xpl, N - 1 - tl.c0), N, outgoing) * CK;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) xr[j] = load8(src + 8 * (xpart + 8 * j));
+    mreg.request(a, tl, 32 * grp + (gt & 31), N, outgoing);  // used by the threads gt < 32
+  };
+  auto ln_store = [&](int k) {  // LayerNorm of the half of local tile k held in xr
+    const int zb = k & 1, mb = k % 3;
+    f32x8 v[2];
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      v[j] = TypeOps<T>::to_f32(xr[j]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += v[j][e];
+    }
+    s = sum8_dpp(s);
+    const float mean = s * (1.0f / CK);
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = v[j][e] - mean;
+        q += d * d;
+      }
+    q = sum8_dpp(q);
+    const float rstd = __builtin_amdgcn_rsqf(q * (1.0f / CK) + a.eps);  // as torch's rsqrt
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int kk = 8 * (xpart + 8 * j);
+      const f32x4 w0 = *reinterpret_cast<const f32x4*>(lnw + kk);
+      const f32x4 w1 = *reinterpret_cast<const f32x4*>(lnw + kk + 4);
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(lnb + kk);
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(lnb + kk + 4);
+      f32x8 z;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        z[e] = (v[j][e] - mean) * rstd * w0[e] + b0[e];
+        z[e + 4] = (v[j][e + 4] - mean) * rstd * w1[e] + b1[e];
+      }
+      store8(&zs[(zb * PTP + xpl) * ZR + kk], TypeOps<T>::from_f32(z));
+    }
+    if (gt < 32) {  // first wave of the group: its half's mask values and whether all are one
+      const float mv = mreg.value();
+      mk[mb * PTP + 32 * grp + gt] = mv;
+      const bool all1 = __ballot(mv != 1.f) == 0;
+      if (gt == 0) mk1[2 * mb + grp] = all1;
+    }
+  };
+
+  // ---- the wave's weights (one projection unit, one gate item), for the whole launch
+  const int u = wave, ch = 32 * u + l32;
+  const int uo = wave & 3, so = grp;  // gate item: channels 32 uo .., pixels 32 so ..
+  V8 wpf[NKS], wgf[NKS];
+  {
+    const T* wprow = (const T*)a.p_in_w + (int64_t)ch * CK + 8 * g;
+    const T* wgrow = (const T*)a.g_in_w + (int64_t)ch * CK + 8 * g;
+#pragma unroll
+    for (int k = 0; k < NKS; ++k) {
+      wpf[k] = load8(wprow + 16 * k);
+      wgf[k] = load8(wgrow + 16 * k);
+    }
+  }
+  const float bp = ld_or<T>(a.p_in_b, ch, 0.f);
+  const float bg = ld_or<T>(a.g_in_b, ch, 0.f) * NLOG2E;  // the exp2 argument's bias term
+  T* __restrict__ a_cm = (T*)((unsigned char*)a.workspace + off_a);
+  T* __restrict__ b_cm = (T*)((unsigned char*)a.workspace + off_b);
+  T* __restrict__ gout = (T*)(a.gate ? (unsigned char*)a.gate : (unsigned char*)a.workspace + off_g);
+
+  // accumulators carried from a wave's MFMA interval to its epilogue interval:
+  // accp / accg [sub][r]: pixel 32 sub' + 8(r/4) + 4g + r%4 (sub' = so for sub 0, 1 - so for
+  // sub 1), channel ch; accgo[r]: gate channel 32 uo + 8(r/4) + 4g + r%4, pixel 32 so + l32
+  f32x16 accp[PSUB], accg[PSUB], accgo;
+  auto mfma = [&](int k) {
+    const T* z = zs + (k & 1) * PTP * ZR;
+    const T* zrow0 = z + (32 * so + l32) * ZR + 8 * g;        // the gate item's half first
+    const T* zrow1 = z + (32 * (1 - so) + l32) * ZR + 8 * g;
+    const T* wgrow_s = wgo_s + (32 * uo + l32) * ZR + 8 * g;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      accp[0][r] = 0.f;
+      accp[1][r] = 0.f;
+      accg[0][r] = 0.f;
+      accg[1][r] = 0.f;
+      accgo[r] = 0.f;
+    }
+#pragma unroll
+    for (int kk = 0; kk < NKS; ++kk) {
+      const V8 z0 = load8(zrow0 + 16 * kk);
+      const V8 z1 = load8(zrow1 + 16 * kk);
+      const V8 wg = load8(wgrow_s + 16 * kk);
+      Mma<T, PREC_NATIVE>::step(accp[0], z0, wpf[kk]);
+      Mma<T, PREC_NATIVE>::step(accg[0], z0, wgf[kk]);
+      Mma<T, PREC_NATIVE>::step(accgo, wg, z0);
+      Mma<T, PREC_NATIVE>::step(accp[1], z1, wpf[kk]);
+      Mma<T, PREC_NATIVE>::step(accg[1], z1, wgf[kk]);
+    }
+  };
+  // epilogue, first half: the gated values into the wave's staging tiles (LDS)
+  auto epilogue_stage = [&](int k) {
+    const int mb = k % 3;
+    const float* m = mk + mb * PTP;
+    const bool all1 = mk1[2 * mb] != 0 && mk1[2 * mb + 1] != 0;
+#pragma unroll
+    for (int s = 0; s < PSUB; ++s) {
+      const int sub = s == 0 ? so : 1 - so;
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int pt = 32 * sub + 8 * rg + 4 * g;  // pixel within the tile
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = (accp[s][4 * rg + e] + bp) *
+                 __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(accg[s][4 * rg + e], NLOG2E, bg)));
+        if (!all1) {
+          const f32x4 m4 = *reinterpret_cast<const f32x4*>(&m[pt]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] *= m4[e];
+        }
+        store4(&ebuf[l32 * ER + (pt ^ EBSW(l32))], TypeOps<T>::from_f32(v));
+      }
+    }
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      const f32x4 nb4 = *reinterpret_cast<const f32x4*>(&bgo_s[32 * uo + 8 * rg + 4 * g]);
+      f32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[e] = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(accgo[4 * rg + e], NLOG2E, nb4[e])));
+      store4(&gbuf[l32 * EG + ((8 * rg + 4 * g) ^ EBSW(l32))], TypeOps<T>::from_f32(v));
+    }
+    wave_lds_sync();
+  };
+  // epilogue, second half: the staging tiles to global memory with 16-byte stores. Issued
+  // after the interval's LayerNorm: its wait for the x loads (vmcnt counts loads and stores
+  // in order) then covers no store of this tile.
+  auto epilogue_store = [&](int k) {
+    const PTile tl = tile_of(k);
+    // unit: 8 lanes per 64-pixel channel row (store i: 8 channel planes on)
+    {
+      const int crow0 = lane >> 3, p0 = (lane & 7) * 8;
+      const bool in_a = 32 * u < Ch;
+      const int chh0 = 32 * u + crow0 - (in_a ? 0 : Ch);
+      T* drow = (in_a ? a_cm : b_cm) + ab_offset<T>((int64_t)tl.b * Ch + chh0, tl.row, tl.c0 + p0, N, NP);
+      const int64_t pstep = ab_offset<T>(8, 0, 0, N, NP);
+      const bool full = tl.c0 + p0 + 8 <= N, tail = !full && tl.c0 + p0 < NP;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const V8 val = load8(&ebuf[(crow0 + 8 * i) * ER + (p0 ^ EBSW(crow0 + 8 * i))]);
+        if (full) {
+          store8(drow + i * pstep, val);
+        } else if (tail) {  // row tail: pixels N .. NP-1 are written as zeros
+          V8 vv = val;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (tl.c0 + p0 + e >= N) vv[e] = TypeOps<T>::from_f32(0.f);
+          store8(drow + i * pstep, vv);
+        }
+      }
+    }
+    // gate item: 4 lanes per 32-channel pixel row segment
+    {
+      const int px = lane >> 2, k0 = (lane & 3) * 8, pl = 32 * so + px;
+      T* dst = gout + proj_pix(tl, pl, N, outgoing) * CK + 32 * uo + k0;
+      const int64_t step16 = (outgoing ? 16 : 16 * (int64_t)N) * CK;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        if (tl.c0 + pl + 16 * i < N) store8(dst + i * step16, load8(&gbuf[(px + 16 * i) * EG + (k0 ^ EBSW(px + 16 * i))]));
+    }
+    wave_lds_sync();  // the staging tiles are rewritten by the next epilogue
+  };
+
+  // ---- prologue: tile 0 normalised by both groups; B requests its half of tile 1
+  load_x(tile_of(0));
+  __syncthreads();  // LN parameters and gate weights in LDS
+  ln_store(0);
+  if (grp == 1) load_x(tile_of(min(1, nt - 1)));
+  __syncthreads();
+
+  // Each group runs its own loop, so that the compiler sees the real alternation of its
+  // intervals (a loop over s with both kinds of interval behind a branch makes it assume an
+  // MFMA interval may follow another, and wait there for loads that have long completed,
+  // and with them, vmcnt being in order, for every store since). Both loops execute 2 nt + 1
+  // barriers.
+  // The x loads and LayerNorms past the last tile are done anyway, on the last tile's x into
+  // slots nobody reads any more (z slot (nt + 1) % 2 and mask slots nt % 3, (nt + 1) % 3 are
+  // free by then): kept unconditional, they leave the compiler no path on which a load is
+  // still in flight at the next interval.
+  if (grp == 0) {
+    for (int k = 0; k < nt; ++k) {
+      mfma(k);  // s = 2k
+      load_x(tile_of(min(k + 1, nt - 1)));
+      __syncthreads();
+      epilogue_stage(k);  // s = 2k + 1
+      ln_store(k + 1);
+      epilogue_store(k);
+      __syncthreads();
+    }
+    __syncthreads();  // s = 2 nt: B's last epilogue
+  } else {
+    ln_store(1);  // s = 0
+    __syncthreads();
+    for (int k = 0; k < nt; ++k) {
+      mfma(k);  // s = 2k + 1
+      load_x(tile_of(min(k + 2, nt - 1)));
+      __syncthreads();
+      epilogue_stage(k);  // s = 2k + 2
+      ln_store(k + 2);
+      epilogue_store(k);
+      __syncthreads();
+    }
   }
 }
 
@@ -1317,9 +1639,26 @@ int launch_proj_fast(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_
   return (int)hipGetLastError();
 }
 
+#ifndef GNN_PROJ_PINGPONG  // 1: trimul_proj_pp_kernel for C = c_hidden = 128 (measured slower)
+#define GNN_PROJ_PINGPONG 0
+#endif
+template <typename T>
+int launch_proj_pp(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
+  const int64_t NP = round_up(a.N, 32);
+  const int64_t ntiles = a.B * a.N * ((a.N + PTP - 1) / PTP);
+  constexpr size_t smem = ProjPPLds::total;
+  const void* fn = (const void*)trimul_proj_pp_kernel<T>;
+  (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  const int64_t grid = std::min<int64_t>(ntiles, persistent_grid(fn, PNT, smem));
+  hipLaunchKernelGGL((trimul_proj_pp_kernel<T>), dim3((uint32_t)grid), dim3(PNT), smem, st, a, NP, L.off_a,
+                     L.off_b, L.off_g);
+  return (int)hipGetLastError();
+}
+
 template <typename T, int PREC>
 int launch_proj(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
   if constexpr (sizeof(T) == 2) {
+    if (GNN_PROJ_PINGPONG && a.C == 128 && a.Ch == 128) return launch_proj_pp<T>(a, L, st);
     if (a.C == 128 && a.Ch == 128) return launch_proj_fast<T, 128, 128>(a, L, st);
     if (a.C == 128) return launch_proj_fast<T, 128, 0>(a, L, st);
     if (a.C == 64) return launch_proj_fast<T, 64, 0>(a, L, st);
