@@ -520,6 +520,17 @@ def main():
         public = {"triangle_attention_ms": round(pa[0], 5), "c_abi_triattn_fwd_ms": per_kernel["triattn_fwd"]["ms"],
                   "triangle_multiplicative_update_outgoing_ms": round(pt[0], 5),
                   "c_abi_trimul_fwd_outgoing_ms": round(capi_trimul[0], 5)}
+        # the cueq shim's return_aux (o, lse and the row maximum from one forward) against a
+        # plain shim call, on the same inputs in cueq's (B, N, H, S, D) layout
+        import cuequivariance_ops_torch as cueq
+
+        cq, ck, cv = (t.transpose(2, 3) for t in (qd, kd, vd))
+        with torch.inference_mode():
+            plain = window_ms(lambda: cueq.triangle_attention(cq, ck, cv, bd, scale=D**-0.5), stream)
+            aux = window_ms(lambda: cueq.triangle_attention(cq, ck, cv, bd, scale=D**-0.5, return_aux=True), stream)
+        public.update({"cueq_triangle_attention_ms": round(plain[0], 5),
+                       "cueq_triangle_attention_return_aux_ms": round(aux[0], 5),
+                       "return_aux_over_plain": round(aux[0] / plain[0], 3)})
 
     # ---- the public ops: the reference harness's trimul size sweep, the attention ops, and
     # peak memory per call

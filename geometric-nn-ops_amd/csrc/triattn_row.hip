@@ -233,7 +233,9 @@ __device__ __forceinline__ typename TypeOps<T>::V4 tr_read4_r(const unsigned cha
   return __builtin_bit_cast(typename TypeOps<T>::V4, v);
 }
 
-template <typename T, bool HAS_BIAS, int NW>
+// WMAX: the caller asked for the exact row maximum (a separate instantiation, so that the
+// common one carries no maximum tracking in its fast sweep: it would spill at 128 VGPRs)
+template <typename T, bool HAS_BIAS, int NW, bool WMAX>
 __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_kernel(const gnn_triattn_args a) {
   constexpr int NT = NW * 64;
   constexpr bool QPF_SWEEP = GNN_ROW_QPREFETCH && (GNN_ROW_QPREFETCH == 2 || !HAS_BIAS);
@@ -413,7 +415,7 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
   int tr_off = ((tr_r >> 2) * 32 + 16 * ((lane >> 4) & 1) + 4 * (tr_r & 3)) * 2 + 4 * g * ROW_BYTES;
 
   // exact row maxima are only tracked for callers that ask for them
-  const bool want_max = a.row_max != nullptr;
+  constexpr bool want_max = WMAX;
   for (int qblk = q0; qblk < qhi; qblk += NW) {
     // The first tiles' LDS reads are the same for every query block; keeping the compiler
     // from hoisting them out of this loop keeps their registers free for the key loop.
@@ -643,9 +645,9 @@ __global__ __launch_bounds__(NW * 64, GNN_ROW_WAVES_PER_SIMD) void triattn_row_k
   }
 }
 
-template <typename T, bool HAS_BIAS, int NW>
+template <typename T, bool HAS_BIAS, int NW, bool WMAX>
 int launch_row_nw(const gnn_triattn_args& a, hipStream_t stream, size_t smem) {
-  const void* fn = (const void*)triattn_row_kernel<T, HAS_BIAS, NW>;
+  const void* fn = (const void*)triattn_row_kernel<T, HAS_BIAS, NW, WMAX>;
   if (smem > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   const int64_t nblk = a.B * a.S * a.H;
   // split rows (first halves first, second halves last): as many as one workgroup per CU,
@@ -657,8 +659,8 @@ int launch_row_nw(const gnn_triattn_args& a, hipStream_t stream, size_t smem) {
         hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
       nsplit = std::min<int64_t>(ncu, nblk);
   }
-  hipLaunchKernelGGL((triattn_row_kernel<T, HAS_BIAS, NW>), dim3((uint32_t)(nblk + nsplit)), dim3(NW * 64), smem,
-                     stream, a);
+  hipLaunchKernelGGL((triattn_row_kernel<T, HAS_BIAS, NW, WMAX>), dim3((uint32_t)(nblk + nsplit)), dim3(NW * 64),
+                     smem, stream, a);
   return (int)hipGetLastError();
 }
 
@@ -670,8 +672,12 @@ int launch_row(const gnn_triattn_args& a, hipStream_t stream) {
                        (T*)a.workspace, nchunks);
   }
   const size_t smem = row_smem_bytes(a.N);
-  if (smem > ROW_TWO_PER_CU_BYTES) return launch_row_nw<T, HAS_BIAS, 16>(a, stream, smem);
-  return launch_row_nw<T, HAS_BIAS, 8>(a, stream, smem);
+  if (a.row_max) {
+    if (smem > ROW_TWO_PER_CU_BYTES) return launch_row_nw<T, HAS_BIAS, 16, true>(a, stream, smem);
+    return launch_row_nw<T, HAS_BIAS, 8, true>(a, stream, smem);
+  }
+  if (smem > ROW_TWO_PER_CU_BYTES) return launch_row_nw<T, HAS_BIAS, 16, false>(a, stream, smem);
+  return launch_row_nw<T, HAS_BIAS, 8, false>(a, stream, smem);
 }
 
 }  // namespace
