@@ -759,6 +759,33 @@ def public_sweep(dev, stream):
     res["triangle_attention_n512"] = columns(lambda: triangle_attention(q, k, v, bias), [q, k, v, bias])
     del q, k, v, bias
 
+    # fp32 attention gradients at the C5 fp32 size (N_seq = N_res = 384): the HIP backward under
+    # both fp32 precision settings against autograd through the torch restatement (which
+    # materialises the [B, S, H, N, N] fp32 logits), forward + backward and its peak memory
+    from geometric_nn_ops_torch.triangle._reference.triangle_attention import triangle_attention_torch
+
+    gen = Gen()
+    N, H, D = 384, 4, 32
+    q, k, v = (gen.randn(1, N, N, H, D).to(dev).requires_grad_() for _ in range(3))
+    bias = gen.randn(1, 1, H, N, N).to(dev).requires_grad_()
+    gout = gen.randn(1, N, N, H, D).to(dev)
+    fp32 = {}
+    old_prec = torch.backends.cuda.matmul.fp32_precision
+    try:
+        for label, prec, fn in (("hip_ieee", "ieee", triangle_attention), ("hip_tf32", "tf32", triangle_attention),
+                                ("torch_autograd", "ieee", triangle_attention_torch)):
+            torch.backends.cuda.matmul.fp32_precision = prec
+
+            def fwd_bwd():
+                torch.autograd.grad([fn(q, k, v, bias)], [q, k, v, bias], grad_outputs=[gout])
+
+            fp32[label] = {"fwd_bwd_ms": round(window_ms(fwd_bwd, stream, warmup=2, min_reps=3)[0], 4),
+                           "peak": peak_gib(fwd_bwd)}
+    finally:
+        torch.backends.cuda.matmul.fp32_precision = old_prec
+    res["triangle_attention_fp32_n384_fwd_bwd"] = fp32
+    del q, k, v, bias, gout
+
     gen = Gen()
     B, H, U, DH, Zc, Cs = 1, 16, 384, 24, 128, 384
     s = gen.randn(B, U, Cs, dtype=torch.bfloat16).to(dev).requires_grad_()

@@ -56,6 +56,11 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // XOR-swizzled by (r / 4) % 4: row-major fragment reads of 32 consecutive rows and the
 // transposed reads of 4-row groups both hit distinct bank groups.
 __device__ __forceinline__ int swz(int r, int c) { return r * ROWB + 16 * (c ^ ((r >> 2) & 3)); }
+// The same for a [row][32] tile of T: rows of 32 elements, chunks of 8 elements (16 bytes for
+// 16-bit types, as swz; 32 bytes for fp32) XOR-swizzled by (r / 4) % 4.
+template <typename T> __host__ __device__ constexpr int rowb() { return 32 * (int)sizeof(T); }
+template <typename T>
+__device__ __forceinline__ int swzt(int r, int c) { return r * rowb<T>() + 8 * (int)sizeof(T) * (c ^ ((r >> 2) & 3)); }
 
 template <typename T>
 __device__ __forceinline__ typename TypeOps<T>::V4 tr4(const unsigned char* p) {
@@ -85,9 +90,34 @@ __device__ __forceinline__ typename TypeOps<T>::V8 tr_frag(const unsigned char* 
   return f;
 }
 
+// fp32: the transposed fragment from scalar LDS reads, same element order
+template <>
+__device__ __forceinline__ f32x8 tr_frag<float>(const unsigned char* tile, int row0, int kk, int lane) {
+  const int g = lane >> 5, col = lane & 31;
+  f32x8 f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int row = row0 + 16 * kk + 8 * (e >> 2) + 4 * g + (e & 3);
+    f[e] = *reinterpret_cast<const float*>(tile + swzt<float>(row, col >> 3) + 4 * (col & 7));
+  }
+  return f;
+}
+
 template <typename T>
 __device__ __forceinline__ typename TypeOps<T>::V8 lds_row8(const unsigned char* tile, int row, int chunk) {
-  return *reinterpret_cast<const typename TypeOps<T>::V8*>(tile + swz(row, chunk));
+  return *reinterpret_cast<const typename TypeOps<T>::V8*>(tile + swzt<T>(row, chunk));
+}
+
+// -x of a fragment (a sign flip per element)
+template <typename T>
+__device__ __forceinline__ typename TypeOps<T>::V8 neg8(const typename TypeOps<T>::V8& x) {
+  if constexpr (sizeof(T) == 2) {
+    u32x4 u = __builtin_bit_cast(u32x4, x);
+    u ^= 0x80008000u;
+    return __builtin_bit_cast(typename TypeOps<T>::V8, u);
+  } else {
+    return -x;
+  }
 }
 
 template <typename T>
@@ -115,18 +145,18 @@ __device__ __forceinline__ typename TypeOps<T>::V8 row8(const T* row, int d0, in
 
 // ------------------------------------------------------------------------- dK, dV
 // LDS: Q' tile and dO tile [64][32] (swizzled), lse and Delta of the tile's queries.
-template <int DC>
+template <typename T, int DC>
 struct DkdvLds {
-  unsigned char q[DC][BT * ROWB];
-  unsigned char d[DC][BT * ROWB];
+  unsigned char q[DC][BT * rowb<T>()];
+  unsigned char d[DC][BT * rowb<T>()];
   float lse[BT];
   float delta[BT];
 };
 
-template <typename T, bool HAS_BIAS, int DC>
+template <typename T, bool HAS_BIAS, int DC, int PREC>
 __global__ __launch_bounds__(BNT, DC > 2 ? 1 : 2) void bwd_dkdv_kernel(const gnn_triattn_bwd_args a) {
   typedef typename TypeOps<T>::V8 V8;
-  __shared__ __align__(16) DkdvLds<DC> sm;
+  __shared__ __align__(16) DkdvLds<T, DC> sm;
   const int N = (int)a.N, H = (int)a.H, D = (int)a.D;
   const int nkb = (N + 127) / 128;
   const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
@@ -191,8 +221,8 @@ __global__ __launch_bounds__(BNT, DC > 2 ? 1 : 2) void bwd_dkdv_kernel(const gnn
       for (int dc = 0; dc < DC; ++dc) {
         V8 x = row8(qp + (int64_t)(ok ? qi : 0) * a.q_stride[2], 32 * dc + 8 * c, D, ok);
         const f32x8 xf = TypeOps<T>::to_f32(x) * a.scale;
-        *reinterpret_cast<V8*>(sm.q[dc] + swz(r, c)) = TypeOps<T>::from_f32(xf);
-        *reinterpret_cast<V8*>(sm.d[dc] + swz(r, c)) =
+        *reinterpret_cast<V8*>(sm.q[dc] + swzt<T>(r, c)) = TypeOps<T>::from_f32(xf);
+        *reinterpret_cast<V8*>(sm.d[dc] + swzt<T>(r, c)) =
             row8(dop + (int64_t)(ok ? qi : 0) * a.do_stride[2], 32 * dc + 8 * c, D, ok);
       }
       if (tid < BT) {
@@ -214,8 +244,8 @@ __global__ __launch_bounds__(BNT, DC > 2 ? 1 : 2) void bwd_dkdv_kernel(const gnn
       for (int dc = 0; dc < DC; ++dc)
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          Mma<T, PREC_NATIVE>::step(sc, lds_row8<T>(sm.q[dc], r0 + l32, 2 * kk + g), kf[dc][kk]);
-          Mma<T, PREC_NATIVE>::step(dp, lds_row8<T>(sm.d[dc], r0 + l32, 2 * kk + g), vf[dc][kk]);
+          Mma<T, PREC>::step(sc, lds_row8<T>(sm.q[dc], r0 + l32, 2 * kk + g), kf[dc][kk]);
+          Mma<T, PREC>::step(dp, lds_row8<T>(sm.d[dc], r0 + l32, 2 * kk + g), vf[dc][kk]);
         }
       if constexpr (HAS_BIAS) {
         // A = bias rows (lane = query, 8 consecutive keys of the wave's 32), B = identity
@@ -225,7 +255,7 @@ __global__ __launch_bounds__(BNT, DC > 2 ? 1 : 2) void bwd_dkdv_kernel(const gnn
         for (int t = 0; t < 2; ++t) {
           const int k0 = kb * 128 + wave * 32 + 16 * t + 8 * g;
           const V8 bfr = qi < N ? load8_bias_tail<T>(brow, k0, N) : zero8<T>();
-          Mma<T, PREC_NATIVE>::step(sc, bfr, idf[t]);
+          Mma<T, PREC>::step(sc, bfr, idf[t]);
         }
       }
       // P and dS for this lane's key and its 16 queries
@@ -250,8 +280,8 @@ __global__ __launch_bounds__(BNT, DC > 2 ? 1 : 2) void bwd_dkdv_kernel(const gnn
       for (int dc = 0; dc < DC; ++dc)
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          Mma<T, PREC_NATIVE>::step(dv[dc], acc_to_frag<T>(p, kk), tr_frag<T>(sm.d[dc], r0, kk, lane));
-          Mma<T, PREC_NATIVE>::step(dk[dc], acc_to_frag<T>(ds, kk), tr_frag<T>(sm.q[dc], r0, kk, lane));
+          Mma<T, PREC>::step(dv[dc], acc_to_frag<T>(p, kk), tr_frag<T>(sm.d[dc], r0, kk, lane));
+          Mma<T, PREC>::step(dk[dc], acc_to_frag<T>(ds, kk), tr_frag<T>(sm.q[dc], r0, kk, lane));
         }
     }
   }
@@ -275,16 +305,16 @@ __global__ __launch_bounds__(BNT, DC > 2 ? 1 : 2) void bwd_dkdv_kernel(const gnn
 }
 
 // ------------------------------------------------------------------------- dQ
-template <int DC>
+template <typename T, int DC>
 struct DqLds {
-  unsigned char k[DC][BT * ROWB];
-  unsigned char v[DC][BT * ROWB];
+  unsigned char k[DC][BT * rowb<T>()];
+  unsigned char v[DC][BT * rowb<T>()];
 };
 
-template <typename T, bool HAS_BIAS, int DC>
+template <typename T, bool HAS_BIAS, int DC, int PREC>
 __global__ __launch_bounds__(BNT, DC > 2 ? 1 : 2) void bwd_dq_kernel(const gnn_triattn_bwd_args a) {
   typedef typename TypeOps<T>::V8 V8;
-  __shared__ __align__(16) DqLds<DC> sm;
+  __shared__ __align__(16) DqLds<T, DC> sm;
   const int N = (int)a.N, H = (int)a.H, D = (int)a.D;
   const int nqb = (N + 127) / 128;
   const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
@@ -355,9 +385,9 @@ __global__ __launch_bounds__(BNT, DC > 2 ? 1 : 2) void bwd_dq_kernel(const gnn_t
       const bool ok = kj < N;
 #pragma unroll
       for (int dc = 0; dc < DC; ++dc) {
-        *reinterpret_cast<V8*>(sm.k[dc] + swz(r, c)) =
+        *reinterpret_cast<V8*>(sm.k[dc] + swzt<T>(r, c)) =
             row8(kp + (int64_t)(ok ? kj : 0) * a.k_stride[2], 32 * dc + 8 * c, D, ok);
-        *reinterpret_cast<V8*>(sm.v[dc] + swz(r, c)) =
+        *reinterpret_cast<V8*>(sm.v[dc] + swzt<T>(r, c)) =
             row8(vp + (int64_t)(ok ? kj : 0) * a.v_stride[2], 32 * dc + 8 * c, D, ok);
       }
     }
@@ -373,14 +403,14 @@ __global__ __launch_bounds__(BNT, DC > 2 ? 1 : 2) void bwd_dq_kernel(const gnn_t
       for (int dc = 0; dc < DC; ++dc)
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          Mma<T, PREC_NATIVE>::step(sc, lds_row8<T>(sm.k[dc], r0 + l32, 2 * kk + g), qf[dc][kk]);
-          Mma<T, PREC_NATIVE>::step(dp, lds_row8<T>(sm.v[dc], r0 + l32, 2 * kk + g), dof[dc][kk]);
+          Mma<T, PREC>::step(sc, lds_row8<T>(sm.k[dc], r0 + l32, 2 * kk + g), qf[dc][kk]);
+          Mma<T, PREC>::step(dp, lds_row8<T>(sm.v[dc], r0 + l32, 2 * kk + g), dof[dc][kk]);
         }
       if constexpr (HAS_BIAS) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const V8 bfr = qok ? load8_bias_tail<T>(brow, k0 + r0 + 16 * t + 8 * g, N) : zero8<T>();
-          Mma<T, PREC_NATIVE>::step(sc, idf[t], bfr);
+          Mma<T, PREC>::step(sc, idf[t], bfr);
         }
       }
       f32x16 ds;
@@ -404,7 +434,7 @@ __global__ __launch_bounds__(BNT, DC > 2 ? 1 : 2) void bwd_dq_kernel(const gnn_t
       for (int dc = 0; dc < DC; ++dc)
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
-          Mma<T, PREC_NATIVE>::step(dq[dc], acc_to_frag<T>(ds, kk), tr_frag<T>(sm.k[dc], r0, kk, lane));
+          Mma<T, PREC>::step(dq[dc], acc_to_frag<T>(ds, kk), tr_frag<T>(sm.k[dc], r0, kk, lane));
     }
   }
   // dq[m = query][n = d]: lane = d (32 dc + l32), rows = queries wave*32 + 8 (i / 4) + 4 g + i % 4
@@ -434,23 +464,23 @@ __global__ __launch_bounds__(BNT, DC > 2 ? 1 : 2) void bwd_dq_kernel(const gnn_t
 // tile in LDS; 405 us) and a 128 x 64 tile with two workgroups per CU (384 us).
 constexpr int DB_T = 128;
 constexpr int DB_NT = 512;
-template <int DC>
-struct DbLds {  // DC > 1 exceeds 64 KB: dynamic LDS
-  unsigned char q[DC][DB_T * ROWB];
-  unsigned char d[DC][DB_T * ROWB];
-  unsigned char k[DC][DB_T * ROWB];
-  unsigned char v[DC][DB_T * ROWB];
+template <typename T, int DC>
+struct DbLds {  // beyond 64 KB (16-bit DC > 1, fp32): dynamic LDS
+  unsigned char q[DC][DB_T * rowb<T>()];
+  unsigned char d[DC][DB_T * rowb<T>()];
+  unsigned char k[DC][DB_T * rowb<T>()];
+  unsigned char v[DC][DB_T * rowb<T>()];
   float lse[DB_T];
   float delta[DB_T];
   float kb[DB_T];
   float pl2;  // -log2(N_res) when the row's keys are all masked, else 0
 };
 
-template <typename T, int DC>
+template <typename T, int DC, int PREC>
 __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_bwd_args a) {
   typedef typename TypeOps<T>::V8 V8;
   extern __shared__ __align__(16) unsigned char db_smem[];
-  DbLds<DC>& sm = *reinterpret_cast<DbLds<DC>*>(db_smem);
+  DbLds<T, DC>& sm = *reinterpret_cast<DbLds<T, DC>*>(db_smem);
   const int N = (int)a.N, H = (int)a.H, D = (int)a.D, S = (int)a.S;
   const int nt = (N + DB_T - 1) / DB_T;
   const int splits = a.dbias_splits > 1 ? a.dbias_splits : 1;
@@ -526,10 +556,10 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
     for (int dc = 0; dc < DC; ++dc) asm volatile("" : "+v"(pq[set][dc]), "+v"(pd[set][dc]), "+v"(pk[set][dc]), "+v"(pv[set][dc]));
 #pragma unroll
     for (int dc = 0; dc < DC; ++dc) {
-      *reinterpret_cast<V8*>(sm.q[dc] + swz(sr, sc4)) = TypeOps<T>::from_f32(TypeOps<T>::to_f32(pq[set][dc]) * a.scale);
-      *reinterpret_cast<V8*>(sm.d[dc] + swz(sr, sc4)) = pd[set][dc];
-      *reinterpret_cast<V8*>(sm.k[dc] + swz(sr, sc4)) = pk[set][dc];
-      *reinterpret_cast<V8*>(sm.v[dc] + swz(sr, sc4)) = pv[set][dc];
+      *reinterpret_cast<V8*>(sm.q[dc] + swzt<T>(sr, sc4)) = TypeOps<T>::from_f32(TypeOps<T>::to_f32(pq[set][dc]) * a.scale);
+      *reinterpret_cast<V8*>(sm.d[dc] + swzt<T>(sr, sc4)) = pd[set][dc];
+      *reinterpret_cast<V8*>(sm.k[dc] + swzt<T>(sr, sc4)) = pk[set][dc];
+      *reinterpret_cast<V8*>(sm.v[dc] + swzt<T>(sr, sc4)) = pv[set][dc];
     }
     if (sc4 == 0) {
       asm volatile("" : "+v"(plse[set]), "+v"(pdel[set]), "+v"(pmk[set]));
@@ -549,9 +579,7 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         qf[dc][kk] = lds_row8<T>(sm.q[dc], qw + l32, 2 * kk + g);
-        u32x4 u = __builtin_bit_cast(u32x4, lds_row8<T>(sm.d[dc], qw + l32, 2 * kk + g));
-        u ^= 0x80008000u;
-        ndof[dc][kk] = __builtin_bit_cast(V8, u);
+        ndof[dc][kk] = neg8<T>(lds_row8<T>(sm.d[dc], qw + l32, 2 * kk + g));
       }
     f32x4 l4[4];
     f32x16 dinit;
@@ -570,8 +598,8 @@ __global__ __launch_bounds__(DB_NT, 1) void bwd_dbias_kernel(const gnn_triattn_b
       for (int dc = 0; dc < DC; ++dc)
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          Mma<T, PREC_NATIVE>::step(scv, qf[dc][kk], lds_row8<T>(sm.k[dc], kr, 2 * kk + g));
-          Mma<T, PREC_NATIVE>::step(ndp, ndof[dc][kk], lds_row8<T>(sm.v[dc], kr, 2 * kk + g));
+          Mma<T, PREC>::step(scv, qf[dc][kk], lds_row8<T>(sm.k[dc], kr, 2 * kk + g));
+          Mma<T, PREC>::step(ndp, ndof[dc][kk], lds_row8<T>(sm.v[dc], kr, 2 * kk + g));
         }
       const float kb = sm.kb[kr], pl2 = sm.pl2;
 #pragma unroll
@@ -835,41 +863,54 @@ bool dbias_dma_ok(const gnn_triattn_bwd_args& a) {
   return true;
 }
 
-template <typename T, int DC>
+template <typename T, int DC, int PREC>
 int launch_bwd(const gnn_triattn_bwd_args& a, hipStream_t stream) {
   const int64_t nb128 = (a.N + 127) / 128;
   const dim3 grid((uint32_t)(nb128 * a.H * a.S * a.B));
-  // dq first: it also writes Delta, which dk / dv and dbias read
-  if (DC == 1 && triattn_bwd_row_applicable(a)) {
-    const int rc = triattn_bwd_row_dq_dkdv(a, stream);
-    if (rc != 0) return rc;
-  } else if (a.bias) {
-    hipLaunchKernelGGL((bwd_dq_kernel<T, true, DC>), grid, dim3(BNT), 0, stream, a);
-    hipLaunchKernelGGL((bwd_dkdv_kernel<T, true, DC>), grid, dim3(BNT), 0, stream, a);
-  } else {
-    hipLaunchKernelGGL((bwd_dq_kernel<T, false, DC>), grid, dim3(BNT), 0, stream, a);
-    hipLaunchKernelGGL((bwd_dkdv_kernel<T, false, DC>), grid, dim3(BNT), 0, stream, a);
+  constexpr bool B16 = sizeof(T) == 2;
+  // dq first: it also writes Delta, which dk / dv and dbias read. 16-bit D <= 32 rows take
+  // the row-resident kernels and the DMA-ring pair-bias gradient.
+  bool row_done = false, dma_ok = false;
+  if constexpr (B16) {
+    if (DC == 1 && triattn_bwd_row_applicable(a)) {
+      const int rc = triattn_bwd_row_dq_dkdv(a, stream);
+      if (rc != 0) return rc;
+      row_done = true;
+    }
+    dma_ok = DC == 1 && dbias_dma_ok(a);
+  }
+  if (!row_done) {
+    if (a.bias) {
+      hipLaunchKernelGGL((bwd_dq_kernel<T, true, DC, PREC>), grid, dim3(BNT), 0, stream, a);
+      hipLaunchKernelGGL((bwd_dkdv_kernel<T, true, DC, PREC>), grid, dim3(BNT), 0, stream, a);
+    } else {
+      hipLaunchKernelGGL((bwd_dq_kernel<T, false, DC, PREC>), grid, dim3(BNT), 0, stream, a);
+      hipLaunchKernelGGL((bwd_dkdv_kernel<T, false, DC, PREC>), grid, dim3(BNT), 0, stream, a);
+    }
   }
   if (a.bias && a.dbias) {
     const int64_t nt = (a.N + DB_T - 1) / DB_T;
     const int splits = a.dbias_splits > 1 ? a.dbias_splits : 1;
     const dim3 dgrid((uint32_t)(a.B * a.H * nt * nt * splits));
-    if (DC == 1 && dbias_dma_ok(a)) {
-      const size_t smem = sizeof(DbdLds);
-      if (a.mask) {
-        (void)hipFuncSetAttribute((const void*)bwd_dbias_dma_kernel<T, true>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-        hipLaunchKernelGGL((bwd_dbias_dma_kernel<T, true>), dgrid, dim3(DB_NT), smem, stream, a);
-      } else {
-        (void)hipFuncSetAttribute((const void*)bwd_dbias_dma_kernel<T, false>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-        hipLaunchKernelGGL((bwd_dbias_dma_kernel<T, false>), dgrid, dim3(DB_NT), smem, stream, a);
+    if constexpr (B16) {
+      if (dma_ok) {
+        const size_t smem = sizeof(DbdLds);
+        if (a.mask) {
+          (void)hipFuncSetAttribute((const void*)bwd_dbias_dma_kernel<T, true>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+          hipLaunchKernelGGL((bwd_dbias_dma_kernel<T, true>), dgrid, dim3(DB_NT), smem, stream, a);
+        } else {
+          (void)hipFuncSetAttribute((const void*)bwd_dbias_dma_kernel<T, false>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+          hipLaunchKernelGGL((bwd_dbias_dma_kernel<T, false>), dgrid, dim3(DB_NT), smem, stream, a);
+        }
       }
-    } else {
-      const size_t smem = sizeof(DbLds<DC>);
-      const void* fn = (const void*)bwd_dbias_kernel<T, DC>;
+    }
+    if (!dma_ok) {
+      const size_t smem = sizeof(DbLds<T, DC>);
+      const void* fn = (const void*)bwd_dbias_kernel<T, DC, PREC>;
       if (smem > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-      hipLaunchKernelGGL((bwd_dbias_kernel<T, DC>), dgrid, dim3(DB_NT), smem, stream, a);
+      hipLaunchKernelGGL((bwd_dbias_kernel<T, DC, PREC>), dgrid, dim3(DB_NT), smem, stream, a);
     }
     if (splits > 1) {
       const int64_t n = a.B * a.H * a.N * a.N;
@@ -893,12 +934,22 @@ int triattn_bwd(const gnn_triattn_bwd_args& a, hipStream_t stream) {
     return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention backward: grid too large");
   const int dc = a.D <= 32 ? 1 : a.D <= 64 ? 2 : 4;  // 32-column chunks of the head dim
   switch (a.dtype) {
-    case GNN_BF16: return dc == 1 ? launch_bwd<bf16, 1>(a, stream) : dc == 2 ? launch_bwd<bf16, 2>(a, stream)
-                                                                             : launch_bwd<bf16, 4>(a, stream);
-    case GNN_F16: return dc == 1 ? launch_bwd<f16, 1>(a, stream) : dc == 2 ? launch_bwd<f16, 2>(a, stream)
-                                                                           : launch_bwd<f16, 4>(a, stream);
+    case GNN_BF16:
+      return dc == 1 ? launch_bwd<bf16, 1, PREC_NATIVE>(a, stream)
+                     : dc == 2 ? launch_bwd<bf16, 2, PREC_NATIVE>(a, stream) : launch_bwd<bf16, 4, PREC_NATIVE>(a, stream);
+    case GNN_F16:
+      return dc == 1 ? launch_bwd<f16, 1, PREC_NATIVE>(a, stream)
+                     : dc == 2 ? launch_bwd<f16, 2, PREC_NATIVE>(a, stream) : launch_bwd<f16, 4, PREC_NATIVE>(a, stream);
+    case GNN_F32:
+      // fp32 tiles are twice the bytes: head dims up to 64 (the pair-bias gradient's four
+      // [128][64] fp32 tiles take 128 KB of LDS)
+      if (dc > 2)
+        return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention backward: fp32 head dim must be at most 64");
+      if (a.precision == GNN_PREC_BF16X3)
+        return dc == 1 ? launch_bwd<float, 1, PREC_BF16X3>(a, stream) : launch_bwd<float, 2, PREC_BF16X3>(a, stream);
+      return dc == 1 ? launch_bwd<float, 1, PREC_IEEE>(a, stream) : launch_bwd<float, 2, PREC_IEEE>(a, stream);
   }
-  return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention backward: bf16 / fp16 only");
+  return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention backward: bf16 / fp16 / fp32 only");
 }
 
 }  // namespace gnn

@@ -91,7 +91,7 @@ def workspace_for(args, device) -> torch.Tensor | None:
 
 
 def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=False, use_exp2=False,
-                           lse=None, mask_value=None, row_max=None):
+                           lse=None, mask_value=None, row_max=None, precision=None):
     """Triangle attention forward on the canonical 5D layout.
 
     q/k/v ``[B, N_seq, N_res, H, D]`` (bf16, fp16 or fp32, on a HIP device); bias
@@ -145,7 +145,8 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
         args.row_max = row_max.data_ptr()
     args.scale = float(scale)
     args.mask_value = rounded_mask_value(q.dtype) if mask_value is None else float(mask_value)
-    precision = _precision.matmul_precision(fp32_operands=q.dtype == torch.float32)
+    if precision is None:
+        precision = _precision.matmul_precision(fp32_operands=q.dtype == torch.float32)
     args.precision = _lib.PRECISION_CODE[precision]
 
     ws = workspace_for(args, q.device)
@@ -157,9 +158,14 @@ def triangle_attention_hip(q, k, v, bias=None, mask=None, scale=None, dynamic=Fa
 
 
 def backward_supported(q: torch.Tensor) -> bool:
-    """Whether the HIP backward covers these inputs: 16-bit, head dim <= 128 and a multiple of 8."""
+    """Whether the HIP backward covers these inputs: a head dim that is a multiple of 8, at
+    most 128 for bf16 / fp16 and at most 64 for fp32 (whose tiles take twice the LDS)."""
     d = q.shape[-1]
-    return q.dtype in (torch.bfloat16, torch.float16) and d <= 128 and d % 8 == 0
+    if d % 8 != 0:
+        return False
+    if q.dtype in (torch.bfloat16, torch.float16):
+        return d <= 128
+    return q.dtype == torch.float32 and d <= 64
 
 
 _CUS = 256  # MI355X compute units; the pair-bias kernel's LDS ring holds one workgroup each
@@ -184,11 +190,13 @@ def dbias_splits(B: int, S: int, N: int, H: int) -> int:
 
 
 def triangle_attention_bwd_hip(q, k, v, o, dout, lse, bias=None, mask=None, scale=None, mask_value=None,
-                               need_dbias=True):
+                               need_dbias=True, precision=None):
     """Gradients of the HIP forward: ``(dq, dk, dv, dbias)`` with dq/dk/dv like q and dbias
     ``[B, 1, H, N, N]`` fp32 (``None`` without a bias or when ``need_dbias`` is false).
     Replaces EvoformerAttention.backward (triangle_attention.py:1278-1442); ``lse`` is the
-    forward's ``[B, N_seq, H, N]`` natural-log log-sum-exp."""
+    forward's ``[B, N_seq, H, N]`` natural-log log-sum-exp. fp32 products run as the
+    forward's did: ``precision`` is the resolved ``'ieee'`` or ``'bf16x3'`` (``None``:
+    resolved now from ``torch.backends.cuda.matmul.fp32_precision``)."""
     B, S, N, H, D = q.shape
     if scale is None:
         scale = D**-0.5
@@ -230,6 +238,8 @@ def triangle_attention_bwd_hip(q, k, v, o, dout, lse, bias=None, mask=None, scal
     a.scale = float(scale)
     a.mask_value = rounded_mask_value(q.dtype) if mask_value is None else float(mask_value)
     a.dtype = _lib.DTYPE_CODE[q.dtype]
-    a.precision = _lib.GNN_PREC_IEEE
+    if precision is None:
+        precision = _precision.matmul_precision(fp32_operands=q.dtype == torch.float32)
+    a.precision = _lib.PRECISION_CODE[precision]
     _lib.call("gnn_triattn_bwd", a, q.device)
     return dq, dk, dv, dbias

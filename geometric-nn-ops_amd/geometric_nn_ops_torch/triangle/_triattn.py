@@ -8,17 +8,18 @@ fp64 is computed in fp32, and the output has the input's shape and dtype.
 Dispatch: the gfx950 HIP kernel serves every forward-only call on a HIP device, through
 the ``gnn_amd::triangle_attention_fwd`` operator (``geometric_nn_ops_torch._ops``).
 Calls that need a backward run the HIP forward (saving the log-sum-exp) and the HIP
-backward kernels (dq, dk, dv and the N_seq-summed pair-bias gradient) for bf16 / fp16 with
-a head dim <= 32 that is a multiple of 8, as the reference runs its Triton forward and
-backward; other grad-requiring calls, CPU tensors and head dims above the forward kernel's
-tile take the differentiable torch path. There is no fallback when the HIP library is
+backward kernels (dq, dk, dv and the N_seq-summed pair-bias gradient) for a head dim that is
+a multiple of 8 (at most 128 for bf16 / fp16, 64 for fp32, whose products follow the fp32
+precision setting resolved at the forward, 'ieee' or 'bf16x3'), as the reference runs its
+Triton forward and backward; other grad-requiring calls, CPU tensors and head dims above the
+forward kernel's tile take the differentiable torch path. There is no fallback when the HIP library is
 missing: a GPU call then raises.
 """
 
 import torch
 from torch.autograd.function import once_differentiable
 
-from .. import _ops
+from .. import _ops, _precision
 from ._kernels import triangle_attention as _hip
 from ._reference.triangle_attention import triangle_attention_torch
 
@@ -45,9 +46,12 @@ class _TriangleAttentionHip(torch.autograd.Function):
     def forward(ctx, q, k, v, bias, mask, scale):
         B, S, N, H, _ = q.shape
         lse = torch.empty((B, S, H, N), device=q.device, dtype=torch.float32)
-        o = _hip.triangle_attention_hip(q, k, v, bias=bias, mask=mask, scale=scale, lse=lse)
+        # fp32: the backward runs with the precision the forward resolved
+        precision = _precision.matmul_precision(fp32_operands=q.dtype == torch.float32)
+        o = _hip.triangle_attention_hip(q, k, v, bias=bias, mask=mask, scale=scale, lse=lse, precision=precision)
         ctx.save_for_backward(q, k, v, bias, mask, o, lse)
         ctx.scale = scale
+        ctx.precision = precision
         ctx.bias_grad = bias is not None and bias.requires_grad
         return o
 
@@ -56,7 +60,8 @@ class _TriangleAttentionHip(torch.autograd.Function):
     def backward(ctx, do):
         q, k, v, bias, mask, o, lse = ctx.saved_tensors
         dq, dk, dv, dbias = _hip.triangle_attention_bwd_hip(q, k, v, o, do, lse, bias=bias, mask=mask,
-                                                            scale=ctx.scale, need_dbias=ctx.bias_grad)
+                                                            scale=ctx.scale, need_dbias=ctx.bias_grad,
+                                                            precision=ctx.precision)
         if dbias is not None:
             dbias = dbias.to(bias.dtype)
         return dq, dk, dv, dbias, None, None

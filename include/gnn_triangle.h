@@ -121,7 +121,9 @@ size_t gnn_triattn_workspace_bytes(const gnn_triattn_args* args);
 int gnn_triattn_fwd_noalloc(const gnn_triattn_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------------
- * Triangle attention backward (bf16 / fp16, head dim a multiple of 8 and at most 128).
+ * Triangle attention backward (head dim a multiple of 8: bf16 / fp16 up to 128; fp32 up to
+ * 64, its products full fp32 (precision GNN_PREC_IEEE) or split into bf16 hi / lo parts
+ * (GNN_PREC_BF16X3), as the forward that wrote the lse ran them).
  * Given the forward's inputs, its output o, the upstream gradient dout and the forward's
  * lse (fp32 [B, S, H, N] contiguous, natural log; gnn_triattn_fwd writes it when args->lse
  * is set), writes dq, dk, dv (input dtype, [B, S, N, H, D] by strides) and, when both bias

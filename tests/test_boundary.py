@@ -252,10 +252,14 @@ def test_triattn_bwd_argument_errors():
     a.D = 136  # above the 128 the chunked kernels cover (refused before the dtype is looked at)
     assert lib.gnn_triattn_bwd(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
     assert b"head dim" in lib.gnn_last_error()
-    a.D = 32
+    a.D = 96  # fp32 tiles take twice the LDS: fp32 head dims up to 64
     a.dtype = _lib.GNN_F32
     assert lib.gnn_triattn_bwd(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
-    assert b"bf16 / fp16" in lib.gnn_last_error()
+    assert b"fp32 head dim" in lib.gnn_last_error()
+    a.D = 32
+    a.dtype = 7  # no such dtype code
+    assert lib.gnn_triattn_bwd(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
+    assert b"bf16 / fp16 / fp32" in lib.gnn_last_error()
 
 
 def test_trimul_backward_helper_argument_errors():

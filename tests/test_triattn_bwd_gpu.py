@@ -25,18 +25,34 @@ def run(q, k, v, bias, mask, scale, dout):
     return o, [t.grad for t in leaves], None if b is None else b.grad
 
 
-def check_against_oracle(shape, dtype, *, with_bias=True, with_mask=True, seed=0, scale=None, dead_rows=()):
+class matmul_precision:
+    """Sets torch.backends.cuda.matmul.fp32_precision for a block (not thread safe)."""
+
+    def __init__(self, value):
+        self.value = value
+
+    def __enter__(self):
+        self.old = torch.backends.cuda.matmul.fp32_precision
+        torch.backends.cuda.matmul.fp32_precision = self.value
+
+    def __exit__(self, *exc):
+        torch.backends.cuda.matmul.fp32_precision = self.old
+
+
+def check_against_oracle(shape, dtype, *, with_bias=True, with_mask=True, seed=0, scale=None, dead_rows=(),
+                         precision="ieee"):
     B, S, N, H, D = shape
     t = attention_inputs(B, S, N, H, D, dtype, seed=seed, with_bias=with_bias, bias_scale=0.5, device=DEV)
     mask = key_mask(B, S, N, seed=seed + 1, frac_keep=0.75, device=DEV) if with_mask else None
     for s in dead_rows:  # every key of N_seq row s masked
         mask[:, s] = False
     dout = (torch.randn(B, S, N, H, D, generator=gen(seed + 2))).to(DEV, dtype)
-    o, (dq, dk, dv), db = run(t["q"], t["k"], t["v"], t.get("bias"), mask, scale, dout)
+    with matmul_precision(precision if dtype == torch.float32 else "ieee"):
+        o, (dq, dk, dv), db = run(t["q"], t["k"], t["v"], t.get("bias"), mask, scale, dout)
     want = O.triangle_attention_grad(to_np(t["q"]), to_np(t["k"]), to_np(t["v"]),
                                      None if not with_bias else to_np(t["bias"]),
                                      None if mask is None else mask.cpu().numpy(), scale, to_np(dout))
-    tol = TRIANGLE_ATTENTION_TOL[dtype, "ieee"]
+    tol = TRIANGLE_ATTENTION_TOL[dtype, precision if dtype == torch.float32 else "ieee"]
     for name, got, ref in zip(("dq", "dk", "dv"), (dq, dk, dv), want[:3]):
         assert_close_to_oracle(name, got, ref, tol)
     if with_bias:
@@ -133,14 +149,57 @@ def test_headline_rows_bf16():
     check_against_oracle((1, 8, 512, 4, 32), torch.bfloat16, seed=41)
 
 
-def test_fp32_keeps_the_torch_gradient(monkeypatch):
-    """fp32 inputs are differentiated by the torch path (no HIP backward call)."""
+@pytest.mark.parametrize("precision", ["ieee", "tf32"])
+@pytest.mark.parametrize("shape", [(1, 1, 32, 4, 32), (1, 4, 32, 8, 8), (1, 1, 64, 16, 48), (2, 2, 48, 4, 32),
+                                   (1, 3, 130, 2, 64)],
+                         ids=["pairformer_32", "msa_d8", "atom_d48", "batched", "n130_d64"])
+def test_fp32_hip_backward(shape, precision, monkeypatch):
+    """fp32 gradients through the HIP backward under both fp32_precision settings ('tf32'
+    resolves to the bf16x3 split on gfx950), at the reference's SHAPES
+    (tests/test_triangle_attention.py:46-51, its fp32 ieee / tf32 accuracy cases :493-512)
+    and a ragged N = 130 at the largest fp32 head dim, against the fp64 oracle with the
+    reference's fp32 tolerances."""
+    from geometric_nn_ops_torch.triangle._kernels import triangle_attention as K
+
+    calls = []
+    real = K.triangle_attention_bwd_hip
+    monkeypatch.setattr(K, "triangle_attention_bwd_hip", lambda *a, **kw: calls.append(kw.get("precision")) or real(*a, **kw))
+    check_against_oracle(shape, torch.float32, seed=51, precision=precision)
+    assert calls == ["ieee" if precision == "ieee" else "bf16x3"]
+
+
+def test_fp32_fully_masked_rows():
+    """fp32 rows whose keys are all masked beside ordinary ones, through the HIP backward."""
+    check_against_oracle((1, 4, 96, 2, 32), torch.float32, seed=63, dead_rows=(0, 2))
+
+
+def test_fp32_tf32_changes_the_gradients():
+    """The split products differ from the full fp32 ones (the reference's
+    test_tf32_changes_the_result, tests/test_triangle_attention.py:460-490)."""
+    from geometric_nn_ops_torch.triangle import triangle_attention
+
+    B, S, N, H, D = 1, 1, 32, 4, 32
+    t = attention_inputs(B, S, N, H, D, torch.float32, seed=3, with_bias=True, device=DEV)
+    mask = key_mask(B, S, N, seed=5, device=DEV)
+    dout = torch.randn(B, S, N, H, D, generator=gen(31)).to(DEV)
+    grads = {}
+    for precision in ("ieee", "tf32"):
+        with matmul_precision(precision):
+            leaves = [t[n].detach().requires_grad_(True) for n in ("q", "k", "v", "bias")]
+            triangle_attention(*leaves[:3], leaves[3], mask).backward(dout)
+            grads[precision] = [x.grad for x in leaves]
+    for full, reduced in zip(grads["ieee"], grads["tf32"]):
+        assert not torch.equal(full, reduced)
+
+
+def test_fp32_wide_head_keeps_the_torch_gradient(monkeypatch):
+    """fp32 head dims above 64 are differentiated by the torch path (no HIP backward call)."""
     from geometric_nn_ops_torch.triangle._kernels import triangle_attention as K
 
     calls = []
     real = K.triangle_attention_bwd_hip
     monkeypatch.setattr(K, "triangle_attention_bwd_hip", lambda *a, **kw: calls.append(1) or real(*a, **kw))
-    check_against_oracle((1, 2, 40, 2, 32), torch.float32, seed=51)
+    check_against_oracle((1, 2, 40, 2, 96), torch.float32, seed=51)
     assert calls == []
 
 
