@@ -200,6 +200,22 @@ struct ProjMask {
   }
 };
 
+// LayerNorm over the first n of the W channels of a row whose other channels are zeros (the
+// caller's padding to a multiple of 32; n = 0 means all): the sums over all W channels give
+// mean = sum / n, and the sum of squared deviations from that mean over the n real channels
+// is the one over all W minus the padded zeros' (W - n) mean^2.
+struct LnWidth {
+  float inv_n;  // 1 / n
+  float npad;   // W - n
+  __device__ __forceinline__ LnWidth(int64_t n, int W) {
+    const int nn = n > 0 && n < W ? (int)n : W;
+    inv_n = 1.0f / (float)nn;
+    npad = (float)(W - nn);
+  }
+  // the variance from the sum of squared deviations q over all W channels about `mean`
+  __device__ __forceinline__ float var(float q, float mean) const { return (q - npad * mean * mean) * inv_n; }
+};
+
 // Chunks of x per thread that the tile load must hold: ceil(C / 64), rounded up to 2, 4, 8.
 __host__ __device__ inline int proj_xm(int64_t C) { return C <= 128 ? 2 : C <= 256 ? 4 : 8; }
 
@@ -287,7 +303,15 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_kernel(const gnn_trimul_ar
       const float d = pr[j].x - mean;
       m2 += pr[j].y + nj[j] * d * d;
     }
-    const float rstd = 1.0f / sqrtf(m2 / (float)C + a.eps);
+    float var = m2 / (float)C;
+    if (a.ln_in_channels > 0 && a.ln_in_channels < C) {  // padded channels: real-width statistics
+      const LnWidth lw(a.ln_in_channels, C);
+      const float mean_r = mean * (float)C * lw.inv_n;
+      const float dm = mean - mean_r;
+      var = lw.var(m2 + (float)C * dm * dm, mean_r);
+      mean = mean_r;
+    }
+    const float rstd = 1.0f / sqrtf(var + a.eps);
 #pragma unroll
     for (int j = 0; j < XM; ++j) {
       const int ci = xpart + 8 * j;
@@ -534,6 +558,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
   float* lnb = lnw + CK;
   float* mk = reinterpret_cast<float*>(smem_raw + LD::mk);
   int* mk1 = reinterpret_cast<int*>(smem_raw + LD::mk1);
+  const LnWidth lnw_in(a.ln_in_channels, CK);
   const bool outgoing = a.outgoing != 0;
   const int64_t ntiles = (int64_t)a.B * N * ((N + PTP - 1) / PTP);
   constexpr float NLOG2E = -1.4426950408889634f;
@@ -573,7 +598,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
       for (int e = 0; e < 8; ++e) s += v[j][e];
     }
     s = sum8_dpp(s);
-    const float mean = s * (1.0f / CK);
+    const float mean = s * lnw_in.inv_n;
     float q = 0.f;
 #pragma unroll
     for (int j = 0; j < XMF; ++j)
@@ -583,7 +608,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
         q += d * d;
       }
     q = sum8_dpp(q);
-    const float rstd = __builtin_amdgcn_rsqf(q * (1.0f / CK) + a.eps);  // as torch's rsqrt
+    const float rstd = __builtin_amdgcn_rsqf(lnw_in.var(q, mean) + a.eps);  // as torch's rsqrt
 #pragma unroll
     for (int j = 0; j < XMF; ++j) {
       const int k = 8 * (xpart + 8 * j);
@@ -839,6 +864,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_pp_kernel(const gnn_trimul
   float* lnb = lnw + CK;
   float* mk = reinterpret_cast<float*>(smem_raw + LD::mk);
   int* mk1 = reinterpret_cast<int*>(smem_raw + LD::mk1);
+  const LnWidth lnw_in(a.ln_in_channels, CK);
   const bool outgoing = a.outgoing != 0;
   const int64_t ntiles = (int64_t)a.B * N * ((N + PTP - 1) / PTP);
   if ((int64_t)blockIdx.x >= ntiles) return;  // uniform over the workgroup
@@ -882,7 +908,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_pp_kernel(const gnn_trimul
       for (int e = 0; e < 8; ++e) s += v[j][e];
     }
     s = sum8_dpp(s);
-    const float mean = s * (1.0f / CK);
+    const float mean = s * lnw_in.inv_n;
     float q = 0.f;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -892,7 +918,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_pp_kernel(const gnn_trimul
         q += d * d;
       }
     q = sum8_dpp(q);
-    const float rstd = __builtin_amdgcn_rsqf(q * (1.0f / CK) + a.eps);  // as torch's rsqrt
+    const float rstd = __builtin_amdgcn_rsqf(lnw_in.var(q, mean) + a.eps);  // as torch's rsqrt
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int kk = 8 * (xpart + 8 * j);
@@ -1327,7 +1353,8 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
       const float2 v = red2[j * 32 + pp];
       mean += f32x2{v.x, v.y};
     }
-    mean *= 1.0f / (float)Ch;
+    const LnWidth lw(a.ln_out_channels, Ch);
+    mean *= lw.inv_n;
     f32x2 q2 = {0.f, 0.f};
     for (int k = k0; k < k0 + kc; ++k) {
       const f32x2 d = pair(k) - mean;
@@ -1342,8 +1369,8 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
       const float2 v = red2[j * 32 + pp];
       var += f32x2{v.x, v.y};
     }
-    const float rs0 = __builtin_amdgcn_rsqf(var[0] * (1.0f / (float)Ch) + a.eps);  // as torch's rsqrt
-    const float rs1 = __builtin_amdgcn_rsqf(var[1] * (1.0f / (float)Ch) + a.eps);
+    const float rs0 = __builtin_amdgcn_rsqf(lw.var(var[0], mean[0]) + a.eps);  // as torch's rsqrt
+    const float rs1 = __builtin_amdgcn_rsqf(lw.var(var[1], mean[1]) + a.eps);
     for (int k = k0; k < k0 + kc; k += 8) {
       f32x8 v0, v1;
 #pragma unroll
@@ -1729,6 +1756,8 @@ int check_args(const gnn_trimul_args& a, const char* who) {
     return set_error(GNN_ERR_UNSUPPORTED, "trimul: c_z and c_hidden above 512 are not supported");
   if (a.dtype != GNN_BF16 && a.dtype != GNN_F16 && a.dtype != GNN_F32)
     return set_error(GNN_ERR_ARG, "trimul: unknown dtype");
+  if (a.ln_in_channels < 0 || a.ln_in_channels > a.C || a.ln_out_channels < 0 || a.ln_out_channels > a.Ch)
+    return set_error(GNN_ERR_ARG, "trimul: ln_in_channels / ln_out_channels must lie in [0, C] / [0, Ch]");
   const void* vec[] = {a.x, a.out, a.p_in_w, a.g_in_w, a.p_out_w, a.g_out_w, a.workspace, a.gate};
   for (const void* ptr : vec)
     if (((uintptr_t)ptr) % 16 != 0)

@@ -129,6 +129,8 @@ class TrimulArgs(ctypes.Structure):
         ("dtype", ctypes.c_int32),
         ("precision", ctypes.c_int32),
         ("gate", ctypes.c_void_p),
+        ("ln_in_channels", ctypes.c_int64),
+        ("ln_out_channels", ctypes.c_int64),
     ]
 
 

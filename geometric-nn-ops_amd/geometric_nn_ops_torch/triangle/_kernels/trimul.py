@@ -30,11 +30,65 @@ _ARG_FIELD = {
 MAX_CHANNELS = 512
 
 
-def supports(x: torch.Tensor, p_in_weight: torch.Tensor) -> bool:
-    """Whether the HIP kernels cover these channel counts (multiples of 32, at most 512)."""
+def _pad32(n: int) -> int:
+    return (n + 31) // 32 * 32
+
+
+def supports(x: torch.Tensor, p_in_weight: torch.Tensor, *, padded: bool = True) -> bool:
+    """Whether the HIP kernels cover these channel counts: at most 512 once rounded up to a
+    multiple of 32 (256 for fp32). Widths that are not multiples of 32 run the forward on
+    zero-padded copies (``padded``); the HIP backward takes multiples of 32 only."""
     c_z, c_hidden = x.shape[-1], p_in_weight.shape[0] // 2
-    return (c_z % 32 == 0 and c_hidden % 32 == 0 and c_z <= MAX_CHANNELS
-            and c_hidden <= MAX_CHANNELS and x.dim() >= 3)
+    if c_z < 1 or c_hidden < 1 or x.dim() < 3:
+        return False
+    if not padded and (c_z % 32 or c_hidden % 32):
+        return False
+    limit = 256 if x.dtype == torch.float32 else MAX_CHANNELS
+    return _pad32(c_z) <= limit and _pad32(c_hidden) <= limit
+
+
+def _pad_channels(x, weights):
+    """x and the weights zero-padded to channel counts that are multiples of 32, for the
+    forward kernels, with the real widths the LayerNorms average over. The a / b halves of
+    the stacked input projections are padded separately (rows [0, Ch) and [Ch', Ch' + Ch)),
+    so padded hidden channels give a = b = 0, o = 0, and padded input channels meet zero
+    weight columns; the padded output channels are sliced off by the caller.
+
+    Returns (x', weights', C', Ch')."""
+    C = x.shape[-1]
+    Ch = weights["p_in_weight"].shape[0] // 2
+    Cp, Chp = _pad32(C), _pad32(Ch)
+
+    def pad(t, shape, blocks):
+        """t copied into zeros of ``shape``; blocks: per dim, the offsets of its parts."""
+        out = t.new_zeros(shape)
+        if t.dim() == 1:
+            for o, (lo, hi) in zip(blocks[0], _parts(t.shape[0], len(blocks[0]))):
+                out[o:o + hi - lo] = t[lo:hi]
+        else:
+            for o, (lo, hi) in zip(blocks[0], _parts(t.shape[0], len(blocks[0]))):
+                out[o:o + hi - lo, :t.shape[1]] = t[lo:hi]
+        return out
+
+    xp = torch.nn.functional.pad(x, (0, Cp - C))
+    w = dict(weights)
+    stacked = {"p_in_weight": (2 * Chp, Cp), "g_in_weight": (2 * Chp, Cp), "p_in_bias": (2 * Chp,),
+               "g_in_bias": (2 * Chp,)}
+    plain = {"p_out_weight": (Cp, Chp), "g_out_weight": (Cp, Cp), "p_out_bias": (Cp,), "g_out_bias": (Cp,),
+             "norm_in_weight": (Cp,), "norm_in_bias": (Cp,), "norm_out_weight": (Chp,), "norm_out_bias": (Chp,)}
+    for key, shape in stacked.items():
+        if w.get(key) is not None:
+            w[key] = pad(w[key], shape, [(0, Chp)])
+    for key, shape in plain.items():
+        if w.get(key) is not None:
+            w[key] = pad(w[key], shape, [(0,)])
+    return xp, w, Cp, Chp
+
+
+def _parts(n, k):
+    """k equal consecutive parts of range(n)."""
+    step = n // k
+    return [(i * step, (i + 1) * step) for i in range(k)]
 
 
 def _expect(name, t, shape):
@@ -156,6 +210,14 @@ def trimul_hip(
         p_out_weight=p_out_weight, p_out_bias=p_out_bias,
         g_out_weight=g_out_weight, g_out_bias=g_out_bias,
     )
+    C, Ch = x.shape[-1], p_in_weight.shape[0] // 2
+    if C % 32 or Ch % 32:  # zero-padded copies; the LayerNorms average over the real widths
+        xp, wp, _, _ = _pad_channels(x, weights)
+        args, keep, out, workspace, _ = build_args(xp, direction, mask, eps, wp)
+        args.ln_in_channels, args.ln_out_channels = C, Ch
+        run_stage("gnn_trimul_fwd", args, x.device)
+        del keep, workspace
+        return out[..., :C].reshape(x.shape)
     args, keep, out, workspace, _ = build_args(x, direction, mask, eps, weights)
     run_stage("gnn_trimul_fwd", args, x.device)
     del keep, workspace

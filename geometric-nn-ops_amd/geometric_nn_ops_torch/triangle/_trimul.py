@@ -8,9 +8,11 @@ Where a call goes:
   * a call that needs gradients, on the same tensors, runs ``_TrimulHip``: the kernels'
     forward, then this library's backward (the reference's own grad calls run autograd
     through its torch code, _trimul.py:31-36);
-  * CPU tensors, other dtypes, channel counts outside the kernels' tiling (c_z or c_hidden
-    not a multiple of 32, or above 512) and a mask that itself requires grad run the
-    autograd-differentiable torch restatement in ``_reference.trimul``.
+  * CPU tensors, other dtypes, channel counts above the kernels' tiles (c_z or c_hidden
+    above 512 once rounded up to a multiple of 32; 256 for fp32), calls that need gradients
+    with a width that is not a multiple of 32 (the forward pads such widths; the backward
+    kernels do not), and a mask that itself requires grad run the autograd-differentiable
+    torch restatement in ``_reference.trimul``.
 The kernels are never silently replaced: without the HIP library a GPU call raises.
 
 The input projections come stacked: rows ``[0, C_hidden)`` of ``p_in_weight`` and
@@ -40,7 +42,8 @@ def _needs_torch_path(x: torch.Tensor, weights, mask=None) -> bool:
     weights = dict(weights)
     if not x.is_cuda or x.dtype not in _KERNEL_DTYPES:
         return True
-    if weights.get("p_in_weight") is not None and not _hip.supports(x, weights["p_in_weight"]):
+    if weights.get("p_in_weight") is not None and not _hip.supports(
+            x, weights["p_in_weight"], padded=not _needs_grad(x, weights)):
         return True
     return _needs_grad(x, weights) and mask is not None and mask.requires_grad
 

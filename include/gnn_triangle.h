@@ -214,6 +214,14 @@ typedef struct gnn_trimul_args {
    * out last), so a caller keeping a, b and o for a backward can release g after the
    * forward. No reference counterpart. */
   void* gate;
+  /* Channels the LayerNorms average over: LN-in over the first ln_in_channels of C, LN-out
+   * over the first ln_out_channels of Ch (0: all). A caller whose widths are not multiples
+   * of 32 pads x and the weights with zeros up to the next multiple (and the LayerNorm
+   * weights and biases too, so the padded channels normalise to zero) and passes the real
+   * widths here; the padded output channels then come out as zeros. No reference
+   * counterpart: the reference's Triton kernels mask any width (trimul.py:310-314). */
+  int64_t ln_in_channels;
+  int64_t ln_out_channels;
 } gnn_trimul_args;
 
 /* Workspace size in bytes for one call (a, b, the output gate and o, each in the

@@ -187,7 +187,11 @@ def test_kernel_dispatch_rule_for_gpu_tensors():
     with torch.no_grad():
         assert not _trimul._needs_grad(FakeCuda(), w_req.items())
         assert not _trimul._needs_torch_path(FakeCuda(), w_req.items(), torch.ones(8, 8, requires_grad=True))
-    assert _trimul._needs_torch_path(FakeCuda(), {"p_in_weight": torch.zeros(96, 128)}.items())
+    # c_hidden = 48 (not a multiple of 32): the forward pads it, the backward does not
+    assert not _trimul._needs_torch_path(FakeCuda(), {"p_in_weight": torch.zeros(96, 128)}.items())
+    assert _trimul._needs_torch_path(FakeCuda(), {"p_in_weight": torch.zeros(96, 128, requires_grad=True)}.items())
+    # widths above the tiles once rounded up to a multiple of 32
+    assert _trimul._needs_torch_path(FakeCuda(), {"p_in_weight": torch.zeros(1088, 128)}.items())
 
 
 def test_operators_have_fake_implementations():

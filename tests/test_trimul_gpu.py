@@ -325,19 +325,49 @@ def test_module_parameters_take_the_direct_implementation():
     torch.testing.assert_close(got, want, rtol=0, atol=0)
 
 
-@pytest.mark.parametrize("case", ["float64", "c_hidden_48"])
+@pytest.mark.parametrize("case", ["float64", "c_z_544", "fp32_c_z_288", "c_hidden_48_grad"])
 def test_unsupported_configs_use_the_torch_path(case):
-    """Configurations without kernels. (Calls that need gradients run the HIP forward and
-    backward: tests/test_trimul_bwd_gpu.py.)"""
+    """Configurations without kernels: fp64, widths above the tiles once rounded up to a
+    multiple of 32 (512; 256 for fp32), and gradients with a width that is not a multiple of
+    32 (the backward kernels take multiples of 32). (Other calls that need gradients run the
+    HIP forward and backward: tests/test_trimul_bwd_gpu.py.)"""
     from geometric_nn_ops_torch.triangle import triangle_multiplicative_update
 
-    dtype = torch.float64 if case == "float64" else torch.float32
-    w = {k: v.to(DEV) for k, v in trimul_weights(32, 48 if case == "c_hidden_48" else 32, dtype, seed=1).items()}
-    x, mask = pair_input(1, 12, 32, dtype, seed=3)
+    dtype = {"float64": torch.float64, "c_z_544": torch.bfloat16}.get(case, torch.float32)
+    c_z = {"c_z_544": 544, "fp32_c_z_288": 288}.get(case, 32)
+    c_hidden = 48 if case == "c_hidden_48_grad" else 32
+    w = {k: v.to(DEV) for k, v in trimul_weights(c_z, c_hidden, dtype, seed=1).items()}
+    x, mask = pair_input(1, 12, c_z, dtype, seed=3)
     x = x.to(DEV)
+    if case == "c_hidden_48_grad":
+        x.requires_grad_()
     with dispatch_spy() as (ref, kern):
         triangle_multiplicative_update(x, "outgoing", mask.to(DEV), **w)
     assert ref.called and not kern.called
+
+
+@DIRECTIONS
+@pytest.mark.parametrize(("dtype", "c_z", "c_hidden"),
+                         [(torch.bfloat16, 40, 24), (torch.bfloat16, 100, 70), (torch.bfloat16, 130, 128),
+                          (torch.bfloat16, 496, 250), (torch.float16, 72, 40), (torch.float32, 40, 20)],
+                         ids=["bf16_40_24", "bf16_100_70", "bf16_130_128", "bf16_496_250", "fp16_72_40",
+                              "fp32_40_20"])
+def test_odd_channel_widths(direction, dtype, c_z, c_hidden):
+    """Widths that are not multiples of 32 (the reference's Triton kernels mask any width,
+    trimul.py:310-314) on the forward kernels: x and the weights zero-padded to multiples of
+    32 and the LayerNorms averaging over the real widths, with projection biases, random
+    LayerNorm parameters and a padded mask, through the public op, against the fp64 oracle."""
+    from geometric_nn_ops_torch.triangle import triangle_multiplicative_update
+
+    w = trimul_weights(c_z, c_hidden, dtype, seed=27, biases=True, ln_random=True)
+    x, mask = pair_input(1, 36, c_z, dtype, seed=28)
+    with dispatch_spy() as (ref, kern), torch.no_grad():
+        got = triangle_multiplicative_update(x.to(DEV), direction, mask.to(DEV), **{k: v.to(DEV) for k, v in w.items()})
+    assert kern.called and not ref.called
+    assert got.shape == x.shape and got.dtype == dtype
+    tol = TRIMUL_TOL[torch.float32, "ieee"] if dtype == torch.float32 else Tolerance(1 - 1e-4, 2e-2)
+    assert_close_to_oracle("out", got, oracle(x, direction, mask, w), tol,
+                           rel_fro_max=None if dtype == torch.float32 else NORTH_STAR_REL_FRO)
 
 
 # ------------------------------------------------------------------ BASELINE configs (full size)
