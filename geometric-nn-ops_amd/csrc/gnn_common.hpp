@@ -159,10 +159,20 @@ template <> struct Mma<float, PREC_IEEE> {
 
 // bf16x3 emulation of an fp32 product: x = hi + lo with hi = bf16(x), lo = bf16(x - hi);
 // a*b ~= hi_a*hi_b + hi_a*lo_b + lo_a*hi_b (the lo*lo term is dropped), accumulated in fp32.
+// hi widens back to fp32 from its packed pairs (element 2i in the low half of dword i: a
+// shift, element 2i + 1 in the high half: a mask), one instruction per element; converting
+// each element of x again for it costs two.
 __device__ __forceinline__ void split_bf16(const f32x8& x, bf16x8& hi, bf16x8& lo) {
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
   hi = __builtin_convertvector(x, bf16x8);
-  f32x8 r = x - __builtin_convertvector(hi, f32x8);
-  lo = __builtin_convertvector(r, bf16x8);
+  const u32x4_t hp = __builtin_bit_cast(u32x4_t, hi);
+  f32x8 back;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    back[2 * i] = __uint_as_float(hp[i] << 16);
+    back[2 * i + 1] = __uint_as_float(hp[i] & 0xffff0000u);
+  }
+  lo = __builtin_convertvector(x - back, bf16x8);
 }
 
 template <> struct Mma<float, PREC_BF16X3> {

@@ -31,8 +31,8 @@
 //     caller's sentinel (mask_val rounded to the input dtype, in fp32, after the bias)
 //     and -inf for keys past N, on the VALU.
 //   * p = exp2(s * log2 e - m * log2 e): one FMA and one v_exp_f32 per score for 16-bit
-//     inputs; fp32 inputs and rows with no live key (m is then the -1e9 sentinel) use the
-//     exact (s - m) * log2 e. The row sum adds the fp32 probabilities before they are
+//     inputs and fp32 under the bf16x3 split; fp32 under 'ieee' and rows with no live key
+//     (m is then the -1e9 sentinel) use the exact (s - m) * log2 e. The row sum adds the fp32 probabilities before they are
 //     rounded for the PV product, as the reference's tl.sum(P_block, 1) does (v_add_f32
 //     issues alongside other waves' MFMAs; a v_dot2 on the rounded values holds the
 //     matrix pipe).
@@ -46,6 +46,8 @@
 //     bias plane, then hit that XCD's L2.
 #include "gnn_common.hpp"
 #include "gnn_internal.hpp"
+
+#include <type_traits>
 
 namespace gnn {
 
@@ -74,19 +76,25 @@ constexpr float RESCALE_THRESHOLD = 8.0f / LOG2E;  // natural-log units: p <= 2^
 constexpr int QB = 128;              // queries per workgroup (32 per wave)
 constexpr int R = GNN_ATTN_ROWS;     // N_seq rows per workgroup (sharing the bias plane)
 
-template <typename T, int DP>
+// X3: fp32 inputs under the bf16x3 split with DP <= 64 stage K and V as two bf16 planes
+// each (hi, lo), split once where the tile is written to LDS, instead of splitting every
+// fragment in every wave at every product; the planes are laid out and read like a 16-bit
+// input's.
+template <typename T, int DP, bool X3 = false>
 struct Smem {
-  static constexpr int KPAD = (sizeof(T) == 2) ? 8 : 4;  // 16 B per row
+  typedef typename std::conditional<X3, bf16, T>::type E;  // staged element type
+  static constexpr int PL = X3 ? 2 : 1;                    // planes
+  static constexpr int KPAD = (sizeof(E) == 2) ? 8 : 4;    // 16 B per row
   static constexpr int KROW = DP + KPAD;
   // 16-bit types keep V as [key][d] and read V^T fragments with ds_read_b64_tr_b16: a row
   // pitch of 64 B modulo 256 B puts the four 64-byte row windows of one read pass on
   // disjoint banks. fp32 stores V^T [d][key].
-  static constexpr bool VTR = sizeof(T) == 2;
+  static constexpr bool VTR = sizeof(E) == 2;
   static constexpr int VROW = VTR ? (DP == 32 ? 32 : DP + 32) : KT + 4;
   static constexpr int VSIZE = VTR ? KT * VROW : DP * VROW;
   static constexpr int NBUF = GNN_ATTN_NBUF;
-  T k[NBUF][R][KT * KROW];
-  T vt[NBUF][R][VSIZE];
+  E k[NBUF][R][PL][KT * KROW];
+  E vt[NBUF][R][PL][VSIZE];
   uint64_t tile_live[R][MAX_TILES];  // bit j: key tile*64+j is < N and unmasked in row r
   uint16_t tile_list[MAX_TILES];     // tiles with a live key in some row (all if a row is dead)
   int ntiles_run;
@@ -168,7 +176,9 @@ template <typename T, int PREC, int DP, bool HAS_BIAS>
 __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kernel(const gnn_triattn_args a) {
   typedef typename TypeOps<T>::V8 V8;
   typedef typename TypeOps<T>::V4 V4;
-  typedef Smem<T, DP> S;
+  // fp32 under bf16x3, DP <= 64: q, K, V and P split into bf16 hi / lo halves once each
+  constexpr bool X3 = sizeof(T) == 4 && PREC == PREC_BF16X3 && DP <= 64;
+  typedef Smem<T, DP, X3> S;
   __shared__ S sm;
 
   const int N = (int)a.N;
@@ -245,6 +255,7 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
                                  (int64_t)(qok ? myq : 0) * a.bias_stride[2]
                            : nullptr;
   V8 qf[R][DP / 16];
+  bf16x8 qh[R][DP / 16], ql[R][DP / 16];  // X3: the halves of Q'
   f32x16 o[R][DP / 32];
   float m[R], lsum[R], mx[R];  // mx: exact running maximum (m moves lazily)
 #pragma unroll
@@ -256,9 +267,15 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
       const int d0 = 16 * t + 8 * g;
       if (qok && d0 < D) {
         f32x8 x = TypeOps<T>::to_f32(load8(qp + myq * a.q_stride[2] + d0));
-        qf[r][t] = TypeOps<T>::from_f32(x * a.scale);
+        if constexpr (X3)
+          split_bf16(x * a.scale, qh[r][t], ql[r][t]);
+        else
+          qf[r][t] = TypeOps<T>::from_f32(x * a.scale);
       } else {
-        qf[r][t] = zero8<T>();
+        if constexpr (X3)
+          qh[r][t] = ql[r][t] = zero8<bf16>();
+        else
+          qf[r][t] = zero8<T>();
       }
     }
 #pragma unroll
@@ -341,12 +358,22 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
         const int c = tid + i * NTHREADS;
         const int kl = c / CPK;
         const int d0 = (c % CPK) * 8;
-        store8(&sm.k[buf][r][kl * S::KROW + d0], kreg[r][i]);
-        if constexpr (S::VTR) {
-          store8(&sm.vt[buf][r][kl * S::VROW + d0], vreg[r][i]);
+        if constexpr (X3) {
+          bf16x8 hi, lo;
+          split_bf16(kreg[r][i], hi, lo);
+          store8(&sm.k[buf][r][0][kl * S::KROW + d0], hi);
+          store8(&sm.k[buf][r][1][kl * S::KROW + d0], lo);
+          split_bf16(vreg[r][i], hi, lo);
+          store8(&sm.vt[buf][r][0][kl * S::VROW + d0], hi);
+          store8(&sm.vt[buf][r][1][kl * S::VROW + d0], lo);
         } else {
+          store8(&sm.k[buf][r][0][kl * S::KROW + d0], kreg[r][i]);
+          if constexpr (S::VTR) {
+            store8(&sm.vt[buf][r][0][kl * S::VROW + d0], vreg[r][i]);
+          } else {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) sm.vt[buf][r][(d0 + e) * S::VROW + kl] = vreg[r][i][e];
+            for (int e = 0; e < 8; ++e) sm.vt[buf][r][0][(d0 + e) * S::VROW + kl] = vreg[r][i][e];
+          }
         }
       }
   };
@@ -393,17 +420,30 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
       if (state[r] == ROW_ABSENT || (!dead && live == 0)) continue;
 
       // S^T (+ bias): sc[sub][i] is key t*64 + sub*32 + 8*(i/4) + 4g + i%4, query myq.
-      const T* ks = sm.k[cur][r];
       f32x16 sc[2];
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
         for (int i = 0; i < 16; ++i) sc[sub][i] = 0.f;
+      if constexpr (X3) {  // lo * hi + hi * lo + hi * hi
 #pragma unroll
-      for (int kk = 0; kk < DP / 16; ++kk)
+        for (int kk = 0; kk < DP / 16; ++kk)
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-          Mma<T, PREC>::step(sc[sub], load8(&ks[(sub * 32 + l32) * S::KROW + 16 * kk + 8 * g]), qf[r][kk]);
+          for (int sub = 0; sub < 2; ++sub) {
+            const int off = (sub * 32 + l32) * S::KROW + 16 * kk + 8 * g;
+            const bf16x8 kh = load8(&sm.k[cur][r][0][off]), klo = load8(&sm.k[cur][r][1][off]);
+            sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(klo, qh[r][kk], sc[sub], 0, 0, 0);
+            sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, ql[r][kk], sc[sub], 0, 0, 0);
+            sc[sub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qh[r][kk], sc[sub], 0, 0, 0);
+          }
+      } else {
+        const T* ks = sm.k[cur][r][0];
+#pragma unroll
+        for (int kk = 0; kk < DP / 16; ++kk)
+#pragma unroll
+          for (int sub = 0; sub < 2; ++sub)
+            Mma<T, PREC>::step(sc[sub], load8(&ks[(sub * 32 + l32) * S::KROW + 16 * kk + 8 * g]), qf[r][kk]);
+      }
       if constexpr (HAS_BIAS) {
         if constexpr (sizeof(T) == 2) {
 #pragma unroll
@@ -462,12 +502,15 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
           for (int i = 0; i < 16; ++i) o[r][cc][i] *= alpha;
       }
       V8 pf[2][2];
+      bf16x8 ph[2][2], pl[2][2];  // X3: the halves of P^T
       const float nm = -m[r] * LOG2E;
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
-        if (sizeof(T) == 2 && !dead) {
+        if ((sizeof(T) == 2 || X3) && !dead) {
           // the folded FMA leaves a residual below half an ulp of s * log2 e; after the
-          // 16-bit rounding of p the row maximum still maps to exactly 1
+          // 16-bit rounding of p the row maximum still maps to exactly 1 (under the bf16x3
+          // split the residual, a relative 2^-24 of s * log2 e, is far below the split's
+          // own error on the scores)
 #pragma unroll
           for (int i = 0; i < 16; ++i) sc[sub][i] = fast_exp2(__builtin_fmaf(sc[sub][i], LOG2E, nm));
         } else {  // fp32, or m is the collapsed sentinel: subtract first so s - m is exact
@@ -476,38 +519,67 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
         }
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          pf[sub][kk] = frag_from_acc<T>(sc[sub], kk);
+          if constexpr (X3)
+            split_bf16(frag_from_acc<float>(sc[sub], kk), ph[sub][kk], pl[sub][kk]);
+          else
+            pf[sub][kk] = frag_from_acc<T>(sc[sub], kk);
           lsum[r] = rowsum_add(sc[sub], kk, lsum[r]);
         }
       }
 
       // O^T += V^T P^T. Fragment element e of k-step kk of sub-tile sub is key
       // sub*32 + 16*kk + 8*(e/4) + 4g + e%4 in both operands.
-      const T* vs = sm.vt[cur][r];
+      if constexpr (X3) {
 #pragma unroll
-      for (int cc = 0; cc < DP / 32; ++cc)
+        for (int cc = 0; cc < DP / 32; ++cc)
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
+          for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-          for (int kk = 0; kk < 2; ++kk) {
-            V4 lo, hi;
-            if constexpr (S::VTR) {
-              const T* vb = &vs[(sub * 32 + 16 * kk + 4 * g) * S::VROW + 32 * cc + tr_off];
-              lo = tr_read4<T>(vb);
-              hi = tr_read4<T>(vb + 8 * S::VROW);
-            } else {
-              const T* vrow = &vs[(32 * cc + l32) * S::VROW + sub * 32 + 16 * kk + 4 * g];
-              lo = load4(vrow);
-              hi = load4(vrow + 8);
+            for (int kk = 0; kk < 2; ++kk) {
+              const int off = (sub * 32 + 16 * kk + 4 * g) * S::VROW + 32 * cc + tr_off;
+              bf16x8 vh, vl;
+#pragma unroll
+              for (int p = 0; p < 2; ++p) {
+                const bf16* vb = &sm.vt[cur][r][p][off];
+                const bf16x4 lo4 = tr_read4<bf16>(vb), hi4 = tr_read4<bf16>(vb + 8 * S::VROW);
+                bf16x8& vf = p == 0 ? vh : vl;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  vf[e] = lo4[e];
+                  vf[e + 4] = hi4[e];
+                }
+              }
+              o[r][cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, ph[sub][kk], o[r][cc], 0, 0, 0);
+              o[r][cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, pl[sub][kk], o[r][cc], 0, 0, 0);
+              o[r][cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, ph[sub][kk], o[r][cc], 0, 0, 0);
             }
-            V8 vf;
+      } else {
+        const T* vs = sm.vt[cur][r][0];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              vf[e] = lo[e];
-              vf[e + 4] = hi[e];
+        for (int cc = 0; cc < DP / 32; ++cc)
+#pragma unroll
+          for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+              V4 lo, hi;
+              if constexpr (S::VTR) {
+                const T* vb = &vs[(sub * 32 + 16 * kk + 4 * g) * S::VROW + 32 * cc + tr_off];
+                lo = tr_read4<T>(vb);
+                hi = tr_read4<T>(vb + 8 * S::VROW);
+              } else {
+                const T* vrow = &vs[(32 * cc + l32) * S::VROW + sub * 32 + 16 * kk + 4 * g];
+                lo = load4(vrow);
+                hi = load4(vrow + 8);
+              }
+              V8 vf;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                vf[e] = lo[e];
+                vf[e + 4] = hi[e];
+              }
+              Mma<T, PREC>::step(o[r][cc], vf, pf[sub][kk]);
             }
-            Mma<T, PREC>::step(o[r][cc], vf, pf[sub][kk]);
-          }
+      }
     }
 
     if (HAS_BIAS && has_next && !bias_next) load_bias<T>(bc, brow, qok, tn * KT, N, g);

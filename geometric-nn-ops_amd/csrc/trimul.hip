@@ -499,6 +499,284 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_kernel(const gnn_trimul_ar
   }
 }
 
+// ---- stage 1, fp32 under bf16x3: C = CK in {64, 128}, c_hidden <= 128 ---------------------
+// The generic kernel's tile walk, two-barrier LayerNorm and epilogues, with every MFMA
+// operand split into bf16 hi / lo halves once instead of at each product: z where the
+// LayerNorm writes it to LDS (two bf16 planes), a wave's projection weights (its one unit:
+// 32 rows of p_in and of g_in, 2 Ch / 32 <= PW) when the launch starts (registers, for the
+// whole launch) and the output-gate weights when the workgroup starts (two bf16 planes in
+// LDS). The MFMA loops then only read fragments; a product is lo*hi + hi*lo + hi*hi in fp32
+// accumulators. Accumulators start at zero and the biases join after the product.
+template <int CK>
+struct ProjX3Lds {
+  static constexpr int ZB = CK + 8;  // bf16 per z / gate-weight row (16 B of padding)
+  static constexpr int ER = 32 + 4;  // fp32 per staging row
+  static constexpr size_t zh = 0;
+  static constexpr size_t zl = zh + (size_t)PTP * ZB * 2;
+  static constexpr size_t woh = zl + (size_t)PTP * ZB * 2;
+  static constexpr size_t wol = woh + (size_t)CK * ZB * 2;
+  static constexpr size_t ebuf = wol + (size_t)CK * ZB * 2;
+  static constexpr size_t red = ebuf + (size_t)PW * 32 * ER * 4;
+  static constexpr size_t lnw = red + 8 * (size_t)PTP * 8;
+  static constexpr size_t lnb = lnw + CK * 4;
+  static constexpr size_t bgo = lnb + CK * 4;
+  static constexpr size_t mk = bgo + CK * 4;
+  static constexpr size_t total = mk + PTP * 4;
+};
+
+__device__ __forceinline__ f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+template <int CK>
+__global__ __launch_bounds__(PNT, 1) void trimul_proj_x3_kernel(const gnn_trimul_args a, int64_t NP,
+                                                                size_t off_a, size_t off_b, size_t off_g) {
+  typedef ProjX3Lds<CK> S;
+  constexpr int XM = CK / 64;  // 8-channel chunks of x per thread
+  constexpr int NK = CK / 16;  // k-steps
+  constexpr int ZB = S::ZB, ER = S::ER;
+  constexpr int NGO = CK / 32;  // output-gate units
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  bf16* zh = reinterpret_cast<bf16*>(smem_raw + S::zh);
+  bf16* zl = reinterpret_cast<bf16*>(smem_raw + S::zl);
+  bf16* woh = reinterpret_cast<bf16*>(smem_raw + S::woh);
+  bf16* wol = reinterpret_cast<bf16*>(smem_raw + S::wol);
+  float2* red = reinterpret_cast<float2*>(smem_raw + S::red);
+  float* lnw = reinterpret_cast<float*>(smem_raw + S::lnw);
+  float* lnb = reinterpret_cast<float*>(smem_raw + S::lnb);
+  float* bgo = reinterpret_cast<float*>(smem_raw + S::bgo);
+  float* mk = reinterpret_cast<float*>(smem_raw + S::mk);
+  const int Ch = (int)a.Ch, N = (int)a.N;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
+  float* ebuf = reinterpret_cast<float*>(smem_raw + S::ebuf) + wave * 32 * ER;
+  const bool outgoing = a.outgoing != 0;
+  const int64_t ntiles = (int64_t)a.B * N * ((N + PTP - 1) / PTP);
+
+  // ---- once per workgroup: LayerNorm parameters, gate-out weights (split) and biases
+  for (int c = tid; c < CK; c += PNT) {
+    lnw[c] = ld_or<float>(a.ln_in_w, c, 1.f);
+    lnb[c] = ld_or<float>(a.ln_in_b, c, 0.f);
+    bgo[c] = ld_or<float>(a.g_out_b, c, 0.f);
+  }
+  for (int c = tid; c < CK * CK / 8; c += PNT) {
+    const int row = c / (CK / 8), k0 = (c % (CK / 8)) * 8;
+    bf16x8 hi, lo;
+    split_bf16(load8((const float*)a.g_out_w + (int64_t)row * CK + k0), hi, lo);
+    store8(&woh[row * ZB + k0], hi);
+    store8(&wol[row * ZB + k0], lo);
+  }
+  // ---- once per wave: its projection unit's weights, split (B operand: column = channel
+  // 32 * wave + l32, k = 16 kk + 8 g + e)
+  const int npg = 2 * Ch / 32;
+  const bool has_unit = wave < npg;  // uniform over the wave
+  bf16x8 wph[NK], wpl[NK], wgh[NK], wgl[NK];
+  float bp = 0.f, bg = 0.f;
+  {
+    const int ch = has_unit ? 32 * wave + l32 : 0;
+    const float* wprow = (const float*)a.p_in_w + (int64_t)ch * CK + 8 * g;
+    const float* wgrow = (const float*)a.g_in_w + (int64_t)ch * CK + 8 * g;
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+      split_bf16(load8(wprow + 16 * k), wph[k], wpl[k]);
+      split_bf16(load8(wgrow + 16 * k), wgh[k], wgl[k]);
+    }
+    bp = ld_or<float>(a.p_in_b, ch, 0.f);
+    bg = ld_or<float>(a.g_in_b, ch, 0.f);
+  }
+
+  // ---- tile load + LayerNorm: thread = (pixel xpl, part xpart) holding chunks xpart + 8j.
+  // Pixels past N read pixel N - 1 (in bounds); their results are never stored.
+  const int xpl = tid >> 3, xpart = tid & 7;
+  f32x8 xr[XM];
+  ProjMask<float> mreg;
+  auto load_x = [&](const PTile& tl) {
+    const float* src = (const float*)a.x + proj_pix(tl, min(xpl, N - 1 - tl.c0), N, outgoing) * CK;
+#pragma unroll
+    for (int j = 0; j < XM; ++j) xr[j] = load8(src + 8 * (xpart + 8 * j));
+    mreg.request(a, tl, tid & (PTP - 1), N, outgoing);  // used by the threads tid < PTP
+  };
+  auto ln_partial = [&]() {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < XM; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += xr[j][e];
+    const float mean = s * (1.0f / (8 * XM));
+    float m2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < XM; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = xr[j][e] - mean;
+        m2 += d * d;
+      }
+    red[xpart * PTP + xpl] = make_float2(mean, m2);
+  };
+  const LnWidth lw(a.ln_in_channels, CK);
+  auto ln_finish = [&]() {
+    float2 pr[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pr[j] = red[j * PTP + xpl];
+    float mean = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mean += pr[j].x;
+    mean *= 0.125f;  // every part holds 8 * XM channels
+    float m2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float d = pr[j].x - mean;
+      m2 += pr[j].y + (float)(8 * XM) * d * d;
+    }
+    // real-width statistics when the channels past ln_in_channels are padding zeros
+    const float mean_r = mean * (float)CK * lw.inv_n;
+    const float dm = mean - mean_r;
+    const float var = lw.var(m2 + (float)CK * dm * dm, mean_r);
+    const float rstd = 1.0f / sqrtf(var + a.eps);
+#pragma unroll
+    for (int j = 0; j < XM; ++j) {
+      const int ci = xpart + 8 * j;
+      const f32x4 w0 = *reinterpret_cast<const f32x4*>(lnw + 8 * ci);
+      const f32x4 w1 = *reinterpret_cast<const f32x4*>(lnw + 8 * ci + 4);
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(lnb + 8 * ci);
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(lnb + 8 * ci + 4);
+      f32x8 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = (xr[j][e] - mean_r) * rstd * w0[e] + b0[e];
+        v[e + 4] = (xr[j][e + 4] - mean_r) * rstd * w1[e] + b1[e];
+      }
+      bf16x8 hi, lo;
+      split_bf16(v, hi, lo);
+      store8(&zh[xpl * ZB + 8 * ci], hi);
+      store8(&zl[xpl * ZB + 8 * ci], lo);
+    }
+    if (tid < PTP) mk[tid] = mreg.value();
+  };
+
+  float* __restrict__ a_cm = (float*)((unsigned char*)a.workspace + off_a);
+  float* __restrict__ b_cm = (float*)((unsigned char*)a.workspace + off_b);
+  float* __restrict__ gout = (float*)(a.gate ? (unsigned char*)a.gate : (unsigned char*)a.workspace + off_g);
+
+  auto compute = [&](const PTile& tl) {
+    // gated projection unit: acc = [pixel][channel], row = pixel 32s + 8(r/4) + 4g + r%4,
+    // col = channel 32 * wave + l32; staged as [channel][pixel] for 128-byte row stores
+    if (has_unit) {
+#pragma unroll 1
+      for (int s = 0; s < PSUB; ++s) {
+        f32x16 accp, accg;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) accp[r] = accg[r] = 0.f;
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+          const int o = (32 * s + l32) * ZB + 16 * k + 8 * g;
+          const bf16x8 h = load8(&zh[o]), l = load8(&zl[o]);
+          accp = mfma_bf16(l, wph[k], accp);
+          accg = mfma_bf16(l, wgh[k], accg);
+          accp = mfma_bf16(h, wpl[k], accp);
+          accg = mfma_bf16(h, wgl[k], accg);
+          accp = mfma_bf16(h, wph[k], accp);
+          accg = mfma_bf16(h, wgh[k], accg);
+        }
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const int pt = 8 * rg + 4 * g;  // pixel within the sub-tile
+          const f32x4 m4 = *reinterpret_cast<const f32x4*>(&mk[32 * s + pt]);
+          f32x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            v[e] = (accp[4 * rg + e] + bp) * sigmoid_acc(accg[4 * rg + e] + bg) * m4[e];
+          store4(&ebuf[l32 * ER + pt], v);
+        }
+        wave_lds_sync();
+        // 32-byte stores, 4 lanes per channel row of 32 pixels
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int c = lane + 64 * i;
+          const int crow = c / 4, p0 = (c % 4) * 8;
+          const int chg = 32 * wave + crow;
+          float* dst = chg < Ch ? a_cm : b_cm;
+          const int chh = chg < Ch ? chg : chg - Ch;
+          const int pl = 32 * s + p0;
+          float* drow = dst + ab_offset<float>((int64_t)tl.b * Ch + chh, tl.row, tl.c0 + pl, N, NP);
+          f32x8 val = load8(&ebuf[crow * ER + p0]);
+          if (tl.c0 + pl + 8 <= N) {
+            store8(drow, val);
+          } else if (tl.c0 + pl < NP) {  // row tail: pixels N .. NP-1 are written as zeros
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (tl.c0 + pl + e >= N) val[e] = 0.f;
+            store8(drow, val);
+          }
+        }
+        wave_lds_sync();
+      }
+    }
+    // output-gate items (unit uo, sub-tile s): acc = [channel][pixel], row = channel
+    // 32uo + 8(r/4) + 4g + r%4, col = pixel 32s + l32; staged as [pixel][channel]
+#pragma unroll 1
+    for (int it = wave; it < NGO * PSUB; it += PW) {
+      const int uo = it % NGO, s = it / NGO;
+      const int c00 = 32 * uo;
+      f32x16 accx, acch;  // cross terms, hi * hi
+#pragma unroll
+      for (int r = 0; r < 16; ++r) accx[r] = acch[r] = 0.f;
+#pragma unroll
+      for (int k = 0; k < NK; ++k) {
+        const int ow = (c00 + l32) * ZB + 16 * k + 8 * g;
+        const int oz = (32 * s + l32) * ZB + 16 * k + 8 * g;
+        const bf16x8 whf = load8(&woh[ow]), wlf = load8(&wol[ow]);
+        const bf16x8 zhf = load8(&zh[oz]), zlf = load8(&zl[oz]);
+        accx = mfma_bf16(wlf, zhf, accx);
+        acch = mfma_bf16(whf, zhf, acch);
+        accx = mfma_bf16(whf, zlf, accx);
+      }
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int c0 = c00 + 8 * rg + 4 * g;
+        const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bgo[c0]);
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = sigmoid_acc(accx[4 * rg + e] + acch[4 * rg + e] + b4[e]);
+        store4(&ebuf[l32 * ER + 8 * rg + 4 * g], v);
+      }
+      wave_lds_sync();
+      // 32-byte stores, 4 lanes per 32-channel pixel row segment
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int c = lane + 64 * i;
+        const int px = c / 4, k0 = (c % 4) * 8;
+        const int pl = 32 * s + px;
+        if (tl.c0 + pl < N) store8(gout + proj_pix(tl, pl, N, outgoing) * CK + c00 + k0, load8(&ebuf[px * ER + k0]));
+      }
+      wave_lds_sync();
+    }
+  };
+
+  int64_t t = blockIdx.x;
+  if (t >= ntiles) return;  // uniform over the workgroup
+  PTile cur = proj_tile(t, N, outgoing);
+  load_x(cur);
+  ln_partial();
+  __syncthreads();  // partials, LayerNorm parameters and gate weights published
+  ln_finish();
+  __syncthreads();
+  for (; t < ntiles; t += gridDim.x) {
+    const int64_t tn = t + gridDim.x;
+    const bool has_next = tn < ntiles;  // uniform over the workgroup
+    PTile nxt = cur;
+    if (has_next) {
+      nxt = proj_tile(tn, N, outgoing);
+      load_x(nxt);
+    }
+    compute(cur);
+    if (has_next) ln_partial();
+    __syncthreads();  // z / mask of this tile consumed, partials of the next one published
+    if (has_next) ln_finish();
+    __syncthreads();
+    cur = nxt;
+  }
+}
+
 // ---- stage 1, fixed-width variant: 16-bit types with C = CK in {64, 128} ----------------
 // Same work split and tile order as trimul_proj_kernel, with C known at compile time so the
 // k loops unroll and a wave's gate MFMAs and second sub-tile can overlap the first
@@ -1223,6 +1501,137 @@ __global__ __launch_bounds__(NT, 2) void trimul_contract_kernel(const T* __restr
     }
 }
 
+// fp32 under bf16x3 (what 'tf32' resolves to on gfx950): the same tiles and schedule as
+// trimul_contract_kernel, but each fp32 stage is split into bf16 hi / lo planes once, where it
+// is written to LDS, so the inner loop reads hi / lo fragments and issues the three bf16
+// MFMAs (lo hi + hi lo + hi hi) with no VALU work; splitting per product instead repeats the
+// split of every fragment for each of the MFMAs that reuse it.
+struct ContractX3 {
+  static constexpr int BM = 128, BN = 128, BK = 32;
+  static constexpr int ROW = BK + 8;  // bf16 elements per LDS row (16 B of padding)
+};
+
+__global__ __launch_bounds__(NT, 2) void trimul_contract_x3_kernel(const float* __restrict__ A,
+                                                                  const float* __restrict__ Bm,
+                                                                  float* __restrict__ O, int N, int64_t NP) {
+  typedef ContractX3 Cfg;
+  __shared__ __align__(16) bf16 ash[Cfg::BM * Cfg::ROW], asl[Cfg::BM * Cfg::ROW];
+  __shared__ __align__(16) bf16 bsh[Cfg::BN * Cfg::ROW], bsl[Cfg::BN * Cfg::ROW];
+
+  const int nti = (N + Cfg::BM - 1) / Cfg::BM;
+  const int ntj = (N + Cfg::BN - 1) / Cfg::BN;
+  const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
+  const int tj = w % ntj;
+  const int ti = (w / ntj) % nti;
+  const int64_t plane = w / ((uint32_t)ntj * nti);
+  const int64_t poff = plane * N * NP;
+  const float* Ap = A + poff;
+  const float* Bp = Bm + poff;
+  float* Op = O + poff;
+  const int i0 = ti * Cfg::BM, j0 = tj * Cfg::BN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  constexpr int CPR = Cfg::BK / 8;        // 8-element chunks per row per stage
+  constexpr int CH = Cfg::BM * CPR / NT;  // chunks per thread per operand
+  f32x8 ra[CH], rb[CH];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + i * NT;
+      const int r = c / CPR, kc = k0 + (c % CPR) * 8;
+      ra[i] = f32x8{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      rb[i] = ra[i];
+      if (kc < N) {
+        if (kc + 8 <= N) {
+          if (i0 + r < N) ra[i] = load8(Ap + (int64_t)(i0 + r) * NP + kc);
+          if (j0 + r < N) rb[i] = load8(Bp + (int64_t)(j0 + r) * NP + kc);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (kc + e < N) {
+              if (i0 + r < N) ra[i][e] = Ap[(int64_t)(i0 + r) * NP + kc + e];
+              if (j0 + r < N) rb[i][e] = Bp[(int64_t)(j0 + r) * NP + kc + e];
+            }
+        }
+      }
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + i * NT;
+      const int r = c / CPR, kl = (c % CPR) * 8;
+      bf16x8 hi, lo;
+      split_bf16(ra[i], hi, lo);
+      store8(&ash[r * Cfg::ROW + kl], hi);
+      store8(&asl[r * Cfg::ROW + kl], lo);
+      split_bf16(rb[i], hi, lo);
+      store8(&bsh[r * Cfg::ROW + kl], hi);
+      store8(&bsl[r * Cfg::ROW + kl], lo);
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
+
+  const int nkt = (N + Cfg::BK - 1) / Cfg::BK;
+  load(0);
+  store();
+  __syncthreads();
+  for (int kt = 0; kt < nkt; ++kt) {
+    const bool has_next = kt + 1 < nkt;
+    if (has_next) load((kt + 1) * Cfg::BK);
+#pragma unroll
+    for (int kk = 0; kk < Cfg::BK / 16; ++kk) {
+      bf16x8 ah[2], al[2], bh[2], bl[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const int o = (64 * wm + 32 * x + l32) * Cfg::ROW + 16 * kk + 8 * g;
+        ah[x] = load8(&ash[o]);
+        al[x] = load8(&asl[o]);
+      }
+#pragma unroll
+      for (int y = 0; y < 2; ++y) {
+        const int o = (64 * wn + 32 * y + l32) * Cfg::ROW + 16 * kk + 8 * g;
+        bh[y] = load8(&bsh[o]);
+        bl[y] = load8(&bsl[o]);
+      }
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) {
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[x], bh[y], acc[x][y], 0, 0, 0);
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[x], bl[y], acc[x][y], 0, 0, 0);
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[x], bh[y], acc[x][y], 0, 0, 0);
+        }
+    }
+    __syncthreads();
+    if (has_next) store();
+    __syncthreads();
+  }
+
+  // acc[x][y][r] = o[i0 + 64wm + 32x + 8(r/4) + 4g + r%4][j0 + 64wn + 32y + l32]
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      const int j = j0 + 64 * wn + 32 * y + l32;
+      if (j >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = i0 + 64 * wm + 32 * x + 8 * (r / 4) + 4 * g + (r % 4);
+        if (i < N) Op[(int64_t)i * NP + j] = acc[x][y][r];
+      }
+    }
+}
+
 // ============================== stage 3: LN-out + p_out + gate ============================
 // One workgroup = PTO consecutive pixels of one row of the pair grid; their g and out rows
 // form one contiguous block of PTO * C elements (pixel-major). The channel-major o tile is
@@ -1682,8 +2091,27 @@ int launch_proj_pp(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t 
   return (int)hipGetLastError();
 }
 
+template <int CK>
+int launch_proj_x3(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
+  const int64_t NP = round_up(a.N, 32);
+  const int64_t ntiles = a.B * a.N * ((a.N + PTP - 1) / PTP);
+  constexpr size_t smem = ProjX3Lds<CK>::total;
+  const void* fn = (const void*)trimul_proj_x3_kernel<CK>;
+  (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  const int64_t grid = std::min<int64_t>(ntiles, persistent_grid(fn, PNT, smem));
+  hipLaunchKernelGGL((trimul_proj_x3_kernel<CK>), dim3((uint32_t)grid), dim3(PNT), smem, st, a, NP, L.off_a,
+                     L.off_b, L.off_g);
+  return (int)hipGetLastError();
+}
+
 template <typename T, int PREC>
 int launch_proj(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
+  if constexpr (sizeof(T) == 4 && PREC == PREC_BF16X3) {
+    if (2 * a.Ch <= 32 * PW) {  // one projection unit per wave
+      if (a.C == 128) return launch_proj_x3<128>(a, L, st);
+      if (a.C == 64) return launch_proj_x3<64>(a, L, st);
+    }
+  }
   if constexpr (sizeof(T) == 2) {
     if (GNN_PROJ_PINGPONG && a.C == 128 && a.Ch == 128) return launch_proj_pp<T>(a, L, st);
     if (a.C == 128 && a.Ch == 128) return launch_proj_fast<T, 128, 128>(a, L, st);
@@ -1720,9 +2148,16 @@ int launch_contract(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t
   typedef ContractCfg<T> Cfg;
   const int64_t nblk = a.B * a.Ch * ((a.N + Cfg::BM - 1) / Cfg::BM) * ((a.N + Cfg::BN - 1) / Cfg::BN);
   unsigned char* ws = (unsigned char*)a.workspace;
-  hipLaunchKernelGGL((trimul_contract_kernel<T, PREC>), dim3((uint32_t)nblk), dim3(NT), 0, st,
-                     (const T*)(ws + L.off_a), (const T*)(ws + L.off_b), (T*)(ws + L.off_o), (int)a.N,
-                     NP);
+  if constexpr (sizeof(T) == 4 && PREC == PREC_BF16X3) {
+    static_assert(ContractX3::BM == Cfg::BM && ContractX3::BN == Cfg::BN, "same tiles as the fp32 kernel");
+    hipLaunchKernelGGL(trimul_contract_x3_kernel, dim3((uint32_t)nblk), dim3(NT), 0, st,
+                       (const float*)(ws + L.off_a), (const float*)(ws + L.off_b), (float*)(ws + L.off_o),
+                       (int)a.N, NP);
+  } else {
+    hipLaunchKernelGGL((trimul_contract_kernel<T, PREC>), dim3((uint32_t)nblk), dim3(NT), 0, st,
+                       (const T*)(ws + L.off_a), (const T*)(ws + L.off_b), (T*)(ws + L.off_o), (int)a.N,
+                       NP);
+  }
   return (int)hipGetLastError();
 }
 

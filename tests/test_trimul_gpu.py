@@ -63,18 +63,21 @@ def test_accuracy(direction, dtype, precision):
 
 
 @DIRECTIONS
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
-def test_stages_against_oracle(direction, dtype):
+@pytest.mark.parametrize(("dtype", "precision"),
+                         [(torch.bfloat16, "ieee"), (torch.float32, "ieee"), (torch.float32, "tf32")],
+                         ids=["bf16", "fp32", "fp32_tf32"])
+def test_stages_against_oracle(direction, dtype, precision):
     """Each kernel's output region of the workspace against the oracle's intermediate:
     a, b (channel-major, transposed per channel for 'incoming'; k-blocked for 16-bit types,
-    zero in the row padding), g and o."""
+    zero in the row padding), g and o. fp32 under 'tf32' takes the projection kernel that
+    splits its operands into bf16 halves once (c_z = 64)."""
     from geometric_nn_ops_torch.triangle._kernels import trimul as K
 
     B, N, C, Ch = 2, 40, 64, 32
     w = trimul_weights(C, Ch, dtype, seed=5, biases=True, ln_random=True)
     x, mask = pair_input(B, N, C, dtype, seed=6)
     wd = {k: v.to(DEV) for k, v in w.items()}
-    with torch.no_grad():
+    with torch.no_grad(), matmul_precision(precision):
         args, keep, out, ws, off = K.build_args(x.to(DEV), direction, mask.to(DEV), 1e-5, wd)
         K.run_stage("gnn_trimul_proj", args, x.device if x.is_cuda else torch.device(DEV))
         K.run_stage("gnn_trimul_contract", args, torch.device(DEV))
@@ -88,7 +91,7 @@ def test_stages_against_oracle(direction, dtype):
         return ws[off[i]:off[i] + n * el].view(dtype).reshape(shape)
 
     st = O.trimul_stages(to_np(x), direction, to_np(mask), **np_weights(w))
-    tol = TRIMUL_TOL[dtype, "ieee"]
+    tol = TRIMUL_TOL[dtype, precision]
     def operand(i):
         if dtype == torch.float32:  # row-major [B, Ch, N, NP]
             return region(i, (B, Ch, N, NP))
@@ -368,6 +371,21 @@ def test_odd_channel_widths(direction, dtype, c_z, c_hidden):
     tol = TRIMUL_TOL[torch.float32, "ieee"] if dtype == torch.float32 else Tolerance(1 - 1e-4, 2e-2)
     assert_close_to_oracle("out", got, oracle(x, direction, mask, w), tol,
                            rel_fro_max=None if dtype == torch.float32 else NORTH_STAR_REL_FRO)
+
+
+@DIRECTIONS
+@pytest.mark.parametrize(("c_z", "c_hidden"), [(128, 128), (128, 64), (64, 32), (100, 70)],
+                         ids=["128_128", "128_64", "64_32", "odd_100_70"])
+def test_fp32_tf32_projection(direction, c_z, c_hidden):
+    """fp32 under 'tf32' with c_z 64 or 128 (after padding) and c_hidden <= 128: the
+    projection kernel that splits z, its weights and the gate weights into bf16 halves once.
+    Ragged N (70: a partial last tile, row tails past N), batch 2, projection biases, random
+    LayerNorm parameters and a padded mask, against the fp64 oracle."""
+    w = trimul_weights(c_z, c_hidden, torch.float32, seed=41, biases=True, ln_random=True)
+    x, mask = pair_input(2, 70, c_z, torch.float32, seed=42)
+    with matmul_precision("tf32"):
+        got = hip(x, direction, mask, w)
+    assert_close_to_oracle("out", got, oracle(x, direction, mask, w), TRIMUL_TOL[torch.float32, "tf32"])
 
 
 # ------------------------------------------------------------------ BASELINE configs (full size)
