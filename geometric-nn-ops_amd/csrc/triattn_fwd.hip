@@ -172,14 +172,26 @@ __device__ __forceinline__ void load_bias<float>(BiasFrag<float>& bf, const floa
 
 enum RowState { ROW_LIVE = 0, ROW_DEAD = 1, ROW_ABSENT = 2 };
 
+// fp32 under the bf16x3 split with DP = 32 runs at GNN_ATTN_X3_WAVES waves per SIMD; above
+// two it loads each tile's bias fragments at the top of that tile (not a tile ahead), which
+// frees the 32 registers the early copy holds for the whole key loop.
+#ifndef GNN_ATTN_X3_WAVES
+#define GNN_ATTN_X3_WAVES 3
+#endif
+template <typename T, int PREC, int DP>
+__host__ __device__ constexpr int attn_min_blocks() {
+  return (sizeof(T) == 4 && PREC == PREC_BF16X3 && DP <= 32) ? GNN_ATTN_X3_WAVES : GNN_ATTN_MINBLOCKS;
+}
+
 template <typename T, int PREC, int DP, bool HAS_BIAS>
-__global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kernel(const gnn_triattn_args a) {
+__global__ __launch_bounds__(NTHREADS, (attn_min_blocks<T, PREC, DP>())) void triattn_fwd_kernel(const gnn_triattn_args a) {
   typedef typename TypeOps<T>::V8 V8;
   typedef typename TypeOps<T>::V4 V4;
   // fp32 under bf16x3, DP <= 64: q, K, V and P split into bf16 hi / lo halves once each
   constexpr bool X3 = sizeof(T) == 4 && PREC == PREC_BF16X3 && DP <= 64;
   typedef Smem<T, DP, X3> S;
   __shared__ S sm;
+  constexpr bool BIAS_AHEAD = attn_min_blocks<T, PREC, DP>() <= 2;
 
   const int N = (int)a.N;
   const int H = (int)a.H;
@@ -396,7 +408,7 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
   if (nrun > 0) {
     const int t0 = sm.tile_list[0];
     load_kv(t0);
-    if constexpr (HAS_BIAS) load_bias<T>(bias0, brow, qok, t0 * KT, N, g);
+    if constexpr (HAS_BIAS && BIAS_AHEAD) load_bias<T>(bias0, brow, qok, t0 * KT, N, g);
     store_kv(0);
   }
   __syncthreads();
@@ -411,6 +423,7 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
     const bool has_next = it + 1 < nrun;
     const int tn = has_next ? sm.tile_list[it + 1] : t;
     if (has_next) load_kv(tn);
+    if constexpr (HAS_BIAS && !BIAS_AHEAD) load_bias<T>(bc, brow, qok, t * KT, N, g);
     bool bias_next = false;  // bc already holds the next tile's bias
 
 #pragma unroll
@@ -458,7 +471,7 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
 #pragma unroll
               for (int e = 0; e < 4; ++e) sc[sub][4 * rg + e] += TypeOps<T>::to_f32(bc.f[sub][rg][e]);
         }
-        if (R == 1 && has_next) {  // the next tile's fragments, as early as possible
+        if (BIAS_AHEAD && R == 1 && has_next) {  // the next tile's fragments, as early as possible
           load_bias<T>(bc, brow, qok, tn * KT, N, g);
           bias_next = true;
         }
@@ -582,7 +595,7 @@ __global__ __launch_bounds__(NTHREADS, GNN_ATTN_MINBLOCKS) void triattn_fwd_kern
       }
     }
 
-    if (HAS_BIAS && has_next && !bias_next) load_bias<T>(bc, brow, qok, tn * KT, N, g);
+    if (BIAS_AHEAD && HAS_BIAS && has_next && !bias_next) load_bias<T>(bc, brow, qok, tn * KT, N, g);
     if constexpr (S::NBUF == 2) {
       // the other stage was last read in the previous iteration, before its barrier
       if (has_next) store_kv(cur ^ 1);

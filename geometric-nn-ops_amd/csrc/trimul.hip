@@ -1505,7 +1505,11 @@ __global__ __launch_bounds__(NT, 2) void trimul_contract_kernel(const T* __restr
 // trimul_contract_kernel, but each fp32 stage is split into bf16 hi / lo planes once, where it
 // is written to LDS, so the inner loop reads hi / lo fragments and issues the three bf16
 // MFMAs (lo hi + hi lo + hi hi) with no VALU work; splitting per product instead repeats the
-// split of every fragment for each of the MFMAs that reuse it.
+// split of every fragment for each of the MFMAs that reuse it. The kernel is bound by its
+// fp32 operand traffic, not by the split (72 against 73 us at N = 384). Measured slower: the
+// projection writing a and b as bf16 hi / lo planes in the 16-bit layout and the DMA-fed
+// 16-bit contraction reading both planes (128 x 256 tiles, three 48 KB stages, one workgroup
+// per CU: 81 us).
 struct ContractX3 {
   static constexpr int BM = 128, BN = 128, BK = 32;
   static constexpr int ROW = BK + 8;  // bf16 elements per LDS row (16 B of padding)
@@ -1641,7 +1645,10 @@ __global__ __launch_bounds__(NT, 2) void trimul_contract_x3_kernel(const float* 
 // layer does, into an LDS tile; the workgroup then streams the tile out with 16-byte g loads
 // and 16-byte out stores over the contiguous block, multiplying in fp32 and rounding once.
 // The g chunk of a pass is loaded into registers one pass ahead (the first before the o
-// tile), so its latency hides behind the LayerNorm / the previous pass.
+// tile), so its latency hides behind the LayerNorm / the previous pass. fp32 under bf16x3
+// splits each fragment at its product; writing the normalised tile as bf16 hi / lo planes
+// once and splitting each p_out fragment once measured slower (65 against 61 us at
+// N = 384, C = c_hidden = 128).
 constexpr int PTO = 64;
 constexpr int OPC = 128;                  // output channels per pass (4 waves x 32)
 constexpr int OCH = PTO * OPC / 8 / NT;  // 8-element chunks per thread per pass
@@ -1879,14 +1886,19 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
 // staged in LDS, 128 rows at a time, and written with 16-byte row stores. The larger tile
 // halves the L2 -> LDS bytes per flop, which bound the 128-row tile. At N = 512 the kernel
 // moves its a / b / o bytes at about 4.5 TB/s, near the 4.9 TB/s a device-to-device copy
-// reaches; measured without gain: a fifth stage (160 KB of LDS), and reading the next
-// stage's fragments into a second register set while the current stage multiplies.
+// reaches; measured without gain: a fifth stage (160 KB of LDS: GNN_CONTRACT_STAGES256=5,
+// also slower at N = 1024, 303 against 294 us), and reading the next stage's fragments into
+// a second register set while the current stage multiplies. At N = 1024 (37% of the MFMA
+// peak) the vendor's batched GEMM on the same operands (torch.bmm, hipBLASLt) takes 279 us.
+#ifndef GNN_CONTRACT_STAGES256  // DMA pipeline stages of the 256-row tile (32 KB each)
+#define GNN_CONTRACT_STAGES256 4
+#endif
 template <int BM>
 struct ContractDma {
   static constexpr int BN = 256, BK = 32;
   static constexpr int NW = BM / 32;                      // waves
   static constexpr int NTH = 64 * NW;                     // threads
-  static constexpr int STAGES = BM == 256 ? 4 : 3;
+  static constexpr int STAGES = BM == 256 ? GNN_CONTRACT_STAGES256 : 3;
   static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   static constexpr int QA = BM / 16 / NW, QB = BN / 16 / NW;  // DMA instructions per wave
@@ -1900,10 +1912,12 @@ struct ContractDma {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
+// s_waitcnt vmcnt(N_) expcnt(7) lgkmcnt(0); the 6-bit vmcnt field is split into bits 3:0
+// and 15:14 of the immediate
 template <int N_>
 __device__ __forceinline__ void wait_vm_lgkm0() {
-  static_assert(N_ >= 0 && N_ < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(0x070 | N_);  // vmcnt(N_) expcnt(7) lgkmcnt(0)
+  static_assert(N_ >= 0 && N_ < 64, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x070 | (N_ & 15) | ((N_ >> 4) << 14));
 }
 
 template <typename T, int BM>
@@ -1985,7 +1999,9 @@ __global__ __launch_bounds__(ContractDma<BM>::NTH, BM == 256 ? 1 : 2) void trimu
     // longer read. A plain s_barrier (with a compiler memory clobber) replaces
     // __syncthreads, whose fence would also wait for the DMA of the later stages.
     const int ahead = min(Cfg::STAGES - 2, nkt - 1 - kt);  // stages issued after kt
-    if (ahead >= 2)
+    if (Cfg::STAGES >= 5 && ahead >= 3)
+      wait_vm_lgkm0<3 * Cfg::QPS>();
+    else if (ahead >= 2)
       wait_vm_lgkm0<2 * Cfg::QPS>();
     else if (ahead == 1)
       wait_vm_lgkm0<Cfg::QPS>();
@@ -2137,12 +2153,18 @@ int launch_contract_dma(const gnn_trimul_args& a, const TrimulLayout& L, hipStre
   return (int)hipGetLastError();
 }
 
+// Smallest N that takes the 256-row contraction tile. Measured at N = 512: the 128-row tile
+// is faster on warm inputs (43.8 against 48.5 us) but slower inside the step (56 against
+// 49 us), where a and b arrive from the projection kernel rather than from the cache.
+#ifndef GNN_CONTRACT_BM256_N
+#define GNN_CONTRACT_BM256_N 512
+#endif
 template <typename T, int PREC>
 int launch_contract(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
   const int64_t NP = round_up(a.N, 32);
   if constexpr (sizeof(T) == 2) {
     // 256-row tiles once N fills them (half the L2 -> LDS bytes per flop), 128 below
-    if (a.N >= 512) return launch_contract_dma<T, 256>(a, L, st, NP);
+    if (a.N >= GNN_CONTRACT_BM256_N) return launch_contract_dma<T, 256>(a, L, st, NP);
     return launch_contract_dma<T, 128>(a, L, st, NP);
   }
   typedef ContractCfg<T> Cfg;
