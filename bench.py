@@ -946,6 +946,14 @@ def block(dev, stream, N, dtype, precision):
         res["trimul_outgoing_kernels"] = {
             name: rates(sfl[name], sby[name], window_ms(t_out.stage(name), stream)[0], peak)
             for name in ("proj", "contract", "out")}
+        # the vendor's batched GEMM (torch.bmm, hipBLASLt) on operands of the contraction's
+        # shape: C planes of [N, N] x [N, N]^T, the right operand made contiguous first
+        va = torch.randn(C, N, N, dtype=dtype, device=dev)
+        vb = torch.randn(C, N, N, dtype=dtype, device=dev).transpose(1, 2).contiguous()
+        vo = torch.empty(C, N, N, dtype=dtype, device=dev)
+        res["trimul_outgoing_kernels"]["contract_vendor_bmm"] = rates(
+            sfl["contract"], sby["contract"], window_ms(lambda: torch.bmm(va, vb, out=vo), stream)[0], peak)
+        del va, vb, vo
     return res
 
 
