@@ -180,7 +180,9 @@ enum RowState { ROW_LIVE = 0, ROW_DEAD = 1, ROW_ABSENT = 2 };
 #endif
 template <typename T, int PREC, int DP>
 __host__ __device__ constexpr int attn_min_blocks() {
-  return (sizeof(T) == 4 && PREC == PREC_BF16X3 && DP <= 32) ? GNN_ATTN_X3_WAVES : GNN_ATTN_MINBLOCKS;
+  // DP = 256 (16-bit only): one workgroup per CU, the 128 O accumulator registers of a wave
+  // in AGPRs beside the q, K / V staging and score registers
+  return DP > 128 ? 1 : (sizeof(T) == 4 && PREC == PREC_BF16X3 && DP <= 32) ? GNN_ATTN_X3_WAVES : GNN_ATTN_MINBLOCKS;
 }
 
 template <typename T, int PREC, int DP, bool HAS_BIAS>
@@ -641,8 +643,10 @@ int launch_bias(const gnn_triattn_args& a, hipStream_t stream) {
     hipLaunchKernelGGL((triattn_fwd_kernel<T, PREC, 32, HAS_BIAS>), grid, block, 0, stream, a);
   else if (a.D <= 64)
     hipLaunchKernelGGL((triattn_fwd_kernel<T, PREC, 64, HAS_BIAS>), grid, block, 0, stream, a);
-  else
+  else if (a.D <= 128)
     hipLaunchKernelGGL((triattn_fwd_kernel<T, PREC, 128, HAS_BIAS>), grid, block, 0, stream, a);
+  else if constexpr (sizeof(T) == 2)
+    hipLaunchKernelGGL((triattn_fwd_kernel<T, PREC, 256, HAS_BIAS>), grid, block, 0, stream, a);
   return (int)hipGetLastError();
 }
 
@@ -656,8 +660,10 @@ int launch_dp(const gnn_triattn_args& a, hipStream_t stream) {
 int triattn_fwd(const gnn_triattn_args& a, hipStream_t stream) {
   if (a.N > (int64_t)MAX_TILES * KT)
     return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention: N_res > 32768 is not supported");
-  if (a.D > 128)
-    return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention: head dim > 128 is not supported");
+  if (a.D > 256)
+    return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention: head dim > 256 is not supported");
+  if (a.D > 128 && a.dtype == GNN_F32)
+    return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention: fp32 head dim > 128 is not supported");
   const int64_t nqb = (a.N + QB - 1) / QB;
   if (nqb * a.H * ((a.S + R - 1) / R) * a.B >= (int64_t)1 << 31)
     return set_error(GNN_ERR_UNSUPPORTED, "triangle_attention: grid too large");

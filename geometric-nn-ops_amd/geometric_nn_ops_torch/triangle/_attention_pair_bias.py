@@ -26,7 +26,7 @@ def _needs_torch_path(s, q, k, v, z, weights, z_is_projected) -> bool:
         return True
     if q.dtype not in _KERNEL_DTYPES or q.dtype != k.dtype or q.dtype != v.dtype or z.dtype != q.dtype:
         return True
-    if q.shape[2] != k.shape[2] or q.shape[-1] > _hip_attn.MAX_HEAD_DIM:
+    if q.shape[2] != k.shape[2] or q.shape[-1] > _hip_attn.max_head_dim(q.dtype):
         return True
     if not z_is_projected and weights[0] is None:
         return True

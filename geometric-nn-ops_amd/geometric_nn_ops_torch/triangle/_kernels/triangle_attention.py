@@ -16,13 +16,18 @@ import torch
 from ... import _lib, _precision
 from .._masking import rounded_mask_value
 
-MAX_HEAD_DIM = 128  # the kernel's largest head-dim tile
+MAX_HEAD_DIM = 256  # the kernel's largest head-dim tile (16-bit inputs)
+MAX_HEAD_DIM_FP32 = 128  # fp32 tiles take twice the LDS
 MAX_N_RES = 32768
+
+
+def max_head_dim(dtype: torch.dtype) -> int:
+    return MAX_HEAD_DIM_FP32 if dtype == torch.float32 else MAX_HEAD_DIM
 
 
 def supports(q: torch.Tensor) -> bool:
     """Whether the HIP kernel covers this input (dtype handled by the caller)."""
-    return q.shape[-1] <= MAX_HEAD_DIM and q.shape[-3] <= MAX_N_RES
+    return q.shape[-1] <= max_head_dim(q.dtype) and q.shape[-3] <= MAX_N_RES
 
 
 def _vectorizable(t: torch.Tensor) -> bool:

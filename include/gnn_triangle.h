@@ -84,7 +84,7 @@ typedef struct gnn_triattn_args {
   const uint8_t* mask;  /* bool [B,S,N] (nonzero = keep), or NULL for all-keep */
   float* lse;           /* optional fp32 [B,S,H,N] log-sum-exp (natural log), or NULL */
   float* row_max;       /* optional fp32 [B,S,H,N] largest logit of each query row, or NULL */
-  int64_t B, S, N, H, D;
+  int64_t B, S, N, H, D; /* D a multiple of 8, at most 256 (fp32: 128); N at most 32768 */
   int64_t q_stride[4];  /* strides of dims b, s, n, h (d stride must be 1) */
   int64_t k_stride[4];
   int64_t v_stride[4];

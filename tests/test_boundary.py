@@ -130,6 +130,21 @@ def test_triattn_argument_errors():
         _lib.check(_lib.GNN_ERR_ARG, "gnn_triattn_fwd")
 
 
+def test_triattn_head_dim_limits():
+    """Head dims up to 256 for 16-bit inputs and 128 for fp32; wider ones are refused
+    before any launch."""
+    lib = _lib.load()
+    a = _lib.TriAttnArgs()
+    a.q = a.k = a.v = a.o = 4096
+    a.B, a.S, a.N, a.H = 1, 2, 40, 2
+    for D, dtype, msg in ((264, _lib.GNN_BF16, b"head dim > 256"), (136, _lib.GNN_F32, b"fp32 head dim > 128")):
+        a.D, a.dtype = D, dtype
+        for st in ("q_stride", "k_stride", "v_stride", "o_stride"):
+            setattr(a, st, _lib.I64x4(2 * 40 * 2 * D, 40 * 2 * D, 2 * D, D))
+        assert lib.gnn_triattn_fwd(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
+        assert msg in lib.gnn_last_error()
+
+
 def test_triattn_workspace():
     """The 16-bit row path with a pair bias needs caller scratch for the bias in fragment
     order (4 KB per 32-query x 64-key tile per (batch, head)); other calls need none, and a

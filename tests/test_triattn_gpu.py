@@ -101,6 +101,42 @@ def test_public_op_accuracy_and_exp2(dtype):
                                rel_fro_max=NORTH_STAR_REL_FRO if dtype != torch.float32 else None)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("D", [136, 256])
+def test_head_dim_above_128(dtype, D):
+    """Head dims 129-256 (the reference pads any D, triangle_attention.py:1168) on the
+    kernel's 256-wide head-dim tile: ragged N, a key mask and the pair bias, through the
+    public op (which must take the kernel), against the fp64 oracle."""
+    from unittest import mock
+
+    from geometric_nn_ops_torch.triangle import _triattn
+
+    B, S, N, H = 1, 2, 70, 2
+    t = attention_inputs(B, S, N, H, D, dtype, seed=5)
+    mask = key_mask(B, S, N, seed=3)
+    want = oracle_of(t, mask, D**-0.5)
+    with mock.patch.object(_triattn, "triangle_attention_torch", wraps=_triattn.triangle_attention_torch) as ref:
+        got = public(**dev(t), mask=mask.to(DEV), scale=D**-0.5)
+    assert not ref.called
+    assert_close_to_oracle("out", got, want, TRIANGLE_ATTENTION_TOL[dtype, "ieee"], rel_fro_max=NORTH_STAR_REL_FRO)
+
+
+def test_fp32_head_dim_above_128_uses_the_torch_path():
+    """fp32 tiles stop at a head dim of 128 (twice the LDS of a 16-bit tile): D = 160 takes the
+    torch path, with the same results."""
+    from unittest import mock
+
+    from geometric_nn_ops_torch.triangle import _triattn
+
+    B, S, N, H, D = 1, 1, 40, 2, 160
+    t = attention_inputs(B, S, N, H, D, torch.float32, seed=6)
+    mask = key_mask(B, S, N, seed=4)
+    with mock.patch.object(_triattn, "triangle_attention_torch", wraps=_triattn.triangle_attention_torch) as ref:
+        got = public(**dev(t), mask=mask.to(DEV))
+    assert ref.called
+    assert_close_to_oracle("out", got, oracle_of(t, mask), TRIANGLE_ATTENTION_TOL[torch.float32, "ieee"])
+
+
 def test_pairformer_shape():
     """N=384, H=16, D=48 (reference test_triangle_attention.py:591-607)."""
     B, S, N, H, D = 1, 1, 384, 16, 48
