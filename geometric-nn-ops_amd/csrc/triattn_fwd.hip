@@ -178,11 +178,22 @@ enum RowState { ROW_LIVE = 0, ROW_DEAD = 1, ROW_ABSENT = 2 };
 #ifndef GNN_ATTN_X3_WAVES
 #define GNN_ATTN_X3_WAVES 3
 #endif
+// fp32 with DP = 128: workgroups per CU the register allocation is held to. At 2 (256
+// registers) the kernel spills 129 registers with a bias; one workgroup per CU measured faster
+// (N = 256, 256 rows, H = 4, bias: 449 against 463 us under 'ieee', 316 against 379 under
+// 'tf32'). 16-bit inputs keep 2 (16 spilled registers with a bias; one workgroup: 150 against
+// 138 us).
+#ifndef GNN_ATTN_F32_DP128_BLOCKS
+#define GNN_ATTN_F32_DP128_BLOCKS 1
+#endif
 template <typename T, int PREC, int DP>
 __host__ __device__ constexpr int attn_min_blocks() {
   // DP = 256 (16-bit only): one workgroup per CU, the 128 O accumulator registers of a wave
   // in AGPRs beside the q, K / V staging and score registers
-  return DP > 128 ? 1 : (sizeof(T) == 4 && PREC == PREC_BF16X3 && DP <= 32) ? GNN_ATTN_X3_WAVES : GNN_ATTN_MINBLOCKS;
+  return DP > 128    ? 1
+         : DP == 128 ? (sizeof(T) == 4 ? GNN_ATTN_F32_DP128_BLOCKS : GNN_ATTN_MINBLOCKS)
+         : (sizeof(T) == 4 && PREC == PREC_BF16X3 && DP <= 32) ? GNN_ATTN_X3_WAVES
+                                                               : GNN_ATTN_MINBLOCKS;
 }
 
 template <typename T, int PREC, int DP, bool HAS_BIAS>
