@@ -224,6 +224,29 @@ int gnn_trimul_gate_bwd(const gnn_gate_bwd_args* args, void* stream) {
   return hip_status((hipError_t)rc, "trimul_gate_bwd");
 }
 
+int64_t gnn_trimul_proj_bwd_partials(int64_t rows) { return trimul_proj_bwd_partials(rows); }
+
+int gnn_trimul_proj_bwd(const gnn_trimul_proj_bwd_args* args, void* stream) {
+  if (!args) return set_error(GNN_ERR_ARG, "trimul_proj_bwd: args is NULL");
+  const gnn_trimul_proj_bwd_args& a = *args;
+  if (!a.x || !a.p_in_w || !a.g_in_w || !a.d_ab || !a.d_p || !a.d_g || !a.z || !a.partial)
+    return set_error(GNN_ERR_ARG, "trimul_proj_bwd: x, p_in_w, g_in_w, d_ab, d_p, d_g, z and partial are required");
+  if (a.rows < 1 || a.C < 1 || a.Ch < 1)
+    return set_error(GNN_ERR_ARG, "trimul_proj_bwd: rows, C and c_hidden must be positive");
+  if (a.x_ld < a.C || a.dab_ld < 2 * a.Ch || a.dl_ld < 2 * a.Ch || a.mask_stride < 0)
+    return set_error(GNN_ERR_ARG, "trimul_proj_bwd: a row stride is smaller than its row");
+  const int64_t st[3] = {a.x_ld, a.dab_ld, a.dl_ld};
+  for (int64_t v : st)
+    if ((v * 2) % 16 != 0) return set_error(GNN_ERR_ARG, "trimul_proj_bwd: rows must be 16-byte aligned");
+  const void* ptr[6] = {a.x, a.d_ab, a.d_p, a.d_g, a.z, a.p_in_w};
+  for (const void* q : ptr)
+    if (!aligned(q, 16)) return set_error(GNN_ERR_ARG, "trimul_proj_bwd: tensors must be 16-byte aligned");
+  if (!aligned(a.g_in_w, 16)) return set_error(GNN_ERR_ARG, "trimul_proj_bwd: tensors must be 16-byte aligned");
+  int rc = trimul_proj_bwd(a, (hipStream_t)stream);
+  if (rc < 0) return rc;
+  return hip_status((hipError_t)rc, "trimul_proj_bwd");
+}
+
 int gnn_trimul_contract_bwd(const gnn_trimul_contract_bwd_args* args, void* stream) {
   if (!args) return set_error(GNN_ERR_ARG, "trimul_contract_bwd: args is NULL");
   const gnn_trimul_contract_bwd_args& a = *args;

@@ -50,6 +50,8 @@ int64_t layernorm_partials(int64_t rows, int64_t K);
 int layernorm_rows(const gnn_layernorm_args& a, hipStream_t stream);
 int64_t gate_bwd_partials(int64_t rows, int64_t K);
 int gate_bwd(const gnn_gate_bwd_args& a, hipStream_t stream);
+int64_t trimul_proj_bwd_partials(int64_t rows);
+int trimul_proj_bwd(const gnn_trimul_proj_bwd_args& a, hipStream_t stream);
 int trimul_contract_bwd(const gnn_trimul_contract_bwd_args& a, hipStream_t stream);
 int trimul_relayout(const gnn_trimul_relayout_args& a, hipStream_t stream);
 

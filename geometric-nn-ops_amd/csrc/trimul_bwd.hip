@@ -234,8 +234,10 @@ __global__ __launch_bounds__(GB_THREADS) void gate_bwd_kernel(const gnn_gate_bwd
     f32x8 dv, dg;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      // sigmoid with the hardware exp2 and reciprocal, as the forward's gates
-      const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gp[e] * -1.4426950408889634f));
+      // sigmoid with the hardware exp2 and reciprocal, as the forward's gates (or the saved
+      // gate itself)
+      const float s = a.gate_is_sigmoid ? gp[e]
+                                        : __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gp[e] * -1.4426950408889634f));
       const float gm = gr[e] * m;
       dv[e] = gm * s;
       dg[e] = gm * v[e] * s * (1.0f - s);
@@ -283,12 +285,278 @@ int launch_gate(const gnn_gate_bwd_args& a, hipStream_t st) {
   return (int)hipGetLastError();
 }
 
+// ---- the input side of the backward in one pass (16-bit, C = CK in {64, 128}) -----------
+// Per 64-pixel tile: LN_in of the tile's x rows (fp32 statistics, two barriers, the partials
+// merged as in the forward's projection kernel), z rounded to T, written to z and kept in LDS;
+// wave w owns the 32 stacked channels 32 w .. 32 w + 31 of p_in and g_in (2 Ch <= 256, their
+// weight fragments in registers for the whole launch) and recomputes p and g for the tile's two
+// 32-pixel halves on MFMA as [channel][pixel] blocks (A = the weights, B = z), so that a lane
+// holds one pixel and 4 consecutive channels per register group: d_ab is read and d_p / d_g
+// written 8 bytes at a time straight from the accumulators, each pixel row's 64 bytes per wave
+// covered by its two lanes. The next tile's x is requested before the current tile's MFMAs.
+// The per-channel sums of the stored d_p / d_g stay in registers until the workgroup ends.
+constexpr int PB_W = 8;              // waves
+constexpr int PB_NT = 64 * PB_W;     // threads
+constexpr int PB_TP = 64;            // pixels per tile
+constexpr int PB_MAX_GRID = 512;     // partial rows of the bias gradients
+
+template <typename T, int CK>
+struct PbLds {
+  static constexpr int ZR = CK + (int)(16 / sizeof(T));  // z row pitch (elements)
+  static constexpr size_t zs = 0;
+  static constexpr size_t red = zs + (size_t)PB_TP * ZR * sizeof(T);
+  static constexpr size_t lnw = red + 8 * (size_t)PB_TP * 8;
+  static constexpr size_t lnb = lnw + CK * 4;
+  static constexpr size_t bias = lnb + CK * 4;  // [2][256]: p_in, g_in biases
+  static constexpr size_t mk = bias + 2 * 256 * 4;
+  static constexpr size_t total = mk + PB_TP * 4;
+};
+
+template <typename T, int CK>
+__global__ __launch_bounds__(PB_NT, 1) void trimul_proj_bwd_kernel(const gnn_trimul_proj_bwd_args a) {
+  typedef PbLds<T, CK> S;
+  typedef typename TypeOps<T>::V8 V8;
+  typedef typename TypeOps<T>::V4 V4;
+  constexpr int XM = CK / 64, NK = CK / 16, ZR = S::ZR;
+  __shared__ __align__(16) unsigned char smem[S::total];
+  T* zs = reinterpret_cast<T*>(smem + S::zs);
+  float2* red = reinterpret_cast<float2*>(smem + S::red);
+  float* lnw = reinterpret_cast<float*>(smem + S::lnw);
+  float* lnb = reinterpret_cast<float*>(smem + S::lnb);
+  float* bias = reinterpret_cast<float*>(smem + S::bias);
+  float* mk = reinterpret_cast<float*>(smem + S::mk);
+  const int64_t rows = a.rows;
+  const int Ch2 = 2 * (int)a.Ch;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
+  const int64_t ntiles = (rows + PB_TP - 1) / PB_TP;
+
+  for (int c = tid; c < CK; c += PB_NT) {
+    lnw[c] = a.ln_w ? TypeOps<T>::to_f32(((const T*)a.ln_w)[c]) : 1.f;
+    lnb[c] = a.ln_b ? TypeOps<T>::to_f32(((const T*)a.ln_b)[c]) : 0.f;
+  }
+  for (int c = tid; c < Ch2; c += PB_NT) {
+    bias[c] = a.p_in_b ? TypeOps<T>::to_f32(((const T*)a.p_in_b)[c]) : 0.f;
+    bias[256 + c] = a.g_in_b ? TypeOps<T>::to_f32(((const T*)a.g_in_b)[c]) : 0.f;
+  }
+  // this wave's channels: A fragments, row = channel 32 wave + l32, k = 16 kk + 8 g + e
+  const bool has_unit = 32 * wave < Ch2;  // uniform over the wave
+  V8 wpf[NK], wgf[NK];
+  {
+    const int ch = has_unit ? 32 * wave + l32 : 0;
+    const T* wprow = (const T*)a.p_in_w + (int64_t)ch * CK + 8 * g;
+    const T* wgrow = (const T*)a.g_in_w + (int64_t)ch * CK + 8 * g;
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+      wpf[k] = load8(wprow + 16 * k);
+      wgf[k] = load8(wgrow + 16 * k);
+    }
+  }
+  float sp[16], sg[16];  // sums of the stored d_p / d_g, channel 32 wave + 8 (i / 4) + 4 g + i % 4
+#pragma unroll
+  for (int i = 0; i < 16; ++i) sp[i] = sg[i] = 0.f;
+
+  // ---- tile load + LayerNorm: thread = (pixel xpl, part xpart) holding chunks xpart + 8j;
+  // rows past the end read the last row (in bounds; never stored)
+  const int xpl = tid >> 3, xpart = tid & 7;
+  V8 xr[XM];
+  T mraw = TypeOps<T>::from_f32(1.f);
+  auto load_x = [&](int64_t t) {
+    const int64_t r = min(t * PB_TP + xpl, rows - 1);
+    const T* src = (const T*)a.x + r * a.x_ld;
+#pragma unroll
+    for (int j = 0; j < XM; ++j) xr[j] = load8(src + 8 * (xpart + 8 * j));
+    if (a.mask && tid < PB_TP) mraw = ((const T*)a.mask)[min(t * PB_TP + tid, rows - 1) * a.mask_stride];
+  };
+  auto ln_partial = [&]() {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < XM; ++j) {
+      const f32x8 v = TypeOps<T>::to_f32(xr[j]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += v[e];
+    }
+    const float mean = s * (1.0f / (8 * XM));
+    float m2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < XM; ++j) {
+      const f32x8 v = TypeOps<T>::to_f32(xr[j]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = v[e] - mean;
+        m2 += d * d;
+      }
+    }
+    red[xpart * PB_TP + xpl] = make_float2(mean, m2);
+  };
+  auto ln_finish = [&](int64_t t) {
+    float mean = 0.f;
+    float2 pr[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pr[j] = red[j * PB_TP + xpl];
+      mean += pr[j].x;
+    }
+    mean *= 0.125f;  // every part holds 8 * XM channels
+    float m2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float d = pr[j].x - mean;
+      m2 += pr[j].y + (float)(8 * XM) * d * d;
+    }
+    const float rstd = 1.0f / sqrtf(m2 * (1.0f / CK) + a.eps);
+    const int64_t r = t * PB_TP + xpl;
+#pragma unroll
+    for (int j = 0; j < XM; ++j) {
+      const int ci = xpart + 8 * j;
+      const f32x8 v = TypeOps<T>::to_f32(xr[j]);
+      f32x8 y;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = (v[e] - mean) * rstd * lnw[8 * ci + e] + lnb[8 * ci + e];
+      const V8 yr = TypeOps<T>::from_f32(y);
+      store8(&zs[xpl * ZR + 8 * ci], yr);
+      if (r < rows) store8((T*)a.z + r * CK + 8 * ci, yr);
+    }
+    if (tid < PB_TP) mk[tid] = TypeOps<T>::to_f32(mraw);
+  };
+
+  // d_ab of a tile: this lane's pixel of each 32-pixel half, channels 32 wave + 8 rg + 4 g
+  // .. + 3; requested a tile ahead, with the next tile's x
+  V4 dac[PB_TP / 32][4], dan[PB_TP / 32][4];
+  auto load_d = [&](int64_t t, V4 (&d)[PB_TP / 32][4]) {
+    if (!has_unit) return;
+#pragma unroll
+    for (int s = 0; s < PB_TP / 32; ++s) {
+      const int64_t rr = min(t * PB_TP + 32 * s + l32, rows - 1);
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) d[s][rg] = load4((const T*)a.d_ab + rr * a.dab_ld + 32 * wave + 8 * rg + 4 * g);
+    }
+  };
+
+  auto compute = [&](int64_t t) {
+    if (!has_unit) return;
+#pragma unroll
+    for (int s = 0; s < PB_TP / 32; ++s) {
+      const int64_t row = t * PB_TP + 32 * s + l32;
+      const bool rok = row < rows;
+      const V4 (&da)[4] = dac[s];
+      f32x16 accp, accg;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) accp[i] = accg[i] = 0.f;
+#pragma unroll
+      for (int k = 0; k < NK; ++k) {
+        const V8 zf = load8(&zs[(32 * s + l32) * ZR + 16 * k + 8 * g]);
+        Mma<T, PREC_NATIVE>::step(accp, wpf[k], zf);
+        Mma<T, PREC_NATIVE>::step(accg, wgf[k], zf);
+      }
+      const float m = mk[32 * s + l32];
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int c0 = 32 * wave + 8 * rg + 4 * g;
+        const f32x4 bp = *reinterpret_cast<const f32x4*>(&bias[c0]);
+        const f32x4 bg = *reinterpret_cast<const f32x4*>(&bias[256 + c0]);
+        const f32x4 d = TypeOps<T>::to_f32(da[rg]);
+        f32x4 dp, dg;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          // p and g rounded to T, as the linear layers' outputs are
+          const float p = TypeOps<T>::to_f32(TypeOps<T>::from_f32(accp[4 * rg + e] + bp[e]));
+          const float gg = TypeOps<T>::to_f32(TypeOps<T>::from_f32(accg[4 * rg + e] + bg[e]));
+          const float sgm = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(gg * -1.4426950408889634f));
+          const float gm = d[e] * m;
+          dp[e] = gm * sgm;
+          dg[e] = gm * p * sgm * (1.0f - sgm);
+        }
+        const V4 dpr = TypeOps<T>::from_f32(dp), dgr = TypeOps<T>::from_f32(dg);
+        if (rok) {
+          store4((T*)a.d_p + row * a.dl_ld + c0, dpr);
+          store4((T*)a.d_g + row * a.dl_ld + c0, dgr);
+          const f32x4 dpf = TypeOps<T>::to_f32(dpr), dgf = TypeOps<T>::to_f32(dgr);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            sp[4 * rg + e] += dpf[e];
+            sg[4 * rg + e] += dgf[e];
+          }
+        }
+      }
+    }
+  };
+
+  int64_t t = blockIdx.x;
+  if (t < ntiles) {
+    load_x(t);
+    load_d(t, dac);
+    ln_partial();
+    __syncthreads();  // partials, LayerNorm parameters and biases published
+    ln_finish(t);
+    __syncthreads();
+    for (; t < ntiles; t += gridDim.x) {
+      const int64_t tn = t + gridDim.x;
+      const bool has_next = tn < ntiles;  // uniform over the workgroup
+      if (has_next) {
+        load_x(tn);
+        load_d(tn, dan);
+      }
+      compute(t);
+#pragma unroll
+      for (int s = 0; s < PB_TP / 32; ++s)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) dac[s][rg] = dan[s][rg];
+      if (has_next) ln_partial();
+      __syncthreads();  // z / mask of this tile consumed, partials of the next one published
+      if (has_next) ln_finish(tn);
+      __syncthreads();
+    }
+  }
+  // ---- the workgroup's column sums: over the 32 lanes of each lane group (their pixels)
+  if (has_unit) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) {
+        sp[i] += __shfl_xor(sp[i], o);
+        sg[i] += __shfl_xor(sg[i], o);
+      }
+    }
+    if (l32 == 0) {
+      float* prow = a.partial + (int64_t)blockIdx.x * 2 * Ch2;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int c = 32 * wave + 8 * (i / 4) + 4 * g + (i % 4);
+        prow[c] = sp[i];
+        prow[Ch2 + c] = sg[i];
+      }
+    }
+  }
+}
+
+template <typename T, int CK>
+int launch_proj_bwd(const gnn_trimul_proj_bwd_args& a, hipStream_t st) {
+  const int64_t grid = trimul_proj_bwd_partials(a.rows);
+  hipLaunchKernelGGL((trimul_proj_bwd_kernel<T, CK>), dim3((uint32_t)grid), dim3(PB_NT), 0, st, a);
+  return (int)hipGetLastError();
+}
+
 }  // namespace
 
 int64_t gate_bwd_partials(int64_t rows, int64_t K) {
   if (K < 8 || K % 8 != 0 || GB_THREADS % (K / 8) != 0) return 0;
   const int64_t want = (rows * (K / 8) + GB_THREADS - 1) / GB_THREADS;
   return want < 1 ? 1 : (want > GB_MAX_GRID ? GB_MAX_GRID : want);
+}
+
+int64_t trimul_proj_bwd_partials(int64_t rows) {
+  const int64_t t = (rows + PB_TP - 1) / PB_TP;
+  return t < 1 ? 1 : (t > PB_MAX_GRID ? PB_MAX_GRID : t);
+}
+
+int trimul_proj_bwd(const gnn_trimul_proj_bwd_args& a, hipStream_t st) {
+  if ((a.C != 64 && a.C != 128) || a.Ch < 16 || a.Ch > 128 || (2 * a.Ch) % 32 != 0)
+    return set_error(GNN_ERR_UNSUPPORTED, "trimul_proj_bwd: C must be 64 or 128 and 2 * c_hidden a multiple of 32, at most 256");
+  switch (a.dtype) {
+    case GNN_BF16: return a.C == 128 ? launch_proj_bwd<bf16, 128>(a, st) : launch_proj_bwd<bf16, 64>(a, st);
+    case GNN_F16: return a.C == 128 ? launch_proj_bwd<f16, 128>(a, st) : launch_proj_bwd<f16, 64>(a, st);
+  }
+  return set_error(GNN_ERR_UNSUPPORTED, "trimul_proj_bwd: bf16 / fp16 only");
 }
 
 int64_t layernorm_partials(int64_t rows, int64_t K) {

@@ -216,6 +216,36 @@ class GateBwdArgs(ctypes.Structure):
         ("dv_stride", ctypes.c_int64),
         ("dg_stride", ctypes.c_int64),
         ("dtype", ctypes.c_int32),
+        ("gate_is_sigmoid", ctypes.c_int32),
+    ]
+
+
+class TrimulProjBwdArgs(ctypes.Structure):
+    """Mirror of ``gnn_trimul_proj_bwd_args``."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("ln_w", ctypes.c_void_p),
+        ("ln_b", ctypes.c_void_p),
+        ("p_in_w", ctypes.c_void_p),
+        ("p_in_b", ctypes.c_void_p),
+        ("g_in_w", ctypes.c_void_p),
+        ("g_in_b", ctypes.c_void_p),
+        ("mask", ctypes.c_void_p),
+        ("d_ab", ctypes.c_void_p),
+        ("d_p", ctypes.c_void_p),
+        ("d_g", ctypes.c_void_p),
+        ("z", ctypes.c_void_p),
+        ("partial", ctypes.c_void_p),
+        ("rows", ctypes.c_int64),
+        ("C", ctypes.c_int64),
+        ("Ch", ctypes.c_int64),
+        ("x_ld", ctypes.c_int64),
+        ("dab_ld", ctypes.c_int64),
+        ("dl_ld", ctypes.c_int64),
+        ("mask_stride", ctypes.c_int64),
+        ("eps", ctypes.c_float),
+        ("dtype", ctypes.c_int32),
     ]
 
 
@@ -279,6 +309,8 @@ _SIGNATURES = {
     "gnn_layernorm_rows": (ctypes.c_int, [ctypes.POINTER(LayerNormArgs), ctypes.c_void_p]),
     "gnn_gate_bwd_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int64]),
     "gnn_trimul_gate_bwd": (ctypes.c_int, [ctypes.POINTER(GateBwdArgs), ctypes.c_void_p]),
+    "gnn_trimul_proj_bwd_partials": (ctypes.c_int64, [ctypes.c_int64]),
+    "gnn_trimul_proj_bwd": (ctypes.c_int, [ctypes.POINTER(TrimulProjBwdArgs), ctypes.c_void_p]),
     "gnn_trimul_contract_bwd": (ctypes.c_int, [ctypes.POINTER(TrimulContractBwdArgs), ctypes.c_void_p]),
     "gnn_trimul_relayout": (ctypes.c_int, [ctypes.POINTER(TrimulRelayoutArgs), ctypes.c_void_p]),
     "gnn_last_error": (ctypes.c_char_p, []),

@@ -266,12 +266,14 @@ def layernorm_rows_hip(x2d, weight=None, bias=None, eps=1e-5, *, dy=None, partia
     return out, sums[0], sums[1]
 
 
-def gate_bwd_hip(grad, value, gate_pre, mask_rows=None, *, d_value=None, d_gate_pre=None, sums=False):
+def gate_bwd_hip(grad, value, gate_pre, mask_rows=None, *, d_value=None, d_gate_pre=None, sums=False,
+                 gate_is_sigmoid=False):
     """Backward of ``value * sigmoid(gate_pre) * mask_rows[:, None]`` for ``[R, K]`` row
     views (columns contiguous); writes into ``d_value`` / ``d_gate_pre`` (allocated when
     None) and returns them, followed with ``sums`` by their fp32 column sums (the bias
     gradients of the layers behind value and gate_pre), from the kernel's per-workgroup
-    partial rows where K allows it."""
+    partial rows where K allows it. With ``gate_is_sigmoid`` the third operand is the saved
+    ``sigmoid(gate_pre)`` itself."""
     lib = _lib.load()
     R, K = grad.shape
     if d_value is None:
@@ -290,6 +292,7 @@ def gate_bwd_hip(grad, value, gate_pre, mask_rows=None, *, d_value=None, d_gate_
     a.grad_stride, a.value_stride, a.gate_stride = grad.stride(0), value.stride(0), gate_pre.stride(0)
     a.dv_stride, a.dg_stride = d_value.stride(0), d_gate_pre.stride(0)
     a.dtype = _lib.DTYPE_CODE[grad.dtype]
+    a.gate_is_sigmoid = int(gate_is_sigmoid)
     _lib.call("gnn_trimul_gate_bwd", a, grad.device)
     if not sums:
         return d_value, d_gate_pre
@@ -297,6 +300,38 @@ def gate_bwd_hip(grad, value, gate_pre, mask_rows=None, *, d_value=None, d_gate_
         colsum = part.sum(0)
         return d_value, d_gate_pre, colsum[0], colsum[1]
     return (d_value, d_gate_pre, d_value.sum(0, dtype=torch.float32), d_gate_pre.sum(0, dtype=torch.float32))
+
+
+def proj_bwd_supported(dtype, C, Ch):
+    """Whether gnn_trimul_proj_bwd covers these widths (16-bit, C in {64, 128}, 2 Ch <= 256)."""
+    return dtype in (torch.bfloat16, torch.float16) and C in (64, 128) and 16 <= Ch <= 128 and (2 * Ch) % 32 == 0
+
+
+def proj_bwd_hip(xk, w, mask_rows, dab, d_p, d_g, eps):
+    """gnn_trimul_proj_bwd: z = LN_in(x) and the backward of a|b = p * sigmoid(g) * mask
+    with p / g recomputed on the fly; writes ``d_p`` / ``d_g`` (row views) and returns
+    ``(z, p_in bias gradient, g_in bias gradient)``, the latter two fp32."""
+    lib = _lib.load()
+    M, C = xk.shape
+    Ch = w["p_in_weight"].shape[0] // 2
+    z = torch.empty((M, C), device=xk.device, dtype=xk.dtype)
+    part = torch.empty((lib.gnn_trimul_proj_bwd_partials(M), 2, 2 * Ch), device=xk.device, dtype=torch.float32)
+    w = {k: (None if v is None else _kernel_ready(v, xk)) for k, v in w.items()}
+    a = _lib.TrimulProjBwdArgs()
+    a.x, a.z, a.partial = xk.data_ptr(), z.data_ptr(), part.data_ptr()
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    a.ln_w, a.ln_b = ptr(w.get("norm_in_weight")), ptr(w.get("norm_in_bias"))
+    a.p_in_w, a.p_in_b = w["p_in_weight"].data_ptr(), ptr(w.get("p_in_bias"))
+    a.g_in_w, a.g_in_b = w["g_in_weight"].data_ptr(), ptr(w.get("g_in_bias"))
+    if mask_rows is not None:
+        a.mask, a.mask_stride = mask_rows.data_ptr(), mask_rows.stride(0)
+    a.d_ab, a.d_p, a.d_g = dab.data_ptr(), d_p.data_ptr(), d_g.data_ptr()
+    a.rows, a.C, a.Ch = M, C, Ch
+    a.x_ld, a.dab_ld, a.dl_ld = xk.stride(0), dab.stride(0), d_p.stride(0)
+    a.eps, a.dtype = float(eps), _lib.DTYPE_CODE[xk.dtype]
+    _lib.call("gnn_trimul_proj_bwd", a, xk.device)
+    sums = part.sum(0)
+    return z, sums[0], sums[1]
 
 
 def _wgrad(d, t, slices=64):
@@ -358,9 +393,14 @@ def contract_bwd_hip(workspace, offsets, do_pm, B, Ch, N):
     return da, db
 
 
-def trimul_bwd_hip(x, direction, mask, eps, weights, workspace, offsets, dout):
+def trimul_bwd_hip(x, direction, mask, eps, weights, workspace, offsets, dout, gate=None, fused=None):
     """Gradients ``(dx, {weight name: grad or None})`` of the triangle multiplicative update
-    given the forward's ``workspace`` / ``offsets`` (a, b, g, o) and the output gradient."""
+    given the forward's ``workspace`` / ``offsets`` (a, b, o), its output gate ``gate``
+    (sigmoid(g_out(z)), or None) and the output gradient. With the saved gate, 16-bit inputs
+    and widths gnn_trimul_proj_bwd covers (``fused`` None or True), the input side runs as
+    that one kernel: the output gate's backward uses the saved gate, and z, the recomputed
+    input projections and their gate backward never pass through a [M, 4 Ch + C] tensor;
+    otherwise LN_in(x) and the three input projections are recomputed as one linear."""
     outgoing = is_outgoing(direction)
     N, C = x.shape[-2], x.shape[-1]
     lead = x.shape[:-3]
@@ -375,15 +415,21 @@ def trimul_bwd_hip(x, direction, mask, eps, weights, workspace, offsets, dout):
     def zeros_or(t, n):
         return t if t is not None else torch.zeros(n, device=dev, dtype=dt)
 
+    use_fused = gate is not None and proj_bwd_supported(dt, C, Ch) and fused is not False
+    if fused and not use_fused:
+        raise ValueError("trimul_bwd_hip: the fused input-side backward does not cover this call")
     xk = _aligned(x.reshape(M, C))
     dout2 = _aligned(dout.reshape(M, C).to(dt))
-    z = layernorm_rows_hip(xk, w["norm_in_weight"], w["norm_in_bias"], eps)
     # the three projections of z as one linear: [p_in (2 Ch); g_in (2 Ch); g_out (C)]
     wcat = torch.cat([w["p_in_weight"], w["g_in_weight"], w["g_out_weight"]], 0)
-    bcat = torch.cat([zeros_or(w["p_in_bias"], 2 * Ch), zeros_or(w["g_in_bias"], 2 * Ch),
-                      zeros_or(w["g_out_bias"], C)])
-    lin = torch.nn.functional.linear(z, wcat, bcat)  # [M, 4 Ch + C]
-    p, gpre, gopre = lin[:, :2 * Ch], lin[:, 2 * Ch:4 * Ch], lin[:, 4 * Ch:]
+    if use_fused:
+        gate_pm = _aligned(gate.reshape(M, C))
+    else:
+        z = layernorm_rows_hip(xk, w["norm_in_weight"], w["norm_in_bias"], eps)
+        bcat = torch.cat([zeros_or(w["p_in_bias"], 2 * Ch), zeros_or(w["g_in_bias"], 2 * Ch),
+                          zeros_or(w["g_out_bias"], C)])
+        lin = torch.nn.functional.linear(z, wcat, bcat)  # [M, 4 Ch + C]
+        p, gpre, gopre = lin[:, :2 * Ch], lin[:, 2 * Ch:4 * Ch], lin[:, 4 * Ch:]
     # output stage: out = p_out(LN_out(o)) * sigmoid(gopre)
     o_cm = workspace[offsets[3]:offsets[3] + B * Ch * N * NP * x.element_size()].view(dt).view(B, Ch, N, NP)
     if x.element_size() == 2:
@@ -394,7 +440,11 @@ def trimul_bwd_hip(x, direction, mask, eps, weights, workspace, offsets, dout):
     on = layernorm_rows_hip(o_pm, w["norm_out_weight"], w["norm_out_bias"], eps)
     y = torch.nn.functional.linear(on, w["p_out_weight"], w["p_out_bias"])
     dlin = torch.empty((M, 4 * Ch + C), device=dev, dtype=dt)
-    dy, _, db_pout, db_gout = gate_bwd_hip(dout2, y, gopre, d_gate_pre=dlin[:, 4 * Ch:], sums=True)
+    if use_fused:  # torch's sigmoid backward reads the saved output as well
+        dy, _, db_pout, db_gout = gate_bwd_hip(dout2, y, gate_pm, d_gate_pre=dlin[:, 4 * Ch:], sums=True,
+                                               gate_is_sigmoid=True)
+    else:
+        dy, _, db_pout, db_gout = gate_bwd_hip(dout2, y, gopre, d_gate_pre=dlin[:, 4 * Ch:], sums=True)
     grads = {}
     grads["p_out_weight"] = _wgrad(dy, on)
     grads["p_out_bias"] = db_pout
@@ -423,8 +473,11 @@ def trimul_bwd_hip(x, direction, mask, eps, weights, workspace, offsets, dout):
     m_rows = None
     if mask is not None:
         m_rows = mask.to(device=dev, dtype=dt).expand(*x.shape[:-1]).reshape(M).contiguous()
-    _, _, db_pin, db_gin = gate_bwd_hip(dab, p, gpre, m_rows, d_value=dlin[:, :2 * Ch],
-                                        d_gate_pre=dlin[:, 2 * Ch:4 * Ch], sums=True)
+    if use_fused:
+        z, db_pin, db_gin = proj_bwd_hip(xk, w, m_rows, dab, dlin[:, :2 * Ch], dlin[:, 2 * Ch:4 * Ch], eps)
+    else:
+        _, _, db_pin, db_gin = gate_bwd_hip(dab, p, gpre, m_rows, d_value=dlin[:, :2 * Ch],
+                                            d_gate_pre=dlin[:, 2 * Ch:4 * Ch], sums=True)
     dwcat = _wgrad(dlin, z)
     dbcat = torch.cat([db_pin, db_gin, db_gout])
     grads["p_in_weight"], grads["g_in_weight"], grads["g_out_weight"] = (

@@ -51,8 +51,10 @@ def _needs_torch_path(x: torch.Tensor, weights, mask=None) -> bool:
 class _TrimulHip(torch.autograd.Function):
     """HIP forward whose workspace (the contraction operands a, b and its output o) stays on
     the autograd graph for the HIP backward; the graph owns it, so a backward with
-    ``retain_graph=True`` can run again. The output gate, which the backward recomputes,
-    gets a buffer of its own that is released after the forward. The backward's kernels
+    ``retain_graph=True`` can run again. The output gate gets a buffer of its own, kept for
+    the backward where the fused input-side backward covers the widths (its sigmoid
+    backward reads the saved gate, as torch's does) and released after the forward
+    otherwise (the backward then recomputes it). The backward's kernels
     record no graph of their own, hence ``once_differentiable``: asking for a second
     derivative raises."""
 
@@ -61,9 +63,12 @@ class _TrimulHip(torch.autograd.Function):
         weights = dict(zip(_hip._WEIGHT_KEYS, ws))
         args, keep, out, workspace, offsets = _hip.build_args(x, direction, mask, eps, weights, separate_gate=True)
         _hip.run_stage("gnn_trimul_fwd", args, x.device)
+        gate = keep[-1]  # build_args appends the separate gate buffer last
         del keep
         ctx.direction, ctx.eps, ctx.offsets = direction, eps, offsets
         ctx.workspace = workspace
+        # the output gate is kept where the fused input-side backward will read it
+        ctx.gate = gate if _hip.proj_bwd_supported(x.dtype, x.shape[-1], weights["p_in_weight"].shape[0] // 2) else None
         ctx.mask = mask
         ctx.save_for_backward(x, *ws)
         return out.reshape(x.shape)
@@ -74,7 +79,7 @@ class _TrimulHip(torch.autograd.Function):
         x, *ws = ctx.saved_tensors
         weights = dict(zip(_hip._WEIGHT_KEYS, ws))
         dx, dw = _hip.trimul_bwd_hip(x, ctx.direction, ctx.mask, ctx.eps, weights, ctx.workspace,
-                                      ctx.offsets, dout)
+                                      ctx.offsets, dout, gate=ctx.gate)
         return (dx, None, None, None, *(dw[k] for k in _hip._WEIGHT_KEYS))
 
 

@@ -344,7 +344,9 @@ int64_t gnn_layernorm_partials(int64_t rows, int64_t K);
 int gnn_layernorm_rows(const gnn_layernorm_args* args, void* stream);
 
 /* Backward of out = value * sigmoid(gate_pre) * mask (mask per row, NULL = 1):
- *   d_value = grad * s * mask,  d_gate_pre = grad * value * mask * s * (1 - s),  s = sigmoid(gate_pre).
+ *   d_value = grad * s * mask,  d_gate_pre = grad * value * mask * s * (1 - s),  s = sigmoid(gate_pre)
+ * (with gate_is_sigmoid nonzero, gate_pre holds s itself: the forward's saved gate, which is
+ * what torch's sigmoid backward uses).
  * [rows, K] tensors by row strides (columns contiguous, rows and bases 16-byte aligned),
  * mask [rows] by mask_stride, all in `dtype`; K a multiple of 8.
  * If `partial` is set, partial[w][0][k] / partial[w][1][k] receive the sums of the stored
@@ -362,7 +364,8 @@ typedef struct gnn_gate_bwd_args {
   float* partial; /* optional fp32 [gnn_gate_bwd_partials(rows, K)][2][K] */
   int64_t rows, K;
   int64_t grad_stride, value_stride, gate_stride, mask_stride, dv_stride, dg_stride;
-  int32_t dtype; /* enum gnn_dtype */
+  int32_t dtype;           /* enum gnn_dtype */
+  int32_t gate_is_sigmoid; /* gate_pre holds sigmoid(gate_pre) */
 } gnn_gate_bwd_args;
 
 /* Replaces the sigmoid / multiply autograd nodes of the gated projections in the reference's
@@ -370,6 +373,43 @@ typedef struct gnn_gate_bwd_args {
  * and p_out(o) * sigmoid(g_out(z))); no native counterpart. */
 int64_t gnn_gate_bwd_partials(int64_t rows, int64_t K);
 int gnn_trimul_gate_bwd(const gnn_gate_bwd_args* args, void* stream);
+
+/* The input side of the trimul backward in one pass over the pixel rows (16-bit dtypes,
+ * C in {64, 128}, c_hidden <= 128): z = LN_in(x) is recomputed and written, the gated input
+ * projections p = z p_in_w^T + p_in_b and g = z g_in_w^T + g_in_b (each rounded to the dtype)
+ * are recomputed on MFMA tile by tile and never stored, and the backward of
+ * a|b = p * sigmoid(g) * mask is applied to d_ab:
+ *   d_p = d_ab * s * mask,  d_g = d_ab * p * mask * s * (1 - s),  s = sigmoid(g).
+ * Replaces, in the reference's trimul_torch backward under autograd (triangle/_reference/
+ * trimul.py:85-90), the recompute of F.layer_norm(x) and of the two input linears and the
+ * sigmoid / multiply nodes behind a and b; no native counterpart (the reference has no trimul
+ * backward kernel). Rows are pixels (any order); x [rows, C] by x_ld, mask [rows] by
+ * mask_stride (NULL = 1), d_ab [rows, 2 Ch] by dab_ld, d_p / d_g [rows, 2 Ch] by dl_ld, z
+ * [rows, C] contiguous; rows, bases and strides 16-byte aligned. partial[w][0][c] /
+ * partial[w][1][c] receive the sums of the stored d_p / d_g over the rows workgroup w
+ * handled, w < gnn_trimul_proj_bwd_partials(rows): the bias gradients of p_in and g_in are
+ * their sums over w. */
+typedef struct gnn_trimul_proj_bwd_args {
+  const void* x;
+  const void* ln_w; /* LN_in gamma [C] or NULL (ones) */
+  const void* ln_b; /* LN_in beta [C] or NULL (zeros) */
+  const void* p_in_w; /* [2 Ch, C] */
+  const void* p_in_b; /* [2 Ch] or NULL */
+  const void* g_in_w; /* [2 Ch, C] */
+  const void* g_in_b; /* [2 Ch] or NULL */
+  const void* mask;
+  const void* d_ab;
+  void* d_p;
+  void* d_g;
+  void* z;
+  float* partial; /* fp32 [gnn_trimul_proj_bwd_partials(rows)][2][2 Ch] */
+  int64_t rows, C, Ch;
+  int64_t x_ld, dab_ld, dl_ld, mask_stride;
+  float eps;
+  int32_t dtype; /* GNN_BF16 or GNN_F16 */
+} gnn_trimul_proj_bwd_args;
+int64_t gnn_trimul_proj_bwd_partials(int64_t rows);
+int gnn_trimul_proj_bwd(const gnn_trimul_proj_bwd_args* args, void* stream);
 
 /* The two N^3 products of the contraction's backward, per (batch, channel) plane p < planes
  * (16-bit dtypes):

@@ -54,6 +54,9 @@ def _c_layout():
       printf("gnn_gate_bwd_args %zu\n", sizeof(gnn_gate_bwd_args));
       printf("gnn_trimul_contract_bwd_args %zu\n", sizeof(gnn_trimul_contract_bwd_args));
       printf("gnn_apb_gate_out_args %zu\n", sizeof(gnn_apb_gate_out_args));
+      printf("gnn_trimul_proj_bwd_args %zu\n", sizeof(gnn_trimul_proj_bwd_args));
+      P(gnn_trimul_proj_bwd_args, mask) P(gnn_trimul_proj_bwd_args, partial) P(gnn_trimul_proj_bwd_args, rows)
+      P(gnn_trimul_proj_bwd_args, mask_stride) P(gnn_trimul_proj_bwd_args, eps) P(gnn_trimul_proj_bwd_args, dtype)
       P(gnn_apb_gate_out_args, o_b) P(gnn_apb_gate_out_args, out) P(gnn_apb_gate_out_args, M)
       P(gnn_apb_gate_out_args, Co) P(gnn_apb_gate_out_args, out_ld) P(gnn_apb_gate_out_args, dtype)
       P(gnn_apb_gate_out_args, precision)
@@ -62,7 +65,7 @@ def _c_layout():
       P(gnn_layernorm_args, partial) P(gnn_layernorm_args, rows) P(gnn_layernorm_args, out_stride)
       P(gnn_layernorm_args, eps) P(gnn_layernorm_args, dtype)
       P(gnn_gate_bwd_args, d_gate_pre) P(gnn_gate_bwd_args, partial) P(gnn_gate_bwd_args, rows) P(gnn_gate_bwd_args, mask_stride)
-      P(gnn_gate_bwd_args, dg_stride) P(gnn_gate_bwd_args, dtype)
+      P(gnn_gate_bwd_args, dg_stride) P(gnn_gate_bwd_args, dtype) P(gnn_gate_bwd_args, gate_is_sigmoid)
       P(gnn_triattn_args, lse) P(gnn_triattn_args, row_max) P(gnn_triattn_args, D) P(gnn_triattn_args, bias_stride)
       P(gnn_triattn_args, mask_stride) P(gnn_triattn_args, scale) P(gnn_triattn_args, precision)
       P(gnn_trimul_args, mask_stride) P(gnn_trimul_args, workspace_bytes) P(gnn_trimul_args, Ch)
@@ -92,11 +95,12 @@ def test_ctypes_structs_match_c_layout(tmp_path):
     assert int(lines["gnn_gate_bwd_args"]) == ctypes.sizeof(_lib.GateBwdArgs)
     assert int(lines["gnn_trimul_contract_bwd_args"]) == ctypes.sizeof(_lib.TrimulContractBwdArgs)
     assert int(lines["gnn_apb_gate_out_args"]) == ctypes.sizeof(_lib.ApbGateOutArgs)
+    assert int(lines["gnn_trimul_proj_bwd_args"]) == ctypes.sizeof(_lib.TrimulProjBwdArgs)
     classes = {"gnn_triattn_args": _lib.TriAttnArgs, "gnn_trimul_args": _lib.TrimulArgs,
                "gnn_pair_bias_args": _lib.PairBiasArgs, "gnn_triattn_bwd_args": _lib.TriAttnBwdArgs,
                "gnn_layernorm_args": _lib.LayerNormArgs, "gnn_gate_bwd_args": _lib.GateBwdArgs,
                "gnn_trimul_contract_bwd_args": _lib.TrimulContractBwdArgs,
-               "gnn_apb_gate_out_args": _lib.ApbGateOutArgs}
+               "gnn_apb_gate_out_args": _lib.ApbGateOutArgs, "gnn_trimul_proj_bwd_args": _lib.TrimulProjBwdArgs}
     for key, val in lines.items():
         if "." not in key:
             continue
@@ -318,6 +322,27 @@ def test_trimul_backward_helper_argument_errors():
     g.grad_stride = g.value_stride = g.gate_stride = g.dv_stride = g.dg_stride = 16
     assert lib.gnn_trimul_gate_bwd(ctypes.byref(g), None) == _lib.GNN_ERR_UNSUPPORTED
     assert b"multiple of 8" in lib.gnn_last_error()
+
+    assert lib.gnn_trimul_proj_bwd(None, None) == _lib.GNN_ERR_ARG
+    pb = _lib.TrimulProjBwdArgs()
+    assert lib.gnn_trimul_proj_bwd(ctypes.byref(pb), None) == _lib.GNN_ERR_ARG
+    assert b"required" in lib.gnn_last_error()
+    pb.x = pb.p_in_w = pb.g_in_w = pb.d_ab = pb.d_p = pb.d_g = pb.z = pb.partial = 4096
+    pb.rows, pb.C, pb.Ch = 100, 128, 64
+    pb.x_ld, pb.dab_ld, pb.dl_ld = 128, 100, 384  # d_ab rows shorter than 2 c_hidden
+    assert lib.gnn_trimul_proj_bwd(ctypes.byref(pb), None) == _lib.GNN_ERR_ARG
+    assert b"stride" in lib.gnn_last_error()
+    pb.dab_ld, pb.d_g = 128, 4100
+    assert lib.gnn_trimul_proj_bwd(ctypes.byref(pb), None) == _lib.GNN_ERR_ARG
+    assert b"aligned" in lib.gnn_last_error()
+    pb.d_g, pb.dtype = 4096, _lib.GNN_F32
+    assert lib.gnn_trimul_proj_bwd(ctypes.byref(pb), None) == _lib.GNN_ERR_UNSUPPORTED
+    assert b"bf16 / fp16" in lib.gnn_last_error()
+    pb.dtype, pb.C, pb.x_ld = _lib.GNN_BF16, 96, 96
+    assert lib.gnn_trimul_proj_bwd(ctypes.byref(pb), None) == _lib.GNN_ERR_UNSUPPORTED
+    assert b"C must be 64 or 128" in lib.gnn_last_error()
+    assert lib.gnn_trimul_proj_bwd_partials(100) == 2
+    assert lib.gnn_trimul_proj_bwd_partials(1 << 20) == 512
 
     assert lib.gnn_trimul_contract_bwd(None, None) == _lib.GNN_ERR_ARG
     cb = _lib.TrimulContractBwdArgs()

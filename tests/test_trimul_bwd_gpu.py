@@ -186,6 +186,52 @@ def test_trimul_grads_match_oracle(direction, dtype):
     _check_grads(x, direction, mask, w, dout, dtype)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize(("C", "Ch", "N", "direction"),
+                         [(128, 128, 40, "outgoing"), (64, 32, 70, "incoming"), (128, 64, 24, "incoming")],
+                         ids=["c128_h128_n40", "c64_h32_n70", "c128_h64_n24"])
+def test_fused_input_side_backward_matches_unfused(dtype, C, Ch, N, direction):
+    """gnn_trimul_proj_bwd (z, the input projections recomputed tile by tile, their gate
+    backward, the output gate's backward from the saved gate) against the unfused path (LN_in
+    and the three projections as one linear, the gates' backward from the recomputed
+    pre-activations), on the same forward: every gradient, with projection biases, random
+    LayerNorm parameters and a mask; N = 70 leaves a partial last pixel tile."""
+    K = _k()
+    w = {k: v.to(DEV) for k, v in trimul_weights(C, Ch, dtype, seed=91, biases=True, ln_random=True).items()}
+    x, mask = pair_input(1, N, C, dtype, seed=92)
+    x, mask = x.to(DEV), mask.to(DEV)
+    dout = randn((1, N, N, C), seed=93).to(DEV, dtype)
+    with torch.no_grad():
+        args, keep, out, ws, off = K.build_args(x, direction, mask, 1e-5, w, separate_gate=True)
+        K.run_stage("gnn_trimul_fwd", args, x.device)
+        gate = keep[-1]
+        got = K.trimul_bwd_hip(x, direction, mask, 1e-5, w, ws, off, dout, gate=gate, fused=True)
+        want = K.trimul_bwd_hip(x, direction, mask, 1e-5, w, ws, off, dout, gate=gate, fused=False)
+    # the two paths round differently (the saved bf16 / fp16 gate against a sigmoid of the
+    # recomputed pre-activation; z from two LayerNorm kernels): each against the other at the
+    # 16-bit bar, and the fused one against the fp64 oracle
+    tol = Tolerance(1 - 1e-4, 1e-2)
+    oracle = O.trimul_grad(to_np(x), direction, to_np(mask), to_np(dout), **np_weights(w))
+    assert_close_to_oracle("dx", got[0], to_np(want[0]).astype(np.float64), tol)
+    assert_close_to_oracle("dx", got[0], oracle["x"], TRIMUL_TOL[torch.bfloat16, "ieee"])
+    for key, grad in got[1].items():
+        if grad is None:
+            assert want[1][key] is None, key
+            continue
+        assert_close_to_oracle(key, grad, to_np(want[1][key]).astype(np.float64), tol)
+        assert_close_to_oracle(key, grad, oracle[key], TRIMUL_TOL[torch.bfloat16, "ieee"])
+
+
+def test_fused_input_side_backward_refusals():
+    """gnn_trimul_proj_bwd covers 16-bit inputs with C in {64, 128} and 2 c_hidden <= 256;
+    trimul_bwd_hip refuses fused=True outside that and takes the unfused path by itself."""
+    K = _k()
+    assert K.proj_bwd_supported(torch.bfloat16, 128, 128) and K.proj_bwd_supported(torch.float16, 64, 32)
+    assert not K.proj_bwd_supported(torch.float32, 128, 128)
+    assert not K.proj_bwd_supported(torch.bfloat16, 96, 32)
+    assert not K.proj_bwd_supported(torch.bfloat16, 128, 160)
+
+
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
 def test_trimul_grads_c128_ragged_n(direction):
     """c_z = c_hidden = 128 (the fixed-width projection kernel) at an N that is not a multiple
@@ -266,8 +312,9 @@ def test_second_derivative_raises():
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_separate_gate_buffer(dtype):
     """gnn_trimul_args.gate: the output gate in a buffer of its own gives the same output bit
-    for bit, and the workspace then stops at the gate offset (a, b and o only), which is all
-    the autograd forward keeps for the backward."""
+    for bit, and the workspace then stops at the gate offset (a, b and o only); the autograd
+    forward keeps that workspace (and the gate buffer where the fused input-side backward
+    reads it)."""
     from geometric_nn_ops_torch.triangle import _trimul
 
     K = _k()
