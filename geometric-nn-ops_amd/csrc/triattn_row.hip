@@ -97,6 +97,13 @@ constexpr int64_t ROW_HEADS_FIRST_BYTES = GNN_ROW_HEADS_FIRST_BYTES;
 constexpr bool ROW_HEAD_PAIRS = GNN_ROW_HEAD_PAIRS;
 // waves of a workgroup: 8 while two workgroups fit the CU's LDS, else 16
 constexpr size_t ROW_TWO_PER_CU_BYTES = 80 * 1024;
+// 1: 12-wave workgroups (3 per SIMD) for rows of 12 k query blocks, so that no wave idles in
+// a half-empty second round (N = 768: 24 blocks on 16 waves). Measured slower: 462 against
+// 434 us at C4 (N = 768, ragged), 494 against 470 us at N = 768 without a mask; the 16 waves
+// keep 4 per SIMD through the first round, which outweighs the idle half of the second.
+#ifndef GNN_ROW_W12
+#define GNN_ROW_W12 0
+#endif
 constexpr int ROW_MAX_TILES = (GNN_ROW_MAX_N + KT - 1) / KT;
 
 struct RowHdr {
@@ -672,11 +679,19 @@ int launch_row(const gnn_triattn_args& a, hipStream_t stream) {
                        (T*)a.workspace, nchunks);
   }
   const size_t smem = row_smem_bytes(a.N);
+  // one workgroup per CU: 16 waves (12 with GNN_ROW_W12 where that spreads the row's 32-query
+  // blocks evenly)
+  const int64_t nqb = (a.N + 31) / 32;
+  const bool w12 = GNN_ROW_W12 && nqb % 12 == 0 && nqb % 16 != 0;
   if (a.row_max) {
-    if (smem > ROW_TWO_PER_CU_BYTES) return launch_row_nw<T, HAS_BIAS, 16, true>(a, stream, smem);
+    if (smem > ROW_TWO_PER_CU_BYTES)
+      return w12 ? launch_row_nw<T, HAS_BIAS, 12, true>(a, stream, smem)
+                 : launch_row_nw<T, HAS_BIAS, 16, true>(a, stream, smem);
     return launch_row_nw<T, HAS_BIAS, 8, true>(a, stream, smem);
   }
-  if (smem > ROW_TWO_PER_CU_BYTES) return launch_row_nw<T, HAS_BIAS, 16, false>(a, stream, smem);
+  if (smem > ROW_TWO_PER_CU_BYTES)
+    return w12 ? launch_row_nw<T, HAS_BIAS, 12, false>(a, stream, smem)
+               : launch_row_nw<T, HAS_BIAS, 16, false>(a, stream, smem);
   return launch_row_nw<T, HAS_BIAS, 8, false>(a, stream, smem);
 }
 
