@@ -224,6 +224,25 @@ int gnn_trimul_gate_bwd(const gnn_gate_bwd_args* args, void* stream) {
   return hip_status((hipError_t)rc, "trimul_gate_bwd");
 }
 
+int64_t gnn_trimul_out_bwd_partials(int64_t B, int64_t N) { return trimul_out_bwd_partials(B, N); }
+
+int gnn_trimul_out_bwd(const gnn_trimul_out_bwd_args* args, void* stream) {
+  if (!args) return set_error(GNN_ERR_ARG, "trimul_out_bwd: args is NULL");
+  const gnn_trimul_out_bwd_args& a = *args;
+  if (!a.o || !a.p_out_w || !a.gate || !a.dout || !a.on || !a.dy || !a.d_go || !a.d_o || !a.partial)
+    return set_error(GNN_ERR_ARG, "trimul_out_bwd: o, p_out_w, gate, dout, on, dy, d_go, d_o and partial are required");
+  if (a.B < 1 || a.N < 1 || a.C < 1 || a.Ch < 1)
+    return set_error(GNN_ERR_ARG, "trimul_out_bwd: B, N, C and c_hidden must be positive");
+  if (a.dgo_ld < a.C || (a.dgo_ld * 2) % 16 != 0)
+    return set_error(GNN_ERR_ARG, "trimul_out_bwd: d_go rows must cover C and be 16-byte aligned");
+  const void* ptr[9] = {a.o, a.p_out_w, a.gate, a.dout, a.on, a.dy, a.d_go, a.d_o, a.partial};
+  for (const void* q : ptr)
+    if (!aligned(q, 16)) return set_error(GNN_ERR_ARG, "trimul_out_bwd: tensors must be 16-byte aligned");
+  int rc = trimul_out_bwd(a, (hipStream_t)stream);
+  if (rc < 0) return rc;
+  return hip_status((hipError_t)rc, "trimul_out_bwd");
+}
+
 int64_t gnn_trimul_proj_bwd_partials(int64_t rows) { return trimul_proj_bwd_partials(rows); }
 
 int gnn_trimul_proj_bwd(const gnn_trimul_proj_bwd_args* args, void* stream) {

@@ -51,6 +51,8 @@ int layernorm_rows(const gnn_layernorm_args& a, hipStream_t stream);
 int64_t gate_bwd_partials(int64_t rows, int64_t K);
 int gate_bwd(const gnn_gate_bwd_args& a, hipStream_t stream);
 int64_t trimul_proj_bwd_partials(int64_t rows);
+int64_t trimul_out_bwd_partials(int64_t B, int64_t N);
+int trimul_out_bwd(const gnn_trimul_out_bwd_args& a, hipStream_t stream);
 int trimul_proj_bwd(const gnn_trimul_proj_bwd_args& a, hipStream_t stream);
 int trimul_contract_bwd(const gnn_trimul_contract_bwd_args& a, hipStream_t stream);
 int trimul_relayout(const gnn_trimul_relayout_args& a, hipStream_t stream);

@@ -536,6 +536,344 @@ int launch_proj_bwd(const gnn_trimul_proj_bwd_args& a, hipStream_t st) {
   return (int)hipGetLastError();
 }
 
+// ---- the output side of the backward in one pass (16-bit, C = CK in {64, 128}, c_hidden =
+// CHK in {32, 64, 128}) -------------------------------------------------------------------
+// Per tile of 64 consecutive pixels of one pair-grid row (the forward output stage's tiles):
+// the channel-major o tile is staged in LDS and normalised per pixel (LN_out, two-pass fp32
+// statistics over a pair of pixels per thread, as the forward), on written once (for the
+// p_out weight gradient); y = on p_out_w^T + p_out_b on MFMA as [output channel][pixel]
+// blocks (wave: 32 output channels x 32 pixels), so that a lane holds one pixel and 4
+// consecutive channels: dout and the saved gate are read, and d_go / dy written, 8 bytes at a
+// time straight from the accumulators; dy is also staged in LDS for d(on) = dy p_out_w, again
+// [channel][pixel] blocks, whose per-pixel LayerNorm reductions meet in LDS. Weight fragments
+// stay in registers for the whole launch; the column sums of dy, d_go, d(on) x^ and d(on) stay
+// in registers until the workgroup ends.
+constexpr int OB_W = 8;
+constexpr int OB_NT = 64 * OB_W;
+constexpr int OB_TP = 64;           // pixels per tile
+constexpr int OB_MAX_GRID = 512;    // partial rows of the bias / LayerNorm gradients
+
+template <typename T, int CK, int CHK>
+struct ObLds {
+  static constexpr int OR = OB_TP + (int)(16 / sizeof(T));  // o tile [CHK][OR]
+  static constexpr int ZR = CHK + (int)(16 / sizeof(T));    // on tile [OB_TP][ZR]
+  static constexpr int DR = CK + (int)(16 / sizeof(T));     // dy tile [OB_TP][DR]
+  static constexpr size_t ot = 0;
+  static constexpr size_t zs = ot + (size_t)CHK * OR * sizeof(T);
+  static constexpr size_t dys = zs + (size_t)OB_TP * ZR * sizeof(T);
+  static constexpr size_t red1 = dys + (size_t)OB_TP * DR * sizeof(T);  // [8 parts][32 pairs] f32x2 sums
+  static constexpr size_t red2 = red1 + 8 * 32 * 8;                      // ... squared deviations
+  static constexpr size_t red3 = red2 + 8 * 32 * 8;                      // [CHK / 32][OB_TP] LN-bwd sums
+  static constexpr size_t stat = red3 + (size_t)(CHK / 32) * OB_TP * 8;  // [OB_TP] (mean, rstd)
+  static constexpr size_t lnw = stat + OB_TP * 8;
+  static constexpr size_t lnb = lnw + CHK * 4;
+  static constexpr size_t bpo = lnb + CHK * 4;
+  static constexpr size_t fin = bpo + CK * 4;  // [2 halves][4][128] final column sums
+  static constexpr size_t total = fin + 2 * 4 * 128 * 4;
+};
+
+template <typename T, int CK, int CHK>
+__global__ __launch_bounds__(OB_NT, 1) void trimul_out_bwd_kernel(const gnn_trimul_out_bwd_args a) {
+  typedef ObLds<T, CK, CHK> S;
+  typedef typename TypeOps<T>::V8 V8;
+  typedef typename TypeOps<T>::V4 V4;
+  constexpr int NUY = CK / 32, NUD = CHK / 32;  // output-channel units of y and of d(on)
+  constexpr int NKY = CHK / 16, NKD = CK / 16;   // their k-steps
+  constexpr int OR = S::OR, ZR = S::ZR, DR = S::DR;
+  __shared__ __align__(16) unsigned char smem[S::total];
+  T* ot = reinterpret_cast<T*>(smem + S::ot);
+  T* zs = reinterpret_cast<T*>(smem + S::zs);
+  T* dys = reinterpret_cast<T*>(smem + S::dys);
+  float2* red1 = reinterpret_cast<float2*>(smem + S::red1);
+  float2* red2 = reinterpret_cast<float2*>(smem + S::red2);
+  float2* red3 = reinterpret_cast<float2*>(smem + S::red3);
+  float2* stat = reinterpret_cast<float2*>(smem + S::stat);
+  float* lnw = reinterpret_cast<float*>(smem + S::lnw);
+  float* lnb = reinterpret_cast<float*>(smem + S::lnb);
+  float* bpo = reinterpret_cast<float*>(smem + S::bpo);
+  float* fin = reinterpret_cast<float*>(smem + S::fin);
+  const int N = (int)a.N;
+  const int64_t NP = (a.N + 31) / 32 * 32;
+  const int ntj = (N + OB_TP - 1) / OB_TP;
+  const int64_t ntiles = a.B * a.N * ntj;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
+
+  for (int c = tid; c < CHK; c += OB_NT) {
+    lnw[c] = a.ln_w ? TypeOps<T>::to_f32(((const T*)a.ln_w)[c]) : 1.f;
+    lnb[c] = a.ln_b ? TypeOps<T>::to_f32(((const T*)a.ln_b)[c]) : 0.f;
+  }
+  for (int c = tid; c < CK; c += OB_NT) bpo[c] = a.p_out_b ? TypeOps<T>::to_f32(((const T*)a.p_out_b)[c]) : 0.f;
+
+  // y: wave = (unit uy, pixel half hy); A fragments row = output channel 32 uy + l32, k = 16 kk + 8 g + e
+  const int uy = wave % NUY, hy = wave / NUY;
+  const bool has_y = hy < 2;  // uniform over the wave
+  // d(on): wave = (unit ud, pixel half hd); A fragments row = channel 32 ud + l32, k = output channel
+  const int ud = wave % NUD, hd = wave / NUD;
+  const bool has_d = hd < 2;
+  const T* wpo = (const T*)a.p_out_w;
+  V8 wy[NKY], wd[NKD];
+#pragma unroll
+  for (int k = 0; k < NKY; ++k) wy[k] = load8(wpo + (int64_t)((has_y ? 32 * uy : 0) + l32) * CHK + 16 * k + 8 * g);
+#pragma unroll
+  for (int k = 0; k < NKD; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wd[k][e] = wpo[(int64_t)(16 * k + 8 * g + e) * CHK + (has_d ? 32 * ud : 0) + l32];
+  float s_dy[16], s_dgo[16], s_dx[16], s_db[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s_dy[i] = s_dgo[i] = s_dx[i] = s_db[i] = 0.f;
+
+  for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+    const int jt = (int)(t % ntj);
+    const int64_t rest = t / ntj;
+    const int i = (int)(rest % N);
+    const int64_t b = rest / N;
+    const int j0 = jt * OB_TP;
+    const int64_t pb = (b * N + i) * N + j0;  // the tile's first pixel
+
+    // ---- 1. the o tile [CHK][64] (columns past N zero), and this lane's dout / gate
+    constexpr int OCH = CHK * (OB_TP / 8) / OB_NT;  // 16-byte chunks per thread (0 when CHK < 64)
+#pragma unroll
+    for (int k = 0; k < (OCH > 0 ? OCH : 1); ++k) {
+      const int c = tid + k * OB_NT;
+      if (c < CHK * (OB_TP / 8)) {
+        const int ch = c / (OB_TP / 8), jj = (c % (OB_TP / 8)) * 8;
+        V8 v = zero8<T>();
+        if (j0 + jj < N) {
+          v = load8((const T*)a.o + ((b * CHK + ch) * N + i) * NP + j0 + jj);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (j0 + jj + e >= N) v[e] = TypeOps<T>::from_f32(0.f);
+        }
+        store8(&ot[ch * OR + jj], v);
+      }
+    }
+    const int pxy = 32 * hy + l32;
+    const bool vy = has_y && j0 + pxy < N;
+    const int64_t piy = pb + (vy ? pxy : 0);  // rows past N read the tile's first pixel
+    V4 dout4[4], gate4[4];
+    if (has_y) {
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int c0 = 32 * uy + 8 * rg + 4 * g;
+        dout4[rg] = load4((const T*)a.dout + piy * CK + c0);
+        gate4[rg] = load4((const T*)a.gate + piy * CK + c0);
+      }
+    }
+    __syncthreads();
+
+    // ---- 2. LN_out over the CHK channels of each pixel: thread = (pixel pair pp, part of
+    // CHK / 8 channels), threads 0 .. 255
+    typedef T T2 __attribute__((ext_vector_type(2)));
+    const int pp = tid & 31, part = (tid >> 5) & 7;
+    constexpr int KC = CHK / 8;
+    const int k0 = part * KC;
+    auto pair = [&](int k) -> f32x2 {
+      return __builtin_convertvector(*reinterpret_cast<const T2*>(&ot[k * OR + 2 * pp]), f32x2);
+    };
+    f32x2 mean = {0.f, 0.f};
+    if (tid < 256) {
+      f32x2 s2 = {0.f, 0.f};
+#pragma unroll
+      for (int k = k0; k < k0 + KC; ++k) s2 += pair(k);
+      red1[part * 32 + pp] = make_float2(s2[0], s2[1]);
+    }
+    __syncthreads();
+    f32x2 rs = {0.f, 0.f};
+    if (tid < 256) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float2 v = red1[j * 32 + pp];
+        mean += f32x2{v.x, v.y};
+      }
+      mean *= 1.0f / CHK;
+      f32x2 q2 = {0.f, 0.f};
+#pragma unroll
+      for (int k = k0; k < k0 + KC; ++k) {
+        const f32x2 d = pair(k) - mean;
+        q2 += d * d;
+      }
+      red2[part * 32 + pp] = make_float2(q2[0], q2[1]);
+    }
+    __syncthreads();
+    if (tid < 256) {
+      f32x2 var = {0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float2 v = red2[j * 32 + pp];
+        var += f32x2{v.x, v.y};
+      }
+      rs[0] = 1.0f / sqrtf(var[0] * (1.0f / CHK) + a.eps);
+      rs[1] = 1.0f / sqrtf(var[1] * (1.0f / CHK) + a.eps);
+      if (part == 0) {
+        stat[2 * pp] = make_float2(mean[0], rs[0]);
+        stat[2 * pp + 1] = make_float2(mean[1], rs[1]);
+      }
+#pragma unroll
+      for (int k = k0; k < k0 + KC; ++k) {
+        const f32x2 x = pair(k);
+        zs[(2 * pp) * ZR + k] = TypeOps<T>::from_f32((x[0] - mean[0]) * rs[0] * lnw[k] + lnb[k]);
+        zs[(2 * pp + 1) * ZR + k] = TypeOps<T>::from_f32((x[1] - mean[1]) * rs[1] * lnw[k] + lnb[k]);
+      }
+    }
+    __syncthreads();
+    // on to its pixel-major rows (16-byte chunks)
+    for (int c = tid; c < OB_TP * (CHK / 8); c += OB_NT) {
+      const int px = c / (CHK / 8), k = (c % (CHK / 8)) * 8;
+      if (j0 + px < N) store8((T*)a.on + (pb + px) * CHK + k, load8(&zs[px * ZR + k]));
+    }
+
+    // ---- 3. y and the output gate's backward
+    if (has_y) {
+      f32x16 acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+      for (int k = 0; k < NKY; ++k)
+        Mma<T, PREC_NATIVE>::step(acc, wy[k], load8(&zs[pxy * ZR + 16 * k + 8 * g]));
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int c0 = 32 * uy + 8 * rg + 4 * g;
+        const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bpo[c0]);
+        const f32x4 d4 = TypeOps<T>::to_f32(dout4[rg]), s4 = TypeOps<T>::to_f32(gate4[rg]);
+        f32x4 dy, dg;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float y = TypeOps<T>::to_f32(TypeOps<T>::from_f32(acc[4 * rg + e] + b4[e]));
+          dy[e] = d4[e] * s4[e];
+          dg[e] = d4[e] * y * s4[e] * (1.0f - s4[e]);
+        }
+        const V4 dyr = TypeOps<T>::from_f32(dy), dgr = TypeOps<T>::from_f32(dg);
+        store4(&dys[pxy * DR + c0], dyr);
+        if (vy) {
+          store4((T*)a.dy + piy * CK + c0, dyr);
+          store4((T*)a.d_go + piy * a.dgo_ld + c0, dgr);
+          const f32x4 dyf = TypeOps<T>::to_f32(dyr), dgf = TypeOps<T>::to_f32(dgr);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            s_dy[4 * rg + e] += dyf[e];
+            s_dgo[4 * rg + e] += dgf[e];
+          }
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- 4. d(on) = dy p_out_w and the LN_out backward
+    const int pxd = 32 * hd + l32;
+    const bool vd = has_d && j0 + pxd < N;
+    f32x4 donv[4];  // d(on) rounded as the linear's output; x^ is read again after the barrier
+    float2 st = make_float2(0.f, 1.f);
+    if (has_d) {
+      f32x16 acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+      for (int k = 0; k < NKD; ++k)
+        Mma<T, PREC_NATIVE>::step(acc, wd[k], load8(&dys[pxd * DR + 16 * k + 8 * g]));
+      st = stat[pxd];
+      float sg = 0.f, sgx = 0.f;
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const int c0 = 32 * ud + 8 * rg + 4 * g;
+        const f32x4 w4 = *reinterpret_cast<const f32x4*>(&lnw[c0]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float don = TypeOps<T>::to_f32(TypeOps<T>::from_f32(acc[4 * rg + e]));
+          const float x = (TypeOps<T>::to_f32(ot[(c0 + e) * OR + pxd]) - st.x) * st.y;
+          donv[rg][e] = don;
+          const float gc = don * w4[e];
+          sg += gc;
+          sgx += gc * x;
+          if (vd) {
+            s_dx[4 * rg + e] += don * x;
+            s_db[4 * rg + e] += don;
+          }
+        }
+      }
+      // the pixel's two lanes (l, l ^ 32) hold its other channels of this unit
+      sg += __shfl_xor(sg, 32);
+      sgx += __shfl_xor(sgx, 32);
+      if (g == 0) red3[ud * OB_TP + pxd] = make_float2(sg, sgx);
+    }
+    __syncthreads();
+    if (has_d) {
+      float mg = 0.f, mgx = 0.f;
+#pragma unroll
+      for (int u = 0; u < NUD; ++u) {
+        const float2 v = red3[u * OB_TP + pxd];
+        mg += v.x;
+        mgx += v.y;
+      }
+      mg *= 1.0f / CHK;
+      mgx *= 1.0f / CHK;
+      if (vd) {
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) {
+          const int c0 = 32 * ud + 8 * rg + 4 * g;
+          const f32x4 w4 = *reinterpret_cast<const f32x4*>(&lnw[c0]);
+          f32x4 dx;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float x = (TypeOps<T>::to_f32(ot[(c0 + e) * OR + pxd]) - st.x) * st.y;
+            dx[e] = st.y * (donv[rg][e] * w4[e] - mg - x * mgx);
+          }
+          store4((T*)a.d_o + (pb + pxd) * CHK + c0, TypeOps<T>::from_f32(dx));
+        }
+      }
+    }
+    __syncthreads();  // ot / zs / dys / red3 free for the next tile
+  }
+
+  // ---- the workgroup's column sums: over the 32 pixels of a lane group, then the two halves
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) {
+      s_dy[i] += __shfl_xor(s_dy[i], o);
+      s_dgo[i] += __shfl_xor(s_dgo[i], o);
+      s_dx[i] += __shfl_xor(s_dx[i], o);
+      s_db[i] += __shfl_xor(s_db[i], o);
+    }
+  }
+  for (int c = tid; c < 2 * 4 * 128; c += OB_NT) fin[c] = 0.f;
+  __syncthreads();
+  if (l32 == 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int cc = 8 * (i / 4) + 4 * g + (i % 4);
+      if (has_y) {
+        fin[(hy * 4 + 0) * 128 + 32 * uy + cc] = s_dy[i];
+        fin[(hy * 4 + 1) * 128 + 32 * uy + cc] = s_dgo[i];
+      }
+      if (has_d) {
+        fin[(hd * 4 + 2) * 128 + 32 * ud + cc] = s_dx[i];
+        fin[(hd * 4 + 3) * 128 + 32 * ud + cc] = s_db[i];
+      }
+    }
+  }
+  __syncthreads();
+  for (int c = tid; c < 4 * 128; c += OB_NT) a.partial[(int64_t)blockIdx.x * 4 * 128 + c] = fin[c] + fin[4 * 128 + c];
+}
+
+template <typename T, int CK, int CHK>
+int launch_out_bwd(const gnn_trimul_out_bwd_args& a, hipStream_t st) {
+  const int64_t grid = trimul_out_bwd_partials(a.B, a.N);
+  hipLaunchKernelGGL((trimul_out_bwd_kernel<T, CK, CHK>), dim3((uint32_t)grid), dim3(OB_NT), 0, st, a);
+  return (int)hipGetLastError();
+}
+
+template <typename T>
+int launch_out_bwd_t(const gnn_trimul_out_bwd_args& a, hipStream_t st) {
+  if (a.C == 128) {
+    if (a.Ch == 128) return launch_out_bwd<T, 128, 128>(a, st);
+    if (a.Ch == 64) return launch_out_bwd<T, 128, 64>(a, st);
+    return launch_out_bwd<T, 128, 32>(a, st);
+  }
+  if (a.Ch == 128) return launch_out_bwd<T, 64, 128>(a, st);
+  if (a.Ch == 64) return launch_out_bwd<T, 64, 64>(a, st);
+  return launch_out_bwd<T, 64, 32>(a, st);
+}
+
 }  // namespace
 
 int64_t gate_bwd_partials(int64_t rows, int64_t K) {
@@ -557,6 +895,21 @@ int trimul_proj_bwd(const gnn_trimul_proj_bwd_args& a, hipStream_t st) {
     case GNN_F16: return a.C == 128 ? launch_proj_bwd<f16, 128>(a, st) : launch_proj_bwd<f16, 64>(a, st);
   }
   return set_error(GNN_ERR_UNSUPPORTED, "trimul_proj_bwd: bf16 / fp16 only");
+}
+
+int64_t trimul_out_bwd_partials(int64_t B, int64_t N) {
+  const int64_t t = B * N * ((N + OB_TP - 1) / OB_TP);
+  return t < 1 ? 1 : (t > OB_MAX_GRID ? OB_MAX_GRID : t);
+}
+
+int trimul_out_bwd(const gnn_trimul_out_bwd_args& a, hipStream_t st) {
+  if ((a.C != 64 && a.C != 128) || (a.Ch != 32 && a.Ch != 64 && a.Ch != 128))
+    return set_error(GNN_ERR_UNSUPPORTED, "trimul_out_bwd: C must be 64 or 128 and c_hidden 32, 64 or 128");
+  switch (a.dtype) {
+    case GNN_BF16: return launch_out_bwd_t<bf16>(a, st);
+    case GNN_F16: return launch_out_bwd_t<f16>(a, st);
+  }
+  return set_error(GNN_ERR_UNSUPPORTED, "trimul_out_bwd: bf16 / fp16 only");
 }
 
 int64_t layernorm_partials(int64_t rows, int64_t K) {

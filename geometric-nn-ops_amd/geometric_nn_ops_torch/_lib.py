@@ -220,6 +220,32 @@ class GateBwdArgs(ctypes.Structure):
     ]
 
 
+class TrimulOutBwdArgs(ctypes.Structure):
+    """Mirror of ``gnn_trimul_out_bwd_args``."""
+
+    _fields_ = [
+        ("o", ctypes.c_void_p),
+        ("ln_w", ctypes.c_void_p),
+        ("ln_b", ctypes.c_void_p),
+        ("p_out_w", ctypes.c_void_p),
+        ("p_out_b", ctypes.c_void_p),
+        ("gate", ctypes.c_void_p),
+        ("dout", ctypes.c_void_p),
+        ("on", ctypes.c_void_p),
+        ("dy", ctypes.c_void_p),
+        ("d_go", ctypes.c_void_p),
+        ("d_o", ctypes.c_void_p),
+        ("partial", ctypes.c_void_p),
+        ("B", ctypes.c_int64),
+        ("N", ctypes.c_int64),
+        ("C", ctypes.c_int64),
+        ("Ch", ctypes.c_int64),
+        ("dgo_ld", ctypes.c_int64),
+        ("eps", ctypes.c_float),
+        ("dtype", ctypes.c_int32),
+    ]
+
+
 class TrimulProjBwdArgs(ctypes.Structure):
     """Mirror of ``gnn_trimul_proj_bwd_args``."""
 
@@ -310,6 +336,8 @@ _SIGNATURES = {
     "gnn_gate_bwd_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int64]),
     "gnn_trimul_gate_bwd": (ctypes.c_int, [ctypes.POINTER(GateBwdArgs), ctypes.c_void_p]),
     "gnn_trimul_proj_bwd_partials": (ctypes.c_int64, [ctypes.c_int64]),
+    "gnn_trimul_out_bwd_partials": (ctypes.c_int64, [ctypes.c_int64, ctypes.c_int64]),
+    "gnn_trimul_out_bwd": (ctypes.c_int, [ctypes.POINTER(TrimulOutBwdArgs), ctypes.c_void_p]),
     "gnn_trimul_proj_bwd": (ctypes.c_int, [ctypes.POINTER(TrimulProjBwdArgs), ctypes.c_void_p]),
     "gnn_trimul_contract_bwd": (ctypes.c_int, [ctypes.POINTER(TrimulContractBwdArgs), ctypes.c_void_p]),
     "gnn_trimul_relayout": (ctypes.c_int, [ctypes.POINTER(TrimulRelayoutArgs), ctypes.c_void_p]),

@@ -334,6 +334,39 @@ def proj_bwd_hip(xk, w, mask_rows, dab, d_p, d_g, eps):
     return z, sums[0], sums[1]
 
 
+def out_bwd_supported(dtype, C, Ch):
+    """Whether gnn_trimul_out_bwd covers these widths (16-bit, C in {64, 128}, c_hidden in {32, 64, 128})."""
+    return dtype in (torch.bfloat16, torch.float16) and C in (64, 128) and Ch in (32, 64, 128)
+
+
+def out_bwd_hip(o_cm, w, gate_pm, dout2, d_go, B, N, eps):
+    """gnn_trimul_out_bwd: from the channel-major ``o_cm`` [B, Ch, N, NP], the saved gate and
+    the output gradient (pixel-major rows), ``(on, dy, d_o, sums)`` with on = LN_out(o), dy the
+    gradient of p_out's output, d_o that of o (pixel-major) and ``sums`` [4, 128] fp32 (the
+    p_out / g_out bias and the LN_out weight / bias gradients, each from column 0); d(g_out
+    pre-activation) goes into ``d_go`` (a row view)."""
+    lib = _lib.load()
+    M, C = dout2.shape
+    Ch = o_cm.shape[1]
+    dev, dt = dout2.device, dout2.dtype
+    on = torch.empty((M, Ch), device=dev, dtype=dt)
+    dy = torch.empty((M, C), device=dev, dtype=dt)
+    d_o = torch.empty((M, Ch), device=dev, dtype=dt)
+    part = torch.empty((lib.gnn_trimul_out_bwd_partials(B, N), 4, 128), device=dev, dtype=torch.float32)
+    w = {k: (None if v is None else _kernel_ready(v, dout2)) for k, v in w.items()}
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    a = _lib.TrimulOutBwdArgs()
+    a.o, a.gate, a.dout = o_cm.data_ptr(), gate_pm.data_ptr(), dout2.data_ptr()
+    a.ln_w, a.ln_b = ptr(w.get("norm_out_weight")), ptr(w.get("norm_out_bias"))
+    a.p_out_w, a.p_out_b = w["p_out_weight"].data_ptr(), ptr(w.get("p_out_bias"))
+    a.on, a.dy, a.d_go, a.d_o, a.partial = on.data_ptr(), dy.data_ptr(), d_go.data_ptr(), d_o.data_ptr(), part.data_ptr()
+    a.B, a.N, a.C, a.Ch = B, N, C, Ch
+    a.dgo_ld = d_go.stride(0)
+    a.eps, a.dtype = float(eps), _lib.DTYPE_CODE[dt]
+    _lib.call("gnn_trimul_out_bwd", a, dev)
+    return on, dy, d_o, part.sum(0)
+
+
 def _wgrad(d, t, slices=64):
     """``d^T t`` for ``[M, O]`` / ``[M, I]`` with M in the hundreds of thousands: the sum
     over M split into batched slices (one GEMM each, summed in fp32 in slice order), since a
@@ -432,25 +465,31 @@ def trimul_bwd_hip(x, direction, mask, eps, weights, workspace, offsets, dout, g
         p, gpre, gopre = lin[:, :2 * Ch], lin[:, 2 * Ch:4 * Ch], lin[:, 4 * Ch:]
     # output stage: out = p_out(LN_out(o)) * sigmoid(gopre)
     o_cm = workspace[offsets[3]:offsets[3] + B * Ch * N * NP * x.element_size()].view(dt).view(B, Ch, N, NP)
-    if x.element_size() == 2:
-        o_pm = relayout_hip(o_cm, torch.empty((M, Ch), device=dev, dtype=dt), _lib.RELAYOUT_PLANES_TO_PIXELS,
-                            B, N, Ch, src_ld=NP, dst_ld=Ch)
-    else:
-        o_pm = o_cm[..., :N].permute(0, 2, 3, 1).reshape(M, Ch).contiguous()
-    on = layernorm_rows_hip(o_pm, w["norm_out_weight"], w["norm_out_bias"], eps)
-    y = torch.nn.functional.linear(on, w["p_out_weight"], w["p_out_bias"])
     dlin = torch.empty((M, 4 * Ch + C), device=dev, dtype=dt)
-    if use_fused:  # torch's sigmoid backward reads the saved output as well
-        dy, _, db_pout, db_gout = gate_bwd_hip(dout2, y, gate_pm, d_gate_pre=dlin[:, 4 * Ch:], sums=True,
-                                               gate_is_sigmoid=True)
-    else:
-        dy, _, db_pout, db_gout = gate_bwd_hip(dout2, y, gopre, d_gate_pre=dlin[:, 4 * Ch:], sums=True)
     grads = {}
+    if use_fused and out_bwd_supported(dt, C, Ch):
+        # the output side in one kernel, from the channel-major o and the saved gate
+        on, dy, do_pm, sums = out_bwd_hip(o_cm, w, gate_pm, dout2, dlin[:, 4 * Ch:], B, N, eps)
+        db_pout, db_gout = sums[0, :C], sums[1, :C]
+        grads["norm_out_weight"], grads["norm_out_bias"] = sums[2, :Ch], sums[3, :Ch]
+    else:
+        if x.element_size() == 2:
+            o_pm = relayout_hip(o_cm, torch.empty((M, Ch), device=dev, dtype=dt), _lib.RELAYOUT_PLANES_TO_PIXELS,
+                                B, N, Ch, src_ld=NP, dst_ld=Ch)
+        else:
+            o_pm = o_cm[..., :N].permute(0, 2, 3, 1).reshape(M, Ch).contiguous()
+        on = layernorm_rows_hip(o_pm, w["norm_out_weight"], w["norm_out_bias"], eps)
+        y = torch.nn.functional.linear(on, w["p_out_weight"], w["p_out_bias"])
+        if use_fused:  # torch's sigmoid backward reads the saved output as well
+            dy, _, db_pout, db_gout = gate_bwd_hip(dout2, y, gate_pm, d_gate_pre=dlin[:, 4 * Ch:], sums=True,
+                                                   gate_is_sigmoid=True)
+        else:
+            dy, _, db_pout, db_gout = gate_bwd_hip(dout2, y, gopre, d_gate_pre=dlin[:, 4 * Ch:], sums=True)
+        don = dy @ w["p_out_weight"]
+        do_pm, dlnw, dlnb = layernorm_rows_hip(o_pm, w["norm_out_weight"], eps=eps, dy=don, partials=True)
+        grads["norm_out_weight"], grads["norm_out_bias"] = dlnw, dlnb
     grads["p_out_weight"] = _wgrad(dy, on)
     grads["p_out_bias"] = db_pout
-    don = dy @ w["p_out_weight"]
-    do_pm, dlnw, dlnb = layernorm_rows_hip(o_pm, w["norm_out_weight"], eps=eps, dy=don, partials=True)
-    grads["norm_out_weight"], grads["norm_out_bias"] = dlnw, dlnb
     # contraction: o_c = A_c B_c^T per (batch, channel) plane; dO_c[i, j] is pixel (i, j).
     # dA / dB planes go back to the pixel layout of a / b (plane [i, k] is pixel (i, k)
     # outgoing, (k, i) incoming), into the two halves of dab.

@@ -411,6 +411,45 @@ typedef struct gnn_trimul_proj_bwd_args {
 int64_t gnn_trimul_proj_bwd_partials(int64_t rows);
 int gnn_trimul_proj_bwd(const gnn_trimul_proj_bwd_args* args, void* stream);
 
+/* The output side of the trimul backward in one pass over 64-pixel tiles of the pair grid
+ * (16-bit dtypes, C in {64, 128}, c_hidden in {32, 64, 128}): on = LN_out(o) from the
+ * forward's channel-major o, y = on p_out_w^T + p_out_b (rounded to the dtype) recomputed on
+ * MFMA, the backward of out = y * gate against the forward's saved gate,
+ *   dy = dout * gate,  d_go = dout * y * gate * (1 - gate),
+ * d(on) = dy p_out_w (rounded to the dtype) on MFMA and the LN_out backward
+ *   x^ = (o - mean) * rstd,  g = d(on) * ln_w,  d_o = rstd * (g - mean(g) - x^ * mean(g * x^)).
+ * Replaces, in the reference's trimul_torch backward under autograd (triangle/_reference/
+ * trimul.py:91-97), the recompute of F.layer_norm(o) and of the p_out linear, the sigmoid-
+ * gate / multiply nodes of the output gate, the input gradient of p_out and the LayerNorm's
+ * backward; no native counterpart. o is [B, Ch, N, NP] (NP = round_up(N, 32), the
+ * gnn_trimul_fwd workspace layout); gate, dout [B N N, C] and on, d_o [B N N, Ch] are
+ * pixel-major rows (pixel (b, i, j) at (b N + i) N + j) in the dtype, dy [B N N, C]
+ * contiguous, d_go [B N N, C] by dgo_ld (e.g. the g_out block of the input side's
+ * [M, 4 Ch + C] gradient). partial[w][k][c] (k = 0: sum of dy, 1: of d_go over column c < C;
+ * 2: of d(on) * x^, 3: of d(on) over column c < Ch) over the pixels workgroup w handled,
+ * w < gnn_trimul_out_bwd_partials(B, N): the p_out / g_out bias gradients and the LN_out
+ * weight / bias gradients are their sums over w. All pointers 16-byte aligned. */
+typedef struct gnn_trimul_out_bwd_args {
+  const void* o;
+  const void* ln_w;    /* LN_out gamma [Ch] or NULL (ones) */
+  const void* ln_b;    /* LN_out beta [Ch] or NULL (zeros) */
+  const void* p_out_w; /* [C, Ch] */
+  const void* p_out_b; /* [C] or NULL */
+  const void* gate;
+  const void* dout;
+  void* on;
+  void* dy;
+  void* d_go;
+  void* d_o;
+  float* partial; /* fp32 [gnn_trimul_out_bwd_partials(B, N)][4][128] */
+  int64_t B, N, C, Ch;
+  int64_t dgo_ld;
+  float eps;
+  int32_t dtype; /* GNN_BF16 or GNN_F16 */
+} gnn_trimul_out_bwd_args;
+int64_t gnn_trimul_out_bwd_partials(int64_t B, int64_t N);
+int gnn_trimul_out_bwd(const gnn_trimul_out_bwd_args* args, void* stream);
+
 /* The two N^3 products of the contraction's backward, per (batch, channel) plane p < planes
  * (16-bit dtypes):
  *   dA_p[i][k] = sum_j dO_p[i][j] B_p[j][k],   dB_p[j][k] = sum_i dO_p[i][j] A_p[i][k].

@@ -55,6 +55,9 @@ def _c_layout():
       printf("gnn_trimul_contract_bwd_args %zu\n", sizeof(gnn_trimul_contract_bwd_args));
       printf("gnn_apb_gate_out_args %zu\n", sizeof(gnn_apb_gate_out_args));
       printf("gnn_trimul_proj_bwd_args %zu\n", sizeof(gnn_trimul_proj_bwd_args));
+      printf("gnn_trimul_out_bwd_args %zu\n", sizeof(gnn_trimul_out_bwd_args));
+      P(gnn_trimul_out_bwd_args, gate) P(gnn_trimul_out_bwd_args, partial) P(gnn_trimul_out_bwd_args, B)
+      P(gnn_trimul_out_bwd_args, dgo_ld) P(gnn_trimul_out_bwd_args, eps) P(gnn_trimul_out_bwd_args, dtype)
       P(gnn_trimul_proj_bwd_args, mask) P(gnn_trimul_proj_bwd_args, partial) P(gnn_trimul_proj_bwd_args, rows)
       P(gnn_trimul_proj_bwd_args, mask_stride) P(gnn_trimul_proj_bwd_args, eps) P(gnn_trimul_proj_bwd_args, dtype)
       P(gnn_apb_gate_out_args, o_b) P(gnn_apb_gate_out_args, out) P(gnn_apb_gate_out_args, M)
@@ -96,11 +99,13 @@ def test_ctypes_structs_match_c_layout(tmp_path):
     assert int(lines["gnn_trimul_contract_bwd_args"]) == ctypes.sizeof(_lib.TrimulContractBwdArgs)
     assert int(lines["gnn_apb_gate_out_args"]) == ctypes.sizeof(_lib.ApbGateOutArgs)
     assert int(lines["gnn_trimul_proj_bwd_args"]) == ctypes.sizeof(_lib.TrimulProjBwdArgs)
+    assert int(lines["gnn_trimul_out_bwd_args"]) == ctypes.sizeof(_lib.TrimulOutBwdArgs)
     classes = {"gnn_triattn_args": _lib.TriAttnArgs, "gnn_trimul_args": _lib.TrimulArgs,
                "gnn_pair_bias_args": _lib.PairBiasArgs, "gnn_triattn_bwd_args": _lib.TriAttnBwdArgs,
                "gnn_layernorm_args": _lib.LayerNormArgs, "gnn_gate_bwd_args": _lib.GateBwdArgs,
                "gnn_trimul_contract_bwd_args": _lib.TrimulContractBwdArgs,
-               "gnn_apb_gate_out_args": _lib.ApbGateOutArgs, "gnn_trimul_proj_bwd_args": _lib.TrimulProjBwdArgs}
+               "gnn_apb_gate_out_args": _lib.ApbGateOutArgs, "gnn_trimul_proj_bwd_args": _lib.TrimulProjBwdArgs,
+               "gnn_trimul_out_bwd_args": _lib.TrimulOutBwdArgs}
     for key, val in lines.items():
         if "." not in key:
             continue
@@ -343,6 +348,25 @@ def test_trimul_backward_helper_argument_errors():
     assert b"C must be 64 or 128" in lib.gnn_last_error()
     assert lib.gnn_trimul_proj_bwd_partials(100) == 2
     assert lib.gnn_trimul_proj_bwd_partials(1 << 20) == 512
+
+    assert lib.gnn_trimul_out_bwd(None, None) == _lib.GNN_ERR_ARG
+    ob = _lib.TrimulOutBwdArgs()
+    assert lib.gnn_trimul_out_bwd(ctypes.byref(ob), None) == _lib.GNN_ERR_ARG
+    assert b"required" in lib.gnn_last_error()
+    ob.o = ob.p_out_w = ob.gate = ob.dout = ob.on = ob.dy = ob.d_go = ob.d_o = ob.partial = 4096
+    ob.B, ob.N, ob.C, ob.Ch, ob.dgo_ld = 1, 40, 128, 128, 100
+    assert lib.gnn_trimul_out_bwd(ctypes.byref(ob), None) == _lib.GNN_ERR_ARG
+    assert b"d_go rows" in lib.gnn_last_error()
+    ob.dgo_ld, ob.dy = 640, 4104
+    assert lib.gnn_trimul_out_bwd(ctypes.byref(ob), None) == _lib.GNN_ERR_ARG
+    assert b"aligned" in lib.gnn_last_error()
+    ob.dy, ob.Ch = 4096, 96
+    assert lib.gnn_trimul_out_bwd(ctypes.byref(ob), None) == _lib.GNN_ERR_UNSUPPORTED
+    assert b"c_hidden 32, 64 or 128" in lib.gnn_last_error()
+    ob.Ch, ob.dtype = 128, _lib.GNN_F32
+    assert lib.gnn_trimul_out_bwd(ctypes.byref(ob), None) == _lib.GNN_ERR_UNSUPPORTED
+    assert lib.gnn_trimul_out_bwd_partials(1, 40) == 40
+    assert lib.gnn_trimul_out_bwd_partials(1, 512) == 512
 
     assert lib.gnn_trimul_contract_bwd(None, None) == _lib.GNN_ERR_ARG
     cb = _lib.TrimulContractBwdArgs()

@@ -188,14 +188,17 @@ def test_trimul_grads_match_oracle(direction, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize(("C", "Ch", "N", "direction"),
-                         [(128, 128, 40, "outgoing"), (64, 32, 70, "incoming"), (128, 64, 24, "incoming")],
-                         ids=["c128_h128_n40", "c64_h32_n70", "c128_h64_n24"])
+                         [(128, 128, 40, "outgoing"), (64, 32, 70, "incoming"), (128, 64, 24, "incoming"),
+                          (128, 96, 40, "outgoing")],
+                         ids=["c128_h128_n40", "c64_h32_n70", "c128_h64_n24", "c128_h96_n40"])
 def test_fused_input_side_backward_matches_unfused(dtype, C, Ch, N, direction):
-    """gnn_trimul_proj_bwd (z, the input projections recomputed tile by tile, their gate
-    backward, the output gate's backward from the saved gate) against the unfused path (LN_in
-    and the three projections as one linear, the gates' backward from the recomputed
-    pre-activations), on the same forward: every gradient, with projection biases, random
-    LayerNorm parameters and a mask; N = 70 leaves a partial last pixel tile."""
+    """The fused backward kernels -- gnn_trimul_proj_bwd (z, the input projections recomputed
+    tile by tile, their gate backward) and gnn_trimul_out_bwd (LN_out, p_out recomputed, the
+    output gate's backward from the saved gate, d(on) and the LN_out backward; not for
+    c_hidden = 96, which keeps the unfused output side) -- against the unfused path (LayerNorms,
+    linears and gates as separate launches from recomputed pre-activations), on the same
+    forward: every gradient, with projection biases, random LayerNorm parameters and a mask;
+    N = 70 leaves a partial last pixel tile (and, for the output side, a partial row tile)."""
     K = _k()
     w = {k: v.to(DEV) for k, v in trimul_weights(C, Ch, dtype, seed=91, biases=True, ln_random=True).items()}
     x, mask = pair_input(1, N, C, dtype, seed=92)
@@ -230,6 +233,8 @@ def test_fused_input_side_backward_refusals():
     assert not K.proj_bwd_supported(torch.float32, 128, 128)
     assert not K.proj_bwd_supported(torch.bfloat16, 96, 32)
     assert not K.proj_bwd_supported(torch.bfloat16, 128, 160)
+    assert K.out_bwd_supported(torch.bfloat16, 128, 128) and K.out_bwd_supported(torch.float16, 64, 32)
+    assert not K.out_bwd_supported(torch.bfloat16, 128, 96) and not K.out_bwd_supported(torch.float32, 128, 128)
 
 
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
