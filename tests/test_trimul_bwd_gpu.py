@@ -191,7 +191,7 @@ def test_trimul_grads_match_oracle(direction, dtype):
                          [(128, 128, 40, "outgoing"), (64, 32, 70, "incoming"), (128, 64, 24, "incoming"),
                           (128, 96, 40, "outgoing")],
                          ids=["c128_h128_n40", "c64_h32_n70", "c128_h64_n24", "c128_h96_n40"])
-def test_fused_input_side_backward_matches_unfused(dtype, C, Ch, N, direction):
+def test_fused_backward_matches_unfused(dtype, C, Ch, N, direction):
     """The fused backward kernels -- gnn_trimul_proj_bwd (z, the input projections recomputed
     tile by tile, their gate backward) and gnn_trimul_out_bwd (LN_out, p_out recomputed, the
     output gate's backward from the saved gate, d(on) and the LN_out backward; not for
@@ -225,9 +225,10 @@ def test_fused_input_side_backward_matches_unfused(dtype, C, Ch, N, direction):
         assert_close_to_oracle(key, grad, oracle[key], TRIMUL_TOL[torch.bfloat16, "ieee"])
 
 
-def test_fused_input_side_backward_refusals():
-    """gnn_trimul_proj_bwd covers 16-bit inputs with C in {64, 128} and 2 c_hidden <= 256;
-    trimul_bwd_hip refuses fused=True outside that and takes the unfused path by itself."""
+def test_fused_backward_refusals():
+    """gnn_trimul_proj_bwd covers 16-bit inputs with C in {64, 128} and 2 c_hidden <= 256,
+    gnn_trimul_out_bwd 16-bit inputs with C in {64, 128} and c_hidden in {32, 64, 128};
+    trimul_bwd_hip takes the unfused path by itself outside them."""
     K = _k()
     assert K.proj_bwd_supported(torch.bfloat16, 128, 128) and K.proj_bwd_supported(torch.float16, 64, 32)
     assert not K.proj_bwd_supported(torch.float32, 128, 128)
