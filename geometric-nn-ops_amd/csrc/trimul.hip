@@ -1872,6 +1872,217 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
   }
 }
 
+// ---- stage 3, persistent variant: 16-bit types with C = c_hidden = 128 -------------------
+// The kernel above starts each 64-pixel tile with its o and g loads and ends it with the out
+// stores, so every workgroup's lifetime carries a memory round trip that only the other
+// workgroups of its CU can hide. Here GNN_OUTP_WGS workgroups per CU walk the tiles t,
+// t + grid, ... and keep the next tile's o and g in registers while the current tile is
+// normalised, projected and written: o of t + grid is requested as soon as o of t is in LDS,
+// g of t + grid as soon as g of t has been used. The p_out fragments of a wave's 32 output
+// channels stay in registers for the whole launch. Every load is issued unconditionally
+// (columns past N read the unused tail of o's rows, pixels past N of g re-read the tile's
+// last pixel: neither reaches a stored result, the LayerNorm and the product being per
+// pixel) and the out stores are buffer stores whose range ends at the tile's last pixel, so
+// the hardware drops the lanes past N. No store sits in a branch, and the compiler's memory
+// counter waits for a tile's loads then never cover the stores issued after them.
+#ifndef GNN_OUTP_WGS  // workgroups per CU the register allocation is held to
+#define GNN_OUTP_WGS 3
+#endif
+#ifndef GNN_OUT_PERSIST  // 0: the per-tile kernel for C = c_hidden = 128 too
+#define GNN_OUT_PERSIST 1
+#endif
+constexpr uint32_t BUFFER_RSRC_WORD3 = 0x00020000;  // raw (unswizzled) buffer, gfx9 family
+
+template <typename T>
+__global__ __launch_bounds__(NT, GNN_OUTP_WGS) void trimul_out_persist_kernel(const gnn_trimul_args a, int64_t NP,
+                                                                                size_t off_g, size_t off_o) {
+  static_assert(sizeof(T) == 2, "persistent output stage: 16-bit types");
+  typedef typename TypeOps<T>::V8 V8;
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  constexpr int C = 128, Ch = 128, PAD = lds_pad<T>();
+  constexpr int OR = PTO + PAD, ZR = Ch + PAD, YR = OPC + PAD;
+  constexpr int NKS = Ch / 16;                 // k-steps of p_out
+  constexpr int OCO = Ch * (PTO / 8) / NT;     // 8-pixel o chunks per thread
+  constexpr int OCG = PTO * C / 8 / NT;        // 8-channel g / out chunks per thread
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* ot = reinterpret_cast<T*>(smem_raw);
+  T* ys = ot;  // the raw o tile is dead once the LayerNorm has written zs
+  T* zs = ot + out_region1_elems(Ch, PAD);
+  float* lnw = reinterpret_cast<float*>(zs + (size_t)PTO * ZR);
+  float* lnb = lnw + Ch;
+  float* red = lnb + Ch;         // LayerNorm partial sums [8 * PTO]
+  float* bpo_s = red + 8 * PTO;  // p_out bias [C]
+  const int N = (int)a.N;
+  const int ntile = (N + PTO - 1) / PTO;
+  const int64_t ntiles = (int64_t)a.B * N * ntile;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
+  const T* __restrict__ ocm = (const T*)((const unsigned char*)a.workspace + off_o);
+  const T* __restrict__ gbase =
+      (const T*)(a.gate ? (const unsigned char*)a.gate : (const unsigned char*)a.workspace + off_g);
+
+  for (int c = tid; c < Ch; c += NT) {
+    lnw[c] = ld_or<T>(a.ln_out_w, c, 1.f);
+    lnb[c] = ld_or<T>(a.ln_out_b, c, 0.f);
+  }
+  for (int c = tid; c < C; c += NT) bpo_s[c] = ld_or<T>(a.p_out_b, c, 0.f);
+  V8 wpf[NKS];  // rows 32 wave + l32 of p_out_w
+  {
+    const T* wrow = (const T*)a.p_out_w + (int64_t)(32 * wave + l32) * Ch + 8 * g;
+#pragma unroll
+    for (int k = 0; k < NKS; ++k) wpf[k] = load8(wrow + 16 * k);
+  }
+
+  // o chunk i of a thread: channel (tid + i NT) / 8, pixels 8 ((tid + i NT) % 8) ..
+  auto load_o = [&](V8 (&ov)[OCO], int64_t t) {
+    const int64_t row = t / ntile;  // b N + p
+    const int q0 = (int)(t - row * ntile) * PTO, p = (int)(row % N), b = (int)(row / N);
+#pragma unroll
+    for (int i = 0; i < OCO; ++i) {
+      const int c = tid + i * NT, ch = c >> 3, col = min(q0 + (c & 7) * 8, (int)NP - 8);
+      ov[i] = load8(ocm + (((int64_t)b * Ch + ch) * N + p) * NP + col);
+    }
+  };
+  // g / out chunk i: pixel (tid + i NT) / 16, channels 8 ((tid + i NT) % 16) ..
+  auto load_g = [&](V8 (&gr)[OCG], int64_t t) {
+    const int64_t row = t / ntile;
+    const int q0 = (int)(t - row * ntile) * PTO, last = min(N - q0, PTO) - 1;
+    const T* gblk = gbase + (row * N + q0) * C;
+#pragma unroll
+    for (int i = 0; i < OCG; ++i) {
+      const int idx = tid + i * NT, px = min(idx >> 4, last);
+      gr[i] = load8(gblk + (int64_t)px * C + 8 * (idx & 15));
+    }
+  };
+
+  // o of tile t is written to LDS at the end of the previous iteration (before the loop for
+  // the first tile), so that every wait for a tile's loads sees the same later requests: the
+  // out stores (OCG) and the g loads (OCG) of the tile before it
+  auto put_o = [&](const V8 (&ov)[OCO]) {
+#pragma unroll
+    for (int i = 0; i < OCO; ++i) {
+      const int c = tid + i * NT;
+      store8(&ot[(c >> 3) * OR + (c & 7) * 8], ov[i]);
+    }
+  };
+  // the tile after t of this workgroup; the last tile requests itself again, so that the
+  // loads stay unconditional
+  auto next_of = [&](int64_t t) { return t + gridDim.x < ntiles ? t + (int64_t)gridDim.x : t; };
+  int64_t t = blockIdx.x;
+  if (t >= ntiles) return;  // uniform over the workgroup
+  V8 ov[OCO], gr[OCG];
+  load_o(ov, t);
+  load_g(gr, t);
+  put_o(ov);
+  load_o(ov, next_of(t));
+  for (; t < ntiles; t += gridDim.x) {
+    const int64_t tn = next_of(t);
+    const int64_t row = t / ntile;
+    const int q0 = (int)(t - row * ntile) * PTO, npix = min(N - q0, PTO);
+    __syncthreads();  // the o tile (and, on the first tile, the LayerNorm parameters) in LDS
+
+    // ---- LayerNorm over channels, as the per-tile kernel: thread = (pixel pair tid % 32,
+    // channel part tid / 32 of 16 channels), two passes through LDS partial sums
+    {
+      const int pp = tid & 31, part = tid >> 5, k0 = part * (Ch / 8);
+      typedef T T2 __attribute__((ext_vector_type(2)));
+      auto pair = [&](int k) -> f32x2 {
+        return __builtin_convertvector(*reinterpret_cast<const T2*>(&ot[k * OR + 2 * pp]), f32x2);
+      };
+      float2* red2 = reinterpret_cast<float2*>(red);  // [8 parts][32 pairs]
+      f32x2 s2 = {0.f, 0.f};
+#pragma unroll
+      for (int k = k0; k < k0 + Ch / 8; ++k) s2 += pair(k);
+      red2[part * 32 + pp] = make_float2(s2[0], s2[1]);
+      __syncthreads();
+      f32x2 mean = {0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float2 v = red2[j * 32 + pp];
+        mean += f32x2{v.x, v.y};
+      }
+      const LnWidth lw(a.ln_out_channels, Ch);
+      mean *= lw.inv_n;
+      f32x2 q2 = {0.f, 0.f};
+#pragma unroll
+      for (int k = k0; k < k0 + Ch / 8; ++k) {
+        const f32x2 d = pair(k) - mean;
+        q2 += d * d;
+      }
+      __syncthreads();  // every part has read the sums
+      red2[part * 32 + pp] = make_float2(q2[0], q2[1]);
+      __syncthreads();
+      f32x2 var = {0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float2 v = red2[j * 32 + pp];
+        var += f32x2{v.x, v.y};
+      }
+      const float rs0 = __builtin_amdgcn_rsqf(lw.var(var[0], mean[0]) + a.eps);  // as torch's rsqrt
+      const float rs1 = __builtin_amdgcn_rsqf(lw.var(var[1], mean[1]) + a.eps);
+#pragma unroll
+      for (int k = k0; k < k0 + Ch / 8; k += 8) {
+        f32x8 v0, v1;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const f32x2 x = pair(k + e);
+          v0[e] = (x[0] - mean[0]) * rs0 * lnw[k + e] + lnb[k + e];
+          v1[e] = (x[1] - mean[1]) * rs1 * lnw[k + e] + lnb[k + e];
+        }
+        store8(&zs[(2 * pp) * ZR + k], TypeOps<T>::from_f32(v0));
+        store8(&zs[(2 * pp + 1) * ZR + k], TypeOps<T>::from_f32(v1));
+      }
+    }
+    __syncthreads();
+
+    // ---- y = z Wpo^T + bpo on MFMA: acc[s] = [cout][pixel], cout = 32 wave + 8(r/4) + 4g +
+    // r%4, pixel = 32s + l32; rounded to T into the pass tile ys
+    {
+      f32x16 acc[PTO / 32];
+#pragma unroll
+      for (int s = 0; s < PTO / 32; ++s)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[s][r] = 0.f;
+#pragma unroll
+      for (int k = 0; k < NKS; ++k)
+#pragma unroll
+        for (int s = 0; s < PTO / 32; ++s)
+          Mma<T, PREC_NATIVE>::step(acc[s], wpf[k], load8(&zs[(32 * s + l32) * ZR + 16 * k + 8 * g]));
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bpo_s[32 * wave + 8 * rg + 4 * g]);
+#pragma unroll
+        for (int s = 0; s < PTO / 32; ++s) {
+          f32x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = acc[s][4 * rg + e] + b4[e];
+          store4(&ys[(32 * s + l32) * YR + 32 * wave + 8 * rg + 4 * g], TypeOps<T>::from_f32(v));
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- out = y * g over the contiguous block of the tile's pixels; the buffer's range
+    // ends at pixel npix, so the lanes of pixels past N are dropped
+    {
+      T* oblk = (T*)a.out + (row * N + q0) * C;
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(oblk, (short)0, npix * C * (int)sizeof(T), BUFFER_RSRC_WORD3);
+#pragma unroll
+      for (int i = 0; i < OCG; ++i) {
+        const int idx = tid + i * NT, px = idx >> 4, c8 = idx & 15;
+        const f32x8 y = TypeOps<T>::to_f32(load8(&ys[px * YR + 8 * c8]));
+        const V8 val = TypeOps<T>::from_f32(y * TypeOps<T>::to_f32(gr[i]));
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, val), rs,
+                                               (px * C + 8 * c8) * (int)sizeof(T), 0, 0);
+      }
+    }
+    load_g(gr, tn);
+    __syncthreads();  // ys (region 1) is rewritten by the next tile's o
+    put_o(ov);
+    load_o(ov, next_of(tn));
+  }
+}
+
 // ---- stage 2, 16-bit types: BM x 256 tiles fed by a global->LDS DMA pipeline -------------
 // Workgroup tile: BM rows of A (i) x 256 rows of B (j), BM = 128 (4 waves, 3 stages) or 256
 // (8 waves, 4 stages); wave (wm, wn) of the (BM / 64) x 2 grid owns 64 i x 128 j as 2 x 4
@@ -2188,6 +2399,16 @@ int launch_out_w(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st
   const int64_t NP = round_up(a.N, 32);
   const int64_t ntile = (a.N + PTO - 1) / PTO;
   const size_t smem = out_smem<T>(a);
+  if constexpr (sizeof(T) == 2 && PREC == PREC_NATIVE && CK == 128 && CHK == 128) {
+    if (GNN_OUT_PERSIST) {
+      const void* pf = (const void*)trimul_out_persist_kernel<T>;
+      if (smem > 64 * 1024) (void)hipFuncSetAttribute(pf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+      const int64_t grid = std::min<int64_t>(a.B * a.N * ntile, persistent_grid(pf, NT, smem));
+      hipLaunchKernelGGL((trimul_out_persist_kernel<T>), dim3((uint32_t)grid), dim3(NT), smem, st, a, NP, L.off_g,
+                         L.off_o);
+      return (int)hipGetLastError();
+    }
+  }
   const void* fn = (const void*)trimul_out_kernel<T, PREC, CK, CHK>;
   if (smem > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   hipLaunchKernelGGL((trimul_out_kernel<T, PREC, CK, CHK>), dim3((uint32_t)(a.B * a.N * ntile)), dim3(NT),

@@ -123,6 +123,35 @@ def test_batched(direction, shape):
 
 
 @DIRECTIONS
+@pytest.mark.parametrize(("B", "N", "dtype"), [(2, 70, torch.bfloat16), (1, 130, torch.float16), (3, 64, torch.bfloat16)],
+                         ids=["b2_n70_bf16", "b1_n130_fp16", "b3_n64_bf16"])
+def test_output_stage_tiles_and_bounds(direction, B, N, dtype):
+    """The output stage at C = c_hidden = 128 (a fixed grid of workgroups walking 64-pixel
+    tiles with the next tile's o and g in flight, out written by buffer stores whose range
+    ends at the tile's last pixel): rows whose last tile is partial, several batches, against
+    the oracle; the stage run again into a buffer with a guard region after the output leaves
+    the guard untouched and writes the same result."""
+    from geometric_nn_ops_torch.triangle._kernels import trimul as K
+
+    C = 128
+    w = trimul_weights(C, C, dtype, seed=61, biases=True, ln_random=True)
+    x, mask = pair_input(B, N, C, dtype, seed=62)
+    wd = {k: v.to(DEV) for k, v in w.items()}
+    with torch.no_grad():
+        args, keep, out, ws, off = K.build_args(x.to(DEV), direction, mask.to(DEV), 1e-5, wd)
+        for stage in ("gnn_trimul_proj", "gnn_trimul_contract", "gnn_trimul_out"):
+            K.run_stage(stage, args, torch.device(DEV))
+        guard = torch.full((out.numel() + 4096,), 7.0, device=DEV, dtype=dtype)
+        args.out = guard.data_ptr()
+        K.run_stage("gnn_trimul_out", args, torch.device(DEV))
+        torch.cuda.synchronize()
+    assert_close_to_oracle("out", out, oracle(x, direction, mask, w), Tolerance(1 - 1e-4, 2e-2),
+                           rel_fro_max=NORTH_STAR_REL_FRO)
+    assert torch.equal(guard[:out.numel()].view(out.shape), out)
+    assert bool((guard[out.numel():] == 7.0).all())
+
+
+@DIRECTIONS
 @pytest.mark.parametrize("true_length", [32, 48])
 def test_block_padded(direction, true_length):
     N, C, batch = 64, 128, 2
@@ -352,9 +381,10 @@ def test_unsupported_configs_use_the_torch_path(case):
 @DIRECTIONS
 @pytest.mark.parametrize(("dtype", "c_z", "c_hidden"),
                          [(torch.bfloat16, 40, 24), (torch.bfloat16, 100, 70), (torch.bfloat16, 130, 128),
-                          (torch.bfloat16, 496, 250), (torch.float16, 72, 40), (torch.float32, 40, 20)],
-                         ids=["bf16_40_24", "bf16_100_70", "bf16_130_128", "bf16_496_250", "fp16_72_40",
-                              "fp32_40_20"])
+                          (torch.bfloat16, 120, 110), (torch.bfloat16, 496, 250), (torch.float16, 72, 40),
+                          (torch.float32, 40, 20)],
+                         ids=["bf16_40_24", "bf16_100_70", "bf16_130_128", "bf16_120_110", "bf16_496_250",
+                              "fp16_72_40", "fp32_40_20"])
 def test_odd_channel_widths(direction, dtype, c_z, c_hidden):
     """Widths that are not multiples of 32 (the reference's Triton kernels mask any width,
     trimul.py:310-314) on the forward kernels: x and the weights zero-padded to multiples of
