@@ -53,6 +53,13 @@ __host__ __device__ constexpr int lds_pad() {
   return (int)(16 / sizeof(T));
 }
 
+// Word 3 of a buffer resource for a raw (unswizzled) buffer on the gfx9 family. A buffer store
+// whose offset lies at or past the resource's byte range is dropped by the hardware, which
+// lets a kernel issue its stores unconditionally (no store in a branch) and still skip
+// lanes past the end of a row or tile.
+constexpr uint32_t BUFFER_RSRC_WORD3 = 0x00020000;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
 // Element offset of (plane, row i, column k) in the a / b operands of the contraction
 // (plane = batch * Ch + channel, k < NP). 16-bit types: k-blocked [plane][NP / 32][N][32], so
 // that one 32-column pipeline stage of a block of rows is a single contiguous range;
@@ -826,7 +833,10 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
   constexpr int NGI = CK / 16;  // gate items (CK / 32 units x 2 sub-tiles), at most one per wave
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int Ch = CHK ? CHK : (int)a.Ch, N = (int)a.N;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+  // the wave index as a scalar, so that unit and gate-item addresses and the buffer
+  // resources built from them stay in scalar registers
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   T* zs = reinterpret_cast<T*>(smem_raw + LD::zs);
   T* wgo_s = reinterpret_cast<T*>(smem_raw + LD::wgo);
   T* ebuf = reinterpret_cast<T*>(smem_raw + LD::ebuf) + wave * 32 * ER;
@@ -918,6 +928,30 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
   V8 wpf[NKS], wgf[NKS];
   float bp = 0.f, bg = 0.f;
   int wp_unit = -1;
+  // FIXED (c_hidden = 128): wave w owns projection unit w for the whole launch. Its weights
+  // are loaded (and waited for) before the tile loop, the tile loop has no unit loop, and
+  // the a / b / g stores are buffer stores issued unconditionally. With a load or a store in
+  // a branch of the tile loop the compiler's memory-counter waits take the count of the
+  // path without it: the k loop then waited for the next tile's x and the next tile's
+  // LayerNorm for the stores just issued.
+  constexpr bool FIXED = CHK != 0 && 2 * CHK == 32 * PW;
+  if constexpr (FIXED) {
+    const int ch = 32 * wave + l32;
+    const T* wprow = (const T*)a.p_in_w + (int64_t)ch * CK + 8 * g;
+    const T* wgrow = (const T*)a.g_in_w + (int64_t)ch * CK + 8 * g;
+#pragma unroll
+    for (int k = 0; k < NKS; ++k) {
+      wpf[k] = load8(wprow + 16 * k);
+      wgf[k] = load8(wgrow + 16 * k);
+    }
+    bp = ld_or<T>(a.p_in_b, ch, 0.f);
+    bg = ld_or<T>(a.g_in_b, ch, 0.f) * NLOG2E;  // the exp2 argument's bias term
+    wp_unit = wave;
+    // consumed here, so that no load before the loop is still counted inside it
+#pragma unroll
+    for (int k = 0; k < NKS; ++k) asm volatile("" ::"v"(wpf[k]), "v"(wgf[k]));
+    asm volatile("" ::"v"(bp), "v"(bg));
+  }
   const bool has_go = wave < NGI;
   const int uo = wave % (CK / 32), so = wave / (CK / 32);  // this wave's gate item
 
@@ -933,9 +967,33 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
     const int crow0 = lane >> 3, p0 = (lane & 7) * 8;
     const bool in_a = 32 * u < Ch;
     const int chh0 = 32 * u + crow0 - (in_a ? 0 : Ch);
-    T* drow = (in_a ? a_cm : b_cm) + ab_offset<T>((int64_t)tl.b * Ch + chh0, tl.row, tl.c0 + p0, N, NP);
     const int64_t pstep = ab_offset<T>(8, 0, 0, N, NP);  // 8 channel planes
     const bool full = tl.c0 + p0 + 8 <= N, tail = !full && tl.c0 + p0 < NP;
+    if constexpr (FIXED) {
+      // store i covers channel planes 8i .. 8i + 7 of the unit: one buffer range each (the
+      // launcher keeps 8 planes below 2^31 bytes); lanes past the padded row are dropped
+      T* base = (in_a ? a_cm : b_cm) + ab_offset<T>((int64_t)tl.b * Ch + 32 * u - (in_a ? 0 : Ch), 0, 0, N, NP);
+      // ab_offset(crow0, row, k) in 32 bits (below 8 planes, so below 2^30 elements)
+      const int k = tl.c0 + p0;
+      const uint32_t off = k < NP ? ((((crow0 * (int)(NP >> 5) + (k >> 5)) * N + tl.row) << 5) + (k & 31)) *
+                                        (uint32_t)sizeof(T)
+                                  : 0x80000000u;
+      const bool tail_tile = tl.c0 + PTP > N;  // uniform
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        V8 v = load8(&ebuf[(crow0 + 8 * i) * ER + (p0 ^ EBSW(crow0 + 8 * i))]);
+        if (tail_tile) {  // row tail: pixels N .. NP-1 are written as zeros
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (k + e >= N) v[e] = TypeOps<T>::from_f32(0.f);
+        }
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            base + i * pstep, (short)0, (int)(pstep * (int64_t)sizeof(T)), BUFFER_RSRC_WORD3);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), rs, off, 0, 0);
+      }
+      return;
+    }
+    T* drow = (in_a ? a_cm : b_cm) + ab_offset<T>((int64_t)tl.b * Ch + chh0, tl.row, tl.c0 + p0, N, NP);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const V8 val = load8(&ebuf[(crow0 + 8 * i) * ER + (p0 ^ EBSW(crow0 + 8 * i))]);
@@ -954,8 +1012,24 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
     // 4 lanes per 32-channel pixel row segment; store 1 is store 0 moved by 16 pixels along
     // the tile (a column step outgoing, a row step incoming)
     const int px = lane >> 2, k0 = (lane & 3) * 8, pl = 32 * so + px;
-    T* dst = gout + proj_pix(tl, pl, N, outgoing) * CK + 32 * uo + k0;
     const int64_t step16 = (outgoing ? 16 : 16 * (int64_t)N) * CK;
+    if constexpr (FIXED) {
+      // one buffer range from the tile's first pixel to the end of its last one (pixel
+      // stride CK outgoing, N CK incoming): the lanes of pixels past N fall outside it
+      const int pstride = outgoing ? CK : N * CK;  // below 2^31 / 128 (the launcher's bound on N)
+      const int npix = min(N - tl.c0, PTP);
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          gout + proj_pix(tl, 0, N, outgoing) * CK, (short)0, ((npix - 1) * pstride + CK) * (int)sizeof(T),
+          BUFFER_RSRC_WORD3);
+      const uint32_t off = (uint32_t)(pl * pstride + 32 * uo + k0) * (uint32_t)sizeof(T);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4_t, load8(&gbuf[(px + 16 * i) * EG + (k0 ^ EBSW(px + 16 * i))])), rs,
+            off + (uint32_t)(16 * i * pstride) * (uint32_t)sizeof(T), 0, 0);
+      return;
+    }
+    T* dst = gout + proj_pix(tl, pl, N, outgoing) * CK + 32 * uo + k0;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       if (tl.c0 + pl + 16 * i < N) store8(dst + i * step16, load8(&gbuf[(px + 16 * i) * EG + (k0 ^ EBSW(px + 16 * i))]));
@@ -976,9 +1050,10 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
     bool go_done = !has_go;
     // gated projection units: acc = [pixel][channel], row = pixel 32s + 8(r/4) + 4g + r%4,
     // col = channel 32u + l32; staged as [channel][pixel] for 128-byte row stores
-    for (int u = wave; u < npg; u += PW) {
+    const int u_end = FIXED ? wave + 1 : npg;  // FIXED: exactly unit `wave`
+    for (int u = wave; u < u_end; u += PW) {
       const int ch = 32 * u + l32;
-      if (u != wp_unit) {
+      if (!FIXED && u != wp_unit) {
         const T* wprow = (const T*)a.p_in_w + (int64_t)ch * CK + 8 * g;
         const T* wgrow = (const T*)a.g_in_w + (int64_t)ch * CK + 8 * g;
 #pragma unroll
@@ -1010,12 +1085,16 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
           Mma<T, PREC_NATIVE>::step(accg[1], z1, wgf[k]);
         }
       };
+      // the matrix pipe first: a wave that reaches its MFMAs takes the pipe ahead of the
+      // other wave of its SIMD, which then runs its epilogue beside them (0.5-1 us)
+      __builtin_amdgcn_s_setprio(1);
       if (!go_done) {
         kloop(std::true_type{});
         go_done = true;
       } else {
         kloop(std::false_type{});
       }
+      __builtin_amdgcn_s_setprio(0);
 #pragma unroll
       for (int s = 0; s < PSUB; ++s) {
         const int sub = s == 0 ? s_first : 1 - s_first;
@@ -1891,14 +1970,11 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
 #ifndef GNN_OUT_PERSIST  // 0: the per-tile kernel for C = c_hidden = 128 too
 #define GNN_OUT_PERSIST 1
 #endif
-constexpr uint32_t BUFFER_RSRC_WORD3 = 0x00020000;  // raw (unswizzled) buffer, gfx9 family
-
 template <typename T>
 __global__ __launch_bounds__(NT, GNN_OUTP_WGS) void trimul_out_persist_kernel(const gnn_trimul_args a, int64_t NP,
                                                                                 size_t off_g, size_t off_o) {
   static_assert(sizeof(T) == 2, "persistent output stage: 16-bit types");
   typedef typename TypeOps<T>::V8 V8;
-  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
   constexpr int C = 128, Ch = 128, PAD = lds_pad<T>();
   constexpr int OR = PTO + PAD, ZR = Ch + PAD, YR = OPC + PAD;
   constexpr int NKS = Ch / 16;                 // k-steps of p_out
@@ -2341,7 +2417,9 @@ int launch_proj(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st)
   }
   if constexpr (sizeof(T) == 2) {
     if (GNN_PROJ_PINGPONG && a.C == 128 && a.Ch == 128) return launch_proj_pp<T>(a, L, st);
-    if (a.C == 128 && a.Ch == 128) return launch_proj_fast<T, 128, 128>(a, L, st);
+    // c_hidden = 128 takes buffer stores over ranges of 8 channel planes (16 N NP bytes)
+    if (a.C == 128 && a.Ch == 128 && 16 * a.N * round_up(a.N, 32) < ((int64_t)1 << 31))
+      return launch_proj_fast<T, 128, 128>(a, L, st);
     if (a.C == 128) return launch_proj_fast<T, 128, 0>(a, L, st);
     if (a.C == 64) return launch_proj_fast<T, 64, 0>(a, L, st);
   }
