@@ -132,6 +132,31 @@ __device__ __forceinline__ typename TypeOps<T>::V8 load8_bias_tail(const T* row,
   return x;
 }
 
+// ---- raw buffer stores (gfx9 family) ------------------------------------------------------
+// A buffer store whose byte offset lies at or past its resource's range is dropped by the
+// hardware. A kernel can then issue its stores unconditionally (no store inside a branch)
+// and still skip lanes: such lanes carry BUFFER_OOB (the range stays below 2^31 bytes). This
+// matters for the compiler's memory-counter waits (vmcnt counts loads and stores in issue
+// order): at the join after a branch holding a store it takes the count of the path without
+// the store, so a later wait for a load issued before that store also waits for the store.
+constexpr uint32_t BUFFER_RSRC_WORD3 = 0x00020000;  // raw, unswizzled buffer
+constexpr uint32_t BUFFER_OOB = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int range_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, range_bytes, BUFFER_RSRC_WORD3);
+}
+template <typename V>
+__device__ __forceinline__ void buffer_store(const V& v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  static_assert(sizeof(V) == 4 || sizeof(V) == 8 || sizeof(V) == 16, "buffer_store: 4, 8 or 16 bytes");
+  if constexpr (sizeof(V) == 16)
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, off, 0, 0);
+  else if constexpr (sizeof(V) == 8)
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, off, 0, 0);
+  else
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, 0);
+}
+
 // ---- 32x32 tile, one K=16 step ----------------------------------------------------------
 // acc[row, col] += sum_k A[row, k] * B[k, col] over the 16 k of this step, with both
 // operands given as fragments (see the file comment).

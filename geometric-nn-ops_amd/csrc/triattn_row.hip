@@ -33,7 +33,9 @@
 // (the extra score registers cost occupancy and it measured slower), and a persistent form
 // (16 waves per CU streaming consecutive rows through two LDS buffers, the next row's K / V
 // DMA issued during the current row's key loop: 20% slower at N = 512, its 16 waves meeting
-// at a barrier every row).
+// at a barrier every row), and unconditional buffer stores for o and lse (so that the wait for
+// the next query block's q, requested during the sweep, would not cover them: the offsets
+// spilled 4 registers at the 128-register cap, 157 against 148 us).
 // Per tile: the transposed score tile S^T = K Q'^T on 32x32x16 MFMA, the pair bias added by
 // MFMA against an identity fragment, and, on tiles with a masked key or keys past N, the
 // per-key mask term (0 / mask_value / -inf from a per-row table in LDS) added by one more

@@ -53,13 +53,6 @@ __host__ __device__ constexpr int lds_pad() {
   return (int)(16 / sizeof(T));
 }
 
-// Word 3 of a buffer resource for a raw (unswizzled) buffer on the gfx9 family. A buffer store
-// whose offset lies at or past the resource's byte range is dropped by the hardware, which
-// lets a kernel issue its stores unconditionally (no store in a branch) and still skip
-// lanes past the end of a row or tile.
-constexpr uint32_t BUFFER_RSRC_WORD3 = 0x00020000;
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
 // Element offset of (plane, row i, column k) in the a / b operands of the contraction
 // (plane = batch * Ch + channel, k < NP). 16-bit types: k-blocked [plane][NP / 32][N][32], so
 // that one 32-column pipeline stage of a block of rows is a single contiguous range;
@@ -977,7 +970,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
       const int k = tl.c0 + p0;
       const uint32_t off = k < NP ? ((((crow0 * (int)(NP >> 5) + (k >> 5)) * N + tl.row) << 5) + (k & 31)) *
                                         (uint32_t)sizeof(T)
-                                  : 0x80000000u;
+                                  : BUFFER_OOB;
       const bool tail_tile = tl.c0 + PTP > N;  // uniform
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -987,9 +980,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
           for (int e = 0; e < 8; ++e)
             if (k + e >= N) v[e] = TypeOps<T>::from_f32(0.f);
         }
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            base + i * pstep, (short)0, (int)(pstep * (int64_t)sizeof(T)), BUFFER_RSRC_WORD3);
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), rs, off, 0, 0);
+        buffer_store(v, buffer_rsrc(base + i * pstep, (int)(pstep * (int64_t)sizeof(T))), off);
       }
       return;
     }
@@ -1018,15 +1009,13 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
       // stride CK outgoing, N CK incoming): the lanes of pixels past N fall outside it
       const int pstride = outgoing ? CK : N * CK;  // below 2^31 / 128 (the launcher's bound on N)
       const int npix = min(N - tl.c0, PTP);
-      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          gout + proj_pix(tl, 0, N, outgoing) * CK, (short)0, ((npix - 1) * pstride + CK) * (int)sizeof(T),
-          BUFFER_RSRC_WORD3);
+      const __amdgpu_buffer_rsrc_t rs =
+          buffer_rsrc(gout + proj_pix(tl, 0, N, outgoing) * CK, ((npix - 1) * pstride + CK) * (int)sizeof(T));
       const uint32_t off = (uint32_t)(pl * pstride + 32 * uo + k0) * (uint32_t)sizeof(T);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        __builtin_amdgcn_raw_buffer_store_b128(
-            __builtin_bit_cast(u32x4_t, load8(&gbuf[(px + 16 * i) * EG + (k0 ^ EBSW(px + 16 * i))])), rs,
-            off + (uint32_t)(16 * i * pstride) * (uint32_t)sizeof(T), 0, 0);
+        buffer_store(load8(&gbuf[(px + 16 * i) * EG + (k0 ^ EBSW(px + 16 * i))]), rs,
+                     off + (uint32_t)(16 * i * pstride) * (uint32_t)sizeof(T));
       return;
     }
     T* dst = gout + proj_pix(tl, pl, N, outgoing) * CK + 32 * uo + k0;
@@ -2141,15 +2130,13 @@ __global__ __launch_bounds__(NT, GNN_OUTP_WGS) void trimul_out_persist_kernel(co
     // ends at pixel npix, so the lanes of pixels past N are dropped
     {
       T* oblk = (T*)a.out + (row * N + q0) * C;
-      const __amdgpu_buffer_rsrc_t rs =
-          __builtin_amdgcn_make_buffer_rsrc(oblk, (short)0, npix * C * (int)sizeof(T), BUFFER_RSRC_WORD3);
+      const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(oblk, npix * C * (int)sizeof(T));
 #pragma unroll
       for (int i = 0; i < OCG; ++i) {
         const int idx = tid + i * NT, px = idx >> 4, c8 = idx & 15;
         const f32x8 y = TypeOps<T>::to_f32(load8(&ys[px * YR + 8 * c8]));
         const V8 val = TypeOps<T>::from_f32(y * TypeOps<T>::to_f32(gr[i]));
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, val), rs,
-                                               (px * C + 8 * c8) * (int)sizeof(T), 0, 0);
+        buffer_store(val, rs, (uint32_t)((px * C + 8 * c8) * (int)sizeof(T)));
       }
     }
     load_g(gr, tn);
