@@ -312,7 +312,11 @@ struct PbLds {
   static constexpr size_t total = mk + PB_TP * 4;
 };
 
-template <typename T, int CK>
+// ALLU: 2 c_hidden = 256, so every wave owns a unit; its tile loop then holds no load or
+// store in a branch (loads of the workgroup's last tile repeat that tile; stores are buffer
+// stores whose range ends at the last row), and the compiler's memory-counter wait for the
+// next tile's x and d_ab leaves the stores just issued in flight.
+template <typename T, int CK, bool ALLU>
 __global__ __launch_bounds__(PB_NT, 1) void trimul_proj_bwd_kernel(const gnn_trimul_proj_bwd_args a) {
   typedef PbLds<T, CK> S;
   typedef typename TypeOps<T>::V8 V8;
@@ -339,7 +343,7 @@ __global__ __launch_bounds__(PB_NT, 1) void trimul_proj_bwd_kernel(const gnn_tri
     bias[256 + c] = a.g_in_b ? TypeOps<T>::to_f32(((const T*)a.g_in_b)[c]) : 0.f;
   }
   // this wave's channels: A fragments, row = channel 32 wave + l32, k = 16 kk + 8 g + e
-  const bool has_unit = 32 * wave < Ch2;  // uniform over the wave
+  const bool has_unit = ALLU || 32 * wave < Ch2;  // uniform over the wave
   V8 wpf[NK], wgf[NK];
   {
     const int ch = has_unit ? 32 * wave + l32 : 0;
@@ -414,7 +418,13 @@ __global__ __launch_bounds__(PB_NT, 1) void trimul_proj_bwd_kernel(const gnn_tri
       for (int e = 0; e < 8; ++e) y[e] = (v[e] - mean) * rstd * lnw[8 * ci + e] + lnb[8 * ci + e];
       const V8 yr = TypeOps<T>::from_f32(y);
       store8(&zs[xpl * ZR + 8 * ci], yr);
-      if (r < rows) store8((T*)a.z + r * CK + 8 * ci, yr);
+      if constexpr (ALLU) {  // the range ends at the last row
+        const int64_t r0 = t * PB_TP;
+        buffer_store(yr, buffer_rsrc((T*)a.z + r0 * CK, (int)(min<int64_t>(PB_TP, rows - r0) * CK * sizeof(T))),
+                     (uint32_t)((xpl * CK + 8 * ci) * (int)sizeof(T)));
+      } else {
+        if (r < rows) store8((T*)a.z + r * CK + 8 * ci, yr);
+      }
     }
     if (tid < PB_TP) mk[tid] = TypeOps<T>::to_f32(mraw);
   };
@@ -467,9 +477,21 @@ __global__ __launch_bounds__(PB_NT, 1) void trimul_proj_bwd_kernel(const gnn_tri
           dg[e] = gm * p * sgm * (1.0f - sgm);
         }
         const V4 dpr = TypeOps<T>::from_f32(dp), dgr = TypeOps<T>::from_f32(dg);
+        if constexpr (ALLU) {
+          // ranges from the tile's first row to the end of its last valid one (the row pitch
+          // is at least 2 c_hidden), so the lanes of rows past the end fall outside them
+          const int64_t r0 = t * PB_TP;
+          const int nv = (int)min<int64_t>(PB_TP, rows - r0);
+          const int range = (int)(((int64_t)(nv - 1) * a.dl_ld + Ch2) * (int64_t)sizeof(T));
+          const uint32_t off = (uint32_t)(((int64_t)(32 * s + l32) * a.dl_ld + c0) * (int64_t)sizeof(T));
+          buffer_store(dpr, buffer_rsrc((T*)a.d_p + r0 * a.dl_ld, range), off);
+          buffer_store(dgr, buffer_rsrc((T*)a.d_g + r0 * a.dl_ld, range), off);
+        }
         if (rok) {
-          store4((T*)a.d_p + row * a.dl_ld + c0, dpr);
-          store4((T*)a.d_g + row * a.dl_ld + c0, dgr);
+          if constexpr (!ALLU) {
+            store4((T*)a.d_p + row * a.dl_ld + c0, dpr);
+            store4((T*)a.d_g + row * a.dl_ld + c0, dgr);
+          }
           const f32x4 dpf = TypeOps<T>::to_f32(dpr), dgf = TypeOps<T>::to_f32(dgr);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -490,8 +512,10 @@ __global__ __launch_bounds__(PB_NT, 1) void trimul_proj_bwd_kernel(const gnn_tri
     ln_finish(t);
     __syncthreads();
     for (; t < ntiles; t += gridDim.x) {
-      const int64_t tn = t + gridDim.x;
-      const bool has_next = tn < ntiles;  // uniform over the workgroup
+      // ALLU: the last tile is requested (and normalised, and its z stored) again, so that
+      // no load or store of the loop sits in a branch
+      const int64_t tn = ALLU && t + gridDim.x >= ntiles ? t : t + gridDim.x;
+      const bool has_next = ALLU || tn < ntiles;  // uniform over the workgroup
       if (has_next) {
         load_x(tn);
         load_d(tn, dan);
@@ -532,7 +556,11 @@ __global__ __launch_bounds__(PB_NT, 1) void trimul_proj_bwd_kernel(const gnn_tri
 template <typename T, int CK>
 int launch_proj_bwd(const gnn_trimul_proj_bwd_args& a, hipStream_t st) {
   const int64_t grid = trimul_proj_bwd_partials(a.rows);
-  hipLaunchKernelGGL((trimul_proj_bwd_kernel<T, CK>), dim3((uint32_t)grid), dim3(PB_NT), 0, st, a);
+  // the buffer ranges of one tile: 64 rows of z and of the gradient's row pitch
+  if (2 * a.Ch == 32 * PB_W && (int64_t)PB_TP * std::max<int64_t>(a.dl_ld, CK) * 2 < ((int64_t)1 << 31))
+    hipLaunchKernelGGL((trimul_proj_bwd_kernel<T, CK, true>), dim3((uint32_t)grid), dim3(PB_NT), 0, st, a);
+  else
+    hipLaunchKernelGGL((trimul_proj_bwd_kernel<T, CK, false>), dim3((uint32_t)grid), dim3(PB_NT), 0, st, a);
   return (int)hipGetLastError();
 }
 
