@@ -168,6 +168,45 @@ __device__ __forceinline__ PTile proj_tile(int64_t t, int N, bool outgoing) {
   }
   return r;
 }
+// The tiles t, t + G, t + 2G, ... of a persistent workgroup as mixed-radix digits (d0
+// fastest, radix r0; then d1, radix r1; then d2), advanced by G's digits with carries: a
+// scalar add and compare per digit and step in place of the 64-bit divisions of the tile
+// decomposition, which the compiler emulates on the vector ALU (and moves back to scalar
+// registers) for every tile.
+struct TileWalk {
+  int d0, d1, d2, g0, g1, g2, r0, r1;
+  __device__ __forceinline__ TileWalk(int64_t t, int64_t G, int r0_, int r1_) : r0(r0_), r1(r1_) {
+    d0 = (int)(t % r0);
+    const int64_t q = t / r0;
+    d1 = (int)(q % r1);
+    d2 = (int)(q / r1);
+    g0 = (int)(G % r0);
+    const int64_t h = G / r0;
+    g1 = (int)(h % r1);
+    g2 = (int)(h / r1);
+  }
+  __device__ __forceinline__ void step() {
+    d0 += g0;
+    const int c0 = d0 >= r0;
+    d0 -= c0 ? r0 : 0;
+    d1 += g1 + c0;
+    const int c1 = d1 >= r1;
+    d1 -= c1 ? r1 : 0;
+    d2 += g2 + c1;
+  }
+};
+// proj_tile's decomposition for a walk: outgoing (c0 / PTP, row, b), incoming (row, c0 / PTP, b)
+__device__ __forceinline__ TileWalk proj_walk(int64_t t, int64_t G, int N, bool outgoing) {
+  const int ntp = (N + PTP - 1) / PTP;
+  return outgoing ? TileWalk(t, G, ntp, N) : TileWalk(t, G, N, ntp);
+}
+__device__ __forceinline__ PTile proj_tile(const TileWalk& w, bool outgoing) {
+  PTile r;
+  r.c0 = (outgoing ? w.d0 : w.d1) * PTP;
+  r.row = outgoing ? w.d1 : w.d0;
+  r.b = w.d2;
+  return r;
+}
 __device__ __forceinline__ int64_t proj_pix(const PTile& tl, int pl, int N, bool outgoing) {
   const int cpos = tl.c0 + pl;
   const int pp = outgoing ? tl.row : cpos;
@@ -760,12 +799,15 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_x3_kernel(const gnn_trimul
   __syncthreads();  // partials, LayerNorm parameters and gate weights published
   ln_finish();
   __syncthreads();
+  TileWalk walk = proj_walk(t + gridDim.x, gridDim.x, N, outgoing);  // the next tile
   for (; t < ntiles; t += gridDim.x) {
     const int64_t tn = t + gridDim.x;
     const bool has_next = tn < ntiles;  // uniform over the workgroup
     PTile nxt = cur;
+    const PTile wt = proj_tile(walk, outgoing);
+    walk.step();
     if (has_next) {
-      nxt = proj_tile(tn, N, outgoing);
+      nxt = wt;
       load_x(nxt);
     }
     compute(cur);
@@ -1136,12 +1178,14 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
   ln_store(xr, mreg, 0);
   __syncthreads();
   int cb = 0;
+  TileWalk walk = proj_walk(t + gridDim.x, gridDim.x, N, outgoing);  // the next tile
   for (; t < ntiles; t += gridDim.x) {
     const int64_t tn = t + gridDim.x;
     const bool has_next = tn < ntiles;  // uniform over the workgroup
     // the next tile's x (the current one's again after the last tile: unconditional, so the
     // compiler sees no path on which these loads are still in flight at the next iteration)
-    const PTile nxt = has_next ? proj_tile(tn, N, outgoing) : cur;
+    const PTile nxt = has_next ? proj_tile(walk, outgoing) : cur;
+    walk.step();
     load_x(xr, mreg, nxt);
     compute(cur, cb);
     ln_store(xr, mreg, cb ^ 1);  // after the last tile into the free buffer: nobody reads it
@@ -1997,10 +2041,10 @@ __global__ __launch_bounds__(NT, GNN_OUTP_WGS) void trimul_out_persist_kernel(co
     for (int k = 0; k < NKS; ++k) wpf[k] = load8(wrow + 16 * k);
   }
 
+  // tiles as (pixel tile d0, row p = d1, batch b = d2) digits of a TileWalk
   // o chunk i of a thread: channel (tid + i NT) / 8, pixels 8 ((tid + i NT) % 8) ..
-  auto load_o = [&](V8 (&ov)[OCO], int64_t t) {
-    const int64_t row = t / ntile;  // b N + p
-    const int q0 = (int)(t - row * ntile) * PTO, p = (int)(row % N), b = (int)(row / N);
+  auto load_o = [&](V8 (&ov)[OCO], const TileWalk& w) {
+    const int q0 = w.d0 * PTO, p = w.d1, b = w.d2;
 #pragma unroll
     for (int i = 0; i < OCO; ++i) {
       const int c = tid + i * NT, ch = c >> 3, col = min(q0 + (c & 7) * 8, (int)NP - 8);
@@ -2008,9 +2052,9 @@ __global__ __launch_bounds__(NT, GNN_OUTP_WGS) void trimul_out_persist_kernel(co
     }
   };
   // g / out chunk i: pixel (tid + i NT) / 16, channels 8 ((tid + i NT) % 16) ..
-  auto load_g = [&](V8 (&gr)[OCG], int64_t t) {
-    const int64_t row = t / ntile;
-    const int q0 = (int)(t - row * ntile) * PTO, last = min(N - q0, PTO) - 1;
+  auto load_g = [&](V8 (&gr)[OCG], const TileWalk& w) {
+    const int64_t row = (int64_t)w.d2 * N + w.d1;
+    const int q0 = w.d0 * PTO, last = min(N - q0, PTO) - 1;
     const T* gblk = gbase + (row * N + q0) * C;
 #pragma unroll
     for (int i = 0; i < OCG; ++i) {
@@ -2029,20 +2073,24 @@ __global__ __launch_bounds__(NT, GNN_OUTP_WGS) void trimul_out_persist_kernel(co
       store8(&ot[(c >> 3) * OR + (c & 7) * 8], ov[i]);
     }
   };
-  // the tile after t of this workgroup; the last tile requests itself again, so that the
-  // loads stay unconditional
-  auto next_of = [&](int64_t t) { return t + gridDim.x < ntiles ? t + (int64_t)gridDim.x : t; };
+  // tiles t (w0), t + grid (w1) and t + 2 grid (w2); past the last tile a load requests the
+  // last one again, so that the loads stay unconditional
   int64_t t = blockIdx.x;
   if (t >= ntiles) return;  // uniform over the workgroup
+  const int64_t G = gridDim.x;
+  TileWalk w0(t, G, ntile, N), w1 = w0, w2 = w0;
+  w1.step();
+  w2.step();
+  w2.step();
   V8 ov[OCO], gr[OCG];
-  load_o(ov, t);
-  load_g(gr, t);
+  load_o(ov, w0);
+  load_g(gr, w0);
   put_o(ov);
-  load_o(ov, next_of(t));
-  for (; t < ntiles; t += gridDim.x) {
-    const int64_t tn = next_of(t);
-    const int64_t row = t / ntile;
-    const int q0 = (int)(t - row * ntile) * PTO, npix = min(N - q0, PTO);
+  load_o(ov, t + G < ntiles ? w1 : w0);
+  for (; t < ntiles; t += G) {
+    const bool n1 = t + G < ntiles, n2 = t + 2 * G < ntiles;  // uniform
+    const int64_t row = (int64_t)w0.d2 * N + w0.d1;
+    const int q0 = w0.d0 * PTO, npix = min(N - q0, PTO);
     __syncthreads();  // the o tile (and, on the first tile, the LayerNorm parameters) in LDS
 
     // ---- LayerNorm over channels, as the per-tile kernel: thread = (pixel pair tid % 32,
@@ -2139,10 +2187,13 @@ __global__ __launch_bounds__(NT, GNN_OUTP_WGS) void trimul_out_persist_kernel(co
         buffer_store(val, rs, (uint32_t)((px * C + 8 * c8) * (int)sizeof(T)));
       }
     }
-    load_g(gr, tn);
+    load_g(gr, n1 ? w1 : w0);
     __syncthreads();  // ys (region 1) is rewritten by the next tile's o
     put_o(ov);
-    load_o(ov, next_of(tn));
+    load_o(ov, n2 ? w2 : (n1 ? w1 : w0));
+    w0 = w1;
+    w1 = w2;
+    w2.step();
   }
 }
 
