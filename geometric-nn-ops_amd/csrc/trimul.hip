@@ -1997,27 +1997,48 @@ __global__ __launch_bounds__(NT, 2) void trimul_out_kernel(const gnn_trimul_args
 // pixel) and the out stores are buffer stores whose range ends at the tile's last pixel, so
 // the hardware drops the lanes past N. No store sits in a branch, and the compiler's memory
 // counter waits for a tile's loads then never cover the stores issued after them.
+// fp32 inputs under the bf16x3 split (X3) take the same walk with every operand split into
+// bf16 hi / lo halves once: the p_out fragments at launch, the normalised tile where the
+// LayerNorm writes it (two bf16 planes); the products are lo*hi + hi*lo + hi*hi, as the
+// per-tile kernel's, on the same split values in the same order.
 #ifndef GNN_OUTP_WGS  // workgroups per CU the register allocation is held to
 #define GNN_OUTP_WGS 3
 #endif
 #ifndef GNN_OUT_PERSIST  // 0: the per-tile kernel for C = c_hidden = 128 too
 #define GNN_OUT_PERSIST 1
 #endif
+#ifndef GNN_OUTP_WGS_X3  // the same for the fp32 (bf16x3) instantiation (72 KB of LDS each)
+#define GNN_OUTP_WGS_X3 2
+#endif
+// LDS of the persistent output stage: region 1 (the raw o tile, then the pass tile), the
+// normalised tile (T, or two bf16 planes under X3), LayerNorm gamma / beta, partial sums and
+// the p_out bias (fp32).
 template <typename T>
-__global__ __launch_bounds__(NT, GNN_OUTP_WGS) void trimul_out_persist_kernel(const gnn_trimul_args a, int64_t NP,
-                                                                                size_t off_g, size_t off_o) {
-  static_assert(sizeof(T) == 2, "persistent output stage: 16-bit types");
+__host__ __device__ constexpr size_t outp_zplane_bytes() {
+  return sizeof(T) == 4 ? 2 * (size_t)PTO * (128 + 8) * 2 : (size_t)PTO * (128 + lds_pad<T>()) * sizeof(T);
+}
+template <typename T>
+__host__ __device__ inline size_t outp_lds_bytes() {
+  return out_region1_elems(128, lds_pad<T>()) * sizeof(T) + outp_zplane_bytes<T>() + (2 * 128 + 8 * PTO + OPC) * 4;
+}
+
+template <typename T>
+__global__ __launch_bounds__(NT, sizeof(T) == 4 ? GNN_OUTP_WGS_X3 : GNN_OUTP_WGS) void trimul_out_persist_kernel(
+    const gnn_trimul_args a, int64_t NP, size_t off_g, size_t off_o) {
   typedef typename TypeOps<T>::V8 V8;
+  constexpr bool X3 = sizeof(T) == 4;  // fp32 under bf16x3
   constexpr int C = 128, Ch = 128, PAD = lds_pad<T>();
-  constexpr int OR = PTO + PAD, ZR = Ch + PAD, YR = OPC + PAD;
+  constexpr int OR = PTO + PAD, ZR = Ch + (X3 ? 8 : PAD), YR = OPC + PAD;
   constexpr int NKS = Ch / 16;                 // k-steps of p_out
   constexpr int OCO = Ch * (PTO / 8) / NT;     // 8-pixel o chunks per thread
   constexpr int OCG = PTO * C / 8 / NT;        // 8-channel g / out chunks per thread
+  typedef typename std::conditional<X3, bf16, T>::type ZT;  // the normalised tile's element
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T* ot = reinterpret_cast<T*>(smem_raw);
   T* ys = ot;  // the raw o tile is dead once the LayerNorm has written zs
-  T* zs = ot + out_region1_elems(Ch, PAD);
-  float* lnw = reinterpret_cast<float*>(zs + (size_t)PTO * ZR);
+  ZT* zs = reinterpret_cast<ZT*>(ot + out_region1_elems(Ch, PAD));  // X3: the hi plane
+  ZT* zsl = zs + (size_t)PTO * ZR;                                   // X3: the lo plane
+  float* lnw = reinterpret_cast<float*>(smem_raw + out_region1_elems(Ch, PAD) * sizeof(T) + outp_zplane_bytes<T>());
   float* lnb = lnw + Ch;
   float* red = lnb + Ch;         // LayerNorm partial sums [8 * PTO]
   float* bpo_s = red + 8 * PTO;  // p_out bias [C]
@@ -2034,11 +2055,18 @@ __global__ __launch_bounds__(NT, GNN_OUTP_WGS) void trimul_out_persist_kernel(co
     lnb[c] = ld_or<T>(a.ln_out_b, c, 0.f);
   }
   for (int c = tid; c < C; c += NT) bpo_s[c] = ld_or<T>(a.p_out_b, c, 0.f);
-  V8 wpf[NKS];  // rows 32 wave + l32 of p_out_w
+  // rows 32 wave + l32 of p_out_w: as loaded (16-bit), or split into hi / lo halves (X3)
+  typedef typename std::conditional<X3, bf16x8, V8>::type WF;
+  WF wpf[NKS], wpl[X3 ? NKS : 1];
   {
     const T* wrow = (const T*)a.p_out_w + (int64_t)(32 * wave + l32) * Ch + 8 * g;
 #pragma unroll
-    for (int k = 0; k < NKS; ++k) wpf[k] = load8(wrow + 16 * k);
+    for (int k = 0; k < NKS; ++k) {
+      if constexpr (X3)
+        split_bf16(load8(wrow + 16 * k), wpf[k], wpl[k]);
+      else
+        wpf[k] = load8(wrow + 16 * k);
+    }
   }
 
   // tiles as (pixel tile d0, row p = d1, batch b = d2) digits of a TileWalk
@@ -2141,8 +2169,18 @@ __global__ __launch_bounds__(NT, GNN_OUTP_WGS) void trimul_out_persist_kernel(co
           v0[e] = (x[0] - mean[0]) * rs0 * lnw[k + e] + lnb[k + e];
           v1[e] = (x[1] - mean[1]) * rs1 * lnw[k + e] + lnb[k + e];
         }
-        store8(&zs[(2 * pp) * ZR + k], TypeOps<T>::from_f32(v0));
-        store8(&zs[(2 * pp + 1) * ZR + k], TypeOps<T>::from_f32(v1));
+        if constexpr (X3) {
+          bf16x8 h0, l0, h1, l1;
+          split_bf16(v0, h0, l0);
+          split_bf16(v1, h1, l1);
+          store8(&zs[(2 * pp) * ZR + k], h0);
+          store8(&zsl[(2 * pp) * ZR + k], l0);
+          store8(&zs[(2 * pp + 1) * ZR + k], h1);
+          store8(&zsl[(2 * pp + 1) * ZR + k], l1);
+        } else {
+          store8(&zs[(2 * pp) * ZR + k], TypeOps<T>::from_f32(v0));
+          store8(&zs[(2 * pp + 1) * ZR + k], TypeOps<T>::from_f32(v1));
+        }
       }
     }
     __syncthreads();
@@ -2158,8 +2196,17 @@ __global__ __launch_bounds__(NT, GNN_OUTP_WGS) void trimul_out_persist_kernel(co
 #pragma unroll
       for (int k = 0; k < NKS; ++k)
 #pragma unroll
-        for (int s = 0; s < PTO / 32; ++s)
-          Mma<T, PREC_NATIVE>::step(acc[s], wpf[k], load8(&zs[(32 * s + l32) * ZR + 16 * k + 8 * g]));
+        for (int s = 0; s < PTO / 32; ++s) {
+          const int zo = (32 * s + l32) * ZR + 16 * k + 8 * g;
+          if constexpr (X3) {  // lo * hi + hi * lo + hi * hi, as Mma<float, PREC_BF16X3>
+            const bf16x8 zh = load8(&zs[zo]), zl = load8(&zsl[zo]);
+            acc[s] = mfma_bf16(wpl[k], zh, acc[s]);
+            acc[s] = mfma_bf16(wpf[k], zl, acc[s]);
+            acc[s] = mfma_bf16(wpf[k], zh, acc[s]);
+          } else {
+            Mma<T, PREC_NATIVE>::step(acc[s], wpf[k], load8(&zs[zo]));
+          }
+        }
 #pragma unroll
       for (int rg = 0; rg < 4; ++rg) {
         const f32x4 b4 = *reinterpret_cast<const f32x4*>(&bpo_s[32 * wave + 8 * rg + 4 * g]);
@@ -2184,7 +2231,13 @@ __global__ __launch_bounds__(NT, GNN_OUTP_WGS) void trimul_out_persist_kernel(co
         const int idx = tid + i * NT, px = idx >> 4, c8 = idx & 15;
         const f32x8 y = TypeOps<T>::to_f32(load8(&ys[px * YR + 8 * c8]));
         const V8 val = TypeOps<T>::from_f32(y * TypeOps<T>::to_f32(gr[i]));
-        buffer_store(val, rs, (uint32_t)((px * C + 8 * c8) * (int)sizeof(T)));
+        const uint32_t off = (uint32_t)((px * C + 8 * c8) * (int)sizeof(T));
+        if constexpr (X3) {  // 32 bytes: two 16-byte stores
+          buffer_store(f32x4{val[0], val[1], val[2], val[3]}, rs, off);
+          buffer_store(f32x4{val[4], val[5], val[6], val[7]}, rs, off + 16u);
+        } else {
+          buffer_store(val, rs, off);
+        }
       }
     }
     load_g(gr, n1 ? w1 : w0);
@@ -2515,12 +2568,14 @@ int launch_out_w(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st
   const int64_t NP = round_up(a.N, 32);
   const int64_t ntile = (a.N + PTO - 1) / PTO;
   const size_t smem = out_smem<T>(a);
-  if constexpr (sizeof(T) == 2 && PREC == PREC_NATIVE && CK == 128 && CHK == 128) {
+  if constexpr (((sizeof(T) == 2 && PREC == PREC_NATIVE) || (sizeof(T) == 4 && PREC == PREC_BF16X3)) && CK == 128 &&
+                CHK == 128) {
     if (GNN_OUT_PERSIST) {
+      const size_t psmem = outp_lds_bytes<T>();
       const void* pf = (const void*)trimul_out_persist_kernel<T>;
-      if (smem > 64 * 1024) (void)hipFuncSetAttribute(pf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-      const int64_t grid = std::min<int64_t>(a.B * a.N * ntile, persistent_grid(pf, NT, smem));
-      hipLaunchKernelGGL((trimul_out_persist_kernel<T>), dim3((uint32_t)grid), dim3(NT), smem, st, a, NP, L.off_g,
+      if (psmem > 64 * 1024) (void)hipFuncSetAttribute(pf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)psmem);
+      const int64_t grid = std::min<int64_t>(a.B * a.N * ntile, persistent_grid(pf, NT, psmem));
+      hipLaunchKernelGGL((trimul_out_persist_kernel<T>), dim3((uint32_t)grid), dim3(NT), psmem, st, a, NP, L.off_g,
                          L.off_o);
       return (int)hipGetLastError();
     }

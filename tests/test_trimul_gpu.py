@@ -123,21 +123,24 @@ def test_batched(direction, shape):
 
 
 @DIRECTIONS
-@pytest.mark.parametrize(("B", "N", "dtype"), [(2, 70, torch.bfloat16), (1, 130, torch.float16), (3, 64, torch.bfloat16)],
-                         ids=["b2_n70_bf16", "b1_n130_fp16", "b3_n64_bf16"])
-def test_output_stage_tiles_and_bounds(direction, B, N, dtype):
+@pytest.mark.parametrize(("B", "N", "dtype", "precision"),
+                         [(2, 70, torch.bfloat16, "ieee"), (1, 130, torch.float16, "ieee"), (3, 64, torch.bfloat16, "ieee"),
+                          (2, 70, torch.float32, "tf32")],
+                         ids=["b2_n70_bf16", "b1_n130_fp16", "b3_n64_bf16", "b2_n70_fp32_tf32"])
+def test_output_stage_tiles_and_bounds(direction, B, N, dtype, precision):
     """The output stage at C = c_hidden = 128 (a fixed grid of workgroups walking 64-pixel
     tiles with the next tile's o and g in flight, out written by buffer stores whose range
-    ends at the tile's last pixel): rows whose last tile is partial, several batches, against
-    the oracle; the stage run again into a buffer with a guard region after the output leaves
-    the guard untouched and writes the same result."""
+    ends at the tile's last pixel; fp32 under 'tf32' with the operands split into bf16 halves
+    once): rows whose last tile is partial, several batches, against the oracle; the stage run
+    again into a buffer with a guard region after the output leaves the guard untouched and
+    writes the same result."""
     from geometric_nn_ops_torch.triangle._kernels import trimul as K
 
     C = 128
     w = trimul_weights(C, C, dtype, seed=61, biases=True, ln_random=True)
     x, mask = pair_input(B, N, C, dtype, seed=62)
     wd = {k: v.to(DEV) for k, v in w.items()}
-    with torch.no_grad():
+    with torch.no_grad(), matmul_precision(precision):
         args, keep, out, ws, off = K.build_args(x.to(DEV), direction, mask.to(DEV), 1e-5, wd)
         for stage in ("gnn_trimul_proj", "gnn_trimul_contract", "gnn_trimul_out"):
             K.run_stage(stage, args, torch.device(DEV))
@@ -145,8 +148,9 @@ def test_output_stage_tiles_and_bounds(direction, B, N, dtype):
         args.out = guard.data_ptr()
         K.run_stage("gnn_trimul_out", args, torch.device(DEV))
         torch.cuda.synchronize()
-    assert_close_to_oracle("out", out, oracle(x, direction, mask, w), Tolerance(1 - 1e-4, 2e-2),
-                           rel_fro_max=NORTH_STAR_REL_FRO)
+    tol = TRIMUL_TOL[torch.float32, "tf32"] if dtype == torch.float32 else Tolerance(1 - 1e-4, 2e-2)
+    assert_close_to_oracle("out", out, oracle(x, direction, mask, w), tol,
+                           rel_fro_max=None if dtype == torch.float32 else NORTH_STAR_REL_FRO)
     assert torch.equal(guard[:out.numel()].view(out.shape), out)
     assert bool((guard[out.numel():] == 7.0).all())
 
