@@ -23,6 +23,7 @@
 #include "gnn_internal.hpp"
 
 #include <algorithm>
+#include <string>
 #include <type_traits>
 
 namespace gnn {
@@ -2594,14 +2595,15 @@ int launch_out(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) 
 }
 
 int check_args(const gnn_trimul_args& a, const char* who) {
-  (void)who;
+  // the contraction (stage 2) depends on the B * Ch planes and N only: any width
+  const bool widths = std::string(who) != "contract";
   if (!a.x || !a.out || !a.p_in_w || !a.g_in_w || !a.p_out_w || !a.g_out_w)
     return set_error(GNN_ERR_ARG, "trimul: x, out and the four projection weights are required");
   if (a.B < 1 || a.N < 1 || a.C < 1 || a.Ch < 1)
     return set_error(GNN_ERR_ARG, "trimul: B, N, C and Ch must be positive");
   if (a.C % 32 != 0 || a.Ch % 32 != 0)
     return set_error(GNN_ERR_UNSUPPORTED, "trimul: c_z and c_hidden must be multiples of 32");
-  if (a.C > 512 || a.Ch > 512)
+  if (widths && (a.C > 512 || a.Ch > 512))
     return set_error(GNN_ERR_UNSUPPORTED, "trimul: c_z and c_hidden above 512 are not supported");
   if (a.dtype != GNN_BF16 && a.dtype != GNN_F16 && a.dtype != GNN_F32)
     return set_error(GNN_ERR_ARG, "trimul: unknown dtype");
@@ -2612,11 +2614,11 @@ int check_args(const gnn_trimul_args& a, const char* who) {
     if (((uintptr_t)ptr) % 16 != 0)
       return set_error(GNN_ERR_ARG, "trimul: x, out, weights, workspace and gate must be 16-byte aligned");
   const size_t e = a.dtype == GNN_F32 ? 4 : 2;
-  if (e == 4 && (a.C > 256 || a.Ch > 256))
+  if (widths && e == 4 && (a.C > 256 || a.Ch > 256))
     return set_error(GNN_ERR_UNSUPPORTED, "trimul: fp32 c_z and c_hidden above 256 are not supported");
   const size_t proj_bytes = e == 2 ? proj_lds<bf16>(a.C).total : proj_lds<float>(a.C).total;
   const size_t out_lds = out_lds_bytes(a.Ch, e);
-  if (proj_bytes > 160 * 1024 || out_lds > 160 * 1024)
+  if (widths && (proj_bytes > 160 * 1024 || out_lds > 160 * 1024))
     return set_error(GNN_ERR_UNSUPPORTED, "trimul: channel count too large for the LDS tiles");
   if (a.B * a.N * ((a.N + PTO - 1) / PTO) >= ((int64_t)1 << 31))
     return set_error(GNN_ERR_UNSUPPORTED, "trimul: grid too large");

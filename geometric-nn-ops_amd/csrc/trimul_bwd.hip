@@ -180,6 +180,63 @@ __global__ __launch_bounds__(LN_THREADS) void layernorm_rows_kernel(const gnn_la
   }
 }
 
+// ---- forward LayerNorm of wide rows (512 < K <= LN_WIDE_MAX_K, K a multiple of 32): one
+// wave per row, walking it in 512-column chunks (8 consecutive columns per lane, 16-byte
+// loads) three times -- the sum, the squared deviations from the mean, the normalised output
+// -- so that nothing of the row is held in registers; the row (at most 16 KB) is re-read
+// from the caches. The same two-pass statistics as the narrow kernel.
+constexpr int LN_WIDE_MAX_K = 8192;
+constexpr int LN_WIDE_WAVES = 4;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(64 * LN_WIDE_WAVES) void layernorm_wide_kernel(const gnn_layernorm_args a) {
+  const int K = (int)a.K, lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * LN_WIDE_WAVES + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * LN_WIDE_WAVES;
+  const float inv_k = 1.0f / (float)K;
+  for (int64_t r = wave; r < a.rows; r += nwaves) {
+    const T* xr = (const T*)a.x + r * a.x_stride;
+    float s = 0.f;
+    for (int k = 8 * lane; k < K; k += 512) {
+      const f32x8 v = TypeOps<T>::to_f32(load8(xr + k));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += v[e];
+    }
+    const float mean = wave_sum(s) * inv_k;
+    float q = 0.f;
+    for (int k = 8 * lane; k < K; k += 512) {
+      const f32x8 v = TypeOps<T>::to_f32(load8(xr + k));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = v[e] - mean;
+        q += d * d;
+      }
+    }
+    const float rstd = 1.0f / sqrtf(wave_sum(q) * inv_k + a.eps);
+    T* orow = (T*)a.out + r * a.out_stride;
+    for (int k = 8 * lane; k < K; k += 512) {
+      const f32x8 v = TypeOps<T>::to_f32(load8(xr + k));
+      f32x8 y;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = (v[e] - mean) * rstd * ld1<T>(a.weight, k + e, 1.f) + ld1<T>(a.bias, k + e, 0.f);
+      store8(orow + k, TypeOps<T>::from_f32(y));
+    }
+  }
+}
+
+template <typename T>
+int launch_ln_wide(const gnn_layernorm_args& a, hipStream_t st) {
+  const int64_t grid = std::min<int64_t>((a.rows + LN_WIDE_WAVES - 1) / LN_WIDE_WAVES, 8192);
+  hipLaunchKernelGGL((layernorm_wide_kernel<T>), dim3((uint32_t)grid), dim3(64 * LN_WIDE_WAVES), 0, st, a);
+  return (int)hipGetLastError();
+}
+
 template <typename T, bool BWD>
 int launch_ln(const gnn_layernorm_args& a, hipStream_t st) {
   const int grid = (int)layernorm_partials(a.rows, a.K);
@@ -947,9 +1004,22 @@ int64_t layernorm_partials(int64_t rows, int64_t K) {
 }
 
 int layernorm_rows(const gnn_layernorm_args& a, hipStream_t st) {
-  if (a.K % 32 != 0 || a.K > LN_MAX_K)
-    return set_error(GNN_ERR_UNSUPPORTED, "layernorm_rows: K must be a multiple of 32, at most 512");
   const bool bwd = a.dy != nullptr;
+  if (a.K % 32 == 0 && a.K > LN_MAX_K && a.K <= LN_WIDE_MAX_K && !bwd) {
+    // wide rows: forward only; 16-byte row accesses
+    const int64_t e = a.dtype == GNN_F32 ? 4 : 2;
+    if (((uintptr_t)a.x | (uintptr_t)a.out) % 16 != 0 || (a.x_stride * e) % 16 != 0 || (a.out_stride * e) % 16 != 0)
+      return set_error(GNN_ERR_ARG, "layernorm_rows: rows wider than 512 need 16-byte aligned rows");
+    switch (a.dtype) {
+      case GNN_BF16: return launch_ln_wide<bf16>(a, st);
+      case GNN_F16: return launch_ln_wide<f16>(a, st);
+      case GNN_F32: return launch_ln_wide<float>(a, st);
+    }
+    return set_error(GNN_ERR_ARG, "layernorm_rows: unknown dtype");
+  }
+  if (a.K % 32 != 0 || a.K > LN_MAX_K)
+    return set_error(GNN_ERR_UNSUPPORTED,
+                     "layernorm_rows: K must be a multiple of 32, at most 512 (8192 for the forward)");
   switch (a.dtype) {
     case GNN_BF16: return bwd ? launch_ln<bf16, true>(a, st) : launch_ln<bf16, false>(a, st);
     case GNN_F16: return bwd ? launch_ln<f16, true>(a, st) : launch_ln<f16, false>(a, st);

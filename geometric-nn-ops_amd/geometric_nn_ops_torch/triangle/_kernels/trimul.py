@@ -28,6 +28,7 @@ _ARG_FIELD = {
     "g_out_weight": "g_out_w", "g_out_bias": "g_out_b",
 }
 MAX_CHANNELS = 512
+WIDE_MAX_CHANNELS = 8192  # the wide-row LayerNorm's limit (gnn_layernorm_rows forward)
 
 
 def _pad32(n: int) -> int:
@@ -45,6 +46,14 @@ def supports(x: torch.Tensor, p_in_weight: torch.Tensor, *, padded: bool = True)
         return False
     limit = 256 if x.dtype == torch.float32 else MAX_CHANNELS
     return _pad32(c_z) <= limit and _pad32(c_hidden) <= limit
+
+
+def wide_supported(x: torch.Tensor, p_in_weight: torch.Tensor) -> bool:
+    """Whether ``trimul_wide_hip`` covers these widths: 16-bit inputs whose c_z or c_hidden
+    is above the fused kernels' 512, both multiples of 32 and at most 8192."""
+    C, Ch = x.shape[-1], p_in_weight.shape[0] // 2
+    return (x.dtype in (torch.bfloat16, torch.float16) and x.dim() >= 3 and C % 32 == 0 and Ch % 32 == 0
+            and max(C, Ch) > MAX_CHANNELS and max(C, Ch) <= WIDE_MAX_CHANNELS)
 
 
 def _pad_channels(x, weights):
@@ -211,6 +220,8 @@ def trimul_hip(
         g_out_weight=g_out_weight, g_out_bias=g_out_bias,
     )
     C, Ch = x.shape[-1], p_in_weight.shape[0] // 2
+    if wide_supported(x, p_in_weight):  # widths above the fused kernels' tiles
+        return trimul_wide_hip(x, direction, mask, eps, weights)
     if C % 32 or Ch % 32:  # zero-padded copies; the LayerNorms average over the real widths
         xp, wp, _, _ = _pad_channels(x, weights)
         args, keep, out, workspace, _ = build_args(xp, direction, mask, eps, wp)
@@ -222,6 +233,77 @@ def trimul_hip(
     run_stage("gnn_trimul_fwd", args, x.device)
     del keep, workspace
     return out.reshape(x.shape)
+
+
+def trimul_wide_hip(x, direction, mask, eps, weights):
+    """The forward for 16-bit widths above the fused kernels' 512 (``wide_supported``), on
+    this library's kernels where the math is not a plain matrix product: LN_in and LN_out on
+    ``gnn_layernorm_rows`` (its wide-row kernel), the contraction on ``gnn_trimul_contract``
+    (stage 2 takes any width), a / b moved into the contraction's per-channel planes and o out
+    of them by ``gnn_trimul_relayout``; the three input projections as one ``[4 Ch + C, C]``
+    linear and p_out on the vendor GEMM; the sigmoid gates and the mask in torch, in the
+    reference's order and roundings (``_reference/trimul.py:57-97``). The pair grid is taken
+    to NP = round_up(N, 32) with the pixels past N masked out (a = b = 0 there), so that the
+    relayout's row blocks are the contraction's; the output is cut back to N."""
+    outgoing = is_outgoing(direction)
+    lead, N, C = x.shape[:-3], x.shape[-3], x.shape[-1]
+    Ch = weights["p_in_weight"].shape[0] // 2
+    B, NP = math.prod(lead), _pad32(N)
+    dev, dt = x.device, x.dtype
+    w = {k: (None if v is None else _kernel_ready(v, x)) for k, v in weights.items()}
+    xb = x.reshape(B, N, N, C)
+    m = (torch.ones((B, N, N), device=dev, dtype=dt) if mask is None
+         else mask.to(device=dev, dtype=dt).expand(*x.shape[:-1]).reshape(B, N, N))
+    if NP != N:
+        xb = torch.nn.functional.pad(xb, (0, 0, 0, NP - N, 0, NP - N))
+        m = torch.nn.functional.pad(m, (0, NP - N, 0, NP - N))
+    M = B * NP * NP
+    z = layernorm_rows_hip(_aligned(xb.reshape(M, C)), w.get("norm_in_weight"), w.get("norm_in_bias"), eps)
+
+    def bias(key, n):
+        return torch.zeros(n, device=dev, dtype=dt) if w.get(key) is None else w[key]
+
+    lin = torch.nn.functional.linear(
+        z, torch.cat([w["p_in_weight"], w["g_in_weight"], w["g_out_weight"]], 0),
+        torch.cat([bias("p_in_bias", 2 * Ch), bias("g_in_bias", 2 * Ch), bias("g_out_bias", C)]))
+    del z
+    p = lin[:, :2 * Ch] * torch.sigmoid(lin[:, 2 * Ch:4 * Ch])
+    p = _aligned(p * m.reshape(M, 1))
+    gate_out = torch.sigmoid(lin[:, 4 * Ch:])
+    del lin
+    # a and b into the contraction's k-blocked planes (outgoing: plane row i, column k;
+    # incoming: transposed per channel), then the contraction at NP. The stage-2 call reads
+    # only the workspace's a / b and writes its o (x, out, the weights and the gate buffer it
+    # is given are checked, not read), so the workspace stops before the gate region.
+    dtc = _lib.DTYPE_CODE[dt]
+    off = (ctypes.c_size_t * 4)()
+    _lib.load().gnn_trimul_workspace_bytes(B, NP, C, Ch, dtc, off)
+    workspace = torch.empty(off[2], device=dev, dtype=torch.uint8)
+    args = _lib.TrimulArgs()
+    any_ptr = w["p_in_weight"].data_ptr()
+    args.x = args.out = args.gate = any_ptr
+    args.p_in_w, args.g_in_w = w["p_in_weight"].data_ptr(), w["g_in_weight"].data_ptr()
+    args.p_out_w, args.g_out_w = w["p_out_weight"].data_ptr(), w["g_out_weight"].data_ptr()
+    args.workspace, args.workspace_bytes = workspace.data_ptr(), off[2]
+    args.B, args.N, args.C, args.Ch = B, NP, C, Ch
+    args.eps, args.outgoing, args.dtype = float(eps), int(outgoing), dtc
+    args.precision = _lib.PRECISION_CODE["ieee"]
+    for i, c0 in ((0, 0), (1, Ch)):
+        relayout_hip(p, workspace[off[i]:], _lib.RELAYOUT_PIXELS_TO_BLOCKED, B, NP, Ch, src_ld=2 * Ch,
+                     dst_ld=32, src_c0=c0, transposed=outgoing)
+    del p
+    run_stage("gnn_trimul_contract", args, dev)
+    o = torch.empty((M, Ch), device=dev, dtype=dt)
+    o_planes = workspace[off[3]:off[3] + B * Ch * NP * NP * o.element_size()].view(dt)
+    relayout_hip(o_planes, o, _lib.RELAYOUT_PLANES_TO_PIXELS, B, NP, Ch, src_ld=NP, dst_ld=Ch)
+    del workspace
+    on = layernorm_rows_hip(o, w.get("norm_out_weight"), w.get("norm_out_bias"), eps)
+    del o
+    out = torch.nn.functional.linear(on, w["p_out_weight"], w.get("p_out_bias")) * gate_out
+    out = out.view(B, NP, NP, C)
+    if NP != N:
+        out = out[:, :N, :N]
+    return out.reshape(*lead, N, N, C)
 
 
 # ------------------------------------------------------------------------------ backward

@@ -8,11 +8,14 @@ Where a call goes:
   * a call that needs gradients, on the same tensors, runs ``_TrimulHip``: the kernels'
     forward, then this library's backward (the reference's own grad calls run autograd
     through its torch code, _trimul.py:31-36);
-  * CPU tensors, other dtypes, channel counts above the kernels' tiles (c_z or c_hidden
-    above 512 once rounded up to a multiple of 32; 256 for fp32), calls that need gradients
-    with a width that is not a multiple of 32 (the forward pads such widths; the backward
-    kernels do not), and a mask that itself requires grad run the autograd-differentiable
-    torch restatement in ``_reference.trimul``.
+  * a forward with no backward whose 16-bit widths are above the fused kernels' tiles
+    (c_z or c_hidden above 512, both multiples of 32, at most 8192) runs the composed forward
+    ``trimul_wide_hip`` (this library's LayerNorm, relayout and contraction kernels with the
+    vendor GEMM for the linears);
+  * CPU tensors, other dtypes, other channel counts above the kernels' tiles (256 for fp32),
+    calls that need gradients with a width above 512 or not a multiple of 32 (the forward
+    pads such widths; the backward kernels do not), and a mask that itself requires grad run
+    the autograd-differentiable torch restatement in ``_reference.trimul``.
 The kernels are never silently replaced: without the HIP library a GPU call raises.
 
 The input projections come stacked: rows ``[0, C_hidden)`` of ``p_in_weight`` and
@@ -44,7 +47,8 @@ def _needs_torch_path(x: torch.Tensor, weights, mask=None) -> bool:
         return True
     if weights.get("p_in_weight") is not None and not _hip.supports(
             x, weights["p_in_weight"], padded=not _needs_grad(x, weights)):
-        return True
+        # widths above the fused kernels' tiles: the composed HIP forward, without gradients
+        return _needs_grad(x, weights) or not _hip.wide_supported(x, weights["p_in_weight"])
     return _needs_grad(x, weights) and mask is not None and mask.requires_grad
 
 

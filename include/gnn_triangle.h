@@ -246,7 +246,9 @@ int gnn_trimul_fwd(const gnn_trimul_args* args, void* stream);
  * and b channel-major, and the output gate g. Replaces trimul.py:435-439, :445-447. */
 int gnn_trimul_proj(const gnn_trimul_args* args, void* stream);
 
-/* Stage 2: per-channel N x N x N contraction of a and b into o.
+/* Stage 2: per-channel N x N x N contraction of a and b into o. It depends on the B * Ch
+ * planes and N only, so it takes c_z and c_hidden above the 512 of stages 1 and 3 (the
+ * wide-channel forward composes it with gnn_layernorm_rows and gnn_trimul_relayout).
  * Replaces _combine_projections (_reference/trimul.py:44-54) as called at trimul.py:442. */
 int gnn_trimul_contract(const gnn_trimul_args* args, void* stream);
 
@@ -323,7 +325,8 @@ int gnn_apb_gate_out(const gnn_apb_gate_out_args* args, void* stream);
  *            dy * xh / dy over the rows workgroup w handled (w < gnn_layernorm_partials):
  *            the weight / bias gradients are their sums over w.
  * Every tensor in `dtype` except `partial` (fp32); rows addressed by row strides (elements),
- * columns contiguous; K a multiple of 32 and at most 512.
+ * columns contiguous; K a multiple of 32 and at most 512 (forward: at most 8192; rows wider
+ * than 512 then need 16-byte aligned rows).
  */
 typedef struct gnn_layernorm_args {
   const void* x;      /* [rows, K] */

@@ -190,8 +190,11 @@ def test_kernel_dispatch_rule_for_gpu_tensors():
     # c_hidden = 48 (not a multiple of 32): the forward pads it, the backward does not
     assert not _trimul._needs_torch_path(FakeCuda(), {"p_in_weight": torch.zeros(96, 128)}.items())
     assert _trimul._needs_torch_path(FakeCuda(), {"p_in_weight": torch.zeros(96, 128, requires_grad=True)}.items())
-    # widths above the tiles once rounded up to a multiple of 32
-    assert _trimul._needs_torch_path(FakeCuda(), {"p_in_weight": torch.zeros(1088, 128)}.items())
+    # widths above the fused tiles: c_hidden = 544 (a multiple of 32) takes the composed wide
+    # forward without gradients and the torch path with them; c_hidden = 520 the torch path
+    assert not _trimul._needs_torch_path(FakeCuda(), {"p_in_weight": torch.zeros(1088, 128)}.items())
+    assert _trimul._needs_torch_path(FakeCuda(), {"p_in_weight": torch.zeros(1088, 128, requires_grad=True)}.items())
+    assert _trimul._needs_torch_path(FakeCuda(), {"p_in_weight": torch.zeros(1040, 128)}.items())
 
 
 def test_operators_have_fake_implementations():

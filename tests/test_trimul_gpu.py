@@ -361,25 +361,51 @@ def test_module_parameters_take_the_direct_implementation():
     torch.testing.assert_close(got, want, rtol=0, atol=0)
 
 
-@pytest.mark.parametrize("case", ["float64", "c_z_544", "fp32_c_z_288", "c_hidden_48_grad"])
+@pytest.mark.parametrize("case", ["float64", "c_z_550", "fp32_c_z_288", "c_hidden_48_grad", "c_z_544_grad"])
 def test_unsupported_configs_use_the_torch_path(case):
-    """Configurations without kernels: fp64, widths above the tiles once rounded up to a
-    multiple of 32 (512; 256 for fp32), and gradients with a width that is not a multiple of
-    32 (the backward kernels take multiples of 32). (Other calls that need gradients run the
-    HIP forward and backward: tests/test_trimul_bwd_gpu.py.)"""
+    """Configurations without kernels: fp64, widths above the fused tiles that are not
+    multiples of 32 (the wide-width forward takes multiples of 32 only; fp32 above 256), and
+    gradients with a width that is not a multiple of 32 or above 512 (the backward kernels'
+    limits). (Other calls that need gradients run the HIP forward and backward:
+    tests/test_trimul_bwd_gpu.py.)"""
     from geometric_nn_ops_torch.triangle import triangle_multiplicative_update
 
-    dtype = {"float64": torch.float64, "c_z_544": torch.bfloat16}.get(case, torch.float32)
-    c_z = {"c_z_544": 544, "fp32_c_z_288": 288}.get(case, 32)
+    dtype = {"float64": torch.float64, "c_z_550": torch.bfloat16, "c_z_544_grad": torch.bfloat16}.get(
+        case, torch.float32)
+    c_z = {"c_z_550": 550, "fp32_c_z_288": 288, "c_z_544_grad": 544}.get(case, 32)
     c_hidden = 48 if case == "c_hidden_48_grad" else 32
     w = {k: v.to(DEV) for k, v in trimul_weights(c_z, c_hidden, dtype, seed=1).items()}
     x, mask = pair_input(1, 12, c_z, dtype, seed=3)
     x = x.to(DEV)
-    if case == "c_hidden_48_grad":
+    if case.endswith("_grad"):
         x.requires_grad_()
     with dispatch_spy() as (ref, kern):
         triangle_multiplicative_update(x, "outgoing", mask.to(DEV), **w)
     assert ref.called and not kern.called
+
+
+@DIRECTIONS
+@pytest.mark.parametrize(("dtype", "c_z", "c_hidden", "N"),
+                         [(torch.bfloat16, 544, 576, 40), (torch.float16, 1024, 64, 32), (torch.bfloat16, 128, 640, 24)],
+                         ids=["bf16_544_576_n40", "fp16_1024_64_n32", "bf16_128_640_n24"])
+def test_wide_channel_widths(direction, dtype, c_z, c_hidden, N):
+    """Widths above the fused kernels' 512 (the reference's Triton kernels take any width,
+    trimul.py:310-314): the composed forward (trimul_wide_hip: the wide-row LayerNorm of
+    gnn_layernorm_rows, the input linears on the vendor GEMM, gnn_trimul_relayout into the
+    contraction's planes, gnn_trimul_contract at any width, LN_out, p_out and the gates) through
+    the public op, with projection biases, random LayerNorm parameters and a padded mask;
+    N = 40 and 24 take the pair grid to the next multiple of 32 with the padded pixels masked
+    out. Against the fp64 oracle."""
+    from geometric_nn_ops_torch.triangle import triangle_multiplicative_update
+
+    w = trimul_weights(c_z, c_hidden, dtype, seed=37, biases=True, ln_random=True)
+    x, mask = pair_input(1, N, c_z, dtype, seed=38)
+    with dispatch_spy() as (ref, kern), torch.no_grad():
+        got = triangle_multiplicative_update(x.to(DEV), direction, mask.to(DEV), **{k: v.to(DEV) for k, v in w.items()})
+    assert kern.called and not ref.called
+    assert got.shape == x.shape and got.dtype == dtype
+    assert_close_to_oracle("out", got, oracle(x, direction, mask, w), Tolerance(1 - 1e-4, 2e-2),
+                           rel_fro_max=NORTH_STAR_REL_FRO)
 
 
 @DIRECTIONS
