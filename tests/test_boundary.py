@@ -304,6 +304,16 @@ def test_trimul_backward_helper_argument_errors():
     a.K = a.x_stride = a.out_stride = a.dy_stride = 48
     assert lib.gnn_layernorm_rows(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
     assert b"multiple of 32" in lib.gnn_last_error()
+    # rows wider than 512: forward only, at most 8192, 16-byte aligned rows
+    a.K = a.x_stride = a.out_stride = a.dy_stride = 1024
+    assert lib.gnn_layernorm_rows(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED  # a backward
+    assert b"8192 for the forward" in lib.gnn_last_error()
+    a.dy = None
+    a.K = a.x_stride = a.out_stride = 8224
+    assert lib.gnn_layernorm_rows(ctypes.byref(a), None) == _lib.GNN_ERR_UNSUPPORTED
+    a.K, a.x_stride, a.out_stride, a.x = 1024, 1024, 1024, 4098
+    assert lib.gnn_layernorm_rows(ctypes.byref(a), None) == _lib.GNN_ERR_ARG
+    assert b"16-byte aligned" in lib.gnn_last_error()
     assert lib.gnn_layernorm_partials(1 << 20, 128) == 4096
     assert lib.gnn_layernorm_partials(40, 128) == 2
     assert lib.gnn_gate_bwd_partials(1 << 20, 256) == 1024
