@@ -568,7 +568,13 @@ __device__ __forceinline__ f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, co
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-template <int CK>
+// FIXED (CK = c_hidden = 128, 128 N NP bytes below 2^31): every wave owns one projection unit
+// and one gate item, the next tile's x is requested unconditionally (the last tile requests
+// itself again) and the a / b / g stores are buffer stores over ranges whose ends drop the
+// lanes past the row, so no memory access sits in a branch: with one, the compiler's
+// memory-counter waits at the join count the path without it, and the waits for the next
+// tile's loads also wait for the stores issued after them.
+template <int CK, bool FIXED>
 __global__ __launch_bounds__(PNT, 1) void trimul_proj_x3_kernel(const gnn_trimul_args a, int64_t NP,
                                                                 size_t off_a, size_t off_b, size_t off_g) {
   typedef ProjX3Lds<CK> S;
@@ -607,8 +613,9 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_x3_kernel(const gnn_trimul
   }
   // ---- once per wave: its projection unit's weights, split (B operand: column = channel
   // 32 * wave + l32, k = 16 kk + 8 g + e)
+  static_assert(!FIXED || (CK == 128 && NGO * PSUB == PW), "FIXED: one unit and one gate item per wave");
   const int npg = 2 * Ch / 32;
-  const bool has_unit = wave < npg;  // uniform over the wave
+  const bool has_unit = FIXED || wave < npg;  // uniform over the wave
   bf16x8 wph[NK], wpl[NK], wgh[NK], wgl[NK];
   float bp = 0.f, bg = 0.f;
   {
@@ -706,6 +713,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_x3_kernel(const gnn_trimul
         f32x16 accp, accg;
 #pragma unroll
         for (int r = 0; r < 16; ++r) accp[r] = accg[r] = 0.f;
+        if (FIXED) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int k = 0; k < NK; ++k) {
           const int o = (32 * s + l32) * ZB + 16 * k + 8 * g;
@@ -717,6 +725,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_x3_kernel(const gnn_trimul
           accp = mfma_bf16(h, wph[k], accp);
           accg = mfma_bf16(h, wgh[k], accg);
         }
+        if (FIXED) __builtin_amdgcn_s_setprio(0);
 #pragma unroll
         for (int rg = 0; rg < 4; ++rg) {
           const int pt = 8 * rg + 4 * g;  // pixel within the sub-tile
@@ -728,6 +737,31 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_x3_kernel(const gnn_trimul
           store4(&ebuf[l32 * ER + pt], v);
         }
         wave_lds_sync();
+        if constexpr (FIXED) {
+          // the unit's 32 channel planes all belong to a or all to b (c_hidden = 128): one
+          // buffer range over them; lanes past the padded row are dropped
+          const bool in_a = 32 * wave < Ch;
+          float* base = (in_a ? a_cm : b_cm) + ab_offset<float>((int64_t)tl.b * Ch + 32 * wave - (in_a ? 0 : Ch), 0, 0, N, NP);
+          const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(base, (int)(32 * (int64_t)N * NP * sizeof(float)));
+          const bool tail_tile = tl.c0 + PTP > N;  // uniform
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const int c = lane + 64 * i;
+            const int crow = c / 4, p0 = (c % 4) * 8;
+            const int k = tl.c0 + 32 * s + p0;
+            f32x8 val = load8(&ebuf[crow * ER + p0]);
+            if (tail_tile) {  // row tail: pixels N .. NP-1 are written as zeros
+#pragma unroll
+              for (int e = 0; e < 8; ++e)
+                if (k + e >= N) val[e] = 0.f;
+            }
+            const uint32_t off = k < NP ? (uint32_t)((crow * N + tl.row) * (int)NP + k) * (uint32_t)sizeof(float) : BUFFER_OOB;
+            buffer_store(f32x4{val[0], val[1], val[2], val[3]}, rs, off);
+            buffer_store(f32x4{val[4], val[5], val[6], val[7]}, rs, off + 16u);
+          }
+          wave_lds_sync();
+          continue;
+        }
         // 32-byte stores, 4 lanes per channel row of 32 pixels
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -755,6 +789,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_x3_kernel(const gnn_trimul
     // 32uo + 8(r/4) + 4g + r%4, col = pixel 32s + l32; staged as [pixel][channel]
 #pragma unroll 1
     for (int it = wave; it < NGO * PSUB; it += PW) {
+      if (FIXED) it = wave;  // one item per wave
       const int uo = it % NGO, s = it / NGO;
       const int c00 = 32 * uo;
       f32x16 accx, acch;  // cross terms, hi * hi
@@ -780,6 +815,25 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_x3_kernel(const gnn_trimul
         store4(&ebuf[l32 * ER + 8 * rg + 4 * g], v);
       }
       wave_lds_sync();
+      if constexpr (FIXED) {
+        // one buffer range from the tile's first pixel to the end of its last one (pixel
+        // stride CK outgoing, N CK incoming): the lanes of pixels past N fall outside it
+        const int pstride = outgoing ? CK : N * CK;
+        const int npix = min(N - tl.c0, PTP);
+        const __amdgpu_buffer_rsrc_t rs =
+            buffer_rsrc(gout + proj_pix(tl, 0, N, outgoing) * CK, ((npix - 1) * pstride + CK) * (int)sizeof(float));
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int c = lane + 64 * i;
+          const int px = c / 4, k0 = (c % 4) * 8;
+          const uint32_t off = (uint32_t)((32 * s + px) * pstride + c00 + k0) * (uint32_t)sizeof(float);
+          const f32x8 val = load8(&ebuf[px * ER + k0]);
+          buffer_store(f32x4{val[0], val[1], val[2], val[3]}, rs, off);
+          buffer_store(f32x4{val[4], val[5], val[6], val[7]}, rs, off + 16u);
+        }
+        wave_lds_sync();
+        break;
+      }
       // 32-byte stores, 4 lanes per 32-channel pixel row segment
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
@@ -807,6 +861,17 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_x3_kernel(const gnn_trimul
     PTile nxt = cur;
     const PTile wt = proj_tile(walk, outgoing);
     walk.step();
+    if constexpr (FIXED) {
+      nxt = has_next ? wt : cur;
+      load_x(nxt);
+      compute(cur);
+      ln_partial();
+      __syncthreads();  // z / mask of this tile consumed, partials of the next one published
+      ln_finish();
+      __syncthreads();
+      cur = nxt;
+      continue;
+    }
     if (has_next) {
       nxt = wt;
       load_x(nxt);
@@ -1614,63 +1679,78 @@ __global__ __launch_bounds__(NT, 2) void trimul_contract_kernel(const T* __restr
     }
 }
 
-// fp32 under bf16x3 (what 'tf32' resolves to on gfx950): the same tiles and schedule as
-// trimul_contract_kernel, but each fp32 stage is split into bf16 hi / lo planes once, where it
-// is written to LDS, so the inner loop reads hi / lo fragments and issues the three bf16
-// MFMAs (lo hi + hi lo + hi hi) with no VALU work; splitting per product instead repeats the
-// split of every fragment for each of the MFMAs that reuse it. The kernel is bound by its
-// fp32 operand traffic, not by the split (72 against 73 us at N = 384). Measured slower: the
-// projection writing a and b as bf16 hi / lo planes in the 16-bit layout and the DMA-fed
-// 16-bit contraction reading both planes (128 x 256 tiles, three 48 KB stages, one workgroup
-// per CU: 81 us).
+// fp32 under bf16x3 (what 'tf32' resolves to on gfx950): trimul_contract_kernel's schedule
+// (one stage of k held in registers while the previous one multiplies), but each fp32 stage
+// is split into bf16 hi / lo planes once, where it is written to LDS, so the inner loop reads
+// hi / lo fragments and issues the three bf16 MFMAs (lo hi + hi lo + hi hi) with no VALU
+// work; splitting per product instead repeats the split of every fragment for each of the
+// MFMAs that reuse it. Tiles of BM x BM output elements, 4 waves of BM / 2 x BM / 2, two
+// workgroups per CU. Each k-stage waits for a global load issued one stage earlier, so the
+// kernel's time is about (tile rounds) x (N / 32 stages) x (load latency): BM = 192 cuts the
+// rounds where the tile count allows (C5's N = 384: 512 tiles of 192 fill the 512 slots
+// once; 1152 tiles of 128 took three rounds). With KFULL (N a multiple of 32) the loads are
+// unconditional: rows past N read row N - 1, whose products land in output rows that are not
+// stored. Measured slower: the projection writing a and b as bf16 hi / lo planes in the
+// 16-bit layout and the DMA-fed 16-bit contraction reading both planes (128 x 256 tiles,
+// three 48 KB stages, one workgroup per CU: 81 us).
+template <int BM>
 struct ContractX3 {
-  static constexpr int BM = 128, BN = 128, BK = 32;
+  static constexpr int BK = 32;
   static constexpr int ROW = BK + 8;  // bf16 elements per LDS row (16 B of padding)
+  static constexpr int WT = BM / 64;  // 32 x 32 MFMA tiles per wave and dimension
+  static constexpr size_t lds_bytes() { return (size_t)4 * BM * ROW * sizeof(bf16); }
 };
 
+template <int BM, bool KFULL>
 __global__ __launch_bounds__(NT, 2) void trimul_contract_x3_kernel(const float* __restrict__ A,
                                                                   const float* __restrict__ Bm,
                                                                   float* __restrict__ O, int N, int64_t NP) {
-  typedef ContractX3 Cfg;
-  __shared__ __align__(16) bf16 ash[Cfg::BM * Cfg::ROW], asl[Cfg::BM * Cfg::ROW];
-  __shared__ __align__(16) bf16 bsh[Cfg::BN * Cfg::ROW], bsl[Cfg::BN * Cfg::ROW];
+  typedef ContractX3<BM> Cfg;
+  constexpr int WT = Cfg::WT;
+  __shared__ __align__(16) bf16 ash[BM * Cfg::ROW], asl[BM * Cfg::ROW];
+  __shared__ __align__(16) bf16 bsh[BM * Cfg::ROW], bsl[BM * Cfg::ROW];
 
-  const int nti = (N + Cfg::BM - 1) / Cfg::BM;
-  const int ntj = (N + Cfg::BN - 1) / Cfg::BN;
+  const int nt = (N + BM - 1) / BM;
   const uint32_t w = xcd_remap(blockIdx.x, gridDim.x);
-  const int tj = w % ntj;
-  const int ti = (w / ntj) % nti;
-  const int64_t plane = w / ((uint32_t)ntj * nti);
+  const int tj = w % nt;
+  const int ti = (w / nt) % nt;
+  const int64_t plane = w / ((uint32_t)nt * nt);
   const int64_t poff = plane * N * NP;
   const float* Ap = A + poff;
   const float* Bp = Bm + poff;
   float* Op = O + poff;
-  const int i0 = ti * Cfg::BM, j0 = tj * Cfg::BN;
+  const int i0 = ti * BM, j0 = tj * BM;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
   const int wm = wave >> 1, wn = wave & 1;
 
-  constexpr int CPR = Cfg::BK / 8;        // 8-element chunks per row per stage
-  constexpr int CH = Cfg::BM * CPR / NT;  // chunks per thread per operand
+  constexpr int CPR = Cfg::BK / 8;   // 8-element chunks per row per stage
+  constexpr int CH = BM * CPR / NT;  // chunks per thread per operand
+  static_assert(CH * NT == BM * CPR, "whole chunks per thread");
   f32x8 ra[CH], rb[CH];
   auto load = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + i * NT;
       const int r = c / CPR, kc = k0 + (c % CPR) * 8;
-      ra[i] = f32x8{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      rb[i] = ra[i];
-      if (kc < N) {
-        if (kc + 8 <= N) {
-          if (i0 + r < N) ra[i] = load8(Ap + (int64_t)(i0 + r) * NP + kc);
-          if (j0 + r < N) rb[i] = load8(Bp + (int64_t)(j0 + r) * NP + kc);
-        } else {
+      if constexpr (KFULL) {
+        ra[i] = load8(Ap + (int64_t)min(i0 + r, N - 1) * NP + kc);
+        rb[i] = load8(Bp + (int64_t)min(j0 + r, N - 1) * NP + kc);
+      } else {
+        ra[i] = f32x8{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        rb[i] = ra[i];
+        if (kc < N) {
+          if (kc + 8 <= N) {
+            if (i0 + r < N) ra[i] = load8(Ap + (int64_t)(i0 + r) * NP + kc);
+            if (j0 + r < N) rb[i] = load8(Bp + (int64_t)(j0 + r) * NP + kc);
+          } else {
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (kc + e < N) {
-              if (i0 + r < N) ra[i][e] = Ap[(int64_t)(i0 + r) * NP + kc + e];
-              if (j0 + r < N) rb[i][e] = Bp[(int64_t)(j0 + r) * NP + kc + e];
-            }
+            for (int e = 0; e < 8; ++e)
+              if (kc + e < N) {
+                if (i0 + r < N) ra[i][e] = Ap[(int64_t)(i0 + r) * NP + kc + e];
+                if (j0 + r < N) rb[i][e] = Bp[(int64_t)(j0 + r) * NP + kc + e];
+              }
+          }
         }
       }
     }
@@ -1690,11 +1770,11 @@ __global__ __launch_bounds__(NT, 2) void trimul_contract_x3_kernel(const float* 
     }
   };
 
-  f32x16 acc[2][2];
+  f32x16 acc[WT][WT];
 #pragma unroll
-  for (int x = 0; x < 2; ++x)
+  for (int x = 0; x < WT; ++x)
 #pragma unroll
-    for (int y = 0; y < 2; ++y)
+    for (int y = 0; y < WT; ++y)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
 
@@ -1707,43 +1787,40 @@ __global__ __launch_bounds__(NT, 2) void trimul_contract_x3_kernel(const float* 
     if (has_next) load((kt + 1) * Cfg::BK);
 #pragma unroll
     for (int kk = 0; kk < Cfg::BK / 16; ++kk) {
-      bf16x8 ah[2], al[2], bh[2], bl[2];
+      bf16x8 bh[WT], bl[WT];
 #pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        const int o = (64 * wm + 32 * x + l32) * Cfg::ROW + 16 * kk + 8 * g;
-        ah[x] = load8(&ash[o]);
-        al[x] = load8(&asl[o]);
-      }
-#pragma unroll
-      for (int y = 0; y < 2; ++y) {
-        const int o = (64 * wn + 32 * y + l32) * Cfg::ROW + 16 * kk + 8 * g;
+      for (int y = 0; y < WT; ++y) {
+        const int o = ((BM / 2) * wn + 32 * y + l32) * Cfg::ROW + 16 * kk + 8 * g;
         bh[y] = load8(&bsh[o]);
         bl[y] = load8(&bsl[o]);
       }
 #pragma unroll
-      for (int x = 0; x < 2; ++x)
+      for (int x = 0; x < WT; ++x) {
+        const int o = ((BM / 2) * wm + 32 * x + l32) * Cfg::ROW + 16 * kk + 8 * g;
+        const bf16x8 ah = load8(&ash[o]), al = load8(&asl[o]);
 #pragma unroll
-        for (int y = 0; y < 2; ++y) {
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[x], bh[y], acc[x][y], 0, 0, 0);
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[x], bl[y], acc[x][y], 0, 0, 0);
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[x], bh[y], acc[x][y], 0, 0, 0);
+        for (int y = 0; y < WT; ++y) {
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh[y], acc[x][y], 0, 0, 0);
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl[y], acc[x][y], 0, 0, 0);
+          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh[y], acc[x][y], 0, 0, 0);
         }
+      }
     }
     __syncthreads();
     if (has_next) store();
     __syncthreads();
   }
 
-  // acc[x][y][r] = o[i0 + 64wm + 32x + 8(r/4) + 4g + r%4][j0 + 64wn + 32y + l32]
+  // acc[x][y][r] = o[i0 + (BM / 2)wm + 32x + 8(r/4) + 4g + r%4][j0 + (BM / 2)wn + 32y + l32]
 #pragma unroll
-  for (int x = 0; x < 2; ++x)
+  for (int x = 0; x < WT; ++x)
 #pragma unroll
-    for (int y = 0; y < 2; ++y) {
-      const int j = j0 + 64 * wn + 32 * y + l32;
+    for (int y = 0; y < WT; ++y) {
+      const int j = j0 + (BM / 2) * wn + 32 * y + l32;
       if (j >= N) continue;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int i = i0 + 64 * wm + 32 * x + 8 * (r / 4) + 4 * g + (r % 4);
+        const int i = i0 + (BM / 2) * wm + 32 * x + 8 * (r / 4) + 4 * g + (r % 4);
         if (i < N) Op[(int64_t)i * NP + j] = acc[x][y][r];
       }
     }
@@ -2486,25 +2563,31 @@ int launch_proj_pp(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t 
   return (int)hipGetLastError();
 }
 
-template <int CK>
+template <int CK, bool FIXED>
 int launch_proj_x3(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
   const int64_t NP = round_up(a.N, 32);
   const int64_t ntiles = a.B * a.N * ((a.N + PTP - 1) / PTP);
   constexpr size_t smem = ProjX3Lds<CK>::total;
-  const void* fn = (const void*)trimul_proj_x3_kernel<CK>;
+  const void* fn = (const void*)trimul_proj_x3_kernel<CK, FIXED>;
   (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   const int64_t grid = std::min<int64_t>(ntiles, persistent_grid(fn, PNT, smem));
-  hipLaunchKernelGGL((trimul_proj_x3_kernel<CK>), dim3((uint32_t)grid), dim3(PNT), smem, st, a, NP, L.off_a,
-                     L.off_b, L.off_g);
+  hipLaunchKernelGGL((trimul_proj_x3_kernel<CK, FIXED>), dim3((uint32_t)grid), dim3(PNT), smem, st, a, NP,
+                     L.off_a, L.off_b, L.off_g);
   return (int)hipGetLastError();
 }
 
+#ifndef GNN_PROJX3_FIXED
+#define GNN_PROJX3_FIXED 1
+#endif
 template <typename T, int PREC>
 int launch_proj(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st) {
   if constexpr (sizeof(T) == 4 && PREC == PREC_BF16X3) {
     if (2 * a.Ch <= 32 * PW) {  // one projection unit per wave
-      if (a.C == 128) return launch_proj_x3<128>(a, L, st);
-      if (a.C == 64) return launch_proj_x3<64>(a, L, st);
+      // c_hidden = 128 takes buffer stores over ranges of 32 channel planes (128 N NP bytes)
+      if (GNN_PROJX3_FIXED && a.C == 128 && a.Ch == 128 && 128 * a.N * round_up(a.N, 32) < ((int64_t)1 << 31))
+        return launch_proj_x3<128, true>(a, L, st);
+      if (a.C == 128) return launch_proj_x3<128, false>(a, L, st);
+      if (a.C == 64) return launch_proj_x3<64, false>(a, L, st);
     }
   }
   if constexpr (sizeof(T) == 2) {
@@ -2534,6 +2617,42 @@ int launch_contract_dma(const gnn_trimul_args& a, const TrimulLayout& L, hipStre
   return (int)hipGetLastError();
 }
 
+// fp32 under bf16x3: the tile edge with fewer rounds of workgroups over the device's
+// resident slots (each kernel's own occupancy: 162 VGPRs give the 128-tile kernel three
+// workgroups per CU, 256 give the 192-tile kernel two; ties keep 128, whose stages multiply
+// faster); GNN_CONTRACT_X3_BM = 128 or
+// 192 forces one.
+#ifndef GNN_CONTRACT_X3_BM
+#define GNN_CONTRACT_X3_BM 0
+#endif
+template <int BM>
+int launch_contract_x3_bm(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st, int64_t NP,
+                          int64_t nblk) {
+  unsigned char* ws = (unsigned char*)a.workspace;
+  const float* A = (const float*)(ws + L.off_a);
+  const float* Bm = (const float*)(ws + L.off_b);
+  float* O = (float*)(ws + L.off_o);
+  if (a.N % ContractX3<BM>::BK == 0)
+    hipLaunchKernelGGL((trimul_contract_x3_kernel<BM, true>), dim3((uint32_t)nblk), dim3(NT), 0, st, A, Bm, O,
+                       (int)a.N, NP);
+  else
+    hipLaunchKernelGGL((trimul_contract_x3_kernel<BM, false>), dim3((uint32_t)nblk), dim3(NT), 0, st, A, Bm, O,
+                       (int)a.N, NP);
+  return (int)hipGetLastError();
+}
+
+int launch_contract_x3(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t st, int64_t NP) {
+  auto tiles = [&](int64_t bm) { return a.B * a.Ch * ((a.N + bm - 1) / bm) * ((a.N + bm - 1) / bm); };
+  const int64_t t128 = tiles(128), t192 = tiles(192);
+  int bm = GNN_CONTRACT_X3_BM;
+  if (bm != 128 && bm != 192) {
+    const int64_t s128 = persistent_grid((const void*)trimul_contract_x3_kernel<128, true>, NT, 0);
+    const int64_t s192 = persistent_grid((const void*)trimul_contract_x3_kernel<192, true>, NT, 0);
+    bm = (t192 + s192 - 1) / s192 < (t128 + s128 - 1) / s128 ? 192 : 128;
+  }
+  return bm == 192 ? launch_contract_x3_bm<192>(a, L, st, NP, t192) : launch_contract_x3_bm<128>(a, L, st, NP, t128);
+}
+
 // Smallest N that takes the 256-row contraction tile. Measured at N = 512: the 128-row tile
 // is faster on warm inputs (43.8 against 48.5 us) but slower inside the step (56 against
 // 49 us), where a and b arrive from the projection kernel rather than from the cache.
@@ -2552,10 +2671,7 @@ int launch_contract(const gnn_trimul_args& a, const TrimulLayout& L, hipStream_t
   const int64_t nblk = a.B * a.Ch * ((a.N + Cfg::BM - 1) / Cfg::BM) * ((a.N + Cfg::BN - 1) / Cfg::BN);
   unsigned char* ws = (unsigned char*)a.workspace;
   if constexpr (sizeof(T) == 4 && PREC == PREC_BF16X3) {
-    static_assert(ContractX3::BM == Cfg::BM && ContractX3::BN == Cfg::BN, "same tiles as the fp32 kernel");
-    hipLaunchKernelGGL(trimul_contract_x3_kernel, dim3((uint32_t)nblk), dim3(NT), 0, st,
-                       (const float*)(ws + L.off_a), (const float*)(ws + L.off_b), (float*)(ws + L.off_o),
-                       (int)a.N, NP);
+    return launch_contract_x3(a, L, st, NP);
   } else {
     hipLaunchKernelGGL((trimul_contract_kernel<T, PREC>), dim3((uint32_t)nblk), dim3(NT), 0, st,
                        (const T*)(ws + L.off_a), (const T*)(ws + L.off_b), (T*)(ws + L.off_o), (int)a.N,

@@ -433,6 +433,22 @@ def test_odd_channel_widths(direction, dtype, c_z, c_hidden):
                            rel_fro_max=None if dtype == torch.float32 else NORTH_STAR_REL_FRO)
 
 
+@pytest.mark.parametrize(("b", "n", "direction"), [(2, 150, "incoming"), (1, 288, "outgoing")],
+                         ids=["b2_n150_incoming", "b1_n288_outgoing"])
+def test_fp32_tf32_contraction_tiles(b, n, direction):
+    """fp32 under 'tf32' at sizes where the contraction takes 192-row tiles (on a 256-CU
+    device the 192-row kernel holds two workgroups per CU, the 128-row one three; B = 2,
+    N = 150: 256 tiles of 192 against 1024 of 128, one round against two; B = 1, N = 288:
+    512 against 1152). N = 150 has one partial tile and guarded k-tail loads, N = 288 a
+    whole tile, a ragged second one (96 rows) and unconditional loads; against the fp64
+    oracle."""
+    w = trimul_weights(128, 128, torch.float32, seed=45, biases=True, ln_random=True)
+    x, mask = pair_input(b, n, 128, torch.float32, seed=46)
+    with matmul_precision("tf32"):
+        got = hip(x, direction, mask, w)
+    assert_close_to_oracle("out", got, oracle(x, direction, mask, w), TRIMUL_TOL[torch.float32, "tf32"])
+
+
 @DIRECTIONS
 @pytest.mark.parametrize(("c_z", "c_hidden"), [(128, 128), (128, 64), (64, 32), (100, 70)],
                          ids=["128_128", "128_64", "64_32", "odd_100_70"])
