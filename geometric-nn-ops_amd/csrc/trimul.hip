@@ -1698,7 +1698,6 @@ struct ContractX3 {
   static constexpr int BK = 32;
   static constexpr int ROW = BK + 8;  // bf16 elements per LDS row (16 B of padding)
   static constexpr int WT = BM / 64;  // 32 x 32 MFMA tiles per wave and dimension
-  static constexpr size_t lds_bytes() { return (size_t)4 * BM * ROW * sizeof(bf16); }
 };
 
 template <int BM, bool KFULL>
