@@ -141,8 +141,17 @@ __device__ __forceinline__ typename TypeOps<T>::V8 load8_bias_tail(const T* row,
 // the store, so a later wait for a load issued before that store also waits for the store.
 constexpr uint32_t BUFFER_RSRC_WORD3 = 0x00020000;  // raw, unswizzled buffer
 constexpr uint32_t BUFFER_OOB = 0x80000000u;
+// base and range_bytes must be the same for every lane of the wave. They pass through
+// readfirstlane: where the compiler keeps them in vector registers (tile coordinates it
+// cannot prove uniform) it would otherwise wrap every store in a loop over the lanes'
+// distinct descriptors (readfirstlane, compare, exec mask, branch back).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int range_bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, range_bytes, BUFFER_RSRC_WORD3);
+  const uint64_t p = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  void* u = (void*)(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, __builtin_amdgcn_readfirstlane(range_bytes),
+                                           BUFFER_RSRC_WORD3);
 }
 template <typename V>
 __device__ __forceinline__ void buffer_store(const V& v, __amdgpu_buffer_rsrc_t r, uint32_t off) {

@@ -593,7 +593,10 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_x3_kernel(const gnn_trimul
   float* bgo = reinterpret_cast<float*>(smem_raw + S::bgo);
   float* mk = reinterpret_cast<float*>(smem_raw + S::mk);
   const int Ch = (int)a.Ch, N = (int)a.N;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, g = lane >> 5;
+  // wave from readfirstlane: the buffer-store resources built from it are then scalar (a
+  // resource the compiler cannot prove uniform costs a loop over its distinct values per store)
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l32 = lane & 31,
+            g = lane >> 5;
   float* ebuf = reinterpret_cast<float*>(smem_raw + S::ebuf) + wave * 32 * ER;
   const bool outgoing = a.outgoing != 0;
   const int64_t ntiles = (int64_t)a.B * N * ((N + PTP - 1) / PTP);
@@ -708,7 +711,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_x3_kernel(const gnn_trimul
     // gated projection unit: acc = [pixel][channel], row = pixel 32s + 8(r/4) + 4g + r%4,
     // col = channel 32 * wave + l32; staged as [channel][pixel] for 128-byte row stores
     if (has_unit) {
-#pragma unroll 1
+#pragma unroll FIXED ? PSUB : 1  // FIXED: the store count behind the x loads is then known
       for (int s = 0; s < PSUB; ++s) {
         f32x16 accp, accg;
 #pragma unroll
@@ -788,8 +791,7 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_x3_kernel(const gnn_trimul
     // output-gate items (unit uo, sub-tile s): acc = [channel][pixel], row = channel
     // 32uo + 8(r/4) + 4g + r%4, col = pixel 32s + l32; staged as [pixel][channel]
 #pragma unroll 1
-    for (int it = wave; it < NGO * PSUB; it += PW) {
-      if (FIXED) it = wave;  // one item per wave
+    for (int it = wave; FIXED || it < NGO * PSUB; it += PW) {  // FIXED: item `wave`, always
       const int uo = it % NGO, s = it / NGO;
       const int c00 = 32 * uo;
       f32x16 accx, acch;  // cross terms, hi * hi
