@@ -1055,7 +1055,11 @@ __global__ __launch_bounds__(PNT, 1) void trimul_proj_fast_kernel(const gnn_trim
     for (int k = 0; k < NKS; ++k) asm volatile("" ::"v"(wpf[k]), "v"(wgf[k]));
     asm volatile("" ::"v"(bp), "v"(bg));
   }
-  const bool has_go = wave < NGI;
+  // FIXED (C = c_hidden = 128): 8 gate items for 8 waves, so every wave has one, and the gate
+  // stores are unconditional (a store under a condition makes the next tile's LayerNorm wait
+  // for the unit's stores as well)
+  static_assert(!FIXED || NGI == PW, "FIXED: one gate item per wave");
+  const bool has_go = FIXED || wave < NGI;
   const int uo = wave % (CK / 32), so = wave / (CK / 32);  // this wave's gate item
 
   // the unit's sub-tiles in the order (so, 1 - so): the gate item's sub-tile first
