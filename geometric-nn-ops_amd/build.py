@@ -35,6 +35,15 @@ HIPCC_FLAGS = [
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]
+# Per-source flags. The row-resident attention kernel schedules for instruction-level
+# parallelism (LLVM's AMDGPU max-ilp machine scheduler): 1.5-2 us (1%) less per forward
+# inside the headline step (174.1 -> 172.0 us on one box, 177.3 / 176.8 -> 175.7 / 174.6 on
+# another), at the same 128 VGPRs without spills. The same strategy on trimul.hip slowed the contraction and output stages
+# (+0.7 and +1.5 us) more than it sped up the projection (-0.5 us), and the
+# memory-clause strategy slowed the fp32 'tf32' block (0.815 -> 0.868 ms).
+FILE_FLAGS = {
+    "triattn_row.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+}
 
 
 def hipcc() -> str:
@@ -50,7 +59,7 @@ def hipcc() -> str:
 
 def _compile(src: pathlib.Path, build_dir: pathlib.Path = BUILD_DIR, extra=()) -> pathlib.Path:
     obj = build_dir / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, ()), *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
