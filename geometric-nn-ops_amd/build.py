@@ -40,7 +40,8 @@ HIPCC_FLAGS = [
 # inside the headline step (174.1 -> 172.0 us on one box, 177.3 / 176.8 -> 175.7 / 174.6 on
 # another), at the same 128 VGPRs without spills. The same strategy on trimul.hip slowed the contraction and output stages
 # (+0.7 and +1.5 us) more than it sped up the projection (-0.5 us), and the
-# memory-clause strategy slowed the fp32 'tf32' block (0.815 -> 0.868 ms).
+# memory-clause strategy slowed the fp32 'tf32' block (0.815 -> 0.868 ms). max-ilp on the
+# backward files slowed the attention and trimul backward passes.
 FILE_FLAGS = {
     "triattn_row.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
 }
